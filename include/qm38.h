@@ -1,0 +1,263 @@
+/*
+ * qm38 — MI355X (gfx950) per-token compute path of a Qwen3.8-style hybrid
+ * model: MLX affine-Q4 projections, paged Q8-KV GQA attention and the Gated
+ * DeltaNet conv/recurrent update.
+ *
+ * This is the drop-in C ABI.  Every entry point mirrors one method of the
+ * reference runtime (`MetalRuntime` in /root/reference/src/metal_runtime.rs)
+ * and cites the function it replaces.  The ABI is plain C: device pointers,
+ * sizes and opaque handles, no C++ or torch types.
+ *
+ * Conventions
+ *   - Activation/output pointers are DEVICE pointers (hipMalloc'd or any
+ *     allocator's HBM).  Weight creation helpers take HOST pointers, like the
+ *     reference's `create_*` constructors, and upload them.
+ *   - bf16 values travel as uint16_t bit patterns (bf16 -> f32 is `bits<<16`,
+ *     f32 -> bf16 is round-to-nearest-even, reference qwen38.metal:18-26).
+ *   - Every call is enqueued on the runtime's stream (qm_runtime_set_stream)
+ *     and is asynchronous unless stated otherwise; qm_runtime_synchronize
+ *     waits for completion (the reference's commit()+wait_until_completed()).
+ *   - Calls that share one runtime must not overlap from several threads on
+ *     the same stream unless the caller serialises them; distinct runtimes are
+ *     independent.  Errors are returned as qm_status and the message of the
+ *     last error on the calling thread is available from
+ *     qm_last_error_message().
+ */
+#ifndef QM38_H
+#define QM38_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  One code per variant of MetalRuntimeError
+ * (metal_runtime.rs:9219-9247) that can occur on this path, plus the
+ * LogicalPageTable errors (paged_kv.rs:100-105). */
+typedef enum qm_status {
+  QM_OK = 0,
+  QM_ERR_NO_DEVICE = 1,             /* MetalRuntimeError::NoDevice */
+  QM_ERR_EMPTY_DIMENSION = 2,       /* ::EmptyDimension */
+  QM_ERR_INPUT_NOT_GROUPED = 3,     /* ::InputNotGrouped */
+  QM_ERR_WRONG_LENGTH = 4,          /* ::WrongLength */
+  QM_ERR_INVALID_DELTANET_CONFIG = 5, /* ::InvalidDeltaNetConfig */
+  QM_ERR_INVALID_ATTENTION_SHAPE = 6, /* ::InvalidAttentionShape */
+  QM_ERR_INVALID_SEQUENCE_LENGTH = 7, /* ::InvalidSequenceLength */
+  QM_ERR_INVALID_BUFFER_OFFSET = 8,   /* ::InvalidBufferOffset */
+  QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE = 9, /* ::MappedTensorOutOfRange */
+  QM_ERR_DIMENSION_OVERFLOW = 10,   /* ::DimensionOverflow */
+  QM_ERR_COMMAND_FAILED = 11,       /* ::CommandFailed (HIP launch/runtime error) */
+  QM_ERR_ZERO_CAPACITY = 12,        /* PageTableError::ZeroCapacity */
+  QM_ERR_EMPTY_APPEND = 13,         /* PageTableError::EmptyAppend */
+  QM_ERR_CAPACITY_EXCEEDED = 14,    /* PageTableError::CapacityExceeded */
+  QM_ERR_NULL_POINTER = 15,         /* a required pointer argument is NULL */
+  QM_ERR_OUT_OF_MEMORY = 16,        /* device allocation failed */
+  QM_ERR_MISALIGNED = 17,           /* a device pointer violates the documented alignment */
+  QM_ERR_INVALID_ARGUMENT = 18      /* any other precondition */
+} qm_status;
+
+/* Human-readable name of a status code (static storage). */
+const char* qm_status_string(qm_status status);
+/* Message describing the last error raised on the calling thread. */
+const char* qm_last_error_message(void);
+
+/* ------------------------------------------------------------------ */
+/* Runtime                                                             */
+/* ------------------------------------------------------------------ */
+typedef struct qm_runtime qm_runtime;
+
+/* Replaces MetalRuntime::new (metal_runtime.rs:641-927): binds HIP device
+ * `device`, creates the runtime's scratch pools.  The default stream is the
+ * device's null stream. */
+qm_status qm_runtime_create(int device, qm_runtime** out);
+void qm_runtime_destroy(qm_runtime* rt);
+/* Enqueue all later work of `rt` on `hip_stream` (a hipStream_t; NULL selects
+ * the null stream).  The stream must belong to the runtime's device. */
+qm_status qm_runtime_set_stream(qm_runtime* rt, void* hip_stream);
+/* Blocks until all work enqueued by `rt` has finished; surfaces asynchronous
+ * kernel failures as QM_ERR_COMMAND_FAILED (the reference checks
+ * MTLCommandBufferStatus::Error after wait_until_completed, e.g.
+ * metal_runtime.rs:3660-3665). */
+qm_status qm_runtime_synchronize(qm_runtime* rt);
+
+/* Device buffers owned by the runtime's allocator (256-byte aligned).
+ * Replaces the reference's buffer_from_slice / map_weight_store
+ * (metal_runtime.rs:955-984): on MI355X weights must be resident in HBM, so
+ * the upload realigns them and the reference's byte-addressed `_unaligned`
+ * kernel twins are unnecessary. */
+qm_status qm_device_alloc(qm_runtime* rt, size_t bytes, void** out);
+qm_status qm_device_free(qm_runtime* rt, void* ptr);
+qm_status qm_upload(qm_runtime* rt, const void* host, size_t bytes, void** out);
+/* Synchronous copies between host and device memory on the runtime stream. */
+qm_status qm_copy_to_device(qm_runtime* rt, void* dst, const void* host, size_t bytes);
+qm_status qm_copy_to_host(qm_runtime* rt, void* host, const void* src, size_t bytes);
+
+/* ------------------------------------------------------------------ */
+/* MLX affine-Q4 projections                                           */
+/* ------------------------------------------------------------------ */
+/* One Q4 projection (replaces MappedQ4AffineJob, metal_runtime.rs:155-192).
+ * Layout (native.rs:5384-5516): `weights` u32 [out_rows][in/8], eight 4-bit
+ * values per word, low nibble first; `scales`/`biases` bf16
+ * [out_rows][in/64].  Device pointers; weights and scales/biases must be
+ * 8-byte aligned. */
+typedef struct qm_q4_job {
+  const uint32_t* weights;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  uint32_t out_rows;
+} qm_q4_job;
+
+/* y_j[m][n] = sum_g ( s_j[n][g] * sum_{i in g} q_j[n][i] x[m][i]
+ *                    + b_j[n][g] * sum_{i in g} x[m][i] )
+ * for every job j, all jobs reading the same activation x (bf16 [M][in]).
+ * outputs[j] is bf16 [M][out_rows_j].  fp32 accumulation.
+ * Replaces q4_affine_matvec_mapped_batch (metal_runtime.rs:3599) for M == 1
+ * and q4_affine_matmul_mapped_batch (metal_runtime.rs:3683) for M > 1; rows
+ * M <= 16 take the decode (weight-streaming) kernel, larger M the tiled MFMA
+ * GEMM.  n_jobs <= 8. */
+qm_status qm_q4_project(qm_runtime* rt, const qm_q4_job* jobs, int n_jobs,
+                        const uint16_t* x, uint32_t in_elems, uint32_t M,
+                        uint16_t* const* outputs);
+
+/* h[m][n] = bf16( silu(gate(x)[m][n]) * up(x)[m][n] ): the gate and up
+ * projections of one MLP share the activation read and SwiGLU
+ * (qwen38.metal:4188-4199, silu at 4090-4096) runs in the epilogue.
+ * gate.out_rows must equal up.out_rows.  Replaces the pair kernels
+ * (qwen38.metal:1404..3643, encode_q4_affine_matmul_pair
+ * metal_runtime.rs:6372). */
+qm_status qm_q4_swiglu(qm_runtime* rt, const qm_q4_job* gate, const qm_q4_job* up,
+                       const uint16_t* x, uint32_t in_elems, uint32_t M,
+                       uint16_t* h);
+
+/* y = down( silu(gate(x)) * up(x) ): replaces q4_affine_mlp_mapped_batch
+ * (metal_runtime.rs:4479-4689).  The bf16 intermediate h [M][gate.out_rows]
+ * lives in runtime scratch.  down's input width must equal gate.out_rows. */
+qm_status qm_q4_mlp(qm_runtime* rt, const qm_q4_job* gate, const qm_q4_job* up,
+                    const qm_q4_job* down, const uint16_t* x, uint32_t in_elems,
+                    uint32_t M, uint16_t* y);
+
+/* ------------------------------------------------------------------ */
+/* Paged Q8 KV cache                                                   */
+/* ------------------------------------------------------------------ */
+typedef struct qm_kv qm_kv;
+
+/* Replaces create_q8_kv_state (metal_runtime.rs:7298) and
+ * LogicalPageTable::new (paged_kv.rs:22-35).  K/V are int8 with one fp32
+ * scale per token and KV head.  Physical layout (HBM), per page of
+ * `page_tokens` tokens:
+ *   K pages  int8 [page][kv_head][page_tokens][head_dim]
+ *   V pages  int8 [page][kv_head][head_dim][page_tokens]   (d-major)
+ *   scales   fp32 [page][kv_head][page_tokens]  (one array for K, one for V)
+ * Pages materialise lazily as tokens arrive and receive sequential page ids
+ * (paged_kv.rs:89-97).  page_tokens must be 16; head_dim must be 128 or 64
+ * (multiple of 32, <= 256 in the reference's validate_attention_shape,
+ * metal_runtime.rs:9186-9193).  max_tokens bounds the sequence length. */
+qm_status qm_kv_create(qm_runtime* rt, uint32_t kv_heads, uint32_t head_dim,
+                       uint32_t page_tokens, uint32_t max_tokens, qm_kv** out);
+void qm_kv_destroy(qm_kv* kv);
+/* Active sequence length (Q8KvState::sequence_length, metal_runtime.rs:595). */
+uint32_t qm_kv_length(const qm_kv* kv);
+/* Number of materialised pages (LogicalPageTable::allocated_pages). */
+uint32_t qm_kv_allocated_pages(const qm_kv* kv);
+/* Physical page id backing `token`, or -1 if token >= length
+ * (LogicalPageTable::page_for_token, paged_kv.rs:77-85). */
+int64_t qm_kv_page_for_token(const qm_kv* kv, uint32_t token);
+/* Ensures capacity for `additional` more tokens (reserve_q8_kv_tokens,
+ * metal_runtime.rs:7307-7317): materialises the pages they will need. */
+qm_status qm_kv_reserve(qm_kv* kv, uint32_t additional);
+/* Moves the logical end backwards (truncate_q8_kv_tokens, :7323-7333). */
+qm_status qm_kv_truncate(qm_kv* kv, uint32_t length);
+/* Copies the active prefix into a new cache (clone_q8_kv_state, :7338-7379). */
+qm_status qm_kv_clone(const qm_kv* src, qm_kv** out);
+/* Copies the active tokens' K/V bytes and scales out in the reference's
+ * contiguous token-major layout (Q8KvState, metal_runtime.rs:578-593):
+ * keys/values int8 [len][kv_heads][head_dim], scales fp32 [len][kv_heads].
+ * Host pointers; synchronous.  Any pointer may be NULL to skip it. */
+qm_status qm_kv_read(const qm_kv* kv, int8_t* keys, int8_t* values,
+                     float* key_scales, float* value_scales);
+
+/* Decode attention for a ragged batch of B sequences (B <= 64): appends one
+ * token per sequence (quantised K/V, qwen38_q8_kv_append, qwen38.metal:
+ * 5031-5080) and attends over the whole cache including it.
+ *   q    bf16 [B][H][head_dim]      gate bf16 [B][H][head_dim] or NULL
+ *   k, v fp32 [B][kv_heads][head_dim]
+ *   o    bf16 [B][H][head_dim] = softmax(q K^T / sqrt(d)) V * sigmoid(gate)
+ * Replaces gqa_attention_q8 (metal_runtime.rs:8230-8425; kernels
+ * qwen38_gqa_q8_scores/values, qwen38.metal:5240-5323).  All sequences must
+ * share kv_heads/head_dim; H % kv_heads == 0. */
+qm_status qm_attn_decode(qm_runtime* rt, qm_kv* const* seqs, uint32_t B,
+                         const uint16_t* q, const uint16_t* gate,
+                         const float* k, const float* v, uint32_t H,
+                         uint16_t* o);
+
+/* Causal prefill of M new rows: appends them (qwen38_q8_kv_append_prefill,
+ * qwen38.metal:5085-5140) and computes, for row i, attention over the first
+ * min(start+i+1, total) tokens (qwen38_gqa_q8_prefill_attention,
+ * qwen38.metal:5146-5238).  Layouts as qm_attn_decode with B replaced by M.
+ * Replaces gqa_attention_q8_prefill (metal_runtime.rs:8598). */
+qm_status qm_attn_prefill(qm_runtime* rt, qm_kv* seq, const uint16_t* q,
+                          const uint16_t* gate, const float* k, const float* v,
+                          uint32_t H, uint32_t M, uint16_t* o);
+
+/* ------------------------------------------------------------------ */
+/* Gated DeltaNet                                                      */
+/* ------------------------------------------------------------------ */
+/* DeltaNetConfig (metal_runtime.rs:487-494). */
+typedef struct qm_dn_config {
+  uint32_t key_heads;
+  uint32_t value_heads;
+  uint32_t key_head_dim;
+  uint32_t value_head_dim;
+  uint32_t conv_kernel_size;
+} qm_dn_config;
+
+typedef struct qm_dn_weights qm_dn_weights;
+typedef struct qm_dn_state qm_dn_state;
+
+/* Replaces create_deltanet_weights (metal_runtime.rs:7143-7183).  HOST
+ * pointers: conv_weight fp32 [channels][kernel], a_log/dt_bias fp32
+ * [value_heads], norm fp32 [value_head_dim]; channels =
+ * 2*key_heads*key_head_dim + value_heads*value_head_dim.  This build's
+ * kernels need key_head_dim == value_head_dim == 128 and kernel <= 8. */
+qm_status qm_dn_weights_create(qm_runtime* rt, const qm_dn_config* cfg,
+                               const float* conv_weight, const float* a_log,
+                               const float* dt_bias, const float* norm,
+                               qm_dn_weights** out);
+void qm_dn_weights_destroy(qm_dn_weights* w);
+/* Replaces create_deltanet_state (:7185-7199): zeroed conv history fp32
+ * [channels][kernel-1] and recurrent state fp32
+ * [value_heads][value_head_dim][key_head_dim]. */
+qm_status qm_dn_state_create(qm_runtime* rt, const qm_dn_weights* w, qm_dn_state** out);
+void qm_dn_state_destroy(qm_dn_state* st);
+/* Replaces clone_deltanet_state (:7287-7296). */
+qm_status qm_dn_state_clone(const qm_dn_state* src, qm_dn_state** out);
+/* Synchronous host copies of the current state (either pointer may be NULL). */
+qm_status qm_dn_state_read(const qm_dn_state* st, float* conv_history, float* recurrent);
+qm_status qm_dn_state_write(qm_dn_state* st, const float* conv_history, const float* recurrent);
+
+/* One decode token (replaces deltanet_step, metal_runtime.rs:7459-7636;
+ * kernels qwen38_deltanet_conv/prepare/recurrence/gate_norm,
+ * qwen38.metal:4376-4527).  Device pointers: qkv fp32 [channels], z fp32
+ * [value_heads*value_head_dim], b and a fp32 [value_heads]; out fp32
+ * [value_heads*value_head_dim]. */
+qm_status qm_dn_step(qm_runtime* rt, const qm_dn_weights* w, qm_dn_state* st,
+                     const float* qkv, const float* z, const float* b,
+                     const float* a, float epsilon, float* out);
+
+/* Causal prefill of M tokens with a chunked scan that equals M applications
+ * of qm_dn_step (replaces deltanet_prefill / deltanet_prefill_from,
+ * metal_runtime.rs:7933-7990, kernel qwen38_deltanet_prefill
+ * qwen38.metal:4530-4758).  `from` (may be NULL, meaning `to`) supplies the
+ * initial state and is not modified unless it is `to`.  Layouts as
+ * qm_dn_step with a leading [M] dimension. */
+qm_status qm_dn_prefill(qm_runtime* rt, const qm_dn_weights* w,
+                        const qm_dn_state* from, qm_dn_state* to,
+                        const float* qkv, const float* z, const float* b,
+                        const float* a, uint32_t M, float epsilon, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QM38_H */

@@ -1,0 +1,166 @@
+// qm38 C-ABI runtime: object lifetimes, argument validation and kernel
+// dispatch.  Mirrors the entry points of MetalRuntime
+// (/root/reference/src/metal_runtime.rs); each function below cites the one it
+// replaces in include/qm38.h.
+#include "runtime_internal.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+using namespace qm;
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+qm_status qm::fail(qm_status status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = std::string(qm_status_string(status)) + ": " + buf;
+  return status;
+}
+
+qm_status qm::hip_check(hipError_t err, const char* what) {
+  if (err == hipSuccess) return QM_OK;
+  if (err == hipErrorOutOfMemory) return fail(QM_ERR_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(err));
+  return fail(QM_ERR_COMMAND_FAILED, "%s: %s", what, hipGetErrorString(err));
+}
+
+qm::DeviceGuard::DeviceGuard(int device) {
+  hipGetDevice(&prev_);
+  if (prev_ != device) hipSetDevice(device);
+  dev_ = device;
+}
+qm::DeviceGuard::~DeviceGuard() {
+  if (prev_ != dev_) hipSetDevice(prev_);
+}
+
+qm_status qm::ensure_scratch(qm_runtime* rt, size_t bytes) {
+  if (rt->scratch_bytes >= bytes) return QM_OK;
+  if (rt->scratch) {
+    // Work already enqueued may still use the old buffer.
+    hipError_t e = hipStreamSynchronize(rt->stream);
+    if (e != hipSuccess) return hip_check(e, "scratch resize sync");
+    hipFree(rt->scratch);
+    rt->scratch = nullptr;
+    rt->scratch_bytes = 0;
+  }
+  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  want = (want + 255) & ~size_t(255);
+  hipError_t e = hipMalloc(&rt->scratch, want);
+  if (e != hipSuccess) return hip_check(e, "scratch hipMalloc");
+  rt->scratch_bytes = want;
+  return QM_OK;
+}
+
+extern "C" {
+
+const char* qm_status_string(qm_status status) {
+  switch (status) {
+    case QM_OK: return "QM_OK";
+    case QM_ERR_NO_DEVICE: return "QM_ERR_NO_DEVICE";
+    case QM_ERR_EMPTY_DIMENSION: return "QM_ERR_EMPTY_DIMENSION";
+    case QM_ERR_INPUT_NOT_GROUPED: return "QM_ERR_INPUT_NOT_GROUPED";
+    case QM_ERR_WRONG_LENGTH: return "QM_ERR_WRONG_LENGTH";
+    case QM_ERR_INVALID_DELTANET_CONFIG: return "QM_ERR_INVALID_DELTANET_CONFIG";
+    case QM_ERR_INVALID_ATTENTION_SHAPE: return "QM_ERR_INVALID_ATTENTION_SHAPE";
+    case QM_ERR_INVALID_SEQUENCE_LENGTH: return "QM_ERR_INVALID_SEQUENCE_LENGTH";
+    case QM_ERR_INVALID_BUFFER_OFFSET: return "QM_ERR_INVALID_BUFFER_OFFSET";
+    case QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE: return "QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE";
+    case QM_ERR_DIMENSION_OVERFLOW: return "QM_ERR_DIMENSION_OVERFLOW";
+    case QM_ERR_COMMAND_FAILED: return "QM_ERR_COMMAND_FAILED";
+    case QM_ERR_ZERO_CAPACITY: return "QM_ERR_ZERO_CAPACITY";
+    case QM_ERR_EMPTY_APPEND: return "QM_ERR_EMPTY_APPEND";
+    case QM_ERR_CAPACITY_EXCEEDED: return "QM_ERR_CAPACITY_EXCEEDED";
+    case QM_ERR_NULL_POINTER: return "QM_ERR_NULL_POINTER";
+    case QM_ERR_OUT_OF_MEMORY: return "QM_ERR_OUT_OF_MEMORY";
+    case QM_ERR_MISALIGNED: return "QM_ERR_MISALIGNED";
+    case QM_ERR_INVALID_ARGUMENT: return "QM_ERR_INVALID_ARGUMENT";
+  }
+  return "QM_ERR_UNKNOWN";
+}
+
+const char* qm_last_error_message(void) { return g_last_error.c_str(); }
+
+qm_status qm_runtime_create(int device, qm_runtime** out) {
+  if (!out) return fail(QM_ERR_NULL_POINTER, "out is NULL");
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+    return fail(QM_ERR_NO_DEVICE, "no HIP device is available");
+  if (device < 0 || device >= count)
+    return fail(QM_ERR_NO_DEVICE, "device %d out of range (%d devices)", device, count);
+  qm_runtime* rt = new qm_runtime();
+  rt->device = device;
+  DeviceGuard g(device);
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess) rt->cu_count = prop.multiProcessorCount;
+  *out = rt;
+  return QM_OK;
+}
+
+void qm_runtime_destroy(qm_runtime* rt) {
+  if (!rt) return;
+  DeviceGuard g(rt->device);
+  hipStreamSynchronize(rt->stream);
+  if (rt->scratch) hipFree(rt->scratch);
+  if (rt->counters) hipFree(rt->counters);
+  delete rt;
+}
+
+qm_status qm_runtime_set_stream(qm_runtime* rt, void* hip_stream) {
+  if (!rt) return fail(QM_ERR_NULL_POINTER, "runtime is NULL");
+  rt->stream = (hipStream_t)hip_stream;
+  return QM_OK;
+}
+
+qm_status qm_runtime_synchronize(qm_runtime* rt) {
+  if (!rt) return fail(QM_ERR_NULL_POINTER, "runtime is NULL");
+  DeviceGuard g(rt->device);
+  return hip_check(hipStreamSynchronize(rt->stream), "stream synchronize");
+}
+
+qm_status qm_device_alloc(qm_runtime* rt, size_t bytes, void** out) {
+  if (!rt || !out) return fail(QM_ERR_NULL_POINTER, "runtime/out is NULL");
+  if (bytes == 0) return fail(QM_ERR_EMPTY_DIMENSION, "zero-byte allocation");
+  DeviceGuard g(rt->device);
+  return hip_check(hipMalloc(out, bytes), "hipMalloc");
+}
+
+qm_status qm_device_free(qm_runtime* rt, void* ptr) {
+  if (!rt) return fail(QM_ERR_NULL_POINTER, "runtime is NULL");
+  if (!ptr) return QM_OK;
+  DeviceGuard g(rt->device);
+  return hip_check(hipFree(ptr), "hipFree");
+}
+
+qm_status qm_upload(qm_runtime* rt, const void* host, size_t bytes, void** out) {
+  if (!host) return fail(QM_ERR_NULL_POINTER, "host pointer is NULL");
+  qm_status st = qm_device_alloc(rt, bytes, out);
+  if (st != QM_OK) return st;
+  return qm_copy_to_device(rt, *out, host, bytes);
+}
+
+qm_status qm_copy_to_device(qm_runtime* rt, void* dst, const void* host, size_t bytes) {
+  if (!rt || !dst || !host) return fail(QM_ERR_NULL_POINTER, "NULL argument");
+  DeviceGuard g(rt->device);
+  qm_status st = hip_check(hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, rt->stream), "H2D copy");
+  if (st != QM_OK) return st;
+  return hip_check(hipStreamSynchronize(rt->stream), "H2D sync");
+}
+
+qm_status qm_copy_to_host(qm_runtime* rt, void* host, const void* src, size_t bytes) {
+  if (!rt || !src || !host) return fail(QM_ERR_NULL_POINTER, "NULL argument");
+  DeviceGuard g(rt->device);
+  qm_status st = hip_check(hipMemcpyAsync(host, src, bytes, hipMemcpyDeviceToHost, rt->stream), "D2H copy");
+  if (st != QM_OK) return st;
+  return hip_check(hipStreamSynchronize(rt->stream), "D2H sync");
+}
+
+}  // extern "C"

@@ -1,0 +1,41 @@
+// Private definitions of the C-ABI objects shared by the runtime sources.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <vector>
+
+#include "../../include/qm38.h"
+#include "internal.h"
+
+struct qm_runtime {
+  int device = 0;
+  int cu_count = 256;
+  hipStream_t stream = nullptr;
+  // Grow-only scratch used by calls that need an intermediate buffer (the
+  // MLP's h, attention split partials).  Calls on one runtime are serialised
+  // on its stream, so one buffer suffices.
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+  // Zero-initialised completion counters for kernels whose last workgroup
+  // combines partial results; every such kernel leaves them at zero again.
+  unsigned int* counters = nullptr;
+  size_t counter_count = 0;
+};
+
+namespace qm {
+
+qm_status fail(qm_status status, const char* fmt, ...);
+qm_status hip_check(hipError_t err, const char* what);
+qm_status ensure_scratch(qm_runtime* rt, size_t bytes);
+
+class DeviceGuard {
+ public:
+  explicit DeviceGuard(int device);
+  ~DeviceGuard();
+
+ private:
+  int prev_ = 0;
+  int dev_ = 0;
+};
+
+}  // namespace qm

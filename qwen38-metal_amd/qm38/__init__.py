@@ -1,0 +1,339 @@
+"""Python host-side mirror of the qm38 C ABI (include/qm38.h).
+
+The class and method names follow the reference runtime
+(/root/reference/src/metal_runtime.rs, `MetalRuntime`): `q4_affine_matvec_batch`
+<-> q4_affine_matvec_mapped_batch, `gqa_attention_q8` <-> gqa_attention_q8,
+`deltanet_step` <-> deltanet_step, and so on.  Errors raise `QmError`, whose
+`status` names the reference's `MetalRuntimeError` variant equivalent.
+
+Activations are passed as device tensors (torch is used only to own HBM and
+the stream); every computation runs in libqm38.so.  There is no fallback: if
+the library is missing, `load()` raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = _HERE / "libqm38.so"
+
+QM_STATUS = [
+    "QM_OK", "QM_ERR_NO_DEVICE", "QM_ERR_EMPTY_DIMENSION", "QM_ERR_INPUT_NOT_GROUPED",
+    "QM_ERR_WRONG_LENGTH", "QM_ERR_INVALID_DELTANET_CONFIG", "QM_ERR_INVALID_ATTENTION_SHAPE",
+    "QM_ERR_INVALID_SEQUENCE_LENGTH", "QM_ERR_INVALID_BUFFER_OFFSET",
+    "QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE", "QM_ERR_DIMENSION_OVERFLOW", "QM_ERR_COMMAND_FAILED",
+    "QM_ERR_ZERO_CAPACITY", "QM_ERR_EMPTY_APPEND", "QM_ERR_CAPACITY_EXCEEDED",
+    "QM_ERR_NULL_POINTER", "QM_ERR_OUT_OF_MEMORY", "QM_ERR_MISALIGNED", "QM_ERR_INVALID_ARGUMENT",
+]
+
+# Every symbol include/qm38.h declares (checked by tests/test_abi.py).
+EXPORTS = [
+    "qm_status_string", "qm_last_error_message",
+    "qm_runtime_create", "qm_runtime_destroy", "qm_runtime_set_stream", "qm_runtime_synchronize",
+    "qm_device_alloc", "qm_device_free", "qm_upload", "qm_copy_to_device", "qm_copy_to_host",
+    "qm_q4_project", "qm_q4_swiglu", "qm_q4_mlp",
+    "qm_kv_create", "qm_kv_destroy", "qm_kv_length", "qm_kv_allocated_pages", "qm_kv_page_for_token",
+    "qm_kv_reserve", "qm_kv_truncate", "qm_kv_clone", "qm_kv_read",
+    "qm_attn_decode", "qm_attn_prefill",
+    "qm_dn_weights_create", "qm_dn_weights_destroy", "qm_dn_state_create", "qm_dn_state_destroy",
+    "qm_dn_state_clone", "qm_dn_state_read", "qm_dn_state_write", "qm_dn_step", "qm_dn_prefill",
+]
+
+
+class QmError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        self.status = QM_STATUS[status] if 0 <= status < len(QM_STATUS) else f"status {status}"
+        self.code = status
+        super().__init__(message)
+
+
+class Q4Job(C.Structure):
+    _fields_ = [("weights", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p),
+                ("out_rows", C.c_uint32)]
+
+
+class DnConfig(C.Structure):
+    _fields_ = [("key_heads", C.c_uint32), ("value_heads", C.c_uint32), ("key_head_dim", C.c_uint32),
+                ("value_head_dim", C.c_uint32), ("conv_kernel_size", C.c_uint32)]
+
+
+_lib = None
+
+
+def load(path: str | os.PathLike | None = None) -> C.CDLL:
+    """Loads libqm38.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(f"{p} is missing: run `python qwen38-metal_amd/build.py`")
+    lib = C.CDLL(str(p))
+    vp, u32, i32 = C.c_void_p, C.c_uint32, C.c_int
+    sig = {
+        "qm_status_string": ([i32], C.c_char_p),
+        "qm_last_error_message": ([], C.c_char_p),
+        "qm_runtime_create": ([i32, C.POINTER(vp)], i32),
+        "qm_runtime_destroy": ([vp], None),
+        "qm_runtime_set_stream": ([vp, vp], i32),
+        "qm_runtime_synchronize": ([vp], i32),
+        "qm_device_alloc": ([vp, C.c_size_t, C.POINTER(vp)], i32),
+        "qm_device_free": ([vp, vp], i32),
+        "qm_upload": ([vp, vp, C.c_size_t, C.POINTER(vp)], i32),
+        "qm_copy_to_device": ([vp, vp, vp, C.c_size_t], i32),
+        "qm_copy_to_host": ([vp, vp, vp, C.c_size_t], i32),
+        "qm_q4_project": ([vp, C.POINTER(Q4Job), i32, vp, u32, u32, C.POINTER(vp)], i32),
+        "qm_q4_swiglu": ([vp, C.POINTER(Q4Job), C.POINTER(Q4Job), vp, u32, u32, vp], i32),
+        "qm_q4_mlp": ([vp, C.POINTER(Q4Job), C.POINTER(Q4Job), C.POINTER(Q4Job), vp, u32, u32, vp], i32),
+        "qm_kv_create": ([vp, u32, u32, u32, u32, C.POINTER(vp)], i32),
+        "qm_kv_destroy": ([vp], None),
+        "qm_kv_length": ([vp], u32),
+        "qm_kv_allocated_pages": ([vp], u32),
+        "qm_kv_page_for_token": ([vp, u32], C.c_int64),
+        "qm_kv_reserve": ([vp, u32], i32),
+        "qm_kv_truncate": ([vp, u32], i32),
+        "qm_kv_clone": ([vp, C.POINTER(vp)], i32),
+        "qm_kv_read": ([vp, vp, vp, vp, vp], i32),
+        "qm_attn_decode": ([vp, C.POINTER(vp), u32, vp, vp, vp, vp, u32, vp], i32),
+        "qm_attn_prefill": ([vp, vp, vp, vp, vp, vp, u32, u32, vp], i32),
+        "qm_dn_weights_create": ([vp, C.POINTER(DnConfig), vp, vp, vp, vp, C.POINTER(vp)], i32),
+        "qm_dn_weights_destroy": ([vp], None),
+        "qm_dn_state_create": ([vp, vp, C.POINTER(vp)], i32),
+        "qm_dn_state_destroy": ([vp], None),
+        "qm_dn_state_clone": ([vp, C.POINTER(vp)], i32),
+        "qm_dn_state_read": ([vp, vp, vp], i32),
+        "qm_dn_state_write": ([vp, vp, vp], i32),
+        "qm_dn_step": ([vp, vp, vp, vp, vp, vp, vp, C.c_float, vp], i32),
+        "qm_dn_prefill": ([vp, vp, vp, vp, vp, vp, vp, vp, u32, C.c_float, vp], i32),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        msg = load().qm_last_error_message().decode()
+        raise QmError(status, msg)
+
+
+def _ptr(t) -> int | None:
+    """Device address of a torch tensor / raw int, or None."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+class Runtime:
+    """One runtime per HIP device (MetalRuntime::new, metal_runtime.rs:641)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load()
+        h = C.c_void_p()
+        _check(self.lib.qm_runtime_create(device, C.byref(h)))
+        self.handle = h
+        self.device = device
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.qm_runtime_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_stream(self, stream) -> None:
+        """stream: a torch.cuda.Stream, a raw hipStream_t int, or None."""
+        raw = getattr(stream, "cuda_stream", stream)
+        _check(self.lib.qm_runtime_set_stream(self.handle, raw))
+
+    def synchronize(self) -> None:
+        _check(self.lib.qm_runtime_synchronize(self.handle))
+
+    # ---- Q4 projections --------------------------------------------------
+    @staticmethod
+    def job(weights, scales, biases, out_rows: int) -> Q4Job:
+        return Q4Job(_ptr(weights), _ptr(scales), _ptr(biases), out_rows)
+
+    def q4_project(self, jobs, x, in_elems: int, M: int, outputs) -> None:
+        arr = (Q4Job * len(jobs))(*jobs)
+        outs = (C.c_void_p * len(outputs))(*[_ptr(o) for o in outputs])
+        _check(self.lib.qm_q4_project(self.handle, arr, len(jobs), _ptr(x), in_elems, M, outs))
+
+    def q4_swiglu(self, gate: Q4Job, up: Q4Job, x, in_elems: int, M: int, h) -> None:
+        _check(self.lib.qm_q4_swiglu(self.handle, C.byref(gate), C.byref(up), _ptr(x), in_elems, M, _ptr(h)))
+
+    def q4_mlp(self, gate: Q4Job, up: Q4Job, down: Q4Job, x, in_elems: int, M: int, y) -> None:
+        _check(self.lib.qm_q4_mlp(self.handle, C.byref(gate), C.byref(up), C.byref(down), _ptr(x),
+                                  in_elems, M, _ptr(y)))
+
+    # ---- Q8 KV + attention -------------------------------------------------
+    def create_q8_kv_state(self, kv_heads: int, head_dim: int, max_tokens: int,
+                           page_tokens: int = 16) -> "KvCache":
+        return KvCache(self, kv_heads, head_dim, page_tokens, max_tokens)
+
+    def gqa_attention_q8(self, seqs, q, gate, k, v, num_heads: int, o) -> None:
+        arr = (C.c_void_p * len(seqs))(*[s.handle for s in seqs])
+        _check(self.lib.qm_attn_decode(self.handle, arr, len(seqs), _ptr(q), _ptr(gate), _ptr(k), _ptr(v),
+                                       num_heads, _ptr(o)))
+
+    def gqa_attention_q8_prefill(self, seq, q, gate, k, v, num_heads: int, rows: int, o) -> None:
+        _check(self.lib.qm_attn_prefill(self.handle, seq.handle, _ptr(q), _ptr(gate), _ptr(k), _ptr(v),
+                                        num_heads, rows, _ptr(o)))
+
+    # ---- DeltaNet ---------------------------------------------------------
+    def create_deltanet_weights(self, config: DnConfig, conv_weight, a_log, dt_bias, norm) -> "DnWeights":
+        return DnWeights(self, config, conv_weight, a_log, dt_bias, norm)
+
+    def deltanet_step(self, weights, state, qkv, z, b, a, epsilon: float, out) -> None:
+        _check(self.lib.qm_dn_step(self.handle, weights.handle, state.handle, _ptr(qkv), _ptr(z), _ptr(b),
+                                   _ptr(a), epsilon, _ptr(out)))
+
+    def deltanet_prefill(self, weights, state, qkv, z, b, a, rows: int, epsilon: float, out,
+                         source=None) -> None:
+        src = source.handle if source is not None else None
+        _check(self.lib.qm_dn_prefill(self.handle, weights.handle, src, state.handle, _ptr(qkv), _ptr(z),
+                                      _ptr(b), _ptr(a), rows, epsilon, _ptr(out)))
+
+
+class KvCache:
+    """Paged Q8 KV cache (Q8KvState + LogicalPageTable)."""
+
+    def __init__(self, rt: Runtime, kv_heads: int, head_dim: int, page_tokens: int, max_tokens: int,
+                 handle=None):
+        self.rt = rt
+        self.kv_heads = kv_heads
+        self.head_dim = head_dim
+        if handle is None:
+            h = C.c_void_p()
+            _check(rt.lib.qm_kv_create(rt.handle, kv_heads, head_dim, page_tokens, max_tokens, C.byref(h)))
+            handle = h
+        self.handle = handle
+
+    def close(self) -> None:
+        if self.handle:
+            self.rt.lib.qm_kv_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def sequence_length(self) -> int:
+        return self.rt.lib.qm_kv_length(self.handle)
+
+    def allocated_pages(self) -> int:
+        return self.rt.lib.qm_kv_allocated_pages(self.handle)
+
+    def page_for_token(self, token: int):
+        r = self.rt.lib.qm_kv_page_for_token(self.handle, token)
+        return None if r < 0 else r
+
+    def reserve(self, additional: int) -> None:
+        _check(self.rt.lib.qm_kv_reserve(self.handle, additional))
+
+    def truncate(self, length: int) -> None:
+        _check(self.rt.lib.qm_kv_truncate(self.handle, length))
+
+    def clone(self) -> "KvCache":
+        h = C.c_void_p()
+        _check(self.rt.lib.qm_kv_clone(self.handle, C.byref(h)))
+        return KvCache(self.rt, self.kv_heads, self.head_dim, 16, 0, handle=h)
+
+    def read(self):
+        """Returns (keys int8 [T][KVH][d], values, key_scales f32 [T][KVH], value_scales)."""
+        import numpy as np
+        T = self.sequence_length
+        keys = np.zeros((T, self.kv_heads, self.head_dim), np.int8)
+        values = np.zeros_like(keys)
+        ks = np.zeros((T, self.kv_heads), np.float32)
+        vs = np.zeros_like(ks)
+        _check(self.rt.lib.qm_kv_read(self.handle, keys.ctypes.data, values.ctypes.data, ks.ctypes.data,
+                                      vs.ctypes.data))
+        return keys, values, ks, vs
+
+
+class DnWeights:
+    def __init__(self, rt: Runtime, config: DnConfig, conv_weight, a_log, dt_bias, norm):
+        import numpy as np
+        self.rt = rt
+        self.config = config
+        arrs = [np.ascontiguousarray(a, dtype=np.float32) for a in (conv_weight, a_log, dt_bias, norm)]
+        h = C.c_void_p()
+        _check(rt.lib.qm_dn_weights_create(rt.handle, C.byref(config), *[a.ctypes.data for a in arrs],
+                                           C.byref(h)))
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            self.rt.lib.qm_dn_weights_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def create_state(self) -> "DnState":
+        h = C.c_void_p()
+        _check(self.rt.lib.qm_dn_state_create(self.rt.handle, self.handle, C.byref(h)))
+        return DnState(self, h)
+
+
+class DnState:
+    def __init__(self, weights: DnWeights, handle):
+        self.weights = weights
+        self.rt = weights.rt
+        self.handle = handle
+
+    def close(self) -> None:
+        if self.handle:
+            self.rt.lib.qm_dn_state_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def clone(self) -> "DnState":
+        h = C.c_void_p()
+        _check(self.rt.lib.qm_dn_state_clone(self.handle, C.byref(h)))
+        return DnState(self.weights, h)
+
+    def _shapes(self):
+        c = self.weights.config
+        channels = 2 * c.key_heads * c.key_head_dim + c.value_heads * c.value_head_dim
+        return (channels, max(c.conv_kernel_size - 1, 0)), (c.value_heads, c.value_head_dim, c.key_head_dim)
+
+    def read(self):
+        import numpy as np
+        hs, ss = self._shapes()
+        hist = np.zeros(hs, np.float32)
+        rec = np.zeros(ss, np.float32)
+        _check(self.rt.lib.qm_dn_state_read(self.handle, hist.ctypes.data if hist.size else None,
+                                            rec.ctypes.data))
+        return hist, rec
+
+    def write(self, hist, rec) -> None:
+        import numpy as np
+        hist = np.ascontiguousarray(hist, np.float32)
+        rec = np.ascontiguousarray(rec, np.float32)
+        _check(self.rt.lib.qm_dn_state_write(self.handle, hist.ctypes.data if hist.size else None,
+                                             rec.ctypes.data))

@@ -1,0 +1,185 @@
+"""GPU parity of the MLX affine-Q4 projections against the CPU oracle.
+
+Ports metal_runtime.rs tests q4_affine_matvec_matches_cpu_reference (:9365),
+mapped_q4_batch_reuses_one_input_without_changing_results (:9685),
+mapped_q4_matmul_batch_matches_each_prompt_row (:9766),
+batch_simd_q4_matmul_short_batch_matches_cpu_reference (:9812) and
+fused_q4_mlp_batch_matches_cpu_reference (:10726), plus seeded
+BASELINE-shape cases.  Tolerance: bf16 outputs within 2e-3 of max |ref|
+(fp64-accumulated oracle).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from gpu_util import assert_bf16_close, bf16_dev_to_f32, empty_bf16, to_dev
+from qm38 import QmError, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _upload(dev, packed, s, b):
+    return to_dev(packed, dev), to_dev(s, dev), to_dev(b, dev)
+
+
+def _project(rt, dev, mats, x_bits, M):
+    import qm38
+    K = x_bits.shape[-1]
+    xd = to_dev(x_bits, dev)
+    devm = [_upload(dev, *m) for m in mats]
+    jobs = [qm38.Runtime.job(w, s, b, m[0].shape[0]) for (w, s, b), m in zip(devm, mats)]
+    outs = [empty_bf16((M, m[0].shape[0]), dev) for m in mats]
+    rt.q4_project(jobs, xd, K, M, outs)
+    return [bf16_dev_to_f32(o) for o in outs]
+
+
+def test_reference_vectors_k128_n5(rt, torch_dev):
+    # metal_runtime.rs:9332-9362: ramp input, nibbles (i*7+3)%16, scale/bias tables.
+    K, N = 128, 5
+    x = ((np.arange(K) % 17) - 8.0) * 0.125
+    q = ((np.arange(N * K) * 7 + 3) % 16).astype(np.uint8).reshape(N, K)
+    sv = [0.125, -0.0625, 0.25, 0.03125, -0.125, 0.0625]
+    bv = [0.03125, -0.015625, 0.0625, 0.125, -0.03125, 0.0]
+    s = synth.f32_to_bf16(np.array([sv[i % 6] for i in range(N * 2)], np.float32)).reshape(N, 2)
+    b = synth.f32_to_bf16(np.array([bv[i % 6] for i in range(N * 2)], np.float32)).reshape(N, 2)
+    xb = synth.f32_to_bf16(x.astype(np.float32))[None]
+    mat = (synth.pack_q4(q), s, b)
+    (got,) = _project(rt, torch_dev, [mat], xb, 1)
+    ref = oracle.q4_project(xb, *mat)
+    assert_bf16_close(got, ref, what="k128n5")
+    # reference tolerance: abs < 1e-3 against fp32 outputs (bf16 here: 1 ulp slack)
+    assert np.max(np.abs(got - ref)) < 1e-3 + np.max(np.abs(ref)) * 2 ** -8
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 13, 16])
+@pytest.mark.parametrize("N,K", [(40, 256), (257, 512), (96, 192), (1024, 1024)])
+def test_short_batch_matches_oracle(rt, torch_dev, M, N, K):
+    rng = np.random.default_rng(1000 + M * 31 + N + K)
+    mat = synth.q4_matrix(rng, N, K)
+    xb = synth.bf16_normal(rng, (M, K))
+    (got,) = _project(rt, torch_dev, [mat], xb, M)
+    ref = oracle.q4_project(xb, *mat)
+    assert_bf16_close(got, ref, what=f"M{M} N{N} K{K}")
+
+
+def test_batch_of_jobs_reuses_one_input(rt, torch_dev):
+    # One activation, several projections of different heights in one launch
+    # must equal each projection run alone (metal_runtime.rs:9685).
+    rng = np.random.default_rng(7)
+    K = 512
+    mats = [synth.q4_matrix(rng, n, K) for n in (64, 200, 33, 512)]
+    for M in (1, 4, 8):
+        xb = synth.bf16_normal(rng, (M, K))
+        together = _project(rt, torch_dev, mats, xb, M)
+        for mat, got in zip(mats, together):
+            (alone,) = _project(rt, torch_dev, [mat], xb, M)
+            np.testing.assert_array_equal(got, alone)
+            assert_bf16_close(got, oracle.q4_project(xb, *mat))
+
+
+def test_matmul_rows_equal_per_row_matvec(rt, torch_dev):
+    # metal_runtime.rs:9766: a multi-row call equals one call per row.
+    rng = np.random.default_rng(11)
+    K, N, M = 384, 130, 6
+    mat = synth.q4_matrix(rng, N, K)
+    xb = synth.bf16_normal(rng, (M, K))
+    (batch,) = _project(rt, torch_dev, [mat], xb, M)
+    for m in range(M):
+        (row,) = _project(rt, torch_dev, [mat], xb[m:m + 1], 1)
+        assert_bf16_close(batch[m:m + 1], row.astype(np.float64), rel=4e-3)
+
+
+def test_identity_bias_cancels(rt, torch_dev):
+    # q = 8 everywhere and b = -8 s: every weight is exactly 0, so y is 0 up to
+    # the fp32 rounding of the kernel's s*sum((128+q)x) + (b-128s)*sum(x) form.
+    rng = np.random.default_rng(3)
+    N, K = 64, 256
+    packed = np.full((N, K // 8), 0x88888888, np.uint32)
+    s = synth.f32_to_bf16(rng.uniform(0.005, 0.02, (N, K // 64)).astype(np.float32))
+    b = synth.f32_to_bf16(-8 * synth.bf16_to_f32(s))
+    xb = synth.bf16_normal(rng, (4, K))
+    (got,) = _project(rt, torch_dev, [(packed, s, b)], xb, 4)
+    bound = 1e-5 * np.max(synth.bf16_to_f32(s)) * np.sum(np.abs(synth.bf16_to_f32(xb)), axis=1).max() * 136
+    assert np.max(np.abs(got)) <= bound
+
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_swiglu_pair_and_mlp(rt, torch_dev, M):
+    import qm38
+    rng = np.random.default_rng(50 + M)
+    K, I = 512, 768
+    gate = synth.q4_matrix(rng, I, K)
+    up = synth.q4_matrix(rng, I, K)
+    down = synth.q4_matrix(rng, K, I)
+    xb = synth.bf16_normal(rng, (M, K))
+    g_ref = oracle.q4_project(xb, *gate)
+    u_ref = oracle.q4_project(xb, *up)
+    h_ref = oracle.swiglu(g_ref, u_ref)
+    dg, du, dd = (_upload(torch_dev, *m) for m in (gate, up, down))
+    jg = qm38.Runtime.job(*dg, I)
+    ju = qm38.Runtime.job(*du, I)
+    jd = qm38.Runtime.job(*dd, K)
+    xd = to_dev(xb, torch_dev)
+    h = empty_bf16((M, I), torch_dev)
+    rt.q4_swiglu(jg, ju, xd, K, M, h)
+    h_got = bf16_dev_to_f32(h)
+    assert_bf16_close(h_got, h_ref, what="swiglu h")
+    y = empty_bf16((M, K), torch_dev)
+    rt.q4_mlp(jg, ju, jd, xd, K, M, y)
+    # down consumes the bf16 h the kernel wrote
+    y_ref = oracle.q4_project(synth.f32_to_bf16(h_got), *down)
+    assert_bf16_close(bf16_dev_to_f32(y), y_ref, what="mlp y")
+    # and against the all-fp32 chain (h not rounded): rounding h to bf16 is
+    # the only extra error
+    y_ref32 = oracle.q4_project(synth.f32_to_bf16(h_ref), *down)
+    assert_bf16_close(bf16_dev_to_f32(y), y_ref32, rel=6e-3, what="mlp y vs unrounded-h chain")
+
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_decode_set_27b_shapes(rt, torch_dev, M):
+    # QKV 5120->10240, gate/up 5120->2x17408, down 17408->5120.
+    import qm38
+    rng = np.random.default_rng(2024 + M)
+    H, I, QKV = 5120, 17408, 10240
+    qkv = synth.q4_matrix(rng, QKV, H)
+    xb = synth.bf16_normal(rng, (M, H))
+    (got,) = _project(rt, torch_dev, [qkv], xb, M)
+    assert_bf16_close(got, oracle.q4_project(xb, *qkv), what="qkv")
+    gate = synth.q4_matrix(rng, I, H)
+    up = synth.q4_matrix(rng, I, H)
+    dg, du = _upload(torch_dev, *gate), _upload(torch_dev, *up)
+    h = empty_bf16((M, I), torch_dev)
+    rt.q4_swiglu(qm38.Runtime.job(*dg, I), qm38.Runtime.job(*du, I), to_dev(xb, torch_dev), H, M, h)
+    h_got = bf16_dev_to_f32(h)
+    h_ref = oracle.swiglu(oracle.q4_project(xb, *gate), oracle.q4_project(xb, *up))
+    assert_bf16_close(h_got, h_ref, what="gate/up")
+    down = synth.q4_matrix(rng, H, I)
+    hb = synth.f32_to_bf16(h_got)
+    (y,) = _project(rt, torch_dev, [down], hb, M)
+    assert_bf16_close(y, oracle.q4_project(hb, *down), what="down")
+
+
+def test_config1_4096(rt, torch_dev):
+    rng = np.random.default_rng(1)
+    mat = synth.q4_matrix(rng, 4096, 4096)
+    xb = synth.bf16_normal(rng, (1, 4096))
+    (got,) = _project(rt, torch_dev, [mat], xb, 1)
+    assert_bf16_close(got, oracle.q4_project(xb, *mat), what="cfg1")
+
+
+def test_rejects_incomplete_group(rt, torch_dev):
+    # metal_runtime.rs:11806 q4_affine_matvec_rejects_incomplete_group
+    import qm38
+    rng = np.random.default_rng(0)
+    mat = synth.q4_matrix(rng, 8, 64)
+    w, s, b = _upload(torch_dev, *mat)
+    x = to_dev(synth.bf16_normal(rng, (1, 64)), torch_dev)
+    out = empty_bf16((1, 8), torch_dev)
+    with pytest.raises(QmError) as e:
+        rt.q4_project([qm38.Runtime.job(w, s, b, 8)], x, 63, 1, [out])
+    assert e.value.status == "QM_ERR_INPUT_NOT_GROUPED"
+    with pytest.raises(QmError) as e:
+        rt.q4_project([qm38.Runtime.job(w, s, b, 0)], x, 64, 1, [out])
+    assert e.value.status == "QM_ERR_EMPTY_DIMENSION"
