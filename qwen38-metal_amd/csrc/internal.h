@@ -17,14 +17,26 @@ struct Q4Job {
   uint32_t tile_begin;  // filled by the launcher
 };
 
+// Device workspace for kernels whose workgroups combine partial results:
+// `counters` are zero between launches (each kernel leaves them at zero).
+struct Workspace {
+  float* partials;
+  size_t partial_bytes;
+  unsigned int* counters;
+  size_t counter_count;
+};
+
 // Decode (weight-streaming) Q4 projection: M <= 16 activation rows.
 // swiglu: jobs[0] = gate, jobs[1] = up, result written to jobs[0].out.
+// q4_decode_workspace reports the partial bytes / counters a launch needs.
+void q4_decode_workspace(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M,
+                         size_t* partial_bytes, size_t* counters);
 hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x,
-                            uint32_t K, uint32_t M, hipStream_t stream);
+                            uint32_t K, uint32_t M, const Workspace& ws, hipStream_t stream);
 
 // Prefill Q4 GEMM (M > 16): Y[M][N] = X[M][K] * dequant(W)^T, bf16 out.
 // swiglu as above.
 hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x,
-                          uint32_t K, uint32_t M, hipStream_t stream);
+                          uint32_t K, uint32_t M, const Workspace& ws, hipStream_t stream);
 
 }  // namespace qm

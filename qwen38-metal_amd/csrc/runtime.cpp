@@ -59,6 +59,47 @@ qm_status qm::ensure_scratch(qm_runtime* rt, size_t bytes) {
   return QM_OK;
 }
 
+qm_status qm::ensure_partials(qm_runtime* rt, size_t bytes) {
+  if (rt->partial_bytes >= bytes) return QM_OK;
+  if (rt->partials) {
+    hipError_t e = hipStreamSynchronize(rt->stream);
+    if (e != hipSuccess) return hip_check(e, "partials resize sync");
+    hipFree(rt->partials);
+    rt->partials = nullptr;
+    rt->partial_bytes = 0;
+  }
+  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  want = (want + 255) & ~size_t(255);
+  hipError_t e = hipMalloc(&rt->partials, want);
+  if (e != hipSuccess) return hip_check(e, "partials hipMalloc");
+  rt->partial_bytes = want;
+  return QM_OK;
+}
+
+qm_status qm::ensure_counters(qm_runtime* rt, size_t count) {
+  if (rt->counter_count >= count) return QM_OK;
+  if (rt->counters) {
+    hipError_t e = hipStreamSynchronize(rt->stream);
+    if (e != hipSuccess) return hip_check(e, "counters resize sync");
+    hipFree(rt->counters);
+    rt->counters = nullptr;
+    rt->counter_count = 0;
+  }
+  size_t want = count < 4096 ? 4096 : count;
+  hipError_t e = hipMalloc(&rt->counters, want * sizeof(unsigned int));
+  if (e != hipSuccess) return hip_check(e, "counters hipMalloc");
+  // Counters start at zero once; every kernel that uses them resets them.
+  e = hipMemsetAsync(rt->counters, 0, want * sizeof(unsigned int), rt->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
+  if (e != hipSuccess) return hip_check(e, "counters clear");
+  rt->counter_count = want;
+  return QM_OK;
+}
+
+qm::Workspace qm::workspace(qm_runtime* rt) {
+  return Workspace{(float*)rt->partials, rt->partial_bytes, rt->counters, rt->counter_count};
+}
+
 extern "C" {
 
 const char* qm_status_string(qm_status status) {
@@ -111,6 +152,7 @@ void qm_runtime_destroy(qm_runtime* rt) {
   hipStreamSynchronize(rt->stream);
   if (rt->scratch) hipFree(rt->scratch);
   if (rt->counters) hipFree(rt->counters);
+  if (rt->partials) hipFree(rt->partials);
   delete rt;
 }
 

@@ -20,6 +20,10 @@ struct qm_runtime {
   // combines partial results; every such kernel leaves them at zero again.
   unsigned int* counters = nullptr;
   size_t counter_count = 0;
+  // Split-K partial results of the kernels that combine them in their last
+  // workgroup (no zeroing needed: every slot is written before it is read).
+  void* partials = nullptr;
+  size_t partial_bytes = 0;
 };
 
 namespace qm {
@@ -27,6 +31,10 @@ namespace qm {
 qm_status fail(qm_status status, const char* fmt, ...);
 qm_status hip_check(hipError_t err, const char* what);
 qm_status ensure_scratch(qm_runtime* rt, size_t bytes);
+qm_status ensure_partials(qm_runtime* rt, size_t bytes);
+qm_status ensure_counters(qm_runtime* rt, size_t count);
+// Workspace handed to kernels that split work across workgroups.
+Workspace workspace(qm_runtime* rt);
 
 class DeviceGuard {
  public:

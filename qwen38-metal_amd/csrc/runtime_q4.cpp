@@ -47,10 +47,17 @@ Q4Job to_job(const qm_q4_job& j, uint16_t* out) {
   return q;
 }
 
-hipError_t launch(const Q4Job* jobs, int n, bool swiglu, const uint16_t* x, uint32_t K, uint32_t M,
-                  hipStream_t s) {
-  if (M <= kDecodeMaxRows) return launch_q4_decode(jobs, n, swiglu, x, K, M, s);
-  return launch_q4_gemm(jobs, n, swiglu, x, K, M, s);
+qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const uint16_t* x, uint32_t K,
+                 uint32_t M, const char* what) {
+  size_t pbytes = 0, counters = 0;
+  q4_decode_workspace(jobs, n, swiglu, K, M < kDecodeMaxRows ? M : kDecodeMaxRows, &pbytes, &counters);
+  qm_status st = ensure_partials(rt, pbytes);
+  if (st == QM_OK) st = ensure_counters(rt, counters);
+  if (st != QM_OK) return st;
+  const Workspace ws = workspace(rt);
+  hipError_t e = M <= kDecodeMaxRows ? launch_q4_decode(jobs, n, swiglu, x, K, M, ws, rt->stream)
+                                     : launch_q4_gemm(jobs, n, swiglu, x, K, M, ws, rt->stream);
+  return hip_check(e, what);
 }
 
 }  // namespace
@@ -73,7 +80,7 @@ qm_status qm_q4_project(qm_runtime* rt, const qm_q4_job* jobs, int n_jobs, const
     q[i] = to_job(jobs[i], outputs[i]);
   }
   DeviceGuard g(rt->device);
-  return hip_check(launch(q, n_jobs, false, x, in_elems, M, rt->stream), "Q4 projection launch");
+  return launch(rt, q, n_jobs, false, x, in_elems, M, "Q4 projection launch");
 }
 
 qm_status qm_q4_swiglu(qm_runtime* rt, const qm_q4_job* gate, const qm_q4_job* up, const uint16_t* x,
@@ -88,7 +95,7 @@ qm_status qm_q4_swiglu(qm_runtime* rt, const qm_q4_job* gate, const qm_q4_job* u
   if (!h) return fail(QM_ERR_NULL_POINTER, "h is NULL");
   Q4Job q[2] = {to_job(*gate, h), to_job(*up, nullptr)};
   DeviceGuard g(rt->device);
-  return hip_check(launch(q, 2, true, x, in_elems, M, rt->stream), "Q4 SwiGLU launch");
+  return launch(rt, q, 2, true, x, in_elems, M, "Q4 SwiGLU launch");
 }
 
 qm_status qm_q4_mlp(qm_runtime* rt, const qm_q4_job* gate, const qm_q4_job* up, const qm_q4_job* down,
@@ -107,9 +114,9 @@ qm_status qm_q4_mlp(qm_runtime* rt, const qm_q4_job* gate, const qm_q4_job* up, 
   if ((st = ensure_scratch(rt, h_bytes)) != QM_OK) return st;
   uint16_t* h = (uint16_t*)rt->scratch;
   Q4Job q[2] = {to_job(*gate, h), to_job(*up, nullptr)};
-  if ((st = hip_check(launch(q, 2, true, x, in_elems, M, rt->stream), "MLP gate/up launch")) != QM_OK) return st;
+  if ((st = launch(rt, q, 2, true, x, in_elems, M, "MLP gate/up launch")) != QM_OK) return st;
   Q4Job d = to_job(*down, y);
-  return hip_check(launch(&d, 1, false, h, gate->out_rows, M, rt->stream), "MLP down launch");
+  return launch(rt, &d, 1, false, h, gate->out_rows, M, "MLP down launch");
 }
 
 }  // extern "C"

@@ -164,7 +164,9 @@ class Runtime:
     # ---- Q4 projections --------------------------------------------------
     @staticmethod
     def job(weights, scales, biases, out_rows: int) -> Q4Job:
-        return Q4Job(_ptr(weights), _ptr(scales), _ptr(biases), out_rows)
+        j = Q4Job(_ptr(weights), _ptr(scales), _ptr(biases), out_rows)
+        j._refs = (weights, scales, biases)  # keep device tensors alive while the job exists
+        return j
 
     def q4_project(self, jobs, x, in_elems: int, M: int, outputs) -> None:
         arr = (Q4Job * len(jobs))(*jobs)

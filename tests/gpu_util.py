@@ -32,13 +32,31 @@ def bf16_dev_to_f32(t) -> np.ndarray:
     return (b.astype(np.uint32) << 16).view(np.float32)
 
 
+def bf16_half_ulp(v: np.ndarray) -> np.ndarray:
+    """Half a bf16 ulp at |v| (bf16 keeps 8 significant bits)."""
+    a = np.abs(np.asarray(v, np.float64))
+    e = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    return np.where(a > 0, 2.0 ** (e - 8), 0.0)
+
+
 def assert_bf16_close(got_f32: np.ndarray, ref_f32: np.ndarray, rel: float = 2e-3, what: str = ""):
-    """bf16 outputs: max |got - ref| <= rel * max |ref| (normwise, ref in fp32/fp64)."""
+    """bf16 outputs vs an fp32/fp64 oracle.
+
+    The kernel's result before its final bf16 store must lie within
+    rel * max|ref| of the oracle: |got - ref| - halfulp_bf16(got) <= rel * max|ref|.
+    (The store itself rounds to nearest-even, which alone can move a value by
+    up to 2^-8 relative, more than the 2e-3 budget, so it is accounted for
+    separately instead of being charged to the arithmetic.)
+    Returns the arithmetic error (normwise).
+    """
     got = np.asarray(got_f32, np.float64)
     ref = np.asarray(ref_f32, np.float64)
     assert got.shape == ref.shape, (got.shape, ref.shape)
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"
     scale = max(np.max(np.abs(ref)), 1e-30)
-    err = np.max(np.abs(got - ref)) / scale
-    assert err <= rel, f"{what}: max rel err {err:.3e} > {rel:.1e}"
+    excess = np.maximum(np.abs(got - ref) - bf16_half_ulp(got) * (1 + 1e-6), 0.0)
+    err = np.max(excess) / scale
+    raw = np.max(np.abs(got - ref)) / scale
+    assert err <= rel, f"{what}: arithmetic rel err {err:.3e} > {rel:.1e} (raw incl. bf16 rounding {raw:.3e})"
+    assert raw <= rel + 2.0 ** -8, f"{what}: raw rel err {raw:.3e}"
     return err
