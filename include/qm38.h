@@ -151,7 +151,7 @@ typedef struct qm_kv qm_kv;
  *   V pages  int8 [page][kv_head][head_dim][page_tokens]   (d-major)
  *   scales   fp32 [page][kv_head][page_tokens]  (one array for K, one for V)
  * Pages materialise lazily as tokens arrive and receive sequential page ids
- * (paged_kv.rs:89-97).  page_tokens must be 16; head_dim must be 128 or 64
+ * (paged_kv.rs:89-97).  page_tokens must be 16; head_dim must be 64, 128 or 256
  * (multiple of 32, <= 256 in the reference's validate_attention_shape,
  * metal_runtime.rs:9186-9193).  max_tokens bounds the sequence length. */
 qm_status qm_kv_create(qm_runtime* rt, uint32_t kv_heads, uint32_t head_dim,

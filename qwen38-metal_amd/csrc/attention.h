@@ -1,0 +1,54 @@
+// Launch interface of the paged Q8-KV attention kernels (q8_attention.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qm {
+
+constexpr int kMaxAttnSeqs = 16;  // sequences per launch (kernel-argument table)
+
+struct AttnSeq {
+  int8_t* k;          // K pages   [page][kv_head][16][D]
+  int8_t* v;          // V pages   [page][kv_head][D][16]
+  float* ks;          // K scales  [page][kv_head][16]
+  float* vs;          // V scales  [page][kv_head][16]
+  int32_t* pt;        // page table: logical page -> physical page
+  uint32_t len;       // tokens in the cache after this call's append
+  uint32_t unit_begin;  // first workgroup of this sequence (decode)
+  uint32_t nsplit;      // page splits (decode)
+  uint32_t part_begin;  // first partial row of this sequence (decode)
+  int32_t new_page_first;  // logical index of the first page materialised by this call
+  int32_t new_page_count;
+  int32_t new_page_id;     // physical id of that page (ids are consecutive)
+};
+
+struct AppendArgs {
+  const float* k;  // [items][kv_heads][D]
+  const float* v;
+  uint32_t kv_heads;
+  uint32_t head_dim;
+  uint32_t decode;  // 1: item = sequence (one token each); 0: item = row of seqs[0]
+  uint32_t start;   // prefill: cache position of row 0
+  AttnSeq seqs[kMaxAttnSeqs];
+};
+
+struct AttnArgs {
+  const uint16_t* q;     // bf16 [rows][H][D]
+  const uint16_t* gate;  // bf16 [rows][H][D] or null
+  uint16_t* o;           // bf16 [rows][H][D]
+  float* partials;       // [split rows][H][D + 2]
+  uint32_t heads;
+  uint32_t kv_heads;
+  uint32_t head_dim;
+  uint32_t n_seqs;
+  uint32_t pages_per_split;  // decode
+  uint32_t prefill;
+  uint32_t rows;   // prefill: query rows
+  uint32_t start;  // prefill: cache position of row 0
+  AttnSeq seqs[kMaxAttnSeqs];
+};
+
+hipError_t launch_q8_append(const AppendArgs& a, uint32_t items, hipStream_t st);
+hipError_t launch_q8_attention(const AttnArgs& a, uint32_t units, bool need_combine, hipStream_t st);
+
+}  // namespace qm

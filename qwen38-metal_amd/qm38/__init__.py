@@ -13,6 +13,7 @@ the library is missing, `load()` raises.
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 import os
 from pathlib import Path
 
@@ -141,9 +142,13 @@ class Runtime:
         _check(self.lib.qm_runtime_create(device, C.byref(h)))
         self.handle = h
         self.device = device
+        # Objects created on this runtime; closed before it (they use its stream).
+        self._children = weakref.WeakSet()
 
     def close(self) -> None:
         if self.handle:
+            for child in list(self._children):
+                child.close()
             self.lib.qm_runtime_destroy(self.handle)
             self.handle = None
 
@@ -222,6 +227,7 @@ class KvCache:
             _check(rt.lib.qm_kv_create(rt.handle, kv_heads, head_dim, page_tokens, max_tokens, C.byref(h)))
             handle = h
         self.handle = handle
+        rt._children.add(self)
 
     def close(self) -> None:
         if self.handle:
@@ -238,6 +244,7 @@ class KvCache:
     def sequence_length(self) -> int:
         return self.rt.lib.qm_kv_length(self.handle)
 
+    @property
     def allocated_pages(self) -> int:
         return self.rt.lib.qm_kv_allocated_pages(self.handle)
 
@@ -279,6 +286,7 @@ class DnWeights:
         _check(rt.lib.qm_dn_weights_create(rt.handle, C.byref(config), *[a.ctypes.data for a in arrs],
                                            C.byref(h)))
         self.handle = h
+        rt._children.add(self)
 
     def close(self) -> None:
         if self.handle:
@@ -302,6 +310,7 @@ class DnState:
         self.weights = weights
         self.rt = weights.rt
         self.handle = handle
+        self.rt._children.add(self)
 
     def close(self) -> None:
         if self.handle:
