@@ -219,8 +219,9 @@ typedef struct qm_dn_state qm_dn_state;
 /* Replaces create_deltanet_weights (metal_runtime.rs:7143-7183).  HOST
  * pointers: conv_weight fp32 [channels][kernel], a_log/dt_bias fp32
  * [value_heads], norm fp32 [value_head_dim]; channels =
- * 2*key_heads*key_head_dim + value_heads*value_head_dim.  This build's
- * kernels need key_head_dim == value_head_dim == 128 and kernel <= 8. */
+ * 2*key_heads*key_head_dim + value_heads*value_head_dim.  Head dimensions
+ * up to 256 and value_heads % key_heads == 0 (validate_deltanet_config,
+ * metal_runtime.rs:9151-9168), else QM_ERR_INVALID_DELTANET_CONFIG. */
 qm_status qm_dn_weights_create(qm_runtime* rt, const qm_dn_config* cfg,
                                const float* conv_weight, const float* a_log,
                                const float* dt_bias, const float* norm,

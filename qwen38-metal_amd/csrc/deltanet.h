@@ -1,0 +1,35 @@
+// Launch interface of the Gated DeltaNet kernels (deltanet.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qm {
+
+struct DnArgs {
+  // config
+  uint32_t key_heads, value_heads, dk, dv, kernel, channels;
+  uint32_t M;  // tokens in this call
+  float eps;
+  // weights
+  const float* conv_w;   // [channels][kernel]
+  const float* a_log;    // [VH]
+  const float* dt_bias;  // [VH]
+  const float* norm;     // [dv]
+  // activations
+  const float* qkv;  // [M][channels]
+  const float* z;    // [M][VH][dv]
+  const float* b;    // [M][VH]
+  const float* a;    // [M][VH]
+  // state
+  const float* hist_in;  // [channels][kernel-1]
+  float* hist_out;       // distinct from hist_in
+  const float* s_in;     // [VH][dv][dk]
+  float* s_out;          // may equal s_in
+  // workspace / output
+  float* conv_out;  // [M][channels]: q^, k^, v after conv + prepare
+  float* out;       // [M][VH][dv]
+};
+
+hipError_t launch_deltanet(const DnArgs& a, hipStream_t st);
+
+}  // namespace qm

@@ -1,0 +1,253 @@
+// C-ABI entry points of the Gated DeltaNet layer (see include/qm38.h).
+#include <stdint.h>
+#include <string.h>
+
+#include "deltanet.h"
+#include "runtime_internal.h"
+
+using namespace qm;
+
+struct qm_dn_weights {
+  qm_runtime* rt = nullptr;
+  qm_dn_config cfg{};
+  uint32_t channels = 0;
+  float* conv_w = nullptr;
+  float* a_log = nullptr;
+  float* dt_bias = nullptr;
+  float* norm = nullptr;
+};
+
+// The conv history is double-buffered (hist[cur] is current); see deltanet.hip.
+struct qm_dn_state {
+  qm_runtime* rt = nullptr;
+  qm_dn_config cfg{};
+  uint32_t channels = 0;
+  size_t hist_elems = 0;  // channels * (kernel - 1)
+  size_t rec_elems = 0;   // VH * dv * dk
+  float* hist[2] = {nullptr, nullptr};
+  int cur = 0;
+  float* rec = nullptr;
+};
+
+namespace {
+
+// validate_deltanet_config (metal_runtime.rs:9151-9168).
+qm_status validate_config(const qm_dn_config* c) {
+  if (c->key_heads == 0 || c->value_heads == 0 || c->key_head_dim == 0 || c->value_head_dim == 0 ||
+      c->conv_kernel_size == 0 || c->value_heads % c->key_heads != 0 || c->key_head_dim > 256 ||
+      c->value_head_dim > 256)
+    return fail(QM_ERR_INVALID_DELTANET_CONFIG,
+                "heads and dimensions must be non-zero, value heads must divide by key heads, and head dimensions "
+                "must fit one GPU threadgroup");
+  const uint64_t channels =
+      2ull * c->key_heads * c->key_head_dim + (uint64_t)c->value_heads * c->value_head_dim;
+  if (channels > 0xFFFFFFFFull || channels * c->conv_kernel_size > 0xFFFFFFFFull)
+    return fail(QM_ERR_DIMENSION_OVERFLOW, "DeltaNet channel count");
+  return QM_OK;
+}
+
+uint32_t channels_of(const qm_dn_config& c) {
+  return 2 * c.key_heads * c.key_head_dim + c.value_heads * c.value_head_dim;
+}
+
+void free_weights(qm_dn_weights* w) {
+  DeviceGuard g(w->rt->device);
+  hipFree(w->conv_w);
+  hipFree(w->a_log);
+  hipFree(w->dt_bias);
+  hipFree(w->norm);
+  delete w;
+}
+
+void free_state(qm_dn_state* s) {
+  DeviceGuard g(s->rt->device);
+  hipFree(s->hist[0]);
+  hipFree(s->hist[1]);
+  hipFree(s->rec);
+  delete s;
+}
+
+qm_status alloc_state(qm_runtime* rt, const qm_dn_config& cfg, qm_dn_state** out) {
+  qm_dn_state* s = new qm_dn_state();
+  s->rt = rt;
+  s->cfg = cfg;
+  s->channels = channels_of(cfg);
+  s->hist_elems = (size_t)s->channels * (cfg.conv_kernel_size - 1);
+  s->rec_elems = (size_t)cfg.value_heads * cfg.value_head_dim * cfg.key_head_dim;
+  // A one-element history keeps the pointers valid for a kernel-size-one model.
+  const size_t hb = (s->hist_elems ? s->hist_elems : 1) * sizeof(float);
+  DeviceGuard g(rt->device);
+  hipError_t e = hipMalloc(&s->hist[0], hb);
+  if (e == hipSuccess) e = hipMalloc(&s->hist[1], hb);
+  if (e == hipSuccess) e = hipMalloc(&s->rec, s->rec_elems * sizeof(float));
+  if (e == hipSuccess) e = hipMemsetAsync(s->hist[0], 0, hb, rt->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(s->hist[1], 0, hb, rt->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(s->rec, 0, s->rec_elems * sizeof(float), rt->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
+  if (e != hipSuccess) {
+    free_state(s);
+    return hip_check(e, "DeltaNet state allocation");
+  }
+  *out = s;
+  return QM_OK;
+}
+
+qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, qm_dn_state* to, const float* qkv,
+              const float* z, const float* b, const float* a, uint32_t M, float eps, float* out) {
+  if (!rt || !w || !to || !qkv || !z || !b || !a || !out) return fail(QM_ERR_NULL_POINTER, "NULL argument");
+  if (!from) from = to;
+  if (M == 0) return fail(QM_ERR_EMPTY_DIMENSION, "DeltaNet prefill needs at least one token");
+  if (w->rt != rt || from->rt != rt || to->rt != rt)
+    return fail(QM_ERR_INVALID_ARGUMENT, "weights and states must belong to this runtime");
+  if (memcmp(&from->cfg, &w->cfg, sizeof(qm_dn_config)) != 0 || memcmp(&to->cfg, &w->cfg, sizeof(qm_dn_config)) != 0)
+    return fail(QM_ERR_WRONG_LENGTH, "DeltaNet state was created for another configuration");
+  const qm_dn_config& c = w->cfg;
+  const size_t conv_bytes = (size_t)M * w->channels * sizeof(float);
+  qm_status st = ensure_scratch(rt, conv_bytes);
+  if (st != QM_OK) return st;
+  DnArgs d{};
+  d.key_heads = c.key_heads;
+  d.value_heads = c.value_heads;
+  d.dk = c.key_head_dim;
+  d.dv = c.value_head_dim;
+  d.kernel = c.conv_kernel_size;
+  d.channels = w->channels;
+  d.M = M;
+  d.eps = eps;
+  d.conv_w = w->conv_w;
+  d.a_log = w->a_log;
+  d.dt_bias = w->dt_bias;
+  d.norm = w->norm;
+  d.qkv = qkv;
+  d.z = z;
+  d.b = b;
+  d.a = a;
+  // New history goes to the buffer that is not being read.
+  const int next = from == to ? 1 - from->cur : to->cur;
+  d.hist_in = from->hist[from->cur];
+  d.hist_out = to->hist[next];
+  d.s_in = from->rec;
+  d.s_out = to->rec;
+  d.conv_out = (float*)rt->scratch;
+  d.out = out;
+  DeviceGuard g(rt->device);
+  hipError_t e = launch_deltanet(d, rt->stream);
+  if (e != hipSuccess) return hip_check(e, "DeltaNet launch");
+  if (c.conv_kernel_size > 1) to->cur = next;
+  return QM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+qm_status qm_dn_weights_create(qm_runtime* rt, const qm_dn_config* cfg, const float* conv_weight,
+                               const float* a_log, const float* dt_bias, const float* norm, qm_dn_weights** out) {
+  if (!rt || !cfg || !conv_weight || !a_log || !dt_bias || !norm || !out)
+    return fail(QM_ERR_NULL_POINTER, "NULL argument");
+  *out = nullptr;
+  qm_status st = validate_config(cfg);
+  if (st != QM_OK) return st;
+  qm_dn_weights* w = new qm_dn_weights();
+  w->rt = rt;
+  w->cfg = *cfg;
+  w->channels = channels_of(*cfg);
+  const size_t nconv = (size_t)w->channels * cfg->conv_kernel_size;
+  DeviceGuard g(rt->device);
+  hipError_t e = hipMalloc(&w->conv_w, nconv * 4);
+  if (e == hipSuccess) e = hipMalloc(&w->a_log, cfg->value_heads * 4);
+  if (e == hipSuccess) e = hipMalloc(&w->dt_bias, cfg->value_heads * 4);
+  if (e == hipSuccess) e = hipMalloc(&w->norm, cfg->value_head_dim * 4);
+  if (e == hipSuccess) e = hipMemcpyAsync(w->conv_w, conv_weight, nconv * 4, hipMemcpyHostToDevice, rt->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(w->a_log, a_log, cfg->value_heads * 4, hipMemcpyHostToDevice, rt->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(w->dt_bias, dt_bias, cfg->value_heads * 4, hipMemcpyHostToDevice, rt->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(w->norm, norm, cfg->value_head_dim * 4, hipMemcpyHostToDevice, rt->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
+  if (e != hipSuccess) {
+    free_weights(w);
+    return hip_check(e, "DeltaNet weight upload");
+  }
+  *out = w;
+  return QM_OK;
+}
+
+void qm_dn_weights_destroy(qm_dn_weights* w) {
+  if (!w) return;
+  hipStreamSynchronize(w->rt->stream);
+  free_weights(w);
+}
+
+qm_status qm_dn_state_create(qm_runtime* rt, const qm_dn_weights* w, qm_dn_state** out) {
+  if (!rt || !w || !out) return fail(QM_ERR_NULL_POINTER, "NULL argument");
+  *out = nullptr;
+  return alloc_state(rt, w->cfg, out);
+}
+
+void qm_dn_state_destroy(qm_dn_state* s) {
+  if (!s) return;
+  hipStreamSynchronize(s->rt->stream);
+  free_state(s);
+}
+
+qm_status qm_dn_state_clone(const qm_dn_state* src, qm_dn_state** out) {
+  if (!src || !out) return fail(QM_ERR_NULL_POINTER, "NULL argument");
+  *out = nullptr;
+  qm_dn_state* s = nullptr;
+  qm_status st = alloc_state(src->rt, src->cfg, &s);
+  if (st != QM_OK) return st;
+  DeviceGuard g(src->rt->device);
+  hipStream_t stream = src->rt->stream;
+  hipError_t e = hipSuccess;
+  if (src->hist_elems)
+    e = hipMemcpyAsync(s->hist[0], src->hist[src->cur], src->hist_elems * 4, hipMemcpyDeviceToDevice, stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(s->rec, src->rec, src->rec_elems * 4, hipMemcpyDeviceToDevice, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) {
+    free_state(s);
+    return hip_check(e, "DeltaNet state clone");
+  }
+  *out = s;
+  return QM_OK;
+}
+
+qm_status qm_dn_state_read(const qm_dn_state* s, float* conv_history, float* recurrent) {
+  if (!s) return fail(QM_ERR_NULL_POINTER, "state is NULL");
+  DeviceGuard g(s->rt->device);
+  hipStream_t stream = s->rt->stream;
+  hipError_t e = hipSuccess;
+  if (conv_history && s->hist_elems)
+    e = hipMemcpyAsync(conv_history, s->hist[s->cur], s->hist_elems * 4, hipMemcpyDeviceToHost, stream);
+  if (e == hipSuccess && recurrent)
+    e = hipMemcpyAsync(recurrent, s->rec, s->rec_elems * 4, hipMemcpyDeviceToHost, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  return hip_check(e, "DeltaNet state read");
+}
+
+qm_status qm_dn_state_write(qm_dn_state* s, const float* conv_history, const float* recurrent) {
+  if (!s) return fail(QM_ERR_NULL_POINTER, "state is NULL");
+  DeviceGuard g(s->rt->device);
+  hipStream_t stream = s->rt->stream;
+  hipError_t e = hipSuccess;
+  if (conv_history && s->hist_elems)
+    e = hipMemcpyAsync(s->hist[s->cur], conv_history, s->hist_elems * 4, hipMemcpyHostToDevice, stream);
+  if (e == hipSuccess && recurrent)
+    e = hipMemcpyAsync(s->rec, recurrent, s->rec_elems * 4, hipMemcpyHostToDevice, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  return hip_check(e, "DeltaNet state write");
+}
+
+qm_status qm_dn_step(qm_runtime* rt, const qm_dn_weights* w, qm_dn_state* st, const float* qkv, const float* z,
+                     const float* b, const float* a, float epsilon, float* out) {
+  return run(rt, w, st, st, qkv, z, b, a, 1, epsilon, out);
+}
+
+qm_status qm_dn_prefill(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, qm_dn_state* to,
+                        const float* qkv, const float* z, const float* b, const float* a, uint32_t M, float epsilon,
+                        float* out) {
+  return run(rt, w, from, to, qkv, z, b, a, M, epsilon, out);
+}
+
+}  // extern "C"

@@ -344,7 +344,7 @@ class DnState:
 
     def write(self, hist, rec) -> None:
         import numpy as np
-        hist = np.ascontiguousarray(hist, np.float32)
-        rec = np.ascontiguousarray(rec, np.float32)
-        _check(self.rt.lib.qm_dn_state_write(self.handle, hist.ctypes.data if hist.size else None,
-                                             rec.ctypes.data))
+        hist = None if hist is None else np.ascontiguousarray(hist, np.float32)
+        rec = None if rec is None else np.ascontiguousarray(rec, np.float32)
+        _check(self.rt.lib.qm_dn_state_write(self.handle, hist.ctypes.data if hist is not None and hist.size else None,
+                                             rec.ctypes.data if rec is not None else None))

@@ -1,0 +1,266 @@
+"""GPU parity of the Gated DeltaNet layer against the CPU oracle.
+
+Ports metal_runtime.rs tests deltanet_step_matches_a_scalar_recurrence
+(:10913) and deltanet_prefill_matches_steps_and_keeps_recurrent_state
+(:11202, including the shadow-state prefill), plus seeded cases at the
+BASELINE shape (16 key heads, 32 value heads, head dims 128, conv kernel 4)
+and two closed forms of the recurrence:
+  * beta = 0 leaves S <- g S;
+  * g = 1, beta = 1 makes S k^ = v after the update (delta rule), since k^
+    has unit norm up to eps.
+Bars: outputs and state within 1e-4 of max|ref| against the fp64 oracle
+(the reference's own tests use 1e-3 absolute); prefill bit-identical to
+token-by-token steps (both run the same recurrence).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from gpu_util import from_dev, to_dev
+from qm38 import DnConfig, QmError
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _cfg(kh, vh, dk, dv, ks):
+    return DnConfig(kh, vh, dk, dv, ks), dict(key_heads=kh, value_heads=vh, key_head_dim=dk, value_head_dim=dv,
+                                              conv_kernel_size=ks)
+
+
+def _channels(c):
+    return 2 * c["key_heads"] * c["key_head_dim"] + c["value_heads"] * c["value_head_dim"]
+
+
+def _run(rt, dev, w, st, qkv, z, b, a, eps, source=None):
+    import torch
+    M = qkv.shape[0]
+    vh, dv = w.config.value_heads, w.config.value_head_dim
+    out = torch.full((M, vh * dv), float("nan"), dtype=torch.float32, device=dev)
+    rt.deltanet_prefill(w, st, to_dev(qkv, dev), to_dev(z, dev), to_dev(b, dev), to_dev(a, dev), M, eps, out,
+                        source=source)
+    return from_dev(out)
+
+
+def _step(rt, dev, w, st, qkv, z, b, a, eps):
+    import torch
+    vh, dv = w.config.value_heads, w.config.value_head_dim
+    out = torch.full((vh * dv,), float("nan"), dtype=torch.float32, device=dev)
+    rt.deltanet_step(w, st, to_dev(qkv, dev), to_dev(z, dev), to_dev(b, dev), to_dev(a, dev), eps, out)
+    return from_dev(out)
+
+
+def _close(got, ref, tol=TOL, what=""):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert np.all(np.isfinite(got)), what
+    scale = max(np.max(np.abs(ref)), 1e-30)
+    err = np.max(np.abs(got - ref)) / scale
+    assert err <= tol, f"{what}: rel err {err:.3e} > {tol:.1e}"
+    return err
+
+
+def _zero_state(c):
+    hist = np.zeros((_channels(c), c["conv_kernel_size"] - 1), np.float64)
+    S = np.zeros((c["value_heads"], c["value_head_dim"], c["key_head_dim"]), np.float64)
+    return hist, S
+
+
+# ---------------------------------------------------------------------------
+# Reference tests (head dims 2)
+# ---------------------------------------------------------------------------
+def test_reference_scalar_recurrence(rt, torch_dev):
+    # metal_runtime.rs:10913-10944: kernel size 1, conv weights all 1.
+    cfg, c = _cfg(1, 1, 2, 2, 1)
+    qkv = np.array([[-0.5, 0.25, 0.75, -1.0, 0.2, -0.4]], np.float32)
+    z = np.array([[0.1, -0.2]], np.float32)
+    b, a = np.array([[0.3]], np.float32), np.array([[-0.1]], np.float32)
+    a_log, dt_bias, norm = np.array([0.2], np.float32), np.array([-0.3], np.float32), np.array([1.1, 0.9], np.float32)
+    conv = np.ones((6, 1), np.float32)
+    w = rt.create_deltanet_weights(cfg, conv, a_log, dt_bias, norm)
+    st = w.create_state()
+    got = _step(rt, torch_dev, w, st, qkv[0], z[0], b[0], a[0], 1e-6)
+    hist, S = _zero_state(c)
+    ref, _, S_ref = oracle.deltanet_prefill(c, conv, a_log, dt_bias, norm, qkv, z, b, a, 1e-6, hist, S, f64=True)
+    assert np.max(np.abs(got - ref[0])) < 1e-3  # the reference's bar
+    _close(got, ref[0], what="scalar recurrence")
+    _close(st.read()[1], S_ref, what="state")
+
+
+def _ref_prefill_case():
+    cfg, c = _cfg(1, 1, 2, 2, 2)
+    qkv = np.array([[-0.5, 0.25, 0.75, -1.0, 0.2, -0.4], [0.1, -0.7, -0.2, 0.6, 0.9, 0.3],
+                    [0.8, -0.1, 0.4, -0.5, -0.6, 0.7]], np.float32)
+    z = np.array([[0.1, -0.2], [-0.3, 0.4], [0.5, -0.6]], np.float32)
+    b = np.array([[0.3], [-0.4], [0.2]], np.float32)
+    a = np.array([[-0.1], [0.25], [-0.35]], np.float32)
+    conv = np.array([0.2, 0.8, -0.1, 0.7, 0.3, 0.6, -0.2, 0.9, 0.15, 0.85, -0.25, 0.75], np.float32).reshape(6, 2)
+    a_log, dt_bias, norm = np.array([0.2], np.float32), np.array([-0.3], np.float32), np.array([1.1, 0.9], np.float32)
+    nxt = (np.array([[-0.35, 0.45, 0.55, -0.15, 0.25, 0.65]], np.float32), np.array([[0.2, -0.45]], np.float32),
+           np.array([[0.15]], np.float32), np.array([[-0.05]], np.float32))
+    return cfg, c, (conv, a_log, dt_bias, norm), (qkv, z, b, a), nxt
+
+
+def test_reference_prefill_matches_steps(rt, torch_dev):
+    # metal_runtime.rs:11202-11300
+    cfg, c, wts, (qkv, z, b, a), (nq, nz, nb, na) = _ref_prefill_case()
+    w = rt.create_deltanet_weights(cfg, *wts)
+    step, pre = w.create_state(), w.create_state()
+    expected = np.stack([_step(rt, torch_dev, w, step, qkv[t], z[t], b[t], a[t], 1e-6) for t in range(3)])
+    actual = _run(rt, torch_dev, w, pre, qkv, z, b, a, 1e-6)
+    assert np.max(np.abs(actual - expected)) < 1e-3
+    assert np.array_equal(actual, expected), "prefill and steps run the same recurrence"
+    hist, S = _zero_state(c)
+    ref, h_ref, S_ref = oracle.deltanet_prefill(c, *wts, qkv, z, b, a, 1e-6, hist, S, f64=True)
+    _close(actual, ref, what="prefill vs oracle")
+    for s in (step, pre):
+        h, S_got = s.read()
+        _close(h, h_ref, tol=0, what="history")
+        _close(S_got, S_ref, what="state")
+    e_next = _step(rt, torch_dev, w, step, nq[0], nz[0], nb[0], na[0], 1e-6)
+    a_next = _step(rt, torch_dev, w, pre, nq[0], nz[0], nb[0], na[0], 1e-6)
+    assert np.max(np.abs(a_next - e_next)) < 1e-3
+    ref_next, _, _ = oracle.deltanet_prefill(c, *wts, nq, nz, nb, na, 1e-6, h_ref, S_ref, f64=True)
+    _close(a_next, ref_next[0], what="next step")
+
+
+def test_reference_shadow_prefill(rt, torch_dev):
+    # metal_runtime.rs:11290-11370: prefill_from(active -> shadow) equals an
+    # ordinary prefill on a clone and leaves the source untouched.
+    cfg, c, wts, (qkv, z, b, a), (nq, nz, nb, na) = _ref_prefill_case()
+    w = rt.create_deltanet_weights(cfg, *wts)
+    active = w.create_state()
+    _run(rt, torch_dev, w, active, qkv[:2], z[:2], b[:2], a[:2], 1e-6)
+    before = active.read()
+    shadow = w.create_state()
+    shadow_out = _run(rt, torch_dev, w, shadow, nq, nz, nb, na, 1e-6, source=active)
+    after = active.read()
+    assert np.array_equal(before[0], after[0]) and np.array_equal(before[1], after[1])
+    ordinary = active.clone()
+    ordinary_out = _run(rt, torch_dev, w, ordinary, nq, nz, nb, na, 1e-6)
+    assert np.array_equal(shadow_out, ordinary_out)
+    for x, y in zip(shadow.read(), ordinary.read()):
+        assert np.array_equal(x, y)
+
+
+# ---------------------------------------------------------------------------
+# Seeded cases at model shapes
+# ---------------------------------------------------------------------------
+def _synth(rng, c, M):
+    ch = _channels(c)
+    vh, dv, ks = c["value_heads"], c["value_head_dim"], c["conv_kernel_size"]
+    qkv = rng.standard_normal((M, ch)).astype(np.float32)
+    z = rng.standard_normal((M, vh * dv)).astype(np.float32)
+    b = rng.standard_normal((M, vh)).astype(np.float32)
+    a = rng.standard_normal((M, vh)).astype(np.float32)
+    conv = (rng.standard_normal((ch, ks)) * 0.5).astype(np.float32)
+    a_log = np.zeros(vh, np.float32)
+    dt_bias = np.zeros(vh, np.float32)
+    norm = (1 + 0.1 * rng.standard_normal(dv)).astype(np.float32)
+    return (conv, a_log, dt_bias, norm), (qkv, z, b, a)
+
+
+SHAPES = [(16, 32, 128, 128, 4), (2, 4, 64, 32, 3), (1, 3, 256, 256, 4), (4, 4, 100, 72, 1), (3, 6, 17, 200, 2)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("M", [1, 5, 33, 130])
+def test_prefill_matches_oracle(rt, torch_dev, shape, M):
+    cfg, c = _cfg(*shape)
+    rng = np.random.default_rng(sum(shape) * 100 + M)
+    wts, acts = _synth(rng, c, M + 9)
+    w = rt.create_deltanet_weights(cfg, *wts)
+    st = w.create_state()
+    # start from a non-zero state: 9 warm-up tokens
+    warm = [x[:9] for x in acts]
+    rest = [x[9:] for x in acts]
+    _run(rt, torch_dev, w, st, *warm, 1e-6)
+    got = _run(rt, torch_dev, w, st, *rest, 1e-6)
+    hist, S = _zero_state(c)
+    _, hist, S = oracle.deltanet_prefill(c, *wts, *warm, 1e-6, hist, S, f64=True)
+    ref, h_ref, S_ref = oracle.deltanet_prefill(c, *wts, *rest, 1e-6, hist, S, f64=True)
+    _close(got, ref, what=f"out {shape} M={M}")
+    h, S_got = st.read()
+    if c["conv_kernel_size"] > 1:
+        _close(h, h_ref, tol=0, what="history")
+    _close(S_got, S_ref, what="state")
+
+
+def test_long_prefill_equals_steps(rt, torch_dev):
+    cfg, c = _cfg(16, 32, 128, 128, 4)
+    M = 256
+    rng = np.random.default_rng(77)
+    wts, acts = _synth(rng, c, M)
+    w = rt.create_deltanet_weights(cfg, *wts)
+    pre, step = w.create_state(), w.create_state()
+    got = _run(rt, torch_dev, w, pre, *acts, 1e-6)
+    steps = np.stack([_step(rt, torch_dev, w, step, *(x[t] for x in acts), 1e-6) for t in range(M)])
+    assert np.array_equal(got, steps)
+    for x, y in zip(pre.read(), step.read()):
+        assert np.array_equal(x, y)
+    hist, S = _zero_state(c)
+    ref, _, S_ref = oracle.deltanet_prefill(c, *wts, *acts, 1e-6, hist, S, f64=True)
+    _close(got, ref, what="long prefill")
+    _close(pre.read()[1], S_ref, what="long state")
+
+
+def test_prefill_2048_tokens(rt, torch_dev):
+    # BASELINE prefill length; state compared with the fp32 oracle (fp64 at this size is slow).
+    cfg, c = _cfg(16, 32, 128, 128, 4)
+    M = 2048
+    rng = np.random.default_rng(2048)
+    wts, acts = _synth(rng, c, M)
+    w = rt.create_deltanet_weights(cfg, *wts)
+    st = w.create_state()
+    got = _run(rt, torch_dev, w, st, *acts, 1e-6)
+    hist, S = _zero_state(c)
+    ref, _, S_ref = oracle.deltanet_prefill(c, *wts, *acts, 1e-6, hist.astype(np.float32), S.astype(np.float32))
+    _close(got, ref, tol=2e-4, what="2048 out vs fp32 oracle")
+    _close(st.read()[1], S_ref, tol=2e-4, what="2048 state vs fp32 oracle")
+
+
+def test_beta_zero_only_decays(rt, torch_dev):
+    cfg, c = _cfg(2, 4, 128, 128, 1)
+    rng = np.random.default_rng(3)
+    wts, (qkv, z, b, a) = _synth(rng, c, 1)
+    w = rt.create_deltanet_weights(cfg, *wts)
+    st = w.create_state()
+    S0 = rng.standard_normal((4, 128, 128)).astype(np.float32)
+    st.write(None, S0)
+    b[:] = -200.0  # sigmoid(-200) == 0 in fp32
+    _step(rt, torch_dev, w, st, qkv[0], z[0], b[0], a[0], 1e-6)
+    g = np.exp(-np.log1p(np.exp(a[0].astype(np.float64))))  # A_log = dt_bias = 0
+    _close(st.read()[1], S0 * g[:, None, None], tol=1e-6, what="S <- g S")
+
+
+def test_delta_rule_stores_value(rt, torch_dev):
+    cfg, c = _cfg(2, 4, 128, 128, 1)
+    rng = np.random.default_rng(4)
+    wts, (qkv, z, b, a) = _synth(rng, c, 1)
+    conv = np.ones_like(wts[0])
+    w = rt.create_deltanet_weights(cfg, conv, *wts[1:])
+    st = w.create_state()
+    st.write(None, rng.standard_normal((4, 128, 128)).astype(np.float32))
+    b[:] = 200.0    # beta = 1
+    a[:] = -200.0   # softplus -> 0, g = 1
+    _step(rt, torch_dev, w, st, qkv[0], z[0], b[0], a[0], 0.0)
+    S = st.read()[1].astype(np.float64)
+    x = qkv[0].astype(np.float64)
+    c_all = x / (1 + np.exp(-x))  # kernel size 1, weight 1: silu(x)
+    k = c_all[256:512].reshape(2, 128)
+    k_hat = k / np.linalg.norm(k, axis=1, keepdims=True)  # eps = 0: exactly unit
+    v = c_all[512:].reshape(4, 128)
+    for h in range(4):
+        _close(S[h] @ k_hat[h // 2], v[h], tol=1e-4, what=f"S k^ = v (head {h})")
+
+
+def test_rejects_bad_configs(rt, torch_dev):
+    for shape in [(0, 1, 2, 2, 1), (2, 3, 2, 2, 1), (1, 1, 257, 2, 1), (1, 1, 2, 300, 1), (1, 1, 2, 2, 0)]:
+        cfg, c = _cfg(*shape)
+        ch = max(_channels(c), 1)
+        with pytest.raises(QmError, match="INVALID_DELTANET_CONFIG"):
+            rt.create_deltanet_weights(cfg, np.zeros((ch, max(shape[4], 1)), np.float32), np.zeros(max(shape[1], 1)),
+                                       np.zeros(max(shape[1], 1)), np.zeros(max(shape[3], 1)))
