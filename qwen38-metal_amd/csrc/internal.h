@@ -24,6 +24,8 @@ struct Workspace {
   size_t partial_bytes;
   unsigned int* counters;
   size_t counter_count;
+  uint16_t* xh;  // prefill GEMM: fp16 copy of the activations
+  size_t xh_bytes;
 };
 
 // Decode (weight-streaming) Q4 projection: M <= 16 activation rows.
@@ -36,6 +38,7 @@ hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const ui
 
 // Prefill Q4 GEMM (M > 16): Y[M][N] = X[M][K] * dequant(W)^T, bf16 out.
 // swiglu as above.
+size_t q4_gemm_xh_bytes(uint32_t K, uint32_t M);
 hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x,
                           uint32_t K, uint32_t M, const Workspace& ws, hipStream_t stream);
 

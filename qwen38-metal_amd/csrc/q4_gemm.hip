@@ -1,23 +1,270 @@
-// Q4 prefill projection (M > 16 rows).
+// Q4 prefill projection (M > 16 rows): Y[M][N] = X[M][K] * dequant(W)^T.
+//
+// Numerics follow the reference's prefill path (qwen38_q4_affine_dequantize_f16
+// + fp16 MPS GEMM, /root/reference/shaders/qwen38.metal:4102-4125,
+// src/metal_runtime.rs:3897-4048): weights become fp16(q*s + b), activations
+// fp16, products accumulate in fp32; the result is stored as bf16.
+//
+// Two kernels:
+//  * x_to_f16_kernel: X (bf16) -> Xh (fp16), once per call.  Within every
+//    8-element chunk the elements are stored in the order 0,4,1,5,2,6,3,7,
+//    the order in which one packed Q4 word unpacks into fp16 pairs, so the
+//    GEMM's dequantised B tile and the A tile agree element by element.
+//  * q4_gemm_kernel: 256 x 256 output tile per workgroup (512 threads,
+//    8 waves as 4 (M) x 2 (N), 64 x 128 per wave on v_mfma_f32_32x32x16_f16),
+//    K in steps of one quantisation group (64).  Per step each thread loads
+//    16 B of X and 16 B of packed W, dequantises its four words with
+//    (w >> 4j & 0x000F000F) | 0x64006400 (fp16 1024 + q), one packed subtract
+//    and one packed FMA per pair, and writes both tiles into the other half
+//    of a double-buffered LDS (2 x 64 KiB) while the waves multiply the
+//    current half: one barrier per K step.
+//    SwiGLU: the 256 W rows of a tile are 128 gate rows and the same 128 up
+//    rows, each wave holding gate and up accumulators of the same outputs, so
+//    h = silu(gate) * up is formed in registers.
+//    Tile order is XCD-aware: workgroups are dealt round-robin to the 8 XCDs,
+//    so the tile index is remapped to give each XCD a contiguous run of N
+//    tiles with all of their M tiles (W is read from HBM once per XCD and
+//    stays in that XCD's L2 while its M tiles pass).
 #include "common.h"
 #include "internal.h"
 
 namespace qm {
+namespace {
 
-hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x, uint32_t K,
-                          uint32_t M, const Workspace& ws, hipStream_t stream) {
-  // Row blocks of 16 through the decode kernel.
-  for (uint32_t m0 = 0; m0 < M; m0 += 16) {
-    Q4Job js[kMaxQ4Jobs];
-    for (int i = 0; i < n_jobs; ++i) {
-      js[i] = jobs[i];
-      if (js[i].out) js[i].out += (size_t)m0 * jobs[i].rows;
-    }
-    const uint32_t mm = M - m0 < 16 ? M - m0 : 16;
-    hipError_t e = launch_q4_decode(js, n_jobs, swiglu, x + (size_t)m0 * K, K, mm, ws, stream);
-    if (e != hipSuccess) return e;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+constexpr int kBM = 256, kBN = 256, kThreads = 512;
+constexpr int kTileBytes = 256 * 128;  // 256 rows x 64 fp16
+constexpr int kXcds = 8;
+
+struct GemmArgs {
+  Q4Job jobs[kMaxQ4Jobs];
+  int n_jobs;
+  const uint16_t* xh;  // fp16 bits [M][K], chunk-permuted
+  uint32_t K, M;
+  uint32_t m_tiles, total_tiles;
+};
+
+// Byte offset of 16-byte chunk c (0..7) of row r in a 256 x 128 B tile.  The
+// XOR spreads the 16 rows one ds_read_b128 phase touches over distinct banks.
+__device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t c) {
+  return r * 128u + 16u * (c ^ (r & 7u) ^ ((r >> 3) & 1u));
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint64_t bytes) {
+  const uint32_t n = bytes > 0xFFFFFFF0ull ? 0xFFFFFFF0u : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+
+__device__ __forceinline__ floatx16 mfma_f16(u32x4 a, u32x4 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
+                                                0, 0);
+}
+
+__device__ __forceinline__ uint32_t dq_pair(uint32_t w, int j, half2v s2, half2v b2) {
+  const uint32_t t = ((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+  half2v q = __builtin_bit_cast(half2v, t) - (half2v){(_Float16)1024.0f, (_Float16)1024.0f};
+  return __builtin_bit_cast(uint32_t, q * s2 + b2);
+}
+
+__global__ __launch_bounds__(256) void x_to_f16_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xh,
+                                                       size_t chunks) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= chunks) return;
+  const u32x4 v = *(const u32x4*)(x + 8 * i);
+  // v holds bf16 pairs (x0,x1)(x2,x3)(x4,x5)(x6,x7); emit 0,4,1,5,2,6,3,7.
+  const uint32_t e[8] = {v.x & 0xFFFFu, v.x >> 16, v.y & 0xFFFFu, v.y >> 16,
+                         v.z & 0xFFFFu, v.z >> 16, v.w & 0xFFFFu, v.w >> 16};
+  uint32_t h[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const _Float16 f = (_Float16)bf16_to_f32(e[k]);
+    h[k] = __builtin_bit_cast(uint16_t, f);
   }
-  return hipSuccess;
+  u32x4 o;
+  o.x = h[0] | (h[4] << 16);
+  o.y = h[1] | (h[5] << 16);
+  o.z = h[2] | (h[6] << 16);
+  o.w = h[3] | (h[7] << 16);
+  *(u32x4*)(xh + 8 * i) = o;
+}
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmArgs args) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][kTileBytes];  // [stage][X | W]
+
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t wm = wave & 3, wn = wave >> 2;
+  const uint32_t K = args.K, M = args.M, G = K / 64;
+
+  // ---- XCD-aware tile remap -------------------------------------------------
+  const uint32_t T = args.total_tiles;
+  const uint32_t xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds;
+  const uint32_t q = T / kXcds, rem = T % kXcds;
+  const uint32_t L = xcd * q + min(xcd, rem) + local;
+  const uint32_t n_tile = L / args.m_tiles, m_tile = L % args.m_tiles;
+  const uint32_t m0 = m_tile * kBM;
+
+  // ---- this thread's W row and the tile's job ------------------------------
+  int jt = 0;
+  if (!SWIGLU) {
+    while (jt + 1 < args.n_jobs && n_tile >= args.jobs[jt + 1].tile_begin) ++jt;
+  }
+  const uint32_t srow = tid >> 1, shalf = tid & 1;  // staging: row of the tiles, chunk half
+  const Q4Job& wj = args.jobs[SWIGLU ? (srow >= 128 ? 1 : 0) : jt];
+  uint32_t n_first, wrow;
+  if (SWIGLU) {
+    n_first = n_tile * 128;
+    wrow = n_first + (srow & 127);
+  } else {
+    n_first = (n_tile - wj.tile_begin) * kBN;
+    wrow = n_first + srow;
+  }
+  wrow = min(wrow, wj.rows - 1);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(wj.w, (uint64_t)wj.rows * (K / 2));
+  const uint16_t* s_row = wj.s + (size_t)wrow * G;
+  const uint16_t* b_row = wj.b + (size_t)wrow * G;
+  const uint32_t w_voff = wrow * (K / 2) + shalf * 16;
+  const uint32_t xrow = min(m0 + srow, M - 1);
+  const uint16_t* x_src = args.xh + (size_t)xrow * K + shalf * 32;
+
+  // ---- staging registers ---------------------------------------------------
+  u32x4 xr[4];
+  u32x4 wr;
+  uint16_t sr, br;
+  auto load = [&](uint32_t g) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xr[i] = *(const u32x4*)(x_src + g * 64 + 8 * i);
+    wr = __builtin_amdgcn_raw_buffer_load_b128(rw, w_voff, g * 32, 0);
+    sr = s_row[g];
+    br = b_row[g];
+  };
+  auto store = [&](int stage) {
+    uint8_t* xt = lds[stage][0];
+    uint8_t* wt = lds[stage][1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *(u32x4*)(xt + swz(srow, shalf * 4 + i)) = xr[i];
+    const _Float16 s = (_Float16)bf16_to_f32(sr), b = (_Float16)bf16_to_f32(br);
+    const half2v s2 = {s, s}, b2 = {b, b};
+    const uint32_t wv[4] = {wr.x, wr.y, wr.z, wr.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u32x4 d;
+      d.x = dq_pair(wv[i], 0, s2, b2);
+      d.y = dq_pair(wv[i], 1, s2, b2);
+      d.z = dq_pair(wv[i], 2, s2, b2);
+      d.w = dq_pair(wv[i], 3, s2, b2);
+      *(u32x4*)(wt + swz(srow, shalf * 4 + i)) = d;
+    }
+  };
+
+  floatx16 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = floatx16{};
+
+  // B-tile row bases of this wave's four 32-column blocks.
+  uint32_t brow[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    brow[j] = SWIGLU ? (j < 2 ? 64 * wn + 32 * j : 128 + 64 * wn + 32 * (j - 2)) : 128 * wn + 32 * j;
+  const uint32_t arow0 = 64 * wm + (lane & 31);
+  const uint32_t kh = lane >> 5;
+
+  load(0);
+  store(0);
+  if (G > 1) load(1);
+  __syncthreads();
+
+  for (uint32_t g = 0; g < G; ++g) {
+    const int st = g & 1;
+    const uint8_t* xt = lds[st][0];
+    const uint8_t* wt = lds[st][1];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint32_t c = 2 * s + kh;
+      u32x4 a[2], b[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[i] = *(const u32x4*)(xt + swz(arow0 + 32 * i, c));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = *(const u32x4*)(wt + swz(brow[j] + (lane & 31), c));
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_f16(a[i], b[j], acc[i][j]);
+    }
+    if (g + 1 < G) {
+      store(st ^ 1);
+      if (g + 2 < G) load(g + 2);
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue ------------------------------------------------------------
+  // acc[i][j] element e: row 32 i + 8 (e >> 2) + 4 kh + (e & 3) of the wave's
+  // 64 rows, column (lane & 31) of block j.
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t m = m0 + 64 * wm + 32 * i + 8 * (e >> 2) + 4 * kh + (e & 3);
+      if (m >= M) continue;
+      if (SWIGLU) {
+        const Q4Job& gj = args.jobs[0];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const uint32_t n = n_tile * 128 + 64 * wn + 32 * j + (lane & 31);
+          if (n < gj.rows) {
+            const float gv = acc[i][j][e], uv = acc[i][j + 2][e];
+            gj.out[(size_t)m * gj.rows + n] = f32_to_bf16(silu_f(gv) * uv);
+          }
+        }
+      } else {
+        const Q4Job& oj = args.jobs[jt];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t n = n_first + brow[j] + (lane & 31);
+          if (n < oj.rows) oj.out[(size_t)m * oj.rows + n] = f32_to_bf16(acc[i][j][e]);
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+size_t q4_gemm_xh_bytes(uint32_t K, uint32_t M) { return (size_t)M * K * 2; }
+
+hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x, uint32_t K, uint32_t M,
+                          const Workspace& ws, hipStream_t stream) {
+  if (n_jobs < 1 || n_jobs > kMaxQ4Jobs || K % 64 != 0 || M == 0) return hipErrorInvalidValue;
+  if (!ws.xh || ws.xh_bytes < q4_gemm_xh_bytes(K, M)) return hipErrorInvalidValue;
+  GemmArgs a{};
+  a.n_jobs = n_jobs;
+  a.xh = ws.xh;
+  a.K = K;
+  a.M = M;
+  a.m_tiles = (M + kBM - 1) / kBM;
+  uint32_t n_tiles = 0;
+  for (int i = 0; i < n_jobs; ++i) {
+    a.jobs[i] = jobs[i];
+    a.jobs[i].tile_begin = n_tiles;
+    if (!swiglu) n_tiles += (jobs[i].rows + kBN - 1) / kBN;
+  }
+  if (swiglu) n_tiles = (jobs[0].rows + 127) / 128;
+  a.total_tiles = n_tiles * a.m_tiles;
+
+  const size_t chunks = (size_t)M * K / 8;
+  hipLaunchKernelGGL(x_to_f16_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream, x, ws.xh, chunks);
+  if (swiglu)
+    hipLaunchKernelGGL(q4_gemm_kernel<true>, dim3(a.total_tiles), dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL(q4_gemm_kernel<false>, dim3(a.total_tiles), dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
 }
 
 }  // namespace qm

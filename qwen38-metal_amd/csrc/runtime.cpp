@@ -76,6 +76,22 @@ qm_status qm::ensure_partials(qm_runtime* rt, size_t bytes) {
   return QM_OK;
 }
 
+qm_status qm::ensure_xh(qm_runtime* rt, size_t bytes) {
+  if (rt->xh_bytes >= bytes) return QM_OK;
+  if (rt->xh) {
+    hipError_t e = hipStreamSynchronize(rt->stream);
+    if (e != hipSuccess) return hip_check(e, "xh resize sync");
+    hipFree(rt->xh);
+    rt->xh = nullptr;
+    rt->xh_bytes = 0;
+  }
+  const size_t want = (bytes + 255) & ~size_t(255);
+  hipError_t e = hipMalloc(&rt->xh, want);
+  if (e != hipSuccess) return hip_check(e, "xh hipMalloc");
+  rt->xh_bytes = want;
+  return QM_OK;
+}
+
 qm_status qm::ensure_counters(qm_runtime* rt, size_t count) {
   if (rt->counter_count >= count) return QM_OK;
   if (rt->counters) {
@@ -97,7 +113,8 @@ qm_status qm::ensure_counters(qm_runtime* rt, size_t count) {
 }
 
 qm::Workspace qm::workspace(qm_runtime* rt) {
-  return Workspace{(float*)rt->partials, rt->partial_bytes, rt->counters, rt->counter_count};
+  return Workspace{(float*)rt->partials, rt->partial_bytes, rt->counters, rt->counter_count, (uint16_t*)rt->xh,
+                   rt->xh_bytes};
 }
 
 extern "C" {
@@ -153,6 +170,7 @@ void qm_runtime_destroy(qm_runtime* rt) {
   if (rt->scratch) hipFree(rt->scratch);
   if (rt->counters) hipFree(rt->counters);
   if (rt->partials) hipFree(rt->partials);
+  if (rt->xh) hipFree(rt->xh);
   delete rt;
 }
 

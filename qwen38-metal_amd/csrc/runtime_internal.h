@@ -24,6 +24,10 @@ struct qm_runtime {
   // workgroup (no zeroing needed: every slot is written before it is read).
   void* partials = nullptr;
   size_t partial_bytes = 0;
+  // fp16 activations of the prefill GEMM (separate from `scratch`, which may
+  // hold the MLP's h while h itself is converted).
+  void* xh = nullptr;
+  size_t xh_bytes = 0;
 };
 
 namespace qm {
@@ -33,6 +37,7 @@ qm_status hip_check(hipError_t err, const char* what);
 qm_status ensure_scratch(qm_runtime* rt, size_t bytes);
 qm_status ensure_partials(qm_runtime* rt, size_t bytes);
 qm_status ensure_counters(qm_runtime* rt, size_t count);
+qm_status ensure_xh(qm_runtime* rt, size_t bytes);
 // Workspace handed to kernels that split work across workgroups.
 Workspace workspace(qm_runtime* rt);
 

@@ -53,6 +53,7 @@ qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const ui
   q4_decode_workspace(jobs, n, swiglu, K, M < kDecodeMaxRows ? M : kDecodeMaxRows, &pbytes, &counters);
   qm_status st = ensure_partials(rt, pbytes);
   if (st == QM_OK) st = ensure_counters(rt, counters);
+  if (st == QM_OK && M > kDecodeMaxRows) st = ensure_xh(rt, q4_gemm_xh_bytes(K, M));
   if (st != QM_OK) return st;
   const Workspace ws = workspace(rt);
   hipError_t e = M <= kDecodeMaxRows ? launch_q4_decode(jobs, n, swiglu, x, K, M, ws, rt->stream)
