@@ -3,17 +3,21 @@
 Headline (`value`): MLX affine-Q4 decode projection set at 27B-class shapes
 with one activation row: fused QKV 5120->10240, gate+up
 5120->2x17408 with SwiGLU in the epilogue, down 17408->5120.  One step = one
-pass of the three projections; `value` = algorithmic bytes moved per step /
-step time (GB/s), inputs resident in HBM.
+pass of the three projections; `value` = algorithmic bytes of the step / step
+time (GB/s), inputs resident in HBM.  Three copies of the weights (540 MB)
+rotate between steps so the 256 MB MALL cannot serve them.
 
-Extra fields: the same set at 4 and 8 rows, Q8-KV decode attention at 32K
-(us/token), Q4 prefill GEMM TFLOP/s and DeltaNet timings, each with its
-roofline fraction.  `roofline` describes the dominant kernel of the headline
-(the gate+up SwiGLU projection), timed live with HIP events on the stream it
-is launched on.  `cpu_baseline` runs the same decode-projection math on the
-host (oracle/, OpenMP) over a bounded sample.
+`extras` carries the other legs of the metric, each against its roofline:
+the decode set at 4 and 8 rows; Q8-KV decode attention at 32K context
+(us/token) and a ragged batch of 8 sequences over {4K, 32K, 128K}; causal
+prefill attention (2048 rows onto a 4K cache); the Q4 prefill GEMM set at
+M = 512 and 2048 (TFLOP/s); the Gated DeltaNet decode step and 2048-token
+prefill.  `roofline` describes the dominant kernel of the headline (the
+gate+up SwiGLU projection), timed with HIP events on the stream it is
+launched on.  `cpu_baseline` runs the same decode-projection math on host
+cores (oracle/, OpenMP) over a bounded sample.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -29,10 +33,13 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "qwen38-metal_amd"))
 
-HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
-BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, TFLOP/s
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, GB/s
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 MFMA, TFLOP/s
 
 H, I, QKV = 5120, 17408, 10240
+ATT_H, ATT_KVH, ATT_D = 64, 8, 128
+DN = dict(key_heads=16, value_heads=32, key_head_dim=128, value_head_dim=128, conv_kernel_size=4)
+NCOPY = 3
 
 
 def q4_bytes(rows: int, cols: int) -> int:
@@ -43,76 +50,254 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-class Timer:
-    """HIP-event timing on the stream the kernels are launched on."""
+def dev_array(a, dev):
+    import torch
+    a = np.ascontiguousarray(a)
+    v = {np.dtype(np.uint16): np.int16, np.dtype(np.uint32): np.int32}.get(a.dtype)
+    return torch.from_numpy(a.view(v) if v is not None else a).to(dev)
+
+
+class Events:
+    """HIP events recorded on the stream the kernels are launched on."""
 
     def __init__(self, stream):
         import torch
         self.torch = torch
         self.stream = stream
 
-    def event(self):
+    def mark(self):
         e = self.torch.cuda.Event(enable_timing=True)
         e.record(self.stream)
         return e
 
 
-def decode_set(rt, dev, M: int, rng):
+_BLOCK = {}
+
+
+def gpu_blocker(ms: float = 12.0):
+    """Queues ~ms of unrelated GPU work so that the host enqueues the timed
+    steps while the GPU is busy: the events then see the kernels back to back
+    instead of waiting on Python launch overhead."""
     import torch
+    if "a" not in _BLOCK:
+        _BLOCK["a"] = torch.randn((4096, 4096), dtype=torch.float16, device="cuda")
+        a = _BLOCK["a"]
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(4):
+            torch.mm(a, a)
+        e1.record()
+        torch.cuda.synchronize()
+        _BLOCK["n"] = max(1, int(ms / max(e0.elapsed_time(e1) / 4, 1e-3)))
+    a = _BLOCK["a"]
+    for _ in range(_BLOCK["n"]):
+        torch.mm(a, a)
+
+
+def timed(step, stream, steps: int, warmup: int):
+    """Runs warmup + steps calls of step(i, marks); returns (ms per step, per-step mark lists)."""
+    import torch
+    ev = Events(stream)
+    for i in range(warmup):
+        step(i, None)
+    torch.cuda.synchronize()
+    gpu_blocker()
+    marks_all = []
+    t0 = ev.mark()
+    for i in range(steps):
+        marks = [ev]
+        step(warmup + i, marks)
+        marks_all.append(marks[1:])
+    t1 = ev.mark()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps, marks_all
+
+
+def _mark(marks):
+    if marks is not None:
+        marks.append(marks[0].mark())
+
+
+# ---------------------------------------------------------------------------
+# Q4 projections
+# ---------------------------------------------------------------------------
+def synth_bf16(rng, shape):
+    from qm38 import synth
+    return synth.bf16_normal(rng, shape)
+
+
+def q4_sets(rng, dev):
     import qm38
     from qm38 import synth
+    sets = []
+    for _ in range(NCOPY):
+        mats = {}
+        for name, rows, cols in (("qkv", QKV, H), ("gate", I, H), ("up", I, H), ("down", H, I)):
+            w, s, b = synth.q4_matrix(rng, rows, cols)
+            t = (dev_array(w, dev), dev_array(s, dev), dev_array(b, dev))
+            mats[name] = (qm38.Runtime.job(*t, rows), t)
+        sets.append(mats)
+    return sets
 
-    def up(a):
-        a = np.ascontiguousarray(a)
-        v = {np.dtype(np.uint16): np.int16, np.dtype(np.uint32): np.int32}[a.dtype]
-        return torch.from_numpy(a.view(v)).to(dev)
 
-    mats = {}
-    for name, rows, cols in (("qkv", QKV, H), ("gate", I, H), ("up", I, H), ("down", H, I)):
-        w, s, b = synth.q4_matrix(rng, rows, cols)
-        mats[name] = (up(w), up(s), up(b), rows)
-    jobs = {k: qm38.Runtime.job(v[0], v[1], v[2], v[3]) for k, v in mats.items()}
-    x = up(synth.bf16_normal(rng, (M, H)))
+def q4_leg(rt, dev, sets, M: int, rng, steps, warmup):
+    """QKV, gate+up (SwiGLU), down over M rows; returns timings and byte / flop counts."""
+    import torch
+    from qm38 import synth
+    x = dev_array(synth.bf16_normal(rng, (M, H)), dev)
     qkv_out = torch.empty((M, QKV), dtype=torch.int16, device=dev)
     h = torch.empty((M, I), dtype=torch.int16, device=dev)
     y = torch.empty((M, H), dtype=torch.int16, device=dev)
 
-    def step(timer=None, marks=None):
-        rt.q4_project([jobs["qkv"]], x, H, M, [qkv_out])
-        if marks is not None:
-            marks.append(timer.event())
-        rt.q4_swiglu(jobs["gate"], jobs["up"], x, H, M, h)
-        if marks is not None:
-            marks.append(timer.event())
-        rt.q4_project([jobs["down"]], h, I, M, [y])
+    def step(i, marks):
+        j = sets[i % NCOPY]
+        _mark(marks)
+        rt.q4_project([j["qkv"][0]], x, H, M, [qkv_out])
+        _mark(marks)
+        rt.q4_swiglu(j["gate"][0], j["up"][0], x, H, M, h)
+        _mark(marks)
+        rt.q4_project([j["down"][0]], h, I, M, [y])
+        _mark(marks)
 
-    weight_bytes = q4_bytes(QKV, H) + 2 * q4_bytes(I, H) + q4_bytes(H, I)
-    act_bytes = 2 * M * (H + QKV) + 2 * M * (H + I) + 2 * M * (I + H)
-    gateup_bytes = 2 * q4_bytes(I, H) + 2 * M * (H + I)
-    return step, weight_bytes + act_bytes, gateup_bytes, mats
+    ms, marks = timed(step, torch.cuda.current_stream(), steps, warmup)
+    per = np.array([[a.elapsed_time(b) for a, b in zip(m[:-1], m[1:])] for m in marks]).mean(0)
+    wbytes = {"qkv": q4_bytes(QKV, H), "gateup": 2 * q4_bytes(I, H), "down": q4_bytes(H, I)}
+    abytes = {"qkv": 2 * M * (H + QKV), "gateup": 2 * M * (H + I), "down": 2 * M * (I + H)}
+    flops = {"qkv": 2 * M * QKV * H, "gateup": 4 * M * I * H, "down": 2 * M * H * I}
+    kern = dict(zip(("qkv", "gateup", "down"), per))
+    return ms, kern, wbytes, abytes, flops
 
 
-def time_steps(step, stream, steps: int, warmup: int, with_marks: bool = False):
+# ---------------------------------------------------------------------------
+# Q8-KV attention
+# ---------------------------------------------------------------------------
+def kv_fill(rt, dev, cache, rng, tokens: int, chunk: int = 8192):
+    """Appends `tokens` random K/V rows through the prefill entry point with one
+    query head per KV head (the cheapest causal pass; its output is unused)."""
     import torch
-    timer = Timer(stream)
-    for _ in range(warmup):
-        step()
+    from qm38 import synth
+    done = 0
+    q = dev_array(synth.bf16_normal(rng, (chunk, ATT_KVH, ATT_D)), dev)
+    o = torch.empty((chunk, ATT_KVH, ATT_D), dtype=torch.int16, device=dev)
+    kv = torch.randn((2, chunk, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
+    while done < tokens:
+        n = min(chunk, tokens - done)
+        rt.gqa_attention_q8_prefill(cache, q, None, kv[0], kv[1], ATT_KVH, n, o)
+        done += n
     torch.cuda.synchronize()
-    marks_all = []
-    t0 = timer.event()
-    for _ in range(steps):
-        if with_marks:
-            marks = []
-            step(timer, marks)
-            marks_all.append(marks)
+
+
+def attn_bytes(T: int) -> int:
+    return T * ATT_KVH * ATT_D * 2 + T * ATT_KVH * 2 * 4
+
+
+def attention_legs(rt, dev, rng, steps, warmup):
+    import torch
+    from qm38 import synth
+    out = {}
+    stream = torch.cuda.current_stream()
+    # (a) one sequence at 32K: us per decode token.
+    T0 = 32768
+    cache = rt.create_q8_kv_state(ATT_KVH, ATT_D, T0 + steps + warmup + 8)
+    kv_fill(rt, dev, cache, rng, T0)
+    q = dev_array(synth.bf16_normal(rng, (1, ATT_H, ATT_D)), dev)
+    g = dev_array(synth.bf16_normal(rng, (1, ATT_H, ATT_D)), dev)
+    k = torch.randn((1, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
+    v = torch.randn((1, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
+    o = torch.empty((1, ATT_H, ATT_D), dtype=torch.int16, device=dev)
+    ms, _ = timed(lambda i, m: rt.gqa_attention_q8([cache], q, g, k, v, ATT_H, o), stream, steps, warmup)
+    T_avg = T0 + warmup + (steps + 1) / 2
+    gbs = attn_bytes(int(T_avg)) / (ms * 1e-3) / 1e9
+    out["attn_decode_32k"] = {"us_per_token": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                              "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                              "shape": "H=64 KVH=8 d=128, 1 sequence at 32K"}
+    cache.close()
+    torch.cuda.empty_cache()
+    # (b) ragged batch of 8 over {4K, 32K, 128K}.
+    lens = list(np.random.default_rng(4).choice([4096, 32768, 131072], 8))
+    caches = []
+    for n in lens:
+        c = rt.create_q8_kv_state(ATT_KVH, ATT_D, int(n) + steps + warmup + 8)
+        kv_fill(rt, dev, c, rng, int(n))
+        caches.append(c)
+    B = len(caches)
+    q = dev_array(synth.bf16_normal(rng, (B, ATT_H, ATT_D)), dev)
+    g = dev_array(synth.bf16_normal(rng, (B, ATT_H, ATT_D)), dev)
+    k = torch.randn((B, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
+    v = torch.randn((B, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
+    o = torch.empty((B, ATT_H, ATT_D), dtype=torch.int16, device=dev)
+    ms, _ = timed(lambda i, m: rt.gqa_attention_q8(caches, q, g, k, v, ATT_H, o), stream, steps, warmup)
+    total = sum(attn_bytes(int(n) + warmup + steps // 2) for n in lens)
+    gbs = total / (ms * 1e-3) / 1e9
+    out["attn_decode_ragged_b8"] = {"us_per_step": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                                    "lengths": [int(n) for n in lens]}
+    for c in caches:
+        c.close()
+    torch.cuda.empty_cache()
+    # (c) causal prefill: 2048 rows onto a 4096-token cache.
+    P, T = 2048, 4096
+    reps = max(2, min(steps, 5))
+    caches = [rt.create_q8_kv_state(ATT_KVH, ATT_D, T + P) for _ in range(reps + 1)]
+    for c in caches:
+        kv_fill(rt, dev, c, rng, T)
+    q = dev_array(synth.bf16_normal(rng, (P, ATT_H, ATT_D)), dev)
+    g = dev_array(synth.bf16_normal(rng, (P, ATT_H, ATT_D)), dev)
+    k = torch.randn((P, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
+    v = torch.randn((P, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
+    o = torch.empty((P, ATT_H, ATT_D), dtype=torch.int16, device=dev)
+    ms, _ = timed(lambda i, m: rt.gqa_attention_q8_prefill(caches[i], q, g, k, v, ATT_H, P, o), stream, reps, 1)
+    flops = 4.0 * ATT_H * ATT_D * sum(T + i + 1 for i in range(P))
+    out["attn_prefill_2048_on_4k"] = {"ms": round(ms, 3), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2),
+                                      "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)}
+    for c in caches:
+        c.close()
+    torch.cuda.empty_cache()
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Gated DeltaNet
+# ---------------------------------------------------------------------------
+def deltanet_legs(rt, dev, rng, steps, warmup):
+    import torch
+    import qm38
+    c = DN
+    ch = 2 * c["key_heads"] * c["key_head_dim"] + c["value_heads"] * c["value_head_dim"]
+    VH, dv, dk = c["value_heads"], c["value_head_dim"], c["key_head_dim"]
+    cfg = qm38.DnConfig(c["key_heads"], VH, dk, dv, c["conv_kernel_size"])
+    w = rt.create_deltanet_weights(cfg, (rng.standard_normal((ch, 4)) * 0.5).astype(np.float32),
+                                   np.zeros(VH, np.float32), np.zeros(VH, np.float32),
+                                   (1 + 0.1 * rng.standard_normal(dv)).astype(np.float32))
+    st = w.create_state()
+    out = {}
+    stream = torch.cuda.current_stream()
+    for M in (1, 2048):
+        qkv = torch.randn((M, ch), device=dev)
+        z = torch.randn((M, VH * dv), device=dev)
+        b = torch.randn((M, VH), device=dev)
+        a = torch.randn((M, VH), device=dev)
+        o = torch.empty((M, VH * dv), device=dev)
+        if M == 1:
+            fn = lambda i, m: rt.deltanet_step(w, st, qkv, z, b, a, 1e-6, o)
         else:
-            step()
-    t1 = timer.event()
-    torch.cuda.synchronize()
-    total_ms = t0.elapsed_time(t1)
-    return total_ms / steps, marks_all
+            fn = lambda i, m: rt.deltanet_prefill(w, st, qkv, z, b, a, M, 1e-6, o)
+        ms, _ = timed(fn, stream, steps if M == 1 else max(2, steps // 10), warmup if M == 1 else 1)
+        state = 2 * VH * dv * dk * 4 + 2 * ch * 3 * 4
+        acts = M * (ch + VH * dv + 2 * VH + VH * dv) * 4
+        gbs = (state + acts) / (ms * 1e-3) / 1e9
+        key = "deltanet_step" if M == 1 else "deltanet_prefill_2048"
+        out[key] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                    "tokens_per_s": round(M / (ms * 1e-3), 1)}
+    st.close()
+    w.close()
+    return out
 
 
+# ---------------------------------------------------------------------------
+# CPU baseline
+# ---------------------------------------------------------------------------
 def cpu_baseline_q4(seconds: float = 12.0):
     """Same decode-projection math (oracle/, fp32, OpenMP over rows) on host cores."""
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -135,17 +320,29 @@ def cpu_baseline_q4(seconds: float = 12.0):
                       f"accumulation (oracle qo_q4_project_f32)"}
 
 
+def traffic_from_profiles():
+    """HBM bytes per launch of the gate+up kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE measurement (profiles/), or None."""
+    p = ROOT / "profiles" / "q4_decode_gateup_traffic.json"
+    try:
+        return json.loads(p.read_text()).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--quick", action="store_true", help="skip the extra legs and the CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="headline only: no extra legs, no CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="for rocprofv3 --pmc: 5 launches of a 256 MiB copy, then 5 gate+up M=1 launches")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this path has no multi-GPU mode (see DESIGN.md, sharding)",
-              file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU mode (one GPU per box); "
+              "run with --gpus 1", file=sys.stderr)
         return 2
 
     import torch
@@ -154,26 +351,55 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     dev = torch.device("cuda:0")
-    stream = torch.cuda.current_stream()
     rt = qm38.Runtime(0)
-    rt.set_stream(stream)
+    rt.set_stream(torch.cuda.current_stream())
     rng = np.random.default_rng(2026)
 
+    log("[bench] uploading 3 weight copies")
+    sets = q4_sets(rng, dev)
+    if args.traffic_probe:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        x = dev_array(synth_bf16(rng, (1, H)), dev)
+        h = torch.empty((1, I), dtype=torch.int16, device=dev)
+        for i in range(5):
+            dst.copy_(src)
+        for i in range(5):
+            j = sets[i % NCOPY]
+            rt.q4_swiglu(j["gate"][0], j["up"][0], x, H, 1, h)
+        torch.cuda.synchronize()
+        rt.close()
+        return 0
     extras = {}
     head = None
-    for M in (1, 4, 8):
-        log(f"[bench] decode set M={M}")
-        step, step_bytes, gu_bytes, _mats = decode_set(rt, dev, M, rng)
-        ms, marks = time_steps(step, stream, args.steps, args.warmup, with_marks=True)
-        gu_ms = float(np.mean([a.elapsed_time(b) for a, b in marks]))
+    for M in (1, 4, 8) if not args.quick else (1,):
+        log(f"[bench] q4 decode set M={M}")
+        ms, kern, wb, ab, _ = q4_leg(rt, dev, sets, M, rng, args.steps, args.warmup)
+        step_bytes = sum(wb.values()) + sum(ab.values())
         gbs = step_bytes / (ms * 1e-3) / 1e9
-        extras[f"q4_decode_set_M{M}"] = {"GB/s": round(gbs, 1), "ms_per_step": round(ms, 4),
-                                         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-                                         "gate_up_kernel_us": round(gu_ms * 1e3, 2)}
+        extras[f"q4_decode_set_M{M}"] = {
+            "GB/s": round(gbs, 1), "ms_per_step": round(ms, 4), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "kernel_us": {k: round(v * 1e3, 2) for k, v in kern.items()},
+            "kernel_hbm_frac": {k: round((wb[k] + ab[k]) / (kern[k] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) for k in kern}}
         if M == 1:
-            head = (gbs, ms, step_bytes, gu_bytes, gu_ms)
-        del step, _mats
-        torch.cuda.empty_cache()
+            head = (gbs, ms, step_bytes, wb["gateup"] + ab["gateup"], kern["gateup"])
+    if not args.quick:
+        for M in (512, 2048):
+            log(f"[bench] q4 prefill GEMM set M={M}")
+            steps = max(3, args.steps // 10)
+            ms, kern, wb, ab, fl = q4_leg(rt, dev, sets, M, rng, steps, 2)
+            tf = sum(fl.values()) / (ms * 1e-3) / 1e12
+            extras[f"q4_prefill_set_M{M}"] = {
+                "TFLOP/s": round(tf, 1), "ms_per_step": round(ms, 3), "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4),
+                "kernel_us": {k: round(v * 1e3, 1) for k, v in kern.items()},
+                "kernel_TFLOP/s": {k: round(fl[k] / (kern[k] * 1e-3) / 1e12, 1) for k in kern}}
+    del sets
+    torch.cuda.empty_cache()
+    if not args.quick:
+        log("[bench] attention")
+        extras.update(attention_legs(rt, dev, rng, args.steps, args.warmup))
+        log("[bench] deltanet")
+        extras.update(deltanet_legs(rt, dev, rng, args.steps, args.warmup))
 
     gbs, ms, step_bytes, gu_bytes, gu_ms = head
     gu_achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
@@ -189,13 +415,13 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "q4-affine weights x bf16 activations, fp32 accumulate",
-        "data": "synthetic (seeded; BASELINE config distributions)",
-        "config": {"workload": "Q4 decode projection set, 27B-class: QKV 5120->10240, gate+up "
+        "data": "synthetic (seeded; BASELINE config distributions; 3 rotating weight copies)",
+        "config": {"workload": "BASELINE config 2: Q4 decode projection set, QKV 5120->10240, gate+up "
                                "5120->2x17408 (+SwiGLU), down 17408->5120, M=1",
                    "step_bytes": step_bytes, "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(gu_achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "q4_decode_kernel<2,true,true> (gate+up SwiGLU, M=1)",
+                     "frac": round(gu_achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
+                     "kernel": "q4_decode_kernel (gate+up with SwiGLU epilogue, M=1)",
                      "bytes_per_launch": gu_bytes, "avg_launch_us": round(gu_ms * 1e3, 2)},
         "extras": extras,
     }

@@ -71,6 +71,14 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
     p = Path(path) if path else LIB_PATH
     if not p.exists():
         raise FileNotFoundError(f"{p} is missing: run `python qwen38-metal_amd/build.py`")
+    # One HIP runtime per process: torch ships its own libamdhip64 (same
+    # SONAME as /opt/rocm's).  Loading torch first makes libqm38 bind to the
+    # runtime that owns the tensors and streams handed to it; loading libqm38
+    # first would bring in a second HIP runtime that cannot share the device.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = C.CDLL(str(p))
     vp, u32, i32 = C.c_void_p, C.c_uint32, C.c_int
     sig = {

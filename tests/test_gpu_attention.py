@@ -207,7 +207,8 @@ def _fill(rt, dev, cache, mirror, rng, n, H, KVH, D):
     mirror.append(k, v)
 
 
-@pytest.mark.parametrize("D,H,KVH", [(256, 24, 4), (128, 16, 2), (64, 8, 8), (256, 16, 1), (128, 32, 4)])
+@pytest.mark.parametrize("D,H,KVH", [(256, 24, 4), (128, 64, 8), (128, 16, 2), (64, 8, 8), (256, 16, 1),
+                                      (128, 32, 4)])
 @pytest.mark.parametrize("pps", [0, 1])
 def test_decode_ragged_batch(rt, torch_dev, D, H, KVH, pps):
     rng = np.random.default_rng(D * 7 + H * 3 + KVH + pps)
@@ -233,7 +234,7 @@ def test_decode_ragged_batch(rt, torch_dev, D, H, KVH, pps):
         _check_cache(c, m)
 
 
-@pytest.mark.parametrize("D,H,KVH", [(256, 24, 4), (128, 16, 2), (64, 4, 4), (256, 16, 1)])
+@pytest.mark.parametrize("D,H,KVH", [(256, 24, 4), (128, 64, 8), (128, 16, 2), (64, 4, 4), (256, 16, 1)])
 @pytest.mark.parametrize("start,M", [(0, 1), (0, 5), (0, 16), (0, 77), (13, 40), (32, 33), (200, 300)])
 def test_prefill_matches_oracle(rt, torch_dev, D, H, KVH, start, M):
     rng = np.random.default_rng(start * 1000 + M + D + H)
