@@ -337,6 +337,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="headline only: no extra legs, no CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--legs", default="decode,prefill,attn,deltanet",
+                    help="comma list of extra legs to run (the M=1 headline always runs)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc: 5 launches of a 256 MiB copy, then 5 gate+up M=1 launches")
     args = ap.parse_args()
@@ -372,7 +374,8 @@ def main() -> int:
         return 0
     extras = {}
     head = None
-    for M in (1, 4, 8) if not args.quick else (1,):
+    legs = set() if args.quick else set(args.legs.split(","))
+    for M in (1, 4, 8) if "decode" in legs else (1,):
         log(f"[bench] q4 decode set M={M}")
         ms, kern, wb, ab, _ = q4_leg(rt, dev, sets, M, rng, args.steps, args.warmup)
         step_bytes = sum(wb.values()) + sum(ab.values())
@@ -383,7 +386,7 @@ def main() -> int:
             "kernel_hbm_frac": {k: round((wb[k] + ab[k]) / (kern[k] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) for k in kern}}
         if M == 1:
             head = (gbs, ms, step_bytes, wb["gateup"] + ab["gateup"], kern["gateup"])
-    if not args.quick:
+    if "prefill" in legs:
         for M in (512, 2048):
             log(f"[bench] q4 prefill GEMM set M={M}")
             steps = max(3, args.steps // 10)
@@ -395,9 +398,10 @@ def main() -> int:
                 "kernel_TFLOP/s": {k: round(fl[k] / (kern[k] * 1e-3) / 1e12, 1) for k in kern}}
     del sets
     torch.cuda.empty_cache()
-    if not args.quick:
+    if "attn" in legs:
         log("[bench] attention")
         extras.update(attention_legs(rt, dev, rng, args.steps, args.warmup))
+    if "deltanet" in legs:
         log("[bench] deltanet")
         extras.update(deltanet_legs(rt, dev, rng, args.steps, args.warmup))
 

@@ -6,6 +6,8 @@
 namespace qm {
 
 constexpr int kMaxAttnSeqs = 16;  // sequences per launch (kernel-argument table)
+constexpr int kMaxSplits = 2048;         // page splits per sequence (combine kernel's LDS table)
+constexpr int kMaxPagesPerSplit = 1024;  // pages per decode workgroup (its LDS page-id table)
 
 struct AttnSeq {
   int8_t* k;          // K pages   [page][kv_head][16][D]

@@ -176,40 +176,47 @@ __global__ __launch_bounds__(256) void q8_attn_kernel(AttnArgs args) {
   float m_run = -INFINITY, l_lane = 0.0f, ps_lane = 0.0f;
 
   const size_t kv_page_stride = (size_t)KVH * 16 * D;
-  const int tok = lane & 15;  // A-operand row of QK (token)
-  for (uint32_t p = p_begin + (PREFILL ? 0 : wave); p < p_end; p += PREFILL ? 1 : kWaves) {
-    const int32_t phys = sq.pt[p];
-    const int8_t* kpage = sq.k + (size_t)phys * kv_page_stride + (size_t)kvh * 16 * D;
-    const int8_t* vpage = sq.v + (size_t)phys * kv_page_stride + (size_t)kvh * D * 16;
-    const float* kscale = sq.ks + ((size_t)phys * KVH + kvh) * 16;
-    const float* vscale = sq.vs + ((size_t)phys * KVH + kvh) * 16;
+  const int tok = lane & 15;  // A-operand row: token of QK^T, d row of PV^T
 
-    // S^T[token][col] over D in kKS steps of 32: lane (tok, kq) holds K[tok][D/4*kq + 8j ..].
-    floatx4 s4 = {0.f, 0.f, 0.f, 0.f};
-    {
-      const int8_t* kr = kpage + tok * D + D / 4 * kq;
+  // One page's operands in registers: lane (tok, kq) holds K[tok][D/4*kq ..
+  // + D/4) (16 B per two QK k-steps), V^T[16 db + tok][4 kq .. 4 kq + 3] for
+  // every d block, and the scales of tokens 4 kq .. 4 kq + 3.
+  struct PageRegs {
+    u32x4 k[kKS / 2];
+    uint32_t v[kDB];
+    floatx4 ks, vs;
+  };
+  auto load_page = [&](int32_t phys, PageRegs& r) {
+    const size_t pbase = (size_t)phys * kv_page_stride;
+    const int8_t* kr = sq.k + pbase + (size_t)kvh * 16 * D + tok * D + D / 4 * kq;
 #pragma unroll
-      for (int jj = 0; jj < kKS; jj += 2) {
-        const u32x4 kb = *(const u32x4*)(kr + 8 * jj);  // 16 bytes = steps jj, jj+1
-        u32x4 a0, a1;
-        const u32x2 l0 = q8x4_to_bf16_biased(kb.x), h0 = q8x4_to_bf16_biased(kb.y);
-        const u32x2 l1 = q8x4_to_bf16_biased(kb.z), h1 = q8x4_to_bf16_biased(kb.w);
-        a0 = u32x4{l0.x, l0.y, h0.x, h0.y};
-        a1 = u32x4{l1.x, l1.y, h1.x, h1.y};
-        s4 = mfma16x16x32(a0, qb[jj], s4);
-        s4 = mfma16x16x32(a1, qb[jj + 1], s4);
-      }
+    for (int j = 0; j < kKS / 2; ++j) r.k[j] = *(const u32x4*)(kr + 16 * j);
+    const int8_t* vr = sq.v + pbase + (size_t)kvh * D * 16 + tok * 16 + 4 * kq;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) r.v[db] = *(const uint32_t*)(vr + 256 * db);
+    const size_t sbase = ((size_t)phys * KVH + kvh) * 16 + 4 * kq;
+    r.ks = *(const floatx4*)(sq.ks + sbase);
+    r.vs = *(const floatx4*)(sq.vs + sbase);
+  };
+  auto process_page = [&](uint32_t p, const PageRegs& r) {
+    // S^T[token][col] over D in kKS steps of 32.
+    floatx4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < kKS / 2; ++j) {
+      const u32x4 kb = r.k[j];
+      const u32x2 l0 = q8x4_to_bf16_biased(kb.x), h0 = q8x4_to_bf16_biased(kb.y);
+      const u32x2 l1 = q8x4_to_bf16_biased(kb.z), h1 = q8x4_to_bf16_biased(kb.w);
+      s4 = mfma16x16x32(u32x4{l0.x, l0.y, h0.x, h0.y}, qb[2 * j], s4);
+      s4 = mfma16x16x32(u32x4{l1.x, l1.y, h1.x, h1.y}, qb[2 * j + 1], s4);
     }
-    const floatx4 ks4 = *(const floatx4*)(kscale + 4 * kq);
-    const floatx4 vs4 = *(const floatx4*)(vscale + 4 * kq);
     float sc[4];
     float bmax = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const uint32_t t = p * 16 + 4 * kq + r;
+    for (int rr = 0; rr < 4; ++rr) {
+      const uint32_t t = p * 16 + 4 * kq + rr;
       const bool ok = col_ok && t < visible;
-      sc[r] = ok ? (s4[r] - qcorr) * ks4[r] * sm_scale : -INFINITY;
-      bmax = fmaxf(bmax, sc[r]);
+      sc[rr] = ok ? (s4[rr] - qcorr) * r.ks[rr] * sm_scale : -INFINITY;
+      bmax = fmaxf(bmax, sc[rr]);
     }
     bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
@@ -219,31 +226,55 @@ __global__ __launch_bounds__(256) void q8_attn_kernel(AttnArgs args) {
     float pw[4];
     float psum = 0.0f, pvsum = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float e = sc[r] == -INFINITY ? 0.0f : exp2f(sc[r] - m_new);
+    for (int rr = 0; rr < 4; ++rr) {
+      const float e = sc[rr] == -INFINITY ? 0.0f : exp2f(sc[rr] - m_new);
       psum += e;
-      pw[r] = sc[r] == -INFINITY ? 0.0f : e * vs4[r];  // fold the V scale (never NaN for masked rows)
-      pvsum += pw[r];
+      pw[rr] = sc[rr] == -INFINITY ? 0.0f : e * r.vs[rr];  // fold the V scale (never NaN for masked rows)
+      pvsum += pw[rr];
     }
     l_lane = l_lane * corr + psum;
     ps_lane = ps_lane * corr + pvsum;
     // P'^T as bf16 hi + lo (B operand: k = tokens 4kq..4kq+3, column col).
     uint32_t hi[4], lo[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      hi[r] = __float_as_uint(pw[r]) & 0xFFFF0000u;
-      lo[r] = f32_to_bf16(pw[r] - __uint_as_float(hi[r]));
+    for (int rr = 0; rr < 4; ++rr) {
+      hi[rr] = __float_as_uint(pw[rr]) & 0xFFFF0000u;
+      lo[rr] = f32_to_bf16(pw[rr] - __uint_as_float(hi[rr]));
     }
     const u32x2 phi = {(hi[0] >> 16) | hi[1], (hi[2] >> 16) | hi[3]};
     const u32x2 plo = {lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
 #pragma unroll
     for (int db = 0; db < kDB; ++db) {
-      const uint32_t vw = *(const uint32_t*)(vpage + (16 * db + tok) * 16 + 4 * kq);
-      const u32x2 va = q8x4_to_bf16_biased(vw);
+      const u32x2 va = q8x4_to_bf16_biased(r.v[db]);
       floatx4 od = o[db] * corr;
       od = mfma16x16x16(va, phi, od);
       o[db] = mfma16x16x16(va, plo, od);
     }
+  };
+
+  // Pages of this wave, two register sets deep: the loads of the next page
+  // are in flight while the current one is reduced, and the page-table entry
+  // of the page after that is fetched one step earlier still.
+  const uint32_t step = PREFILL ? 1 : kWaves;
+  uint32_t p = p_begin + (PREFILL ? 0 : wave);
+  PageRegs ra, rb;
+  int32_t phys_next = 0;
+  if (p < p_end) load_page(sq.pt[p], ra);
+  if (p + step < p_end) phys_next = sq.pt[p + step];
+  while (p < p_end) {
+    if (p + step < p_end) {
+      load_page(phys_next, rb);
+      if (p + 2 * step < p_end) phys_next = sq.pt[p + 2 * step];
+    }
+    process_page(p, ra);
+    p += step;
+    if (p >= p_end) break;
+    if (p + step < p_end) {
+      load_page(phys_next, ra);
+      if (p + 2 * step < p_end) phys_next = sq.pt[p + 2 * step];
+    }
+    process_page(p, rb);
+    p += step;
   }
 
   // ---- combine the waves of the workgroup (decode) / finish (prefill) ------
@@ -316,29 +347,406 @@ __global__ __launch_bounds__(256) void q8_attn_kernel(AttnArgs args) {
   }
 }
 
-// Merge the split partials of one (sequence, head): grid (n_seqs * H), D threads.
+// ---------------------------------------------------------------------------
+// Decode: pages stream through a per-wave LDS ring by buffer->LDS DMA
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Lane i's `size` bytes land at lds + i*size.  The builtin exists only in the
+// device pass; the host pass of single-source HIP must not see it.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define QM_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, QM_LDS_PTR(lds), 16, voff, 0, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, QM_LDS_PTR(lds), 4, voff, 0, 0, 0);
+}
+#undef QM_LDS_PTR
+#else
+__device__ void dma16(__amdgpu_buffer_rsrc_t, void*, uint32_t);
+__device__ void dma4(__amdgpu_buffer_rsrc_t, void*, uint32_t);
+#endif
+
+// s_waitcnt vmcnt(n) (gfx9 encoding; expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 0xF) | ((N >> 4) << 14));
+  __asm__ volatile("" ::: "memory");
+}
+
+// XOR swizzle of the 16-byte chunks of one token row of a K page in LDS, so
+// the 16 lanes of one ds_read_b128 phase (16 tokens, same chunk) hit
+// distinct banks.
+template <int D>
+__device__ __forceinline__ uint32_t k_chunk_slot(uint32_t tok, uint32_t j) {
+  constexpr uint32_t kChunks = D / 16;
+  const uint32_t sw = kChunks == 16 ? tok : kChunks == 8 ? ((tok & 7) ^ (tok >> 3)) : (tok & 3);
+  return tok * kChunks + (j ^ sw);
+}
+
+// Two fp32 values -> packed bf16 (round to nearest even, v_cvt_pk_bf16_f32).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float bf16_lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi_f32(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// 4 int8 -> fp16 of 1024 + (int8 + 128), exact: (0x64 << 8 | u) is the fp16
+// 1024 + u.  Element order (b0, b2), (b1, b3): one AND-OR per pair.
+__device__ __forceinline__ u32x2 q8x4_to_f16_biased(uint32_t w) {
+  const uint32_t u = w ^ 0x80808080u;
+  return u32x2{(u & 0x00FF00FFu) | 0x64006400u, ((u >> 8) & 0x00FF00FFu) | 0x64006400u};
+}
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+// 4 signed int8 -> bf16 pairs (b0, b1), (b2, b3), exact (v_cvt_f32_i32 with a
+// sign-extended byte select, then v_cvt_pk_bf16_f32).
+__device__ __forceinline__ u32x2 q8x4_to_bf16_signed(uint32_t w) {
+  return u32x2{pack_bf16x2((float)(int8_t)w, (float)(int8_t)(w >> 8)),
+               pack_bf16x2((float)(int8_t)(w >> 16), (float)(int8_t)(w >> 24))};
+}
+
+__device__ __forceinline__ floatx4 mfma16x16x32_f16(u32x4 a, u32x4 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c,
+                                                0, 0, 0);
+}
+// Maximum over the four lanes l, l^16, l^32, l^48 (the kq lanes of one MFMA
+// column) with the gfx950 row-swap permutes instead of LDS shuffles.
+__device__ __forceinline__ float max4_across_kq(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float x = __uint_as_float(a[0]), y = __uint_as_float(a[1]);
+  const float m = x > y ? x : y;
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  const float p = __uint_as_float(b[0]), q = __uint_as_float(b[1]);
+  return p > q ? p : q;
+}
+
+template <int D>
+struct DecodeLds {
+  static constexpr int kRing = D == 256 ? 2 : 4;  // pages in flight per wave
+  static constexpr int kK = 16 * D, kV = 16 * D, kS = 512;  // K, V, scales (K 256 B + V 256 B)
+  static constexpr int kPage = kK + kV + kS;
+  static constexpr int kWaveRing = kRing * kPage;
+  static constexpr int kRed = 4 * D * 16 * 4 + 3 * 4 * 16 * 4;
+  static constexpr int kBytes = 4 * kWaveRing > kRed ? 4 * kWaveRing : kRed;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
+  using L = DecodeLds<D>;
+  constexpr int kWaves = 4, kDB = D / 16, kKS = D / 32, kRing = L::kRing;
+  constexpr int kKChunks = D / 16;          // 16-byte chunks per K token row
+  constexpr int kKDma = D / 64;             // DMA instructions per K (and V) page
+  constexpr int kDmaPerPage = 2 * kKDma + 2;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[L::kBytes + 4 * kMaxPagesPerSplit];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, kq = lane >> 4, tok = lane & 15;
+  const uint32_t H = args.heads, KVH = args.kv_heads, gh = H / KVH;
+
+  uint32_t b = 0;
+  const uint32_t unit = blockIdx.x;
+  while (b + 1 < args.n_seqs && unit >= args.seqs[b + 1].unit_begin) ++b;
+  const AttnSeq& sq = args.seqs[b];
+  const uint32_t u = unit - sq.unit_begin;
+  const uint32_t kvh = u % KVH, split = u / KVH;
+  const uint32_t pages = (sq.len + 15) / 16;
+  const uint32_t p_begin = split * args.pages_per_split;
+  const uint32_t p_end = min(pages, p_begin + args.pages_per_split);
+
+  const bool col_ok = (uint32_t)col < gh;
+  const uint32_t head = kvh * gh + col;
+  const uint32_t visible = sq.len;
+
+  // Q operand (B of QK^T) in fp16: lane (col, kq) holds q[head][D/4 kq + 8 j
+  // .. + 7] in the element order d0,d2,d1,d3,d4,d6,d5,d7 that the int8 -> fp16
+  // unpack of K produces.  bf16 -> fp16 is exact within fp16's range.
+  u32x4 qb[kKS];
+  float qsum = 0.0f;
+  {
+    const uint16_t* qp = args.q + ((size_t)b * H + head) * D;
+#pragma unroll
+    for (int jj = 0; jj < kKS; ++jj) {
+      const u32x4 v = col_ok ? *(const u32x4*)(qp + D / 4 * kq + 8 * jj) : u32x4{0u, 0u, 0u, 0u};
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f[2 * e] = bf16_to_f32(v[e] & 0xFFFFu);
+        f[2 * e + 1] = bf16_to_f32(v[e] >> 16);
+      }
+      const int order[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+      uint32_t h[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const _Float16 x = (_Float16)f[order[e]];
+        qsum += (float)x;
+        h[e] = __builtin_bit_cast(uint16_t, x);
+      }
+      qb[jj] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    }
+    qsum += __shfl_xor(qsum, 16);
+    qsum += __shfl_xor(qsum, 32);
+  }
+  const float qcorr = 1152.0f * qsum;  // K enters as 1024 + (k + 128)
+  const float sm_scale = kLog2e / sqrtf((float)D);
+
+  floatx4 o[kDB];
+#pragma unroll
+  for (int i = 0; i < kDB; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_lane = 0.0f;
+
+  // ---- this wave's pages: p_begin + wave + 4 i ------------------------------
+  uint8_t* ring = lds + wave * L::kWaveRing;
+  const size_t kv_page_stride = (size_t)KVH * 16 * D;
+  // Per-lane source offsets of the K DMA (chunk slot -> (token, chunk)).
+  uint32_t k_src[kKDma];
+#pragma unroll
+  for (int h = 0; h < kKDma; ++h) {
+    const uint32_t slot = h * 64 + lane;
+    const uint32_t t = slot / kKChunks, jj = slot % kKChunks;
+    const uint32_t sw = kKChunks == 16 ? t : kKChunks == 8 ? ((t & 7) ^ (t >> 3)) : (t & 3);
+    k_src[h] = t * D + (jj ^ sw) * 16;
+  }
+  // Page ids of the split, staged once in LDS: inside the loop an id is an
+  // LDS read (lgkmcnt), never a global load whose vmcnt wait would drain the
+  // DMA ring.
+  const uint32_t first = p_begin + wave;
+  const uint32_t n_mine = first < p_end ? (p_end - first + kWaves - 1) / kWaves : 0;
+  int32_t* ids = reinterpret_cast<int32_t*>(lds + L::kBytes);
+  for (uint32_t i = threadIdx.x; i < p_end - p_begin; i += 256) ids[i] = sq.pt[p_begin + i];
+  __syncthreads();
+  auto issue = [&](uint32_t j, int slot_idx) {
+    const int32_t phys = __builtin_amdgcn_readfirstlane(ids[wave + kWaves * j]);
+    uint8_t* dst = ring + slot_idx * L::kPage;
+    const size_t pbase = (size_t)phys * kv_page_stride;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(sq.k + pbase + (size_t)kvh * 16 * D, 16 * D);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(sq.v + pbase + (size_t)kvh * 16 * D, 16 * D);
+    const size_t sbase = ((size_t)phys * KVH + kvh) * 16;
+    const __amdgpu_buffer_rsrc_t rks = make_rsrc(sq.ks + sbase, 64);
+    const __amdgpu_buffer_rsrc_t rvs = make_rsrc(sq.vs + sbase, 64);
+#pragma unroll
+    for (int h = 0; h < kKDma; ++h) dma16(rk, dst + h * 1024, k_src[h]);
+#pragma unroll
+    for (int h = 0; h < kKDma; ++h) dma16(rv, dst + L::kK + h * 1024, (h * 64 + lane) * 16);
+    dma4(rks, dst + L::kK + L::kV, (lane & 15) * 4);
+    dma4(rvs, dst + L::kK + L::kV + 256, (lane & 15) * 4);
+  };
+  // Scores of one page: S^T[token][col] over D in kKS steps of 32.
+  auto qk = [&](const uint8_t* src) {
+    floatx4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < kKS / 2; ++j) {
+      const uint32_t chunk = (D / 64) * kq + j;
+      const u32x4 kb = *(const u32x4*)(src + 16 * k_chunk_slot<D>(tok, chunk));
+      const u32x2 l0 = q8x4_to_f16_biased(kb.x), h0 = q8x4_to_f16_biased(kb.y);
+      const u32x2 l1 = q8x4_to_f16_biased(kb.z), h1 = q8x4_to_f16_biased(kb.w);
+      s4 = mfma16x16x32_f16(u32x4{l0.x, l0.y, h0.x, h0.y}, qb[2 * j], s4);
+      s4 = mfma16x16x32_f16(u32x4{l1.x, l1.y, h1.x, h1.y}, qb[2 * j + 1], s4);
+    }
+    return s4;
+  };
+  // Two pages per step (the second may be absent): two independent QK
+  // chains, one running-max update per 32 tokens, then P'V for both.
+  auto process2 = [&](uint32_t pA, int sA, uint32_t pB, int sB, bool hasB) {
+    const uint8_t* srcA = ring + sA * L::kPage;
+    const uint8_t* srcB = ring + sB * L::kPage;
+    const floatx4 s4A = qk(srcA);
+    const floatx4 s4B = qk(srcB);
+    const floatx4 ksA = *(const floatx4*)(srcA + L::kK + L::kV + 16 * kq);
+    const floatx4 vsA = *(const floatx4*)(srcA + L::kK + L::kV + 256 + 16 * kq);
+    const floatx4 ksB = *(const floatx4*)(srcB + L::kK + L::kV + 16 * kq);
+    const floatx4 vsB = *(const floatx4*)(srcB + L::kK + L::kV + 256 + 16 * kq);
+    float sc[8];
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const uint32_t tA = pA * 16 + 4 * kq + rr, tB = pB * 16 + 4 * kq + rr;
+      sc[rr] = col_ok && tA < visible ? (s4A[rr] - qcorr) * ksA[rr] * sm_scale : -INFINITY;
+      sc[4 + rr] = col_ok && hasB && tB < visible ? (s4B[rr] - qcorr) * ksB[rr] * sm_scale : -INFINITY;
+      bmax = fmaxf(bmax, fmaxf(sc[rr], sc[4 + rr]));
+    }
+    bmax = max4_across_kq(bmax);
+    // Lazy rescaling: the reference maximum only moves when a score exceeds it
+    // by more than 2^8, so exp2(s - m_run) <= 256 stays exact in fp32 and the
+    // O / l rescale (a pass over every accumulator) is rare.  The final
+    // division by l makes the result independent of the reference chosen.
+    const float m_new = bmax > m_run + 8.0f ? bmax : m_run;
+    const bool moved = m_new != m_run;
+    const float corr = moved ? exp2f(m_run - m_new) : 1.0f;
+    m_run = m_new;
+    float pw[8];
+    float psum = 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      // v_exp_f32 directly: arguments are <= 8 here, and a flushed tiny
+      // probability is below fp32 resolution of the running sum anyway.
+      const float e = sc[rr] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[rr] - m_new);
+      psum += e;
+      pw[rr] = e * (rr < 4 ? vsA[rr] : vsB[rr - 4]);
+    }
+    l_lane = l_lane * corr + psum;
+    if (__builtin_amdgcn_ballot_w64(moved)) {
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) o[db] *= corr;
+    }
+    // P' = p * v_scale as bf16 hi + lo (error ~2^-16).  Both halves ride in
+    // the K dimension of one 16x16x32 MFMA: lane (d, kq) supplies
+    // A = V^T[d][4kq..4kq+3] twice and B = (hi, lo) of the same four tokens.
+    u32x4 pb[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float* w = pw + 4 * h;
+      const uint32_t h01 = pack_bf16x2(w[0], w[1]), h23 = pack_bf16x2(w[2], w[3]);
+      pb[h] = u32x4{h01, h23, pack_bf16x2(w[0] - bf16_lo_f32(h01), w[1] - bf16_hi_f32(h01)),
+                    pack_bf16x2(w[2] - bf16_lo_f32(h23), w[3] - bf16_hi_f32(h23))};
+    }
+    // V enters unbiased (signed bytes -> bf16): nothing accumulates into O but
+    // sum_t v_t p'_t, however long the sequence.
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) {
+      const uint32_t off = L::kK + (16 * db + tok) * 16 + 4 * kq;
+      const u32x2 va = q8x4_to_bf16_signed(*(const uint32_t*)(srcA + off));
+      const u32x2 vb = q8x4_to_bf16_signed(*(const uint32_t*)(srcB + off));
+      o[db] = mfma16x16x32(u32x4{va.x, va.y, va.x, va.y}, pb[0], o[db]);
+      o[db] = mfma16x16x32(u32x4{vb.x, vb.y, vb.x, vb.y}, pb[1], o[db]);
+    }
+  };
+
+  // Pages issued so far land in ring slots in order; a pair (i, i+1) needs
+  // every DMA up to page i+1 complete: vmcnt <= (pages issued after it) *
+  // kDmaPerPage.
+  const uint32_t pre = min(n_mine, (uint32_t)kRing);
+  for (uint32_t i = 0; i < pre; ++i) issue(i, i);
+  uint32_t issued = pre;
+  for (uint32_t i = 0; i < n_mine; i += 2) {
+    const bool hasB = i + 1 < n_mine;
+    const uint32_t last = hasB ? i + 1 : i;
+    const uint32_t later = issued - 1 - last;
+    if (later >= 2) wait_vmcnt<2 * kDmaPerPage>();
+    else if (later == 1) wait_vmcnt<kDmaPerPage>();
+    else wait_vmcnt<0>();
+    process2(first + kWaves * i, i % kRing, first + kWaves * last, last % kRing, hasB);
+    for (uint32_t j = i; j <= last; ++j)
+      if (j + kRing < n_mine) {
+        issue(j + kRing, j % kRing);
+        ++issued;
+      }
+  }
+
+  // ---- combine the waves of the workgroup ------------------------------------
+  float l_tot = l_lane + __shfl_xor(l_lane, 16);
+  l_tot += __shfl_xor(l_tot, 32);
+  __syncthreads();  // the rings are reused for the reduction
+  float(*red_o)[D][16] = reinterpret_cast<float(*)[D][16]>(lds);
+  float(*red_m)[16] = reinterpret_cast<float(*)[16]>(lds + 4 * D * 16 * 4);
+  float(*red_l)[16] = red_m + 4;
+#pragma unroll
+  for (int db = 0; db < kDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red_o[wave][16 * db + 4 * kq + r][col] = o[db][r];
+  if (kq == 0) {
+    red_m[wave][col] = m_run;
+    red_l[wave][col] = l_tot;
+  }
+  __syncthreads();
+  const uint32_t nsplit = sq.nsplit;
+  for (uint32_t e = threadIdx.x; e < (uint32_t)D * 16; e += 256) {
+    const uint32_t c = e % 16, d = e / 16;
+    if (c >= gh) continue;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, red_m[w][c]);
+    float Ls = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = red_m[w][c] == -INFINITY ? 0.0f : exp2f(red_m[w][c] - mx);
+      Ls += f * red_l[w][c];
+      O += f * red_o[w][d][c];
+    }
+    const uint32_t hh = kvh * gh + c;
+    if (nsplit == 1) {
+      float v = O / fmaxf(Ls, FLT_MIN);
+      const size_t oi = ((size_t)b * H + hh) * D + d;
+      if (args.gate) v *= sigmoid_f(bf16_to_f32(args.gate[oi]));
+      args.o[oi] = f32_to_bf16(v);
+    } else {
+      float* part = args.partials + ((size_t)(sq.part_begin + split) * H + hh) * (D + 2);
+      part[d] = O;
+      if (d == 0) {
+        part[D] = mx;
+        part[D + 1] = Ls;
+      }
+    }
+  }
+}
+
+// Merge the split partials of one (sequence, head): grid (n_seqs * H), 256
+// threads.  The split weights exp2(m_s - max) live in LDS; every thread then
+// sums its d over a strided subset of the splits, so the partial rows are
+// read with as many loads in flight as there are threads.
 __global__ __launch_bounds__(256) void q8_combine_kernel(AttnArgs args) {
+  __shared__ float f_s[kMaxSplits];
+  __shared__ float red[256];
+  __shared__ float red_w[4];
   const uint32_t H = args.heads;
   const uint32_t b = blockIdx.x / H, hh = blockIdx.x % H;
   const AttnSeq& sq = args.seqs[b];
-  if (sq.nsplit <= 1) return;
+  const uint32_t ns = sq.nsplit;
+  if (ns <= 1) return;
   const uint32_t D = args.head_dim;
-  const uint32_t d = threadIdx.x;
-  if (d >= D) return;
+  const size_t stride = (size_t)H * (D + 2);
+  const float* base = args.partials + ((size_t)sq.part_begin * H + hh) * (D + 2);
+  const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+
   float mx = -INFINITY;
-  for (uint32_t s = 0; s < sq.nsplit; ++s)
-    mx = fmaxf(mx, args.partials[((size_t)(sq.part_begin + s) * H + hh) * (D + 2) + D]);
-  float L = 0.0f, O = 0.0f;
-  for (uint32_t s = 0; s < sq.nsplit; ++s) {
-    const float* part = args.partials + ((size_t)(sq.part_begin + s) * H + hh) * (D + 2);
-    const float f = part[D] == -INFINITY ? 0.0f : exp2f(part[D] - mx);
-    L += f * part[D + 1];
-    O += f * part[d];
+  for (uint32_t s = t; s < ns; s += 256) mx = fmaxf(mx, base[s * stride + D]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  if (lane == 0) red_w[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red_w[0], red_w[1]), fmaxf(red_w[2], red_w[3]));
+  __syncthreads();
+  float L = 0.0f;
+  for (uint32_t s = t; s < ns; s += 256) {
+    const float m = base[s * stride + D];
+    const float f = m == -INFINITY ? 0.0f : exp2f(m - mx);
+    f_s[s] = f;
+    L += f * base[s * stride + D + 1];
   }
-  float v = O / fmaxf(L, FLT_MIN);
-  const size_t oi = ((size_t)b * H + hh) * D + d;
-  if (args.gate) v *= sigmoid_f(bf16_to_f32(args.gate[oi]));
-  args.o[oi] = f32_to_bf16(v);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off);
+  if (lane == 0) red_w[wave] = L;
+  __syncthreads();
+  L = red_w[0] + red_w[1] + red_w[2] + red_w[3];
+
+  const uint32_t per = 256 / D;  // threads per d (1, 2 or 4)
+  const uint32_t d = t % D, part = t / D;
+  float O = 0.0f;
+  if (part < per) {
+    uint32_t s = part;
+    for (; s + 3 * per < ns; s += 4 * per) {
+      const float o0 = base[s * stride + d], o1 = base[(s + per) * stride + d];
+      const float o2 = base[(s + 2 * per) * stride + d], o3 = base[(s + 3 * per) * stride + d];
+      O += f_s[s] * o0 + f_s[s + per] * o1 + f_s[s + 2 * per] * o2 + f_s[s + 3 * per] * o3;
+    }
+    for (; s < ns; s += per) O += f_s[s] * base[s * stride + d];
+  }
+  red[t] = O;
+  __syncthreads();
+  if (t < D) {
+    float v = 0.0f;
+    for (uint32_t k = 0; k < per; ++k) v += red[t + k * D];
+    v /= fmaxf(L, FLT_MIN);
+    const size_t oi = ((size_t)b * H + hh) * D + t;
+    if (args.gate) v *= sigmoid_f(bf16_to_f32(args.gate[oi]));
+    args.o[oi] = f32_to_bf16(v);
+  }
 }
 
 template <int D>
@@ -346,7 +754,7 @@ hipError_t launch_attn_d(const AttnArgs& a, uint32_t units, hipStream_t st) {
   if (a.prefill)
     hipLaunchKernelGGL((q8_attn_kernel<D, true>), dim3(units), dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((q8_attn_kernel<D, false>), dim3(units), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(q8_decode_kernel<D>, dim3(units), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
@@ -366,7 +774,7 @@ hipError_t launch_q8_attention(const AttnArgs& a, uint32_t units, bool need_comb
     default: return hipErrorInvalidValue;
   }
   if (e != hipSuccess || !need_combine) return e;
-  hipLaunchKernelGGL(q8_combine_kernel, dim3(a.n_seqs * a.heads), dim3(a.head_dim), 0, st, a);
+  hipLaunchKernelGGL(q8_combine_kernel, dim3(a.n_seqs * a.heads), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -264,7 +264,8 @@ qm_status qm_attn_decode(qm_runtime* rt, qm_kv* const* seqs, uint32_t B, const u
       if (seqs[c] == seqs[b]) return fail(QM_ERR_INVALID_ARGUMENT, "sequence %u appears twice", b);
   }
   DeviceGuard g(rt->device);
-  const uint32_t target = (uint32_t)env_int("QM38_ATTN_TARGET_WGS", 1024);
+  // One residency round of the decode kernel: two 256-thread workgroups per CU (LDS-bound).
+  const uint32_t target = (uint32_t)env_int("QM38_ATTN_TARGET_WGS", 2 * rt->cu_count);
   for (uint32_t b0 = 0; b0 < B; b0 += kMaxAttnSeqs) {
     const uint32_t nb = std::min<uint32_t>(kMaxAttnSeqs, B - b0);
     AppendArgs ap{};
@@ -284,6 +285,23 @@ qm_status qm_attn_decode(qm_runtime* rt, qm_kv* const* seqs, uint32_t B, const u
     uint64_t pps = (total_pages * KVH + target - 1) / target;
     pps = std::max<uint64_t>(4, (pps + 3) / 4 * 4);
     if (env_int("QM38_ATTN_PPS", 0) > 0) pps = (uint64_t)env_int("QM38_ATTN_PPS", 4);
+    // The combine kernel holds at most kMaxSplits split weights per sequence.
+    uint32_t max_pages = 0;
+    for (uint32_t i = 0; i < nb; ++i) max_pages = std::max(max_pages, (at.seqs[i].len + 15) / 16);
+    pps = std::max<uint64_t>(pps, (max_pages + kMaxSplits - 1) / kMaxSplits);
+    // Ceil-division per sequence can push the unit count past one residency
+    // round, which would leave a nearly empty second round as long as the
+    // first: grow the split until every unit fits.
+    auto units_for = [&](uint64_t q) {
+      uint64_t u = 0;
+      for (uint32_t i = 0; i < nb; ++i) u += ((at.seqs[i].len + 15) / 16 + q - 1) / q * KVH;
+      return u;
+    };
+    if (env_int("QM38_ATTN_PPS", 0) <= 0)
+      while (pps < kMaxPagesPerSplit && units_for(pps) > target) pps += 4;
+    pps = std::min<uint64_t>(pps, kMaxPagesPerSplit);
+    if ((uint64_t)max_pages > (uint64_t)kMaxSplits * kMaxPagesPerSplit)
+      return fail(QM_ERR_CAPACITY_EXCEEDED, "sequence of %u pages exceeds the decode kernel's limit", max_pages);
     uint32_t units = 0, parts = 0;
     bool combine = false;
     for (uint32_t i = 0; i < nb; ++i) {

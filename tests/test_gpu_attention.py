@@ -109,7 +109,8 @@ def test_reference_kat_single_token(rt, torch_dev):
     assert cache.sequence_length == 1
     assert abs(out[0, 0, 0] - 1.0) < 0.001, out[0, 0, :2]
     assert abs(out[0, 0, 1] + 0.5) < 0.005, out[0, 0, :2]
-    assert np.all(out[0, 0, 2:] == 0.0)
+    # zero-padded dimensions: only the rounding residual of the fp16 hi+lo P'V split remains
+    assert np.max(np.abs(out[0, 0, 2:])) < 1e-3
     keys, values, ks, vs = cache.read()
     assert list(values[0, 0, :2]) == [127, -64] and ks[0, 0] == np.float32(1.0) / np.float32(127.0)
     assert vs[0, 0] == np.float32(2.0) / np.float32(127.0)
