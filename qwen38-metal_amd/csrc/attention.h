@@ -39,6 +39,8 @@ struct AttnArgs {
   const uint16_t* gate;  // bf16 [rows][H][D] or null
   uint16_t* o;           // bf16 [rows][H][D]
   float* partials;       // [split rows][H][D + 2]
+  const float* k_new;    // decode: fp32 [n_seqs][kv_heads][D] rows appended by the kernel
+  const float* v_new;
   uint32_t heads;
   uint32_t kv_heads;
   uint32_t head_dim;

@@ -33,31 +33,13 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// ---------------------------------------------------------------------------
-// Append
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void q8_append_kernel(AppendArgs args) {
-  // blockIdx.x -> (item, kv_head, kind); item = sequence (decode) or row (prefill).
-  const uint32_t kvh_count = args.kv_heads;
-  const uint32_t kind = blockIdx.x % 2;
-  const uint32_t kvh = (blockIdx.x / 2) % kvh_count;
-  const uint32_t item = blockIdx.x / (2 * kvh_count);
-  const int lane = threadIdx.x;
-  const uint32_t D = args.head_dim;
-
-  const AttnSeq& sq = args.seqs[args.decode ? item : 0];
-  const uint32_t token = args.decode ? sq.len - 1 : args.start + item;
-
-  // Page-table entries of newly materialised pages (written once per call).
-  if (kind == 0 && kvh == 0 && (args.decode || item == 0) && lane == 0) {
-    for (int32_t i = 0; i < sq.new_page_count; ++i) sq.pt[sq.new_page_first + i] = sq.new_page_id + i;
-  }
-  const int32_t page = sq.new_page_count > 0 && (int32_t)(token / 16) >= sq.new_page_first
-                           ? sq.new_page_id + ((int32_t)(token / 16) - sq.new_page_first)
-                           : sq.pt[token / 16];
-  const uint32_t slot = token % 16;
-
-  const float* src = (kind == 0 ? args.k : args.v) + ((size_t)item * kvh_count + kvh) * D;
+// Quantises one (token, kv_head) row of K (kind 0) or V (kind 1) with one
+// 64-lane wave and stores it into page `page` slot `slot`.  Matches
+// qwen38_q8_kv_append: s = max(absmax / 127, FLT_MIN), q = round-half-away
+// (clamp(x / s, -127, 127)), IEEE division.
+__device__ __forceinline__ void q8_store_row(const AttnSeq& sq, const float* src, uint32_t kind, int32_t page,
+                                             uint32_t slot, uint32_t kvh, uint32_t kvh_count, uint32_t D,
+                                             int lane) {
   float vals[4];
   float amax = 0.0f;
 #pragma unroll
@@ -72,9 +54,8 @@ __global__ __launch_bounds__(64) void q8_append_kernel(AppendArgs args) {
   int8_t qv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) qv[i] = (int8_t)roundf(fminf(fmaxf(vals[i] / s, -127.0f), 127.0f));
-
   const size_t pkv = (size_t)page * kvh_count + kvh;
-  if (lane * 4 < D) {
+  if ((uint32_t)lane * 4 < D) {
     if (kind == 0) {
       const uint32_t packed = (uint32_t)(uint8_t)qv[0] | ((uint32_t)(uint8_t)qv[1] << 8) |
                               ((uint32_t)(uint8_t)qv[2] << 16) | ((uint32_t)(uint8_t)qv[3] << 24);
@@ -85,6 +66,34 @@ __global__ __launch_bounds__(64) void q8_append_kernel(AppendArgs args) {
     }
   }
   if (lane == 0) (kind == 0 ? sq.ks : sq.vs)[pkv * 16 + slot] = s;
+}
+
+// Physical page of logical page p: pages materialised by this call are not
+// in the device table until this call writes them.
+__device__ __forceinline__ int32_t page_id(const AttnSeq& sq, uint32_t p) {
+  return sq.new_page_count > 0 && (int32_t)p >= sq.new_page_first ? sq.new_page_id + ((int32_t)p - sq.new_page_first)
+                                                                 : sq.pt[p];
+}
+
+// ---------------------------------------------------------------------------
+// Append
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void q8_append_kernel(AppendArgs args) {
+  // blockIdx.x -> (item, kv_head, kind); item = sequence (decode) or row (prefill).
+  const uint32_t kvh_count = args.kv_heads;
+  const uint32_t kind = blockIdx.x % 2;
+  const uint32_t kvh = (blockIdx.x / 2) % kvh_count;
+  const uint32_t item = blockIdx.x / (2 * kvh_count);
+  const int lane = threadIdx.x;
+  const uint32_t D = args.head_dim;
+  const AttnSeq& sq = args.seqs[args.decode ? item : 0];
+  const uint32_t token = args.decode ? sq.len - 1 : args.start + item;
+  // Page-table entries of newly materialised pages (written once per call).
+  if (kind == 0 && kvh == 0 && (args.decode || item == 0) && lane == 0) {
+    for (int32_t i = 0; i < sq.new_page_count; ++i) sq.pt[sq.new_page_first + i] = sq.new_page_id + i;
+  }
+  const float* src = (kind == 0 ? args.k : args.v) + ((size_t)item * kvh_count + kvh) * D;
+  q8_store_row(sq, src, kind, page_id(sq, token / 16), token % 16, kvh, kvh_count, D, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -464,36 +473,9 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   const uint32_t head = kvh * gh + col;
   const uint32_t visible = sq.len;
 
-  // Q operand (B of QK^T) in fp16: lane (col, kq) holds q[head][D/4 kq + 8 j
-  // .. + 7] in the element order d0,d2,d1,d3,d4,d6,d5,d7 that the int8 -> fp16
-  // unpack of K produces.  bf16 -> fp16 is exact within fp16's range.
+  // Q operand (B of QK^T), filled after the first page DMAs are in flight.
   u32x4 qb[kKS];
-  float qsum = 0.0f;
-  {
-    const uint16_t* qp = args.q + ((size_t)b * H + head) * D;
-#pragma unroll
-    for (int jj = 0; jj < kKS; ++jj) {
-      const u32x4 v = col_ok ? *(const u32x4*)(qp + D / 4 * kq + 8 * jj) : u32x4{0u, 0u, 0u, 0u};
-      float f[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        f[2 * e] = bf16_to_f32(v[e] & 0xFFFFu);
-        f[2 * e + 1] = bf16_to_f32(v[e] >> 16);
-      }
-      const int order[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-      uint32_t h[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const _Float16 x = (_Float16)f[order[e]];
-        qsum += (float)x;
-        h[e] = __builtin_bit_cast(uint16_t, x);
-      }
-      qb[jj] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-    }
-    qsum += __shfl_xor(qsum, 16);
-    qsum += __shfl_xor(qsum, 32);
-  }
-  const float qcorr = 1152.0f * qsum;  // K enters as 1024 + (k + 128)
+  float qcorr = 0.0f;
   const float sm_scale = kLog2e / sqrtf((float)D);
 
   floatx4 o[kDB];
@@ -519,7 +501,21 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   const uint32_t first = p_begin + wave;
   const uint32_t n_mine = first < p_end ? (p_end - first + kWaves - 1) / kWaves : 0;
   int32_t* ids = reinterpret_cast<int32_t*>(lds + L::kBytes);
-  for (uint32_t i = threadIdx.x; i < p_end - p_begin; i += 256) ids[i] = sq.pt[p_begin + i];
+  for (uint32_t i = threadIdx.x; i < p_end - p_begin; i += 256) ids[i] = page_id(sq, p_begin + i);
+  // The last split of each (sequence, KV head) appends the new token first
+  // (waves 0 and 1 quantise K and V); the barrier below orders those stores
+  // before any wave's DMA of the last page.  KV head 0 also records pages
+  // materialised by this call in the page table.
+  if (split + 1 == sq.nsplit) {
+    const uint32_t token = sq.len - 1;
+    if (wave < 2) {
+      const float* src = (wave == 0 ? args.k_new : args.v_new) + ((size_t)b * KVH + kvh) * D;
+      q8_store_row(sq, src, wave, page_id(sq, token / 16), token % 16, kvh, KVH, D, lane);
+    } else if (wave == 2 && kvh == 0 && lane == 0) {
+      for (int32_t i = 0; i < sq.new_page_count; ++i) sq.pt[sq.new_page_first + i] = sq.new_page_id + i;
+    }
+    wait_vmcnt<0>();
+  }
   __syncthreads();
   auto issue = [&](uint32_t j, int slot_idx) {
     const int32_t phys = __builtin_amdgcn_readfirstlane(ids[wave + kWaves * j]);
@@ -624,6 +620,36 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   const uint32_t pre = min(n_mine, (uint32_t)kRing);
   for (uint32_t i = 0; i < pre; ++i) issue(i, i);
   uint32_t issued = pre;
+  // Q operand (B of QK^T) in fp16: lane (col, kq) holds q[head][D/4 kq + 8 j
+  // .. + 7] in the element order d0,d2,d1,d3,d4,d6,d5,d7 that the int8 -> fp16
+  // unpack of K produces.  bf16 -> fp16 is exact within fp16's range.
+  {
+    float qsum = 0.0f;
+    const uint16_t* qp = args.q + ((size_t)b * H + head) * D;
+#pragma unroll
+    for (int jj = 0; jj < kKS; ++jj) {
+      const u32x4 v = col_ok ? *(const u32x4*)(qp + D / 4 * kq + 8 * jj) : u32x4{0u, 0u, 0u, 0u};
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f[2 * e] = bf16_to_f32(v[e] & 0xFFFFu);
+        f[2 * e + 1] = bf16_to_f32(v[e] >> 16);
+      }
+      const int order[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+      uint32_t h[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const _Float16 x = (_Float16)f[order[e]];
+        qsum += (float)x;
+        h[e] = __builtin_bit_cast(uint16_t, x);
+      }
+      qb[jj] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    }
+    qsum += __shfl_xor(qsum, 16);
+    qsum += __shfl_xor(qsum, 32);
+    qcorr = 1152.0f * qsum;  // K enters as 1024 + (k + 128)
+  }
+
   for (uint32_t i = 0; i < n_mine; i += 2) {
     const bool hasB = i + 1 < n_mine;
     const uint32_t last = hasB ? i + 1 : i;
@@ -687,74 +713,97 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
 }
 
 // Merge the split partials of one (sequence, head): grid (n_seqs * H), 256
-// threads.  The split weights exp2(m_s - max) live in LDS; every thread then
-// sums its d over a strided subset of the splits, so the partial rows are
-// read with as many loads in flight as there are threads.
+// threads.  Thread t owns the float4 column slice c = t % (D/4) of the splits
+// s = t / (D/4) + k * (256 / (D/4)), and loads every (O slice, m, l) it needs
+// in one go, so the whole merge costs one memory round trip; the per-head
+// maximum and the slice sums then meet in LDS.
+template <int D>
 __global__ __launch_bounds__(256) void q8_combine_kernel(AttnArgs args) {
-  __shared__ float f_s[kMaxSplits];
-  __shared__ float red[256];
-  __shared__ float red_w[4];
+  constexpr int kSlices = D / 4;            // float4 slices of one partial row
+  constexpr int kGroups = 256 / kSlices;    // split groups per pass
+  constexpr int kMaxPer = 16;               // splits a thread holds in registers per pass
+  __shared__ float red_m[256];
+  __shared__ floatx4 red_o[256];
+  __shared__ float red_l[256];
   const uint32_t H = args.heads;
   const uint32_t b = blockIdx.x / H, hh = blockIdx.x % H;
   const AttnSeq& sq = args.seqs[b];
   const uint32_t ns = sq.nsplit;
   if (ns <= 1) return;
-  const uint32_t D = args.head_dim;
   const size_t stride = (size_t)H * (D + 2);
   const float* base = args.partials + ((size_t)sq.part_begin * H + hh) * (D + 2);
-  const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const uint32_t t = threadIdx.x, c = t % kSlices, g = t / kSlices;
 
-  float mx = -INFINITY;
-  for (uint32_t s = t; s < ns; s += 256) mx = fmaxf(mx, base[s * stride + D]);
+  // Pass over the splits of this thread (ns <= kMaxSplits; kGroups * kMaxPer per pass).
+  float mloc = -INFINITY;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  float lacc = 0.0f;
+  for (uint32_t s0 = 0; s0 < ns; s0 += kGroups * kMaxPer) {
+    floatx4 ov[kMaxPer];
+    float mv[kMaxPer], lv[kMaxPer];
+    // Unconditional loads (index clamped, weight masked) so all of them are
+    // in flight together.
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-  if (lane == 0) red_w[wave] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red_w[0], red_w[1]), fmaxf(red_w[2], red_w[3]));
-  __syncthreads();
-  float L = 0.0f;
-  for (uint32_t s = t; s < ns; s += 256) {
-    const float m = base[s * stride + D];
-    const float f = m == -INFINITY ? 0.0f : exp2f(m - mx);
-    f_s[s] = f;
-    L += f * base[s * stride + D + 1];
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off);
-  if (lane == 0) red_w[wave] = L;
-  __syncthreads();
-  L = red_w[0] + red_w[1] + red_w[2] + red_w[3];
-
-  const uint32_t per = 256 / D;  // threads per d (1, 2 or 4)
-  const uint32_t d = t % D, part = t / D;
-  float O = 0.0f;
-  if (part < per) {
-    uint32_t s = part;
-    for (; s + 3 * per < ns; s += 4 * per) {
-      const float o0 = base[s * stride + d], o1 = base[(s + per) * stride + d];
-      const float o2 = base[(s + 2 * per) * stride + d], o3 = base[(s + 3 * per) * stride + d];
-      O += f_s[s] * o0 + f_s[s + per] * o1 + f_s[s + 2 * per] * o2 + f_s[s + 3 * per] * o3;
+    for (int k = 0; k < kMaxPer; ++k) {
+      const uint32_t s = s0 + g + k * kGroups;
+      const float* row = base + (s < ns ? s : ns - 1) * stride;
+      ov[k] = *(const floatx4*)(row + 4 * c);
+      mv[k] = row[D];
+      lv[k] = row[D + 1];
     }
-    for (; s < ns; s += per) O += f_s[s] * base[s * stride + d];
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k)
+      if (s0 + g + k * kGroups >= ns) mv[k] = -INFINITY;
+    float mnew = mloc;
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k) mnew = fmaxf(mnew, mv[k]);
+    if (mnew != -INFINITY) {
+      const float r = mloc == -INFINITY ? 0.0f : exp2f(mloc - mnew);
+      acc *= r;
+      lacc *= r;
+#pragma unroll
+      for (int k = 0; k < kMaxPer; ++k) {
+        const float f = mv[k] == -INFINITY ? 0.0f : exp2f(mv[k] - mnew);
+        acc += ov[k] * f;
+        lacc += lv[k] * f;
+      }
+      mloc = mnew;
+    }
   }
-  red[t] = O;
+  red_m[t] = mloc;
   __syncthreads();
-  if (t < D) {
-    float v = 0.0f;
-    for (uint32_t k = 0; k < per; ++k) v += red[t + k * D];
-    v /= fmaxf(L, FLT_MIN);
-    const size_t oi = ((size_t)b * H + hh) * D + t;
-    if (args.gate) v *= sigmoid_f(bf16_to_f32(args.gate[oi]));
-    args.o[oi] = f32_to_bf16(v);
+  float mx = -INFINITY;
+  for (int k = 0; k < kGroups; ++k) mx = fmaxf(mx, red_m[c + k * kSlices]);
+  const float f = mloc == -INFINITY ? 0.0f : exp2f(mloc - mx);
+  red_o[t] = acc * f;
+  red_l[t] = lacc * f;
+  __syncthreads();
+  if (g == 0) {
+    floatx4 o = red_o[c];
+    float L = red_l[c];
+    for (int k = 1; k < kGroups; ++k) {
+      o += red_o[c + k * kSlices];
+      L += red_l[c + k * kSlices];
+    }
+    const float inv = 1.0f / fmaxf(L, FLT_MIN);
+    const size_t oi = ((size_t)b * H + hh) * D + 4 * c;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v = o[e] * inv;
+      if (args.gate) v *= sigmoid_f(bf16_to_f32(args.gate[oi + e]));
+      args.o[oi + e] = f32_to_bf16(v);
+    }
   }
 }
 
 template <int D>
-hipError_t launch_attn_d(const AttnArgs& a, uint32_t units, hipStream_t st) {
-  if (a.prefill)
+hipError_t launch_attn_d(const AttnArgs& a, uint32_t units, bool need_combine, hipStream_t st) {
+  if (a.prefill) {
     hipLaunchKernelGGL((q8_attn_kernel<D, true>), dim3(units), dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL(q8_decode_kernel<D>, dim3(units), dim3(256), 0, st, a);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL(q8_decode_kernel<D>, dim3(units), dim3(256), 0, st, a);
+  if (need_combine) hipLaunchKernelGGL(q8_combine_kernel<D>, dim3(a.n_seqs * a.heads), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
@@ -766,16 +815,12 @@ hipError_t launch_q8_append(const AppendArgs& a, uint32_t items, hipStream_t st)
 }
 
 hipError_t launch_q8_attention(const AttnArgs& a, uint32_t units, bool need_combine, hipStream_t st) {
-  hipError_t e;
   switch (a.head_dim) {
-    case 64: e = launch_attn_d<64>(a, units, st); break;
-    case 128: e = launch_attn_d<128>(a, units, st); break;
-    case 256: e = launch_attn_d<256>(a, units, st); break;
+    case 64: return launch_attn_d<64>(a, units, need_combine, st);
+    case 128: return launch_attn_d<128>(a, units, need_combine, st);
+    case 256: return launch_attn_d<256>(a, units, need_combine, st);
     default: return hipErrorInvalidValue;
   }
-  if (e != hipSuccess || !need_combine) return e;
-  hipLaunchKernelGGL(q8_combine_kernel, dim3(a.n_seqs * a.heads), dim3(256), 0, st, a);
-  return hipGetLastError();
 }
 
 }  // namespace qm

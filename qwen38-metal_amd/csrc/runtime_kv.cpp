@@ -334,8 +334,9 @@ qm_status qm_attn_decode(qm_runtime* rt, qm_kv* const* seqs, uint32_t B, const u
     at.n_seqs = nb;
     at.pages_per_split = (uint32_t)pps;
     at.prefill = 0;
-    hipError_t e = launch_q8_append(ap, nb, rt->stream);
-    if (e == hipSuccess) e = launch_q8_attention(at, units, combine, rt->stream);
+    at.k_new = ap.k;  // the decode kernel appends the new rows itself
+    at.v_new = ap.v;
+    hipError_t e = launch_q8_attention(at, units, combine, rt->stream);
     if (e != hipSuccess) return hip_check(e, "attention decode launch");
   }
   return QM_OK;
