@@ -114,11 +114,6 @@ def timed(step, stream, steps: int, warmup: int):
     return t0.elapsed_time(t1) / steps, marks_all
 
 
-def _mark(marks):
-    if marks is not None:
-        marks.append(marks[0].mark())
-
-
 # ---------------------------------------------------------------------------
 # Q4 projections
 # ---------------------------------------------------------------------------
@@ -152,16 +147,20 @@ def q4_leg(rt, dev, sets, M: int, rng, steps, warmup):
 
     def step(i, marks):
         j = sets[i % NCOPY]
-        _mark(marks)
         rt.q4_project([j["qkv"][0]], x, H, M, [qkv_out])
-        _mark(marks)
         rt.q4_swiglu(j["gate"][0], j["up"][0], x, H, M, h)
-        _mark(marks)
         rt.q4_project([j["down"][0]], h, I, M, [y])
-        _mark(marks)
 
-    ms, marks = timed(step, torch.cuda.current_stream(), steps, warmup)
-    per = np.array([[a.elapsed_time(b) for a, b in zip(m[:-1], m[1:])] for m in marks]).mean(0)
+    stream = torch.cuda.current_stream()
+    ms, _ = timed(step, stream, steps, warmup)
+    # Per-kernel durations: each projection alone, back to back (events only
+    # around the whole run, so no event sits between the timed kernels).
+    calls = {
+        "qkv": lambda i, m: rt.q4_project([sets[i % NCOPY]["qkv"][0]], x, H, M, [qkv_out]),
+        "gateup": lambda i, m: rt.q4_swiglu(sets[i % NCOPY]["gate"][0], sets[i % NCOPY]["up"][0], x, H, M, h),
+        "down": lambda i, m: rt.q4_project([sets[i % NCOPY]["down"][0]], h, I, M, [y]),
+    }
+    per = [timed(fn, stream, steps, 2)[0] for fn in calls.values()]
     wbytes = {"qkv": q4_bytes(QKV, H), "gateup": 2 * q4_bytes(I, H), "down": q4_bytes(H, I)}
     abytes = {"qkv": 2 * M * (H + QKV), "gateup": 2 * M * (H + I), "down": 2 * M * (I + H)}
     flops = {"qkv": 2 * M * QKV * H, "gateup": 4 * M * I * H, "down": 2 * M * H * I}

@@ -7,17 +7,20 @@
 // (/root/reference/shaders/qwen38.metal:213-246, 1140).
 //
 // Design (HBM-bound weight stream):
-//  * A wave owns NT tiles of 16 output rows and a slice of the K groups; the
-//    waves of one workgroup split K and are reduced through LDS, so every
-//    launch has thousands of waves streaming weights even for the 5120-row
-//    down projection.
-//  * Everything an iteration (4 groups = 128 bytes of every row) needs is
-//    copied straight from HBM into a per-wave LDS slot with buffer->LDS DMA
-//    loads: weights (eight consecutive lanes read one row's 128-byte line),
-//    activations and scales/biases.  Three slots rotate, so two iterations
-//    are always in flight while the third is consumed, without holding the
-//    prefetched data in VGPRs.  Buffer range checks turn any read past a
-//    tensor into zeros.
+//  * A workgroup owns NT tiles of 16 output rows (SwiGLU: 16 gate rows and
+//    the same 16 up rows); its waves split the K groups and meet in LDS at
+//    the end, so even the 5120-row down projection streams from thousands of
+//    waves.
+//  * Weights: each iteration covers 4 groups (128 bytes of every row).  A
+//    wave's loads are coalesced 16-byte buffer loads (eight lanes read one
+//    row's 128-byte line) into a ring of register sets (three with staged
+//    activations, else two), so iterations stay in flight while one is
+//    transposed through a per-wave XOR-swizzled LDS buffer and consumed.
+//  * Activations: when all M rows fit (<= 36 KiB), the workgroup stages them
+//    once in LDS, already in the element order of the weight unpack below, and
+//    every lane reads its MFMA operand from there.  Larger M * K keep a
+//    register path that fetches each iteration's activations as it starts.
+//  * Scales and biases of a wave's K slice are staged once by buffer->LDS DMA.
 //  * Nibbles become bf16 (128+q) with one AND-OR per pair (exact); the dot
 //    products run on MFMA 16x16x32 with the activation rows as the A operand
 //    (rows >= M carry don't-care data and are never stored).  A second MFMA
@@ -25,8 +28,7 @@
 //        acc += s * D(128+q) + (b - 128 s) * D(1)
 //    which equals s*sum(q x) + b*sum(x) in real arithmetic.  Only the R =
 //    min(M, 4) accumulator rows a lane can own are updated.
-//  * SwiGLU mode pairs gate tiles with the same rows of the up projection in
-//    one wave and writes bf16(silu(gate) * up) (qwen38.metal:4090-4096,
+//  * SwiGLU mode writes bf16(silu(gate) * up) (qwen38.metal:4090-4096,
 //    4188-4199).
 #include "common.h"
 #include "internal.h"
@@ -40,13 +42,16 @@ constexpr int kMaxWaves = 8;
 constexpr int kGroupsPerIter = 4;  // 4 groups = 32 words = 128 bytes per row
 constexpr int kTileBytes = 16 * 128;
 constexpr int kNonTemporal = 2;    // buffer cache policy: nt (weights are streamed once)
+constexpr uint32_t kXStageMax = 36 * 1024;  // LDS bytes of workgroup-staged activations
 
 struct DecodeArgs {
   const uint16_t* x;
   uint32_t K;
   uint32_t M;
-  uint32_t G;    // groups per row = K / 64
-  uint32_t gps;  // groups per wave slice (multiple of 4)
+  uint32_t G;        // groups per row = K / 64
+  uint32_t gps;      // groups per wave slice (multiple of 4)
+  uint32_t x_pitch;  // LDS bytes per staged activation row (0: register path)
+  uint32_t x_bytes;  // LDS bytes of the staged activations (16-byte multiple)
   uint32_t n_jobs;
   Q4Job jobs[kMaxQ4Jobs];  // tile_begin: first tile set (workgroup) of the job
 };
@@ -56,17 +61,15 @@ struct DecodeArgs {
 __host__ __device__ constexpr uint32_t sb_tile_entries(bool sb16, uint32_t gps) {
   return ((16 * (sb16 ? gps / 8 : gps) + 63) / 64) * 64;
 }
-// Per-wave LDS layout (bytes):
+// Per-wave LDS layout (bytes), after the workgroup's staged activations:
 //   transpose buffer   NT x 2 KB: one iteration of weights in row-major form
-//   x slice (XS only)  [gps/4 blocks][XR rows][512 B], interleaved in place
 //   scales, biases     raw bf16 per [tile][row][group] (DMA target)
 struct WaveLayout {
-  uint32_t x_off, s_off, b_off, sb_bytes, total;
+  uint32_t s_off, b_off, sb_bytes, total;
 };
-__host__ __device__ inline WaveLayout wave_layout(int nt, int xr, bool sb16, uint32_t gps, bool xs) {
+__host__ __device__ inline WaveLayout wave_layout(int nt, bool sb16, uint32_t gps) {
   WaveLayout l{};
-  l.x_off = nt * kTileBytes;
-  l.s_off = l.x_off + (xs ? (gps / 4) * xr * 512 : 0);
+  l.s_off = nt * kTileBytes;
   l.sb_bytes = nt * sb_tile_entries(sb16, gps) * (sb16 ? 16 : 4);
   l.b_off = l.s_off + l.sb_bytes;
   l.total = l.b_off + l.sb_bytes;
@@ -95,7 +98,12 @@ __device__ void dma16(__amdgpu_buffer_rsrc_t, void*, uint32_t, uint32_t);
 __device__ void dma2(__amdgpu_buffer_rsrc_t, void*, uint32_t, uint32_t);
 #endif
 
-__device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 0xF) | ((N >> 4) << 14));
+}
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 __device__ __forceinline__ u32x4 unpack_word(uint32_t w, uint32_t mask_s, uint32_t or_v) {
@@ -111,13 +119,14 @@ template <int NT>
 struct WRegs {
   u32x4 v[NT][2];
 };
+struct XRegs {
+  u32x4 x[4][2];  // activations of one iteration (register path)
+};
 
-// NT: 16-row tiles per wave.  XR: activation rows staged (>= M, even).
-// R: accumulator rows per lane that can be valid (min(M, 4)).
-// SB16: G % 8 == 0 and gps % 8 == 0 (scales/biases fetched 16 bytes a lane).
-// XS: the wave's whole activation slice is staged (and interleaved) once in
-// LDS; otherwise each iteration loads its activations into registers.
-template <int NT, int XR, int R, bool SWIGLU, bool SB16, bool XS>
+// NT: 16-row tiles per wave.  R: accumulator rows per lane that can be valid
+// (min(M, 4)).  SB16: G % 8 == 0 and gps % 8 == 0 (scales/biases fetched 16
+// bytes a lane).  XW: activations staged per workgroup in LDS.
+template <int NT, int R, bool SWIGLU, bool SB16, bool XW>
 __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int kHalf = SWIGLU ? NT / 2 : NT;  // tiles per projection
@@ -130,10 +139,10 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
   const int kq = lane >> 4;
   const uint32_t tile = blockIdx.x;
   const uint32_t gps = args.gps;
-  const WaveLayout L = wave_layout(NT, XR, SB16, gps, XS);
-  uint8_t* wl = smem + wave * L.total;
+  const WaveLayout L = wave_layout(NT, SB16, gps);
+  uint8_t* xl = smem;  // staged activations (XW)
+  uint8_t* wl = smem + (XW ? args.x_bytes : 0) + wave * L.total;
   uint8_t* tbuf = wl;
-  uint8_t* xl = wl + L.x_off;
   uint8_t* s_tab = wl + L.s_off;
   uint8_t* b_tab = wl + L.b_off;
 
@@ -156,7 +165,6 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
     rs[q] = make_rsrc(jb.s, (uint64_t)jb.rows * G * 2);
     rb[q] = make_rsrc(jb.b, (uint64_t)jb.rows * G * 2);
   }
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(args.x, (uint64_t)args.M * K * 2);
 
   const uint32_t g_begin = wave * gps;
   const uint32_t g_end = min(G, g_begin + gps);
@@ -188,6 +196,10 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
   }
   const uint32_t wst = lrow * 128 + 16 * (lchunk ^ (lrow & 7));  // transpose-buffer store offset
 
+  // Activation row this lane reads as MFMA A operand (rows >= M reuse row 0).
+  const uint32_t am = (uint32_t)nl < args.M ? nl : 0;
+  const uint16_t* xrow_g = args.x + (size_t)am * K + 16 * kq;
+
   auto load_w = [&](uint32_t it, WRegs<NT>& r) {
     const uint32_t g = g_begin + it * kGroupsPerIter;
 #pragma unroll
@@ -197,28 +209,26 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
         r.v[t][h] = __builtin_amdgcn_raw_buffer_load_b128(rw[SWIGLU ? t / kHalf : 0], vw[t][h], g * 32,
                                                           kNonTemporal);
   };
-
-  // Activation DMA into the staged slice: instruction covers rows 2i, 2i+1 of
-  // 4 groups; lane -> row 2i + lane/32, LDS slot lane%32 holding chunk slot ^
-  // (row%8).  Rows >= M read past the buffer and land as zeros.
-  auto stage_x = [&](uint8_t* dst, uint32_t g) {
+  // Register path: an iteration's activations, fetched one iteration ahead.
+  auto load_x = [&](uint32_t it, XRegs& r) {
+    if (XW) return;
+    const uint32_t g = g_begin + it * kGroupsPerIter;
 #pragma unroll
-    for (int i = 0; i < XR / 2; ++i) {
-      const uint32_t m = 2 * i + (lane >> 5);
-      const uint32_t off = m * K * 2 + ((lane & 31) ^ (m & 7)) * 16;
-      dma16(rx, dst + 2 * i * 512, off, g * 128);
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t gx = min(g + u, G - 1);
+      r.x[u][0] = *(const u32x4*)(xrow_g + (size_t)gx * 64);
+      r.x[u][1] = *(const u32x4*)(xrow_g + (size_t)gx * 64 + 8);
     }
   };
 
-  WRegs<NT> wa, wb;
-  if (n_iter > 0) {
-    // --- one-time staging: activation slice, scales and biases -------------
-    if (XS)
-      for (uint32_t b = 0; b < n_iter; ++b) stage_x(xl + b * XR * 512, g_begin + b * kGroupsPerIter);
-    {
-      const uint32_t cols = SB16 ? gps / 8 : gps;  // DMA entries per row
-      const uint32_t per_tile = 16 * cols;
-      const uint32_t pad = sb_tile_entries(SB16, gps);
+  WRegs<NT> wa, wb, wc;
+  XRegs xp;
+  const uint32_t pad = sb_tile_entries(SB16, gps);
+  // --- one-time staging: scales and biases, first weights, activations --------
+  {
+    const uint32_t cols = SB16 ? gps / 8 : gps;  // DMA entries per row
+    const uint32_t per_tile = 16 * cols;
+    if (n_iter > 0) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const int q = SWIGLU ? t / kHalf : 0;
@@ -240,30 +250,52 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
           }
         }
       }
+      // The first iterations' weights stream while everything else lands
+      // (three with staged activations, two on the register path).
+      load_w(0, wa);
+      if (n_iter > 1) load_w(1, wb);
+      if (XW && n_iter > 2) load_w(2, wc);
+      load_x(0, xp);
     }
-    wait_vmcnt0();
-    load_w(0, wa);  // first weights stream while the tables are fixed up
-    // Interleave the x slice in place: (x0..x7) -> (x0,x4)(x1,x5)(x2,x6)(x3,x7).
-    if (XS)
-      for (uint32_t c = lane; c < n_iter * XR * 32; c += 64) {
-        u32x4* p = (u32x4*)(xl + c * 16);
-        *p = interleave_bf16x8(*p);
+    if (XW) {
+      // The workgroup stages all M activation rows, each 8-element chunk
+      // reordered (x0,x4)(x1,x5)(x2,x6)(x3,x7) to match unpack_word.  These
+      // loads are the youngest, so the wait for them below also covers the
+      // table DMA and the first weights.
+      const uint32_t chunks = args.M * (K / 8);
+      for (uint32_t c = threadIdx.x; c < chunks; c += blockDim.x) {
+        const uint32_t m = c / (K / 8), ch = c - m * (K / 8);
+        const u32x4 v = *(const u32x4*)(args.x + (size_t)m * K + 8 * ch);
+        *(u32x4*)(xl + m * args.x_pitch + 16 * ch) = interleave_bf16x8(v);
       }
-    // Groups past the slice end get scale = bias = 0 (they contribute 0).
-    if (span % kGroupsPerIter) {
-      const uint32_t dead = kGroupsPerIter - span % kGroupsPerIter;
-      const uint32_t pad = sb_tile_entries(SB16, gps);
-      for (uint32_t e = lane; e < NT * 16 * dead; e += 64) {
-        const uint32_t t = e / (16 * dead), row = (e / dead) % 16, gl = span + e % dead;
-        if (SB16) {
-          ((uint16_t*)s_tab)[t * pad * 8 + row * gps + gl] = 0;
-          ((uint16_t*)b_tab)[t * pad * 8 + row * gps + gl] = 0;
-        } else {
-          ((uint32_t*)s_tab)[t * pad + row * gps + gl] = 0;
-          ((uint32_t*)b_tab)[t * pad + row * gps + gl] = 0;
+    }
+    if (n_iter > 0) {
+      // Groups past the slice end get scale = bias = 0 (they contribute 0);
+      // the table DMA must have landed first.
+      if (!XW) {
+        constexpr int kW = 2 * NT, kX = 8;
+        if (n_iter > 1)
+          wait_vmcnt<2 * kW + kX>();
+        else
+          wait_vmcnt<kW + kX>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      if (span % kGroupsPerIter) {
+        const uint32_t dead = kGroupsPerIter - span % kGroupsPerIter;
+        for (uint32_t e = lane; e < NT * 16 * dead; e += 64) {
+          const uint32_t t = e / (16 * dead), row = (e / dead) % 16, gl = span + e % dead;
+          if (SB16) {
+            ((uint16_t*)s_tab)[t * pad * 8 + row * gps + gl] = 0;
+            ((uint16_t*)b_tab)[t * pad * 8 + row * gps + gl] = 0;
+          } else {
+            ((uint32_t*)s_tab)[t * pad + row * gps + gl] = 0;
+            ((uint32_t*)b_tab)[t * pad + row * gps + gl] = 0;
+          }
         }
       }
     }
+    if (XW) __syncthreads();  // staged activations visible to every wave
     wait_lgkmcnt0();
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -272,12 +304,9 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
   const uint32_t mask_s = __builtin_amdgcn_readfirstlane(0x000F000Fu);
   uint32_t or_v = 0x43004300u;
   asm volatile("" : "+v"(or_v));
-  // Activation row this lane reads as MFMA A operand (rows >= M reuse row 0).
-  const uint32_t am = (uint32_t)nl < args.M ? nl : 0;
-  const uint32_t pad = sb_tile_entries(SB16, gps);
-  const uint16_t* xrow_g = args.x + (size_t)am * K + 16 * kq;
+  const uint8_t* xlr = xl + am * args.x_pitch + 32 * kq;  // this lane's staged row, chunk pair 2kq
 
-  auto consume = [&](uint32_t it, const WRegs<NT>& r) {
+  auto consume = [&](uint32_t it, const WRegs<NT>& r, const XRegs& xr) {
     const uint32_t gl = it * kGroupsPerIter;  // group offset inside the slice
     // Scales / biases of the 4 groups (bf16 -> fp32 by shifting).
     uint32_t sv[NT][4], bv[NT][4];
@@ -297,32 +326,24 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
         bv[t][0] = b4.x << 16; bv[t][1] = b4.y << 16; bv[t][2] = b4.z << 16; bv[t][3] = b4.w << 16;
       }
     }
-    u32x4 xg[4][2];
-    if (!XS) {
-      const uint32_t g = g_begin + gl;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t gx = min(g + u, G - 1);
-        xg[u][0] = *(const u32x4*)(xrow_g + (size_t)gx * 64);
-        xg[u][1] = *(const u32x4*)(xrow_g + (size_t)gx * 64 + 8);
-      }
-    }
     // Row-major weights -> transpose buffer.
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int h = 0; h < 2; ++h) *(u32x4*)(tbuf + t * kTileBytes + h * 1024 + wst) = r.v[t][h];
     __builtin_amdgcn_wave_barrier();
-    const uint8_t* xs = xl + (it * XR + am) * 512;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       u32x4 xa0, xa1;
-      if (XS) {
-        xa0 = *(const u32x4*)(xs + 16 * (((4 * u + kq) * 2) ^ (am & 7)));
-        xa1 = *(const u32x4*)(xs + 16 * (((4 * u + kq) * 2 + 1) ^ (am & 7)));
+      if (XW) {
+        // Groups past K (dead iterations) read the last group: finite data,
+        // zero scale and bias.
+        const uint8_t* p = xlr + (size_t)min(g_begin + gl + u, G - 1) * 128;
+        xa0 = *(const u32x4*)p;
+        xa1 = *(const u32x4*)(p + 16);
       } else {
-        xa0 = interleave_bf16x8(xg[u][0]);
-        xa1 = interleave_bf16x8(xg[u][1]);
+        xa0 = interleave_bf16x8(xr.x[u][0]);
+        xa1 = interleave_bf16x8(xr.x[u][1]);
       }
       floatx4 dsum = mfma16x16x32(xa0, ones, floatx4{0.f, 0.f, 0.f, 0.f});
       dsum = mfma16x16x32(xa1, ones, dsum);
@@ -342,16 +363,35 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
     __builtin_amdgcn_wave_barrier();
   };
 
-  // Register double buffer: iteration it+1 is in flight while `it` is
-  // transposed and consumed.
-  uint32_t it = 0;
-  for (; it + 2 <= n_iter; it += 2) {
-    load_w(it + 1, wb);
-    consume(it, wa);
-    if (it + 2 < n_iter) load_w(it + 2, wa);
-    consume(it + 1, wb);
+  if constexpr (XW) {
+    // Staged activations: a ring of three weight register sets, two
+    // iterations in flight while one is transposed and consumed.
+    auto step = [&](uint32_t i, WRegs<NT>& w) {
+      consume(i, w, xp);
+      if (i + 3 < n_iter) load_w(i + 3, w);
+    };
+    for (uint32_t it = 0; it < n_iter; it += 3) {
+      step(it, wa);
+      if (it + 1 >= n_iter) break;
+      step(it + 1, wb);
+      if (it + 2 >= n_iter) break;
+      step(it + 2, wc);
+    }
+  } else {
+    // Register path (larger M * K): the activation registers leave room for
+    // two weight sets only, one iteration in flight; each iteration's
+    // activations are fetched at its start.
+    auto step = [&](uint32_t i, WRegs<NT>& w) {
+      if (i > 0) load_x(i, xp);
+      consume(i, w, xp);
+      if (i + 2 < n_iter) load_w(i + 2, w);
+    };
+    for (uint32_t it = 0; it < n_iter; it += 2) {
+      step(it, wa);
+      if (it + 1 >= n_iter) break;
+      step(it + 1, wb);
+    }
   }
-  if (it < n_iter) consume(it, wa);
 
   if (nwaves > 1) {
     __syncthreads();  // all waves are done with their LDS
@@ -399,11 +439,9 @@ int env_int(const char* name, int fallback) {
 
 struct Plan {
   int nt;
-  uint32_t tiles, waves, gps, lds;
-  bool sb16, xs;
+  uint32_t tiles, waves, gps, lds, x_pitch, x_bytes;
+  bool sb16;
 };
-
-int xrows_for(uint32_t M) { return M <= 2 ? 2 : (M <= 4 ? 4 : (M <= 8 ? 8 : 16)); }
 
 // Work decomposition: workgroups own 16*NT rows (a gate/up pair of 16 rows in
 // SwiGLU mode); their waves split K.  HBM throughput here is set by the bytes
@@ -423,12 +461,14 @@ Plan make_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t 
   } else {
     for (int i = 0; i < n_jobs; ++i) p.tiles += (jobs[i].rows + rows_per_set - 1) / rows_per_set;
   }
-  const int xr = xrows_for(M);
+  // Workgroup-staged activations when all M rows fit (rows padded by 16 bytes
+  // so the rows of one ds_read_b128 fall on different banks).
+  p.x_pitch = K * 2 + 16;
+  p.x_bytes = M * p.x_pitch;
+  if (p.x_bytes > kXStageMax || env_int("QM38_Q4_XSTAGE", 1) == 0) p.x_pitch = p.x_bytes = 0;
   const bool g8 = (G % 8) == 0;
   const uint32_t step = g8 ? 8 : 4;
   const uint32_t lds_cu = 160 * 1024;
-  // Stage the activation slices whole when all of them fit comfortably.
-  p.xs = env_int("QM38_Q4_XSTAGE", 0) != 0 && (uint64_t)xr * K * 2 <= 80 * 1024;
   const uint32_t target = (uint32_t)env_int("QM38_Q4_TARGET_WAVES", (int)(cus * 16));
   uint32_t waves = (target + p.tiles - 1) / p.tiles;
   if (env_int("QM38_Q4_SPLIT", 0) > 0) waves = (uint32_t)env_int("QM38_Q4_SPLIT", 1);
@@ -441,27 +481,30 @@ Plan make_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t 
     const uint32_t w = (G + gps - 1) / gps;
     p.gps = gps;
     p.waves = w;
-    p.lds = w * wave_layout(p.nt, xr, g8, gps, p.xs).total;
+    p.lds = p.x_bytes + w * wave_layout(p.nt, g8, gps).total;
     if (p.lds <= lds_cu / 2 || w == 1) break;
     waves = w - 1;
   }
+  // The final cross-wave reduction reuses the LDS from offset 0.
+  const uint32_t red_bytes = p.waves * p.nt * 4 * 64 * 4;
+  if (p.lds < red_bytes) p.lds = red_bytes;
   p.sb16 = g8;
   return p;
 }
 
-template <int NT, int XR, int R, bool SW>
+template <int NT, int R, bool SW>
 hipError_t launch_one(const DecodeArgs& a, const Plan& p, hipStream_t st) {
   const dim3 grid(p.tiles), block(64 * p.waves);
-  if (p.xs) {
+  if (p.x_bytes) {
     if (p.sb16)
-      hipLaunchKernelGGL((q4_decode_kernel<NT, XR, R, SW, true, true>), grid, block, p.lds, st, a);
+      hipLaunchKernelGGL((q4_decode_kernel<NT, R, SW, true, true>), grid, block, p.lds, st, a);
     else
-      hipLaunchKernelGGL((q4_decode_kernel<NT, XR, R, SW, false, true>), grid, block, p.lds, st, a);
+      hipLaunchKernelGGL((q4_decode_kernel<NT, R, SW, false, true>), grid, block, p.lds, st, a);
   } else {
     if (p.sb16)
-      hipLaunchKernelGGL((q4_decode_kernel<NT, XR, R, SW, true, false>), grid, block, p.lds, st, a);
+      hipLaunchKernelGGL((q4_decode_kernel<NT, R, SW, true, false>), grid, block, p.lds, st, a);
     else
-      hipLaunchKernelGGL((q4_decode_kernel<NT, XR, R, SW, false, false>), grid, block, p.lds, st, a);
+      hipLaunchKernelGGL((q4_decode_kernel<NT, R, SW, false, false>), grid, block, p.lds, st, a);
   }
   return hipGetLastError();
 }
@@ -469,15 +512,9 @@ hipError_t launch_one(const DecodeArgs& a, const Plan& p, hipStream_t st) {
 template <int NT, bool SW>
 hipError_t dispatch_m(const DecodeArgs& a, const Plan& p, hipStream_t st) {
   switch (a.M) {
-    case 1: return launch_one<NT, 2, 1, SW>(a, p, st);
-    case 2: return launch_one<NT, 2, 2, SW>(a, p, st);
-    case 3:
-    case 4: return launch_one<NT, 4, 4, SW>(a, p, st);
-    case 5:
-    case 6:
-    case 7:
-    case 8: return launch_one<NT, 8, 4, SW>(a, p, st);
-    default: return launch_one<NT, 16, 4, SW>(a, p, st);
+    case 1: return launch_one<NT, 1, SW>(a, p, st);
+    case 2: return launch_one<NT, 2, SW>(a, p, st);
+    default: return launch_one<NT, 4, SW>(a, p, st);
   }
 }
 
@@ -498,6 +535,8 @@ hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const ui
   a.M = M;
   a.G = K / 64;
   a.gps = p.gps;
+  a.x_pitch = p.x_pitch;
+  a.x_bytes = p.x_bytes;
   a.n_jobs = (uint32_t)n_jobs;
   uint32_t ts = 0;
   const uint32_t rows_per_set = swiglu ? 16u : 16u * p.nt;
