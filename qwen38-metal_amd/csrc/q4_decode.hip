@@ -16,10 +16,12 @@
 //    row's 128-byte line) into a ring of register sets (three with staged
 //    activations, else two), so iterations stay in flight while one is
 //    transposed through a per-wave XOR-swizzled LDS buffer and consumed.
-//  * Activations: when all M rows fit (<= 36 KiB), the workgroup stages them
-//    once in LDS, already in the element order of the weight unpack below, and
-//    every lane reads its MFMA operand from there.  Larger M * K keep a
-//    register path that fetches each iteration's activations as it starts.
+//  * Activations: when all M rows fit (<= 36 KiB), each wave DMAs its K slice
+//    of them into LDS, reorders it in place to the element order of the weight
+//    unpack below, and every lane reads its MFMA operand from there.  The
+//    start-up waits only for these DMAs and the scale/bias tables; the first
+//    weight loads stay in flight.  Larger M * K keep a register path that
+//    fetches each iteration's activations as it starts.
 //  * Scales and biases of a wave's K slice are staged once by buffer->LDS DMA.
 //  * Nibbles become bf16 (128+q) with one AND-OR per pair (exact); the dot
 //    products run on MFMA 16x16x32 with the activation rows as the A operand
@@ -44,14 +46,18 @@ constexpr int kTileBytes = 16 * 128;
 constexpr int kNonTemporal = 2;    // buffer cache policy: nt (weights are streamed once)
 constexpr uint32_t kXStageMax = 36 * 1024;  // LDS bytes of workgroup-staged activations
 
+// Weight ring depth (iterations of register sets in flight): single-tile
+// waves with staged activations have registers for four, the others two.
+// Slices are planned in multiples of 4 * depth groups.
+__host__ __device__ constexpr int ring_depth(int nt, bool xw) { return (xw && nt == 1) ? 4 : 2; }
+
 struct DecodeArgs {
   const uint16_t* x;
   uint32_t K;
   uint32_t M;
   uint32_t G;        // groups per row = K / 64
   uint32_t gps;      // groups per wave slice (multiple of 4)
-  uint32_t x_pitch;  // LDS bytes per staged activation row (0: register path)
-  uint32_t x_bytes;  // LDS bytes of the staged activations (16-byte multiple)
+  uint32_t x_bytes;  // LDS bytes of one wave's staged activations (0: register path)
   uint32_t n_jobs;
   Q4Job jobs[kMaxQ4Jobs];  // tile_begin: first tile set (workgroup) of the job
 };
@@ -61,18 +67,24 @@ struct DecodeArgs {
 __host__ __device__ constexpr uint32_t sb_tile_entries(bool sb16, uint32_t gps) {
   return ((16 * (sb16 ? gps / 8 : gps) + 63) / 64) * 64;
 }
-// Per-wave LDS layout (bytes), after the workgroup's staged activations:
+// LDS bytes per staged activation row of one wave's K slice: the slice's
+// groups (rounded up to whole iterations) plus 16 bytes, so the rows read by
+// one ds_read_b128 fall on different banks.
+__host__ __device__ constexpr uint32_t x_slice_pitch(uint32_t gps) { return gps * 128 + 16; }
+// Per-wave LDS layout (bytes):
 //   transpose buffer   NT x 2 KB: one iteration of weights in row-major form
 //   scales, biases     raw bf16 per [tile][row][group] (DMA target)
+//   activations        (staged mode) M rows of the wave's K slice
 struct WaveLayout {
-  uint32_t s_off, b_off, sb_bytes, total;
+  uint32_t s_off, b_off, sb_bytes, x_off, total;
 };
-__host__ __device__ inline WaveLayout wave_layout(int nt, bool sb16, uint32_t gps) {
+__host__ __device__ inline WaveLayout wave_layout(int nt, bool sb16, uint32_t gps, uint32_t x_bytes) {
   WaveLayout l{};
   l.s_off = nt * kTileBytes;
   l.sb_bytes = nt * sb_tile_entries(sb16, gps) * (sb16 ? 16 : 4);
   l.b_off = l.s_off + l.sb_bytes;
-  l.total = l.b_off + l.sb_bytes;
+  l.x_off = l.b_off + l.sb_bytes;
+  l.total = l.x_off + x_bytes;
   return l;
 }
 
@@ -139,12 +151,13 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
   const int kq = lane >> 4;
   const uint32_t tile = blockIdx.x;
   const uint32_t gps = args.gps;
-  const WaveLayout L = wave_layout(NT, SB16, gps);
-  uint8_t* xl = smem;  // staged activations (XW)
-  uint8_t* wl = smem + (XW ? args.x_bytes : 0) + wave * L.total;
+  const WaveLayout L = wave_layout(NT, SB16, gps, XW ? args.x_bytes : 0);
+  uint8_t* wl = smem + wave * L.total;
   uint8_t* tbuf = wl;
   uint8_t* s_tab = wl + L.s_off;
   uint8_t* b_tab = wl + L.b_off;
+  uint8_t* xl = wl + L.x_off;  // staged activations of this wave's K slice (XW)
+  const uint32_t x_pitch = x_slice_pitch(gps);
 
   int j = 0;
   if (!SWIGLU) {
@@ -170,6 +183,10 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
   const uint32_t g_end = min(G, g_begin + gps);
   const uint32_t span = g_end > g_begin ? g_end - g_begin : 0;
   const uint32_t n_iter = (span + kGroupsPerIter - 1) / kGroupsPerIter;
+  constexpr int kDepth = ring_depth(NT, XW);
+  // Iterations rounded up to whole ring rounds; the extra ones (only in a
+  // workgroup's last, shorter slice) see zero scales and biases.
+  const uint32_t n_pad = (n_iter + kDepth - 1) / kDepth * kDepth;
 
   floatx4 acc[NT];
 #pragma unroll
@@ -200,7 +217,7 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
   const uint32_t am = (uint32_t)nl < args.M ? nl : 0;
   const uint16_t* xrow_g = args.x + (size_t)am * K + 16 * kq;
 
-  auto load_w = [&](uint32_t it, WRegs<NT>& r) {
+  auto load_w = [&](uint32_t it, WRegs<NT>& r) __attribute__((always_inline)) {
     const uint32_t g = g_begin + it * kGroupsPerIter;
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -210,7 +227,7 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
                                                           kNonTemporal);
   };
   // Register path: an iteration's activations, fetched one iteration ahead.
-  auto load_x = [&](uint32_t it, XRegs& r) {
+  auto load_x = [&](uint32_t it, XRegs& r) __attribute__((always_inline)) {
     if (XW) return;
     const uint32_t g = g_begin + it * kGroupsPerIter;
 #pragma unroll
@@ -221,14 +238,24 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
     }
   };
 
-  WRegs<NT> wa, wb, wc;
+  WRegs<NT> wr[kDepth];
   XRegs xp;
   const uint32_t pad = sb_tile_entries(SB16, gps);
   // --- one-time staging: scales and biases, first weights, activations --------
+  const uint32_t x_chunks = span * 8;  // 16-byte activation chunks per row of the slice
   {
     const uint32_t cols = SB16 ? gps / 8 : gps;  // DMA entries per row
     const uint32_t per_tile = 16 * cols;
     if (n_iter > 0) {
+      if (XW) {
+        // The wave's K slice of all M activation rows, by buffer->LDS DMA in
+        // natural order (reordered in place once it has landed).
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(args.x, (uint64_t)args.M * K * 2);
+        for (uint32_t m = 0; m < args.M; ++m)
+          for (uint32_t c0 = 0; c0 < x_chunks; c0 += 64)
+            if (c0 + lane < x_chunks)
+              dma16(rx, xl + m * x_pitch + c0 * 16, (m * K + g_begin * 64) * 2 + (c0 + lane) * 16, 0);
+      }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const int q = SWIGLU ? t / kHalf : 0;
@@ -252,37 +279,26 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
       }
       // The first iterations' weights stream while everything else lands
       // (three with staged activations, two on the register path).
-      load_w(0, wa);
-      if (n_iter > 1) load_w(1, wb);
-      if (XW && n_iter > 2) load_w(2, wc);
+      // Every ring slot is filled (short slices repeat their last iteration)
+      // so all paths below see the same outstanding loads and the compiler's
+      // waits stay exact.
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) {
+        load_w(min((uint32_t)d, n_iter - 1), wr[d]);
+        __builtin_amdgcn_sched_barrier(0);  // keep the slots in issue order
+      }
       load_x(0, xp);
-    }
-    if (XW) {
-      // The workgroup stages all M activation rows, each 8-element chunk
-      // reordered (x0,x4)(x1,x5)(x2,x6)(x3,x7) to match unpack_word.  These
-      // loads are the youngest, so the wait for them below also covers the
-      // table DMA and the first weights.
-      const uint32_t chunks = args.M * (K / 8);
-      for (uint32_t c = threadIdx.x; c < chunks; c += blockDim.x) {
-        const uint32_t m = c / (K / 8), ch = c - m * (K / 8);
-        const u32x4 v = *(const u32x4*)(args.x + (size_t)m * K + 8 * ch);
-        *(u32x4*)(xl + m * args.x_pitch + 16 * ch) = interleave_bf16x8(v);
-      }
-    }
-    if (n_iter > 0) {
-      // Groups past the slice end get scale = bias = 0 (they contribute 0);
-      // the table DMA must have landed first.
-      if (!XW) {
-        constexpr int kW = 2 * NT, kX = 8;
-        if (n_iter > 1)
-          wait_vmcnt<2 * kW + kX>();
-        else
-          wait_vmcnt<kW + kX>();
+      // Wait for the DMAs (activations, tables) only: the weight loads issued
+      // after them stay in flight.
+      if constexpr (!XW) {
+        static_assert(kDepth == 2, "register path waits for two weight sets");
+        wait_vmcnt<2 * (2 * NT) + 8>();
       } else {
-        wait_vmcnt<0>();
+        wait_vmcnt<kDepth * (2 * NT)>();
       }
-      if (span % kGroupsPerIter) {
-        const uint32_t dead = kGroupsPerIter - span % kGroupsPerIter;
+      // Groups past the slice end get scale = bias = 0 (they contribute 0).
+      if (span < n_pad * kGroupsPerIter) {
+        const uint32_t dead = n_pad * kGroupsPerIter - span;
         for (uint32_t e = lane; e < NT * 16 * dead; e += 64) {
           const uint32_t t = e / (16 * dead), row = (e / dead) % 16, gl = span + e % dead;
           if (SB16) {
@@ -294,8 +310,16 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
           }
         }
       }
+      if (XW) {
+        // Each 8-element chunk reordered (x0,x4)(x1,x5)(x2,x6)(x3,x7) to match
+        // unpack_word.
+        for (uint32_t e = lane; e < args.M * x_chunks; e += 64) {
+          const uint32_t m = e / x_chunks, c = e - m * x_chunks;
+          u32x4* px = (u32x4*)(xl + m * x_pitch + c * 16);
+          *px = interleave_bf16x8(*px);
+        }
+      }
     }
-    if (XW) __syncthreads();  // staged activations visible to every wave
     wait_lgkmcnt0();
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -304,9 +328,9 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
   const uint32_t mask_s = __builtin_amdgcn_readfirstlane(0x000F000Fu);
   uint32_t or_v = 0x43004300u;
   asm volatile("" : "+v"(or_v));
-  const uint8_t* xlr = xl + am * args.x_pitch + 32 * kq;  // this lane's staged row, chunk pair 2kq
+  const uint8_t* xlr = xl + am * x_pitch + 32 * kq;  // this lane's staged row, chunk pair 2kq
 
-  auto consume = [&](uint32_t it, const WRegs<NT>& r, const XRegs& xr) {
+  auto consume = [&](uint32_t it, const WRegs<NT>& r, const XRegs& xr) __attribute__((always_inline)) {
     const uint32_t gl = it * kGroupsPerIter;  // group offset inside the slice
     // Scales / biases of the 4 groups (bf16 -> fp32 by shifting).
     uint32_t sv[NT][4], bv[NT][4];
@@ -336,9 +360,9 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
     for (int u = 0; u < 4; ++u) {
       u32x4 xa0, xa1;
       if (XW) {
-        // Groups past K (dead iterations) read the last group: finite data,
-        // zero scale and bias.
-        const uint8_t* p = xlr + (size_t)min(g_begin + gl + u, G - 1) * 128;
+        // Groups past the slice (dead iterations) read its last group: finite
+        // data, zero scale and bias.
+        const uint8_t* p = xlr + min(gl + u, span - 1) * 128;
         xa0 = *(const u32x4*)p;
         xa1 = *(const u32x4*)(p + 16);
       } else {
@@ -363,34 +387,29 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
     __builtin_amdgcn_wave_barrier();
   };
 
-  if constexpr (XW) {
-    // Staged activations: a ring of three weight register sets, two
-    // iterations in flight while one is transposed and consumed.
-    auto step = [&](uint32_t i, WRegs<NT>& w) {
-      consume(i, w, xp);
-      if (i + 3 < n_iter) load_w(i + 3, w);
-    };
-    for (uint32_t it = 0; it < n_iter; it += 3) {
-      step(it, wa);
-      if (it + 1 >= n_iter) break;
-      step(it + 1, wb);
-      if (it + 2 >= n_iter) break;
-      step(it + 2, wc);
+  // Whole ring rounds: each iteration consumes its slot and refills it
+  // kDepth iterations ahead, unconditionally (dead iterations reload the
+  // last real one), so every path carries the same outstanding loads and the
+  // compiler's waits stay exact; the final round drains the ring.  The
+  // register path (larger M * K) fetches an iteration's activations as it
+  // starts.
+  auto step = [&](uint32_t i, WRegs<NT>& w, bool refill) __attribute__((always_inline)) {
+    if (!XW && i > 0) load_x(min(i, n_iter - 1), xp);
+    consume(i, w, xp);
+    if (refill) {
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(min(i + kDepth, n_iter - 1), w);
+      __builtin_amdgcn_sched_barrier(0);  // refills stay in slot order
     }
-  } else {
-    // Register path (larger M * K): the activation registers leave room for
-    // two weight sets only, one iteration in flight; each iteration's
-    // activations are fetched at its start.
-    auto step = [&](uint32_t i, WRegs<NT>& w) {
-      if (i > 0) load_x(i, xp);
-      consume(i, w, xp);
-      if (i + 2 < n_iter) load_w(i + 2, w);
-    };
-    for (uint32_t it = 0; it < n_iter; it += 2) {
-      step(it, wa);
-      if (it + 1 >= n_iter) break;
-      step(it + 1, wb);
+  };
+  if (n_iter > 0) {
+    uint32_t it = 0;
+    for (; it + kDepth < n_pad; it += kDepth) {
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) step(it + d, wr[d], true);
     }
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) step(it + d, wr[d], false);
   }
 
   if (nwaves > 1) {
@@ -439,7 +458,7 @@ int env_int(const char* name, int fallback) {
 
 struct Plan {
   int nt;
-  uint32_t tiles, waves, gps, lds, x_pitch, x_bytes;
+  uint32_t tiles, waves, gps, lds, x_bytes;
   bool sb16;
 };
 
@@ -461,13 +480,10 @@ Plan make_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t 
   } else {
     for (int i = 0; i < n_jobs; ++i) p.tiles += (jobs[i].rows + rows_per_set - 1) / rows_per_set;
   }
-  // Workgroup-staged activations when all M rows fit (rows padded by 16 bytes
-  // so the rows of one ds_read_b128 fall on different banks).
-  p.x_pitch = K * 2 + 16;
-  p.x_bytes = M * p.x_pitch;
-  if (p.x_bytes > kXStageMax || env_int("QM38_Q4_XSTAGE", 1) == 0) p.x_pitch = p.x_bytes = 0;
+  // Staged activations when all M rows fit (each wave holds its K slice).
+  const bool xw = M * (K * 2 + 16) <= kXStageMax && env_int("QM38_Q4_XSTAGE", 1) != 0;
   const bool g8 = (G % 8) == 0;
-  const uint32_t step = g8 ? 8 : 4;
+  const uint32_t step = 4 * ring_depth(p.nt, xw);  // whole ring rounds per slice (also a multiple of 8)
   const uint32_t lds_cu = 160 * 1024;
   const uint32_t target = (uint32_t)env_int("QM38_Q4_TARGET_WAVES", (int)(cus * 16));
   uint32_t waves = (target + p.tiles - 1) / p.tiles;
@@ -481,7 +497,8 @@ Plan make_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t 
     const uint32_t w = (G + gps - 1) / gps;
     p.gps = gps;
     p.waves = w;
-    p.lds = p.x_bytes + w * wave_layout(p.nt, g8, gps).total;
+    p.x_bytes = xw ? M * x_slice_pitch(gps) : 0;
+    p.lds = w * wave_layout(p.nt, g8, gps, p.x_bytes).total;
     if (p.lds <= lds_cu / 2 || w == 1) break;
     waves = w - 1;
   }
@@ -535,7 +552,6 @@ hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const ui
   a.M = M;
   a.G = K / 64;
   a.gps = p.gps;
-  a.x_pitch = p.x_pitch;
   a.x_bytes = p.x_bytes;
   a.n_jobs = (uint32_t)n_jobs;
   uint32_t ts = 0;
