@@ -28,15 +28,23 @@ COMMON = [
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unused-variable",
-    # Packed fp32 ops stay disabled on this pool ("Build").
+    # Packed fp32 VALU ops stay disabled: some of their forms have given
+    # wrong results on this hardware pool; hipcc emits plain fp32 ops instead.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{PKG.parent / 'include'}",
 ]
 
 
+# Per-file flags.  Attention: MFMA accumulators in VGPRs (the compiler would
+# otherwise park them in AGPRs and copy them back every step).
+PER_FILE = {
+    "q8_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.name + ".o")
-    cmd = [HIPCC, *COMMON, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON, *PER_FILE.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")

@@ -441,7 +441,7 @@ struct DecodeLds {
   static constexpr int kK = 16 * D, kV = 16 * D, kS = 512;  // K, V, scales (K 256 B + V 256 B)
   static constexpr int kPage = kK + kV + kS;
   static constexpr int kWaveRing = kRing * kPage;
-  static constexpr int kRed = 4 * D * 16 * 4 + 3 * 4 * 16 * 4;
+  static constexpr int kRed = 4 * D * 16 * 4 + (3 * 4 + 2) * 16 * 4;  // O, m, l, weights, max, sums
   static constexpr int kBytes = 4 * kWaveRing > kRed ? 4 * kWaveRing : kRed;
 };
 
@@ -681,20 +681,35 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
     red_l[wave][col] = l_tot;
   }
   __syncthreads();
+  // Per (wave, column) weights exp2(m_w - max) and the column sums, once;
+  // the element loop below is then multiply-adds only.
+  float(*red_f)[16] = red_l + 4;  // [wave][col]
+  float* red_mx = red_l[4 + kWaves];
+  float* red_L = red_mx + 16;
+  if (threadIdx.x < 16) {
+    const uint32_t c = threadIdx.x;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, red_m[w][c]);
+    float Ls = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = red_m[w][c] == -INFINITY ? 0.0f : exp2f(red_m[w][c] - mx);
+      red_f[w][c] = f;
+      Ls += f * red_l[w][c];
+    }
+    red_mx[c] = mx;
+    red_L[c] = Ls;
+  }
+  __syncthreads();
   const uint32_t nsplit = sq.nsplit;
   for (uint32_t e = threadIdx.x; e < (uint32_t)D * 16; e += 256) {
     const uint32_t c = e % 16, d = e / 16;
     if (c >= gh) continue;
-    float mx = -INFINITY;
+    const float mx = red_mx[c], Ls = red_L[c];
+    float O = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, red_m[w][c]);
-    float Ls = 0.0f, O = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float f = red_m[w][c] == -INFINITY ? 0.0f : exp2f(red_m[w][c] - mx);
-      Ls += f * red_l[w][c];
-      O += f * red_o[w][d][c];
-    }
+    for (int w = 0; w < kWaves; ++w) O += red_f[w][c] * red_o[w][d][c];
     const uint32_t hh = kvh * gh + c;
     if (nsplit == 1) {
       float v = O / fmaxf(Ls, FLT_MIN);
@@ -712,29 +727,32 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   }
 }
 
-// Merge the split partials of one (sequence, head): grid (n_seqs * H), 256
-// threads.  Thread t owns the float4 column slice c = t % (D/4) of the splits
-// s = t / (D/4) + k * (256 / (D/4)), and loads every (O slice, m, l) it needs
-// in one go, so the whole merge costs one memory round trip; the per-head
-// maximum and the slice sums then meet in LDS.
+// Merge the split partials of one (sequence, head, 32-wide d slice): grid
+// (n_seqs * H * D/32), 256 threads.  Thread t owns float4 slice c = t % 8 of
+// the workgroup's 32 d and the splits s = t / 8 + 32 k, and loads every
+// (O slice, m, l) it needs in one go, so the merge costs one memory round
+// trip spread over many workgroups; the per-head maximum and the sums over
+// splits then meet in LDS.
 template <int D>
 __global__ __launch_bounds__(256) void q8_combine_kernel(AttnArgs args) {
-  constexpr int kSlices = D / 4;            // float4 slices of one partial row
-  constexpr int kGroups = 256 / kSlices;    // split groups per pass
-  constexpr int kMaxPer = 16;               // splits a thread holds in registers per pass
+  constexpr int kWgPerHead = D / 32;  // workgroups per (sequence, head)
+  constexpr int kGroups = 32;         // split groups (threads per slice)
+  constexpr int kMaxPer = 4;          // splits a thread holds in registers per pass
   __shared__ float red_m[256];
   __shared__ floatx4 red_o[256];
   __shared__ float red_l[256];
   const uint32_t H = args.heads;
-  const uint32_t b = blockIdx.x / H, hh = blockIdx.x % H;
+  const uint32_t wq = blockIdx.x % kWgPerHead;
+  const uint32_t bh = blockIdx.x / kWgPerHead;
+  const uint32_t b = bh / H, hh = bh % H;
   const AttnSeq& sq = args.seqs[b];
   const uint32_t ns = sq.nsplit;
   if (ns <= 1) return;
   const size_t stride = (size_t)H * (D + 2);
   const float* base = args.partials + ((size_t)sq.part_begin * H + hh) * (D + 2);
-  const uint32_t t = threadIdx.x, c = t % kSlices, g = t / kSlices;
+  const uint32_t t = threadIdx.x, c = t % 8, g = t / 8;
+  const uint32_t d0 = 32 * wq + 4 * c;
 
-  // Pass over the splits of this thread (ns <= kMaxSplits; kGroups * kMaxPer per pass).
   float mloc = -INFINITY;
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
   float lacc = 0.0f;
@@ -747,7 +765,7 @@ __global__ __launch_bounds__(256) void q8_combine_kernel(AttnArgs args) {
     for (int k = 0; k < kMaxPer; ++k) {
       const uint32_t s = s0 + g + k * kGroups;
       const float* row = base + (s < ns ? s : ns - 1) * stride;
-      ov[k] = *(const floatx4*)(row + 4 * c);
+      ov[k] = *(const floatx4*)(row + d0);
       mv[k] = row[D];
       lv[k] = row[D + 1];
     }
@@ -773,7 +791,7 @@ __global__ __launch_bounds__(256) void q8_combine_kernel(AttnArgs args) {
   red_m[t] = mloc;
   __syncthreads();
   float mx = -INFINITY;
-  for (int k = 0; k < kGroups; ++k) mx = fmaxf(mx, red_m[c + k * kSlices]);
+  for (int k = 0; k < kGroups; ++k) mx = fmaxf(mx, red_m[c + 8 * k]);
   const float f = mloc == -INFINITY ? 0.0f : exp2f(mloc - mx);
   red_o[t] = acc * f;
   red_l[t] = lacc * f;
@@ -782,11 +800,11 @@ __global__ __launch_bounds__(256) void q8_combine_kernel(AttnArgs args) {
     floatx4 o = red_o[c];
     float L = red_l[c];
     for (int k = 1; k < kGroups; ++k) {
-      o += red_o[c + k * kSlices];
-      L += red_l[c + k * kSlices];
+      o += red_o[c + 8 * k];
+      L += red_l[c + 8 * k];
     }
     const float inv = 1.0f / fmaxf(L, FLT_MIN);
-    const size_t oi = ((size_t)b * H + hh) * D + 4 * c;
+    const size_t oi = ((size_t)b * H + hh) * D + d0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float v = o[e] * inv;
@@ -803,7 +821,8 @@ hipError_t launch_attn_d(const AttnArgs& a, uint32_t units, bool need_combine, h
     return hipGetLastError();
   }
   hipLaunchKernelGGL(q8_decode_kernel<D>, dim3(units), dim3(256), 0, st, a);
-  if (need_combine) hipLaunchKernelGGL(q8_combine_kernel<D>, dim3(a.n_seqs * a.heads), dim3(256), 0, st, a);
+  if (need_combine)
+    hipLaunchKernelGGL(q8_combine_kernel<D>, dim3(a.n_seqs * a.heads * (D / 32)), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
