@@ -452,7 +452,7 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   constexpr int kKChunks = D / 16;          // 16-byte chunks per K token row
   constexpr int kKDma = D / 64;             // DMA instructions per K (and V) page
   constexpr int kDmaPerPage = 2 * kKDma + 2;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[L::kBytes + 4 * kMaxPagesPerSplit];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[L::kBytes];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -495,13 +495,8 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
     const uint32_t sw = kKChunks == 16 ? t : kKChunks == 8 ? ((t & 7) ^ (t >> 3)) : (t & 3);
     k_src[h] = t * D + (jj ^ sw) * 16;
   }
-  // Page ids of the split, staged once in LDS: inside the loop an id is an
-  // LDS read (lgkmcnt), never a global load whose vmcnt wait would drain the
-  // DMA ring.
   const uint32_t first = p_begin + wave;
   const uint32_t n_mine = first < p_end ? (p_end - first + kWaves - 1) / kWaves : 0;
-  int32_t* ids = reinterpret_cast<int32_t*>(lds + L::kBytes);
-  for (uint32_t i = threadIdx.x; i < p_end - p_begin; i += 256) ids[i] = page_id(sq, p_begin + i);
   // The last split of each (sequence, KV head) appends the new token first
   // (waves 0 and 1 quantise K and V); the barrier below orders those stores
   // before any wave's DMA of the last page.  KV head 0 also records pages
@@ -515,10 +510,19 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
       for (int32_t i = 0; i < sq.new_page_count; ++i) sq.pt[sq.new_page_first + i] = sq.new_page_id + i;
     }
     wait_vmcnt<0>();
+    __syncthreads();
   }
-  __syncthreads();
+  // Page ids are wave-uniform scalar loads (lgkmcnt), never vector loads
+  // whose vmcnt wait would drain the DMA ring.  The table is read through the
+  // constant address space: the only entries this kernel writes are pages
+  // materialised by this call, whose ids page_id() computes without a read.
+  const __attribute__((address_space(4))) int32_t* pt_s =
+      (const __attribute__((address_space(4))) int32_t*)sq.pt;
   auto issue = [&](uint32_t j, int slot_idx) {
-    const int32_t phys = __builtin_amdgcn_readfirstlane(ids[wave + kWaves * j]);
+    const uint32_t p = first + kWaves * j;
+    const int32_t phys = sq.new_page_count > 0 && (int32_t)p >= sq.new_page_first
+                             ? sq.new_page_id + ((int32_t)p - sq.new_page_first)
+                             : pt_s[p];
     uint8_t* dst = ring + slot_idx * L::kPage;
     const size_t pbase = (size_t)phys * kv_page_stride;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(sq.k + pbase + (size_t)kvh * 16 * D, 16 * D);
