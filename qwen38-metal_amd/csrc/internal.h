@@ -39,6 +39,9 @@ hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const ui
 // Prefill Q4 GEMM (M > 16): Y[M][N] = X[M][K] * dequant(W)^T, bf16 out.
 // swiglu as above.
 size_t q4_gemm_xh_bytes(uint32_t K, uint32_t M);
+// Split-K partial bytes / counters a GEMM launch needs (0 when it does not split).
+void q4_gemm_workspace(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M, size_t* partial_bytes,
+                       size_t* counters);
 hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x,
                           uint32_t K, uint32_t M, const Workspace& ws, hipStream_t stream);
 

@@ -25,6 +25,11 @@
 //    so the tile index is remapped to give each XCD a contiguous run of N
 //    tiles with all of their M tiles (W is read from HBM once per XCD and
 //    stays in that XCD's L2 while its M tiles pass).
+//    Split-K when the tiles alone would leave CUs idle (small M, or few N
+//    tiles): each workgroup takes one K slice of a tile and writes its fp32
+//    accumulators through to memory; the last slice of the tile to finish (a
+//    per-tile counter it resets) adds the slices in slice order, so the sum
+//    does not depend on timing, and runs the epilogue.
 #include "common.h"
 #include "internal.h"
 
@@ -44,7 +49,13 @@ struct GemmArgs {
   const uint16_t* xh;  // fp16 bits [M][K], chunk-permuted
   uint32_t K, M;
   uint32_t m_tiles, total_tiles;
+  uint32_t splits, gks;  // K slices per tile, groups per slice
+  float* partials;       // [tile][slice][kThreads * 128] fp32 (splits > 1)
+  unsigned* counters;    // [tile], zero between launches
 };
+
+// s_waitcnt vmcnt(0) (gfx9 encoding; expcnt and lgkmcnt left at their maxima).
+__device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Byte offset of 16-byte chunk c (0..7) of row r in a 256 x 128 B tile.  The
 // XOR spreads the 16 rows one ds_read_b128 phase touches over distinct banks.
@@ -100,12 +111,16 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmArgs args) {
   const uint32_t wm = wave & 3, wn = wave >> 2;
   const uint32_t K = args.K, M = args.M, G = K / 64;
 
-  // ---- XCD-aware tile remap -------------------------------------------------
-  const uint32_t T = args.total_tiles;
+  // ---- XCD-aware tile remap (over tile x K-slice units) -------------------
+  const uint32_t S = args.splits;
+  const uint32_t T = args.total_tiles * S;
   const uint32_t xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds;
   const uint32_t q = T / kXcds, rem = T % kXcds;
-  const uint32_t L = xcd * q + min(xcd, rem) + local;
+  const uint32_t LS = xcd * q + min(xcd, rem) + local;
+  const uint32_t L = LS / S, split = LS - L * S;
   const uint32_t n_tile = L / args.m_tiles, m_tile = L % args.m_tiles;
+  const uint32_t g0 = split * args.gks;
+  const uint32_t NG = min(G, g0 + args.gks) - g0;  // K steps of this slice (>= 1)
   const uint32_t m0 = m_tile * kBM;
 
   // ---- this thread's W row and the tile's job ------------------------------
@@ -175,13 +190,13 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmArgs args) {
   const uint32_t arow0 = 64 * wm + (lane & 31);
   const uint32_t kh = lane >> 5;
 
-  load(0);
+  load(g0);
   store(0);
-  if (G > 1) load(1);
+  if (NG > 1) load(g0 + 1);
   __syncthreads();
 
-  for (uint32_t g = 0; g < G; ++g) {
-    const int st = g & 1;
+  for (uint32_t i = 0; i < NG; ++i) {
+    const int st = i & 1;
     const uint8_t* xt = lds[st][0];
     const uint8_t* wt = lds[st][1];
 #pragma unroll
@@ -197,11 +212,62 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmArgs args) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma_f16(a[i], b[j], acc[i][j]);
     }
-    if (g + 1 < G) {
+    if (i + 1 < NG) {
       store(st ^ 1);
-      if (g + 2 < G) load(g + 2);
+      if (i + 2 < NG) load(g0 + i + 2);
     }
     __syncthreads();
+  }
+
+  // ---- split-K: publish this slice, the last one of the tile adds them -----
+  if (S > 1) {
+    // Thread-major float4 layout: element (k4, tid) at (k4 * kThreads + tid) * 4.
+    // Stores and loads carry sc0 sc1 (system coherence: written through to
+    // memory, read past the caches), so publishing them needs only their
+    // completion before the count, not a cache write-back.
+    constexpr int kSys = 0x11;  // buffer cache policy: sc0 | sc1
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc(args.partials + (size_t)L * S * (kThreads * 128), (uint64_t)S * kThreads * 128 * 4);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const int k4 = (i * 4 + j) * 4 + e4;
+          const u32x4 v = {__float_as_uint(acc[i][j][4 * e4]), __float_as_uint(acc[i][j][4 * e4 + 1]),
+                           __float_as_uint(acc[i][j][4 * e4 + 2]), __float_as_uint(acc[i][j][4 * e4 + 3])};
+          __builtin_amdgcn_raw_buffer_store_b128(v, rp, (k4 * kThreads + tid) * 16, split * (kThreads * 128 * 4),
+                                                 kSys);
+        }
+    wait_vmcnt0();
+    __shared__ unsigned last;
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned prev = __hip_atomic_fetch_add(&args.counters[L], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = prev == S - 1;
+      if (last) __hip_atomic_store(&args.counters[L], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = floatx16{};
+    for (uint32_t sl = 0; sl < S; ++sl) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int e4 = 0; e4 < 4; ++e4) {
+            const int k4 = (i * 4 + j) * 4 + e4;
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rp, (k4 * kThreads + tid) * 16,
+                                                                  sl * (kThreads * 128 * 4), kSys);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][4 * e4 + e] += __uint_as_float(v[e]);
+          }
+    }
   }
 
   // ---- epilogue ------------------------------------------------------------
@@ -239,11 +305,62 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmArgs args) {
 
 size_t q4_gemm_xh_bytes(uint32_t K, uint32_t M) { return (size_t)M * K * 2; }
 
+namespace {
+struct GemmPlan {
+  uint32_t m_tiles, tiles, splits, gks;
+};
+// K slices per tile: when the tiles fill less than one dispatch round of
+// `cus` workgroups, split K so the units fill whole rounds as evenly as
+// possible (at least 8 K steps per slice, at most 8 slices).
+GemmPlan gemm_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M) {
+  GemmPlan p{};
+  p.m_tiles = (M + kBM - 1) / kBM;
+  uint32_t n_tiles = 0;
+  if (swiglu) {
+    n_tiles = (jobs[0].rows + 127) / 128;
+  } else {
+    for (int i = 0; i < n_jobs; ++i) n_tiles += (jobs[i].rows + kBN - 1) / kBN;
+  }
+  p.tiles = n_tiles * p.m_tiles;
+  const uint32_t G = K / 64, cus = 256;
+  p.splits = 1;
+  if (p.tiles < cus) {
+    double best = (double)p.tiles / cus;
+    for (uint32_t s = 2; s <= 8 && G / s >= 8; ++s) {
+      const uint32_t units = p.tiles * s, rounds = (units + cus - 1) / cus;
+      const double eff = (double)units / (rounds * cus);
+      if (eff > best + 0.05) {
+        best = eff;
+        p.splits = s;
+      }
+    }
+  }
+  p.gks = (G + p.splits - 1) / p.splits;
+  p.splits = (G + p.gks - 1) / p.gks;
+  return p;
+}
+}  // namespace
+
+void q4_gemm_workspace(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M, size_t* partial_bytes,
+                       size_t* counters) {
+  const GemmPlan p = gemm_plan(jobs, n_jobs, swiglu, K, M);
+  *partial_bytes = p.splits > 1 ? (size_t)p.tiles * p.splits * kThreads * 128 * sizeof(float) : 0;
+  *counters = p.splits > 1 ? p.tiles : 0;
+}
+
 hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x, uint32_t K, uint32_t M,
                           const Workspace& ws, hipStream_t stream) {
   if (n_jobs < 1 || n_jobs > kMaxQ4Jobs || K % 64 != 0 || M == 0) return hipErrorInvalidValue;
   if (!ws.xh || ws.xh_bytes < q4_gemm_xh_bytes(K, M)) return hipErrorInvalidValue;
+  const GemmPlan plan = gemm_plan(jobs, n_jobs, swiglu, K, M);
+  if (plan.splits > 1 && (ws.partial_bytes < (size_t)plan.tiles * plan.splits * kThreads * 128 * sizeof(float) ||
+                          ws.counter_count < plan.tiles))
+    return hipErrorInvalidValue;
   GemmArgs a{};
+  a.splits = plan.splits;
+  a.gks = plan.gks;
+  a.partials = ws.partials;
+  a.counters = ws.counters;
   a.n_jobs = n_jobs;
   a.xh = ws.xh;
   a.K = K;
@@ -260,10 +377,11 @@ hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint
 
   const size_t chunks = (size_t)M * K / 8;
   hipLaunchKernelGGL(x_to_f16_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream, x, ws.xh, chunks);
+  const dim3 grid(a.total_tiles * a.splits);
   if (swiglu)
-    hipLaunchKernelGGL(q4_gemm_kernel<true>, dim3(a.total_tiles), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(q4_gemm_kernel<true>, grid, dim3(kThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL(q4_gemm_kernel<false>, dim3(a.total_tiles), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(q4_gemm_kernel<false>, grid, dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 

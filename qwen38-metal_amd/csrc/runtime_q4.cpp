@@ -50,7 +50,10 @@ Q4Job to_job(const qm_q4_job& j, uint16_t* out) {
 qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const uint16_t* x, uint32_t K,
                  uint32_t M, const char* what) {
   size_t pbytes = 0, counters = 0;
-  q4_decode_workspace(jobs, n, swiglu, K, M < kDecodeMaxRows ? M : kDecodeMaxRows, &pbytes, &counters);
+  if (M <= kDecodeMaxRows)
+    q4_decode_workspace(jobs, n, swiglu, K, M, &pbytes, &counters);
+  else
+    q4_gemm_workspace(jobs, n, swiglu, K, M, &pbytes, &counters);
   qm_status st = ensure_partials(rt, pbytes);
   if (st == QM_OK) st = ensure_counters(rt, counters);
   if (st == QM_OK && M > kDecodeMaxRows) st = ensure_xh(rt, q4_gemm_xh_bytes(K, M));

@@ -146,3 +146,28 @@ def test_prefill_27b_shapes(rt, torch_dev, M):
     hb = synth.f32_to_bf16(h_got)
     (y,) = _project(rt, torch_dev, [down], hb, M)
     assert_bf16_close(y[rows], oracle.q4_project(hb[rows], *down), what="down")
+
+
+@pytest.mark.parametrize("M", [33, 300])
+def test_split_k_swiglu_and_determinism(rt, torch_dev, M):
+    # K = 2048 (32 groups) with few output tiles: the launch splits K across
+    # workgroups, and the last slice of each tile adds the slices in a fixed
+    # order, so two calls agree bit for bit.
+    import qm38
+    rng = np.random.default_rng(90 + M)
+    K, I = 2048, 384
+    gate = synth.q4_matrix(rng, I, K)
+    up = synth.q4_matrix(rng, I, K)
+    xb = synth.bf16_normal(rng, (M, K))
+    h_ref = oracle.swiglu(oracle.q4_project(xb, *gate), oracle.q4_project(xb, *up))
+    dg, du = _upload(torch_dev, *gate), _upload(torch_dev, *up)
+    jg, ju = qm38.Runtime.job(*dg, I), qm38.Runtime.job(*du, I)
+    xd = to_dev(xb, torch_dev)
+    h1, h2 = empty_bf16((M, I), torch_dev), empty_bf16((M, I), torch_dev)
+    rt.q4_swiglu(jg, ju, xd, K, M, h1)
+    rt.q4_swiglu(jg, ju, xd, K, M, h2)
+    got = bf16_dev_to_f32(h1)
+    assert_bf16_close(got, h_ref, what="split-K swiglu")
+    assert np.array_equal(got, bf16_dev_to_f32(h2)), "split-K result differs between calls"
+    (y,) = _project(rt, torch_dev, [gate], xb, M)
+    assert_bf16_close(y, oracle.q4_project(xb, *gate), what="split-K projection")
