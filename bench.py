@@ -329,6 +329,61 @@ def traffic_from_profiles():
         return None
 
 
+def _counter_rows(d: str, counter: str):
+    """(kernel name, KiB) per dispatch of `counter`, in dispatch order, from a rocprofv3 csv directory."""
+    import csv
+    import glob
+    files = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
+    if not files:
+        raise FileNotFoundError(f"no *counter_collection.csv under {d}")
+    rows = []
+    with open(files[0]) as f:
+        for r in csv.DictReader(f):
+            if r.get("Counter_Name") == counter:
+                rows.append((int(r.get("Dispatch_Id", len(rows))), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return [(k, v) for _, k, v in rows]
+
+
+def traffic_summary(fetch_dir: str, write_dir: str) -> int:
+    """HBM bytes per gate+up M=1 launch from FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each scaled by
+    what the same counter reads for a 256 MiB device copy of known size."""
+    copy_bytes = 256 << 20
+    out = {"kernel": None, "calibration": {"copy_bytes": copy_bytes}, "raw_KiB_per_dispatch": {}}
+    per = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        rows = _counter_rows(d, counter)
+        # The copy dispatches are the large non-q4 ones; the first (a small runtime copy) is excluded.
+        copies = [v for k, v in rows if "q4_decode" not in k and v * 1024 > copy_bytes / 4]
+        q4 = [(k, v) for k, v in rows if "q4_decode" in k]
+        if not copies or not q4:
+            raise RuntimeError(f"{counter}: expected copy and q4_decode dispatches in {d}")
+        factor = copy_bytes / (sum(copies) / len(copies) * 1024)
+        out["calibration"][f"{counter}_KiB"] = round(sum(copies) / len(copies), 3)
+        out["calibration"]["fetch_factor" if counter == "FETCH_SIZE" else "write_factor"] = round(factor, 4)
+        out["raw_KiB_per_dispatch"][counter] = [v for _, v in q4]
+        per[counter] = sum(v for _, v in q4) / len(q4) * 1024 * factor
+        out["kernel"] = q4[0][0][:120] + " (gate+up SwiGLU, M=1, 27B shapes)"
+    alg = 2 * q4_bytes(I, H) + 2 * (H + I)
+    out.update({"bytes_per_launch": int(per["FETCH_SIZE"] + per["WRITE_SIZE"]),
+                "fetch_bytes": int(per["FETCH_SIZE"]), "write_bytes": int(per["WRITE_SIZE"]),
+                "algorithmic_bytes": alg,
+                "traffic_over_algorithmic": round((per["FETCH_SIZE"] + per["WRITE_SIZE"]) / alg, 4),
+                "commands": [
+                    "rocprofv3 --pmc FETCH_SIZE --kernel-trace -d gpurun_out/pmc_fetch -o fetch --output-format csv "
+                    "-- python -u bench.py --traffic-probe",
+                    "rocprofv3 --pmc WRITE_SIZE --kernel-trace -d gpurun_out/pmc_write -o write --output-format csv "
+                    "-- python -u bench.py --traffic-probe",
+                    "python bench.py --traffic-from gpurun_out/pmc_fetch gpurun_out/pmc_write"],
+                "method": "per-dispatch counter (KiB) x (known copy bytes / the counter's reading for a 256 MiB "
+                          "device copy); small copies excluded from the calibration mean"})
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "q4_decode_gateup_traffic.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+    print(path)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -340,7 +395,12 @@ def main() -> int:
                     help="comma list of extra legs to run (the M=1 headline always runs)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc: 5 launches of a 256 MiB copy, then 5 gate+up M=1 launches")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn the two --traffic-probe counter runs (rocprofv3 csv output directories) "
+                         "into profiles/q4_decode_gateup_traffic.json (no GPU needed)")
     args = ap.parse_args()
+    if args.traffic_from:
+        return traffic_summary(*args.traffic_from)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU mode (one GPU per box); "
               "run with --gpus 1", file=sys.stderr)
