@@ -26,20 +26,9 @@ namespace qm {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRowsPerWg = 16;   // S rows per scan workgroup (16 lanes per row)
-constexpr int kTokChunk = 32;    // tokens staged in LDS per scan iteration
-
-__device__ __forceinline__ float block_sum(float v, float* red) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-  const int wave = threadIdx.x >> 6;
-  __syncthreads();  // `red` may still be read from a previous call
-  if ((threadIdx.x & 63) == 0) red[wave] = v;
-  __syncthreads();
-  float s = 0.0f;
-  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) s += red[w];
-  return s;
-}
+constexpr int kLanesPerRow = 16;                   // lanes sharing one S row in the scan
+constexpr int kRowsPerWg = kThreads / kLanesPerRow;  // S rows per scan workgroup
+constexpr int kTokChunk = 32;                      // tokens staged in LDS per scan iteration
 
 // x(t) of channel ch: t >= 0 from this call's input, t < 0 from the history window.
 __device__ __forceinline__ float conv_input(const DnArgs& a, uint32_t ch, int t) {
@@ -61,37 +50,76 @@ __device__ __forceinline__ void shift_history(const DnArgs& a, uint32_t ch) {
     a.hist_out[(size_t)ch * hw + tap] = conv_input(a, ch, (int)a.M - hw + tap);
 }
 
-// grid: M * (KH + VH) blocks of 256 threads.
+// Sum over the 16 lanes of a DPP row: quad swaps, then rotations by 4 and 8
+// within the row; every lane ends with the total.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // quad [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // quad [2,3,0,1]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));  // row_ror:4
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
+  return v;
+}
+// Sum over the 64 lanes of a wave: the 16-lane rows, then the row pairs and
+// halves meet through v_permlane16_swap / v_permlane32_swap.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+// Sum over the lanes sharing one S row in the scan.
+__device__ __forceinline__ float row_sum(float v) {
+  static_assert(kLanesPerRow == 16, "one DPP row per S row");
+  return row16_sum(v);
+}
+
+// One wave per (token, unit); blocks of 1 or 4 waves (grid covers every item).
+// A key unit convolves its head's q and k channels and rms-normalises both
+// (wave reductions, no barriers); a value unit convolves its v channels.
 __global__ __launch_bounds__(kThreads) void dn_conv_prepare_kernel(DnArgs a) {
-  __shared__ float red[kThreads / 64];
   const uint32_t units = a.key_heads + a.value_heads;
-  const uint32_t t = blockIdx.x / units, u = blockIdx.x % units;
-  const uint32_t i = threadIdx.x;
+  const uint32_t item = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (item >= a.M * units) return;
+  const uint32_t t = item / units, u = item % units;
+  const uint32_t lane = threadIdx.x & 63;
   const uint32_t key_el = a.key_heads * a.dk;
   float* row = a.conv_out + (size_t)t * a.channels;
   const bool last = t + 1 == a.M && a.kernel > 1;
   if (u < a.key_heads) {
-    const uint32_t qc = u * a.dk + i, kc = key_el + u * a.dk + i;
-    const bool ok = i < a.dk;
-    const float cq = ok ? conv_silu(a, qc, (int)t) : 0.0f;
-    const float ck = ok ? conv_silu(a, kc, (int)t) : 0.0f;
-    const float qs = block_sum(cq * cq, red);
-    const float ks = block_sum(ck * ck, red);
+    float cq[4], ck[4];  // dk <= 256: channels lane + 64 i
+    float qs = 0.0f, ks = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = lane + 64 * i;
+      const bool ok = c < a.dk;
+      cq[i] = ok ? conv_silu(a, u * a.dk + c, (int)t) : 0.0f;
+      ck[i] = ok ? conv_silu(a, key_el + u * a.dk + c, (int)t) : 0.0f;
+      qs += cq[i] * cq[i];
+      ks += ck[i] * ck[i];
+    }
+    qs = wave_sum(qs);
+    ks = wave_sum(ks);
     const float inv = 1.0f / sqrtf((float)a.dk);
     const float qscale = 1.0f / sqrtf(qs / (float)a.dk + a.eps);
     const float kscale = 1.0f / sqrtf(ks / (float)a.dk + a.eps);
-    if (ok) {
-      row[qc] = cq * qscale * inv * inv;
-      row[kc] = ck * kscale * inv;
-      if (last) {
-        shift_history(a, qc);
-        shift_history(a, kc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = lane + 64 * i;
+      if (c < a.dk) {
+        const uint32_t qc = u * a.dk + c, kc = key_el + u * a.dk + c;
+        row[qc] = cq[i] * qscale * inv * inv;
+        row[kc] = ck[i] * kscale * inv;
+        if (last) {
+          shift_history(a, qc);
+          shift_history(a, kc);
+        }
       }
     }
   } else {
     const uint32_t vh = u - a.key_heads;
-    if (i < a.dv) {
-      const uint32_t ch = 2 * key_el + vh * a.dv + i;
+    for (uint32_t c = lane; c < a.dv; c += 64) {
+      const uint32_t ch = 2 * key_el + vh * a.dv + c;
       row[ch] = conv_silu(a, ch, (int)t);
       if (last) shift_history(a, ch);
     }
@@ -99,11 +127,19 @@ __global__ __launch_bounds__(kThreads) void dn_conv_prepare_kernel(DnArgs a) {
 }
 
 // grid: VH * ceil(dv / 16) blocks; thread (r = tid / 16, l = tid % 16) holds
-// S[row0 + r][l + 16 e] for e < EPT (EPT * 16 >= dk).
+// S[row0 + r][l + 16 e] for e < EPT (EPT * 16 >= dk).  Per token: two
+// 16-lane DPP reductions, k^ and q^ read as EPT contiguous floats per lane.
+// The next chunk of 32 tokens is fetched into registers while the current
+// one is scanned.
 template <int EPT>
 __global__ __launch_bounds__(kThreads) void dn_scan_kernel(DnArgs a) {
-  constexpr int kCols = 16 * EPT;
-  __shared__ float qk_s[kTokChunk][2][kCols];
+  constexpr int kCols = kLanesPerRow * EPT;
+  constexpr int kStage = kTokChunk * 2 * kCols / kThreads;  // k^/q^ floats per thread per chunk
+  constexpr int kVStage = kTokChunk * kRowsPerWg / kThreads;  // v floats per thread per chunk
+  static_assert(kStage * kThreads == kTokChunk * 2 * kCols && kVStage * kThreads == kTokChunk * kRowsPerWg,
+                "staging split");
+  // [token][q | k][lane][e]: lane l's EPT values are contiguous.
+  __shared__ __attribute__((aligned(16))) float qk_s[kTokChunk][2][kLanesPerRow][EPT];
   __shared__ float v_s[kTokChunk][kRowsPerWg];
   __shared__ float o_s[kTokChunk][kRowsPerWg];
   __shared__ float g_s[kTokChunk], beta_s[kTokChunk];
@@ -113,7 +149,7 @@ __global__ __launch_bounds__(kThreads) void dn_scan_kernel(DnArgs a) {
   const uint32_t row0 = (blockIdx.x % groups) * kRowsPerWg;
   const uint32_t kh = vh / (a.value_heads / a.key_heads);
   const uint32_t key_el = a.key_heads * a.dk;
-  const int r = threadIdx.x / 16, l = threadIdx.x % 16;
+  const int r = threadIdx.x / kLanesPerRow, l = threadIdx.x % kLanesPerRow;
   const uint32_t row = row0 + r;
   const bool row_ok = row < a.dv;
 
@@ -121,83 +157,153 @@ __global__ __launch_bounds__(kThreads) void dn_scan_kernel(DnArgs a) {
   const size_t srow = ((size_t)vh * a.dv + row) * a.dk;
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
-    const uint32_t j = l + 16 * e;
+    const uint32_t j = l + kLanesPerRow * e;
     s[e] = row_ok && j < a.dk ? a.s_in[srow + j] : 0.0f;
   }
   const float neg_a = -expf(a.a_log[vh]);
   const float dt_bias = a.dt_bias[vh];
 
-  for (uint32_t t0 = 0; t0 < a.M; t0 += kTokChunk) {
+  // Chunk staging registers: element p of thread t is flat index t + 256 p of
+  // [token][q | k][column] (coalesced global reads), v likewise over [token][row].
+  float qk_r[kStage], v_r[kVStage], a_r = 0.0f, b_r = 0.0f;
+  auto fetch = [&](uint32_t t0) __attribute__((always_inline)) {
     const uint32_t nt = min((uint32_t)kTokChunk, a.M - t0);
-    for (uint32_t idx = threadIdx.x; idx < kTokChunk * kCols; idx += kThreads) {
-      const uint32_t tt = idx / kCols, j = idx % kCols;
+#pragma unroll
+    for (int p = 0; p < kStage; ++p) {
+      const uint32_t idx = threadIdx.x + kThreads * p;
+      const uint32_t tt = idx / (2 * kCols), kind = (idx / kCols) & 1, j = idx % kCols;
       const bool ok = tt < nt && j < a.dk;
       const float* crow = a.conv_out + (size_t)(t0 + tt) * a.channels;
-      qk_s[tt][0][j] = ok ? crow[kh * a.dk + j] : 0.0f;
-      qk_s[tt][1][j] = ok ? crow[key_el + kh * a.dk + j] : 0.0f;
+      qk_r[p] = ok ? crow[(kind ? key_el : 0) + kh * a.dk + j] : 0.0f;
     }
-    for (uint32_t idx = threadIdx.x; idx < kTokChunk * kRowsPerWg; idx += kThreads) {
+#pragma unroll
+    for (int p = 0; p < kVStage; ++p) {
+      const uint32_t idx = threadIdx.x + kThreads * p;
       const uint32_t tt = idx / kRowsPerWg, rr = idx % kRowsPerWg;
       const bool ok = tt < nt && row0 + rr < a.dv;
-      v_s[tt][rr] = ok ? a.conv_out[(size_t)(t0 + tt) * a.channels + 2 * key_el + vh * a.dv + row0 + rr] : 0.0f;
+      v_r[p] = ok ? a.conv_out[(size_t)(t0 + tt) * a.channels + 2 * key_el + vh * a.dv + row0 + rr] : 0.0f;
     }
     if (threadIdx.x < nt) {
       const size_t ti = (size_t)(t0 + threadIdx.x) * a.value_heads + vh;
-      g_s[threadIdx.x] = expf(neg_a * softplus_f(a.a[ti] + dt_bias));
-      beta_s[threadIdx.x] = sigmoid_f(a.b[ti]);
+      a_r = a.a[ti];
+      b_r = a.b[ti];
     }
-    __syncthreads();
+  };
+  auto stage = [&](uint32_t t0) __attribute__((always_inline)) {
+    const uint32_t nt = min((uint32_t)kTokChunk, a.M - t0);
+#pragma unroll
+    for (int p = 0; p < kStage; ++p) {
+      const uint32_t idx = threadIdx.x + kThreads * p;
+      const uint32_t tt = idx / (2 * kCols), kind = (idx / kCols) & 1, j = idx % kCols;
+      qk_s[tt][kind][j % kLanesPerRow][j / kLanesPerRow] = qk_r[p];
+    }
+#pragma unroll
+    for (int p = 0; p < kVStage; ++p) {
+      const uint32_t idx = threadIdx.x + kThreads * p;
+      v_s[idx / kRowsPerWg][idx % kRowsPerWg] = v_r[p];
+    }
+    if (threadIdx.x < nt) {
+      g_s[threadIdx.x] = expf(neg_a * softplus_f(a_r + dt_bias));
+      beta_s[threadIdx.x] = sigmoid_f(b_r);
+    }
+  };
 
+  fetch(0);
+  stage(0);
+  __syncthreads();
+  for (uint32_t t0 = 0; t0 < a.M; t0 += kTokChunk) {
+    const uint32_t nt = min((uint32_t)kTokChunk, a.M - t0);
+    const bool more = t0 + kTokChunk < a.M;
+    if (more) fetch(t0 + kTokChunk);
+
+#pragma unroll 2
     for (uint32_t tt = 0; tt < nt; ++tt) {
       const float g = g_s[tt], beta = beta_s[tt];
-      float kv_mem = 0.0f;
+      float kk[EPT], qq[EPT];
+      if constexpr (EPT % 4 == 0) {
+#pragma unroll
+        for (int e4 = 0; e4 < EPT; e4 += 4) {
+          const floatx4 k4 = *(const floatx4*)&qk_s[tt][1][l][e4];
+          const floatx4 q4 = *(const floatx4*)&qk_s[tt][0][l][e4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            kk[e4 + i] = k4[i];
+            qq[e4 + i] = q4[i];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          kk[e] = qk_s[tt][1][l][e];
+          qq[e] = qk_s[tt][0][l][e];
+        }
+      }
+      float m0 = 0.0f, m1 = 0.0f;
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
         s[e] *= g;
-        kv_mem += s[e] * qk_s[tt][1][l + 16 * e];
+        if (e & 1)
+          m1 = fmaf(s[e], kk[e], m1);
+        else
+          m0 = fmaf(s[e], kk[e], m0);
       }
-#pragma unroll
-      for (int off = 8; off >= 1; off >>= 1) kv_mem += __shfl_xor(kv_mem, off);
+      const float kv_mem = row_sum(m0 + m1);
       const float delta = (v_s[tt][r] - kv_mem) * beta;
-      float acc = 0.0f;
+      float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
-        s[e] += qk_s[tt][1][l + 16 * e] * delta;
-        acc += s[e] * qk_s[tt][0][l + 16 * e];
+        s[e] = fmaf(kk[e], delta, s[e]);
+        if (e & 1)
+          a1 = fmaf(s[e], qq[e], a1);
+        else
+          a0 = fmaf(s[e], qq[e], a0);
       }
-#pragma unroll
-      for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+      const float acc = row_sum(a0 + a1);
       if (l == 0) o_s[tt][r] = acc;
     }
-    __syncthreads();
+    __syncthreads();  // every wave is done with this chunk's LDS
     for (uint32_t idx = threadIdx.x; idx < nt * kRowsPerWg; idx += kThreads) {
       const uint32_t tt = idx / kRowsPerWg, rr = idx % kRowsPerWg;
       if (row0 + rr < a.dv)
         a.out[(size_t)(t0 + tt) * a.value_heads * a.dv + vh * a.dv + row0 + rr] = o_s[tt][rr];
     }
-    // The next chunk's staging overwrites qk_s / v_s only after every wave
-    // passed the barrier above; o_s is rewritten after the next barrier.
+    if (more) {
+      stage(t0 + kTokChunk);
+      __syncthreads();
+    }
   }
 
   if (row_ok) {
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-      const uint32_t j = l + 16 * e;
+      const uint32_t j = l + kLanesPerRow * e;
       if (j < a.dk) a.s_out[srow + j] = s[e];
     }
   }
 }
 
-// grid: M * VH blocks of 256 threads; in place on `out`.
+// One wave per (token, value head), blocks of 1 or 4 waves; in place on `out`.
 __global__ __launch_bounds__(kThreads) void dn_gate_norm_kernel(DnArgs a) {
-  __shared__ float red[kThreads / 64];
-  const uint32_t i = threadIdx.x;
-  float* o = a.out + (size_t)blockIdx.x * a.dv;
-  const float* z = a.z + (size_t)blockIdx.x * a.dv;
-  const float v = i < a.dv ? o[i] : 0.0f;
-  const float ss = block_sum(v * v, red);
+  const uint32_t item = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (item >= a.M * a.value_heads) return;
+  const uint32_t lane = threadIdx.x & 63;
+  float* o = a.out + (size_t)item * a.dv;
+  const float* z = a.z + (size_t)item * a.dv;
+  float v[4];  // dv <= 256
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t c = lane + 64 * i;
+    v[i] = c < a.dv ? o[c] : 0.0f;
+    ss += v[i] * v[i];
+  }
+  ss = wave_sum(ss);
   const float scale = 1.0f / sqrtf(ss / (float)a.dv + a.eps);
-  if (i < a.dv) o[i] = v * scale * a.norm[i] * silu_f(z[i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t c = lane + 64 * i;
+    if (c < a.dv) o[c] = v[i] * scale * a.norm[c] * silu_f(z[c]);
+  }
 }
 
 template <int EPT>
@@ -210,9 +316,11 @@ void launch_scan(const DnArgs& a, hipStream_t st) {
 
 hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
   if (a.dk == 0 || a.dk > 256 || a.dv == 0 || a.dv > 256 || a.M == 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(dn_conv_prepare_kernel, dim3(a.M * (a.key_heads + a.value_heads)), dim3(kThreads), 0, st,
-                     a);
-  const uint32_t ept = (a.dk + 15) / 16;
+  // Few items (decode): one wave per block so they spread over more CUs.
+  const uint32_t prep_items = a.M * (a.key_heads + a.value_heads);
+  const uint32_t wpb = prep_items >= 1024 ? kThreads / 64 : 1;
+  hipLaunchKernelGGL(dn_conv_prepare_kernel, dim3((prep_items + wpb - 1) / wpb), dim3(64 * wpb), 0, st, a);
+  const uint32_t ept = (a.dk + kLanesPerRow - 1) / kLanesPerRow;
   if (ept <= 1)
     launch_scan<1>(a, st);
   else if (ept <= 2)
@@ -223,7 +331,8 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
     launch_scan<8>(a, st);
   else
     launch_scan<16>(a, st);
-  hipLaunchKernelGGL(dn_gate_norm_kernel, dim3(a.M * a.value_heads), dim3(kThreads), 0, st, a);
+  const uint32_t norm_items = a.M * a.value_heads;
+  hipLaunchKernelGGL(dn_gate_norm_kernel, dim3((norm_items + wpb - 1) / wpb), dim3(64 * wpb), 0, st, a);
   return hipGetLastError();
 }
 
