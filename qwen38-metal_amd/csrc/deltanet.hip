@@ -74,6 +74,34 @@ __device__ __forceinline__ float row_sum(float v) {
   return row16_sum(v);
 }
 
+// q^ and k^ of key head kh at token t, computed by one wave: lane holds
+// channels c = lane + 64 i (i < 4; dk <= 256).  Shared by the prefill path
+// and the fused step so both round identically.
+__device__ __forceinline__ void prep_key_head(const DnArgs& a, uint32_t t, uint32_t kh, uint32_t lane, float (&qo)[4],
+                                              float (&ko)[4]) {
+  const uint32_t key_el = a.key_heads * a.dk;
+  float qs = 0.0f, ks = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t c = lane + 64 * i;
+    const bool ok = c < a.dk;
+    qo[i] = ok ? conv_silu(a, kh * a.dk + c, (int)t) : 0.0f;
+    ko[i] = ok ? conv_silu(a, key_el + kh * a.dk + c, (int)t) : 0.0f;
+    qs += qo[i] * qo[i];
+    ks += ko[i] * ko[i];
+  }
+  qs = wave_sum(qs);
+  ks = wave_sum(ks);
+  const float inv = 1.0f / sqrtf((float)a.dk);
+  const float qscale = 1.0f / sqrtf(qs / (float)a.dk + a.eps);
+  const float kscale = 1.0f / sqrtf(ks / (float)a.dk + a.eps);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    qo[i] = qo[i] * qscale * inv * inv;
+    ko[i] = ko[i] * kscale * inv;
+  }
+}
+
 // One wave per (token, unit); blocks of 1 or 4 waves (grid covers every item).
 // A key unit convolves its head's q and k channels and rms-normalises both
 // (wave reductions, no barriers); a value unit convolves its v channels.
@@ -87,29 +115,15 @@ __global__ __launch_bounds__(kThreads) void dn_conv_prepare_kernel(DnArgs a) {
   float* row = a.conv_out + (size_t)t * a.channels;
   const bool last = t + 1 == a.M && a.kernel > 1;
   if (u < a.key_heads) {
-    float cq[4], ck[4];  // dk <= 256: channels lane + 64 i
-    float qs = 0.0f, ks = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t c = lane + 64 * i;
-      const bool ok = c < a.dk;
-      cq[i] = ok ? conv_silu(a, u * a.dk + c, (int)t) : 0.0f;
-      ck[i] = ok ? conv_silu(a, key_el + u * a.dk + c, (int)t) : 0.0f;
-      qs += cq[i] * cq[i];
-      ks += ck[i] * ck[i];
-    }
-    qs = wave_sum(qs);
-    ks = wave_sum(ks);
-    const float inv = 1.0f / sqrtf((float)a.dk);
-    const float qscale = 1.0f / sqrtf(qs / (float)a.dk + a.eps);
-    const float kscale = 1.0f / sqrtf(ks / (float)a.dk + a.eps);
+    float cq[4], ck[4];
+    prep_key_head(a, t, u, lane, cq, ck);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t c = lane + 64 * i;
       if (c < a.dk) {
         const uint32_t qc = u * a.dk + c, kc = key_el + u * a.dk + c;
-        row[qc] = cq[i] * qscale * inv * inv;
-        row[kc] = ck[i] * kscale * inv;
+        row[qc] = cq[i];
+        row[kc] = ck[i];
         if (last) {
           shift_history(a, qc);
           shift_history(a, kc);
@@ -124,6 +138,35 @@ __global__ __launch_bounds__(kThreads) void dn_conv_prepare_kernel(DnArgs a) {
       if (last) shift_history(a, ch);
     }
   }
+}
+
+// One token of the delta rule on the EPT-element segment of one S row that a
+// lane holds (lane l: columns l + 16 e): returns o = S q^ for the row (all
+// 16 lanes of the row get it).  Shared by the scan and the fused step.
+template <int EPT>
+__device__ __forceinline__ float delta_row_token(float (&s)[EPT], const float (&kk)[EPT], const float (&qq)[EPT],
+                                                 float g, float beta, float v) {
+  float m0 = 0.0f, m1 = 0.0f;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    s[e] *= g;
+    if (e & 1)
+      m1 = fmaf(s[e], kk[e], m1);
+    else
+      m0 = fmaf(s[e], kk[e], m0);
+  }
+  const float kv_mem = row_sum(m0 + m1);
+  const float delta = (v - kv_mem) * beta;
+  float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    s[e] = fmaf(kk[e], delta, s[e]);
+    if (e & 1)
+      a1 = fmaf(s[e], qq[e], a1);
+    else
+      a0 = fmaf(s[e], qq[e], a0);
+  }
+  return row_sum(a0 + a1);
 }
 
 // grid: VH * ceil(dv / 16) blocks; thread (r = tid / 16, l = tid % 16) holds
@@ -238,27 +281,7 @@ __global__ __launch_bounds__(kThreads) void dn_scan_kernel(DnArgs a) {
           qq[e] = qk_s[tt][0][l][e];
         }
       }
-      float m0 = 0.0f, m1 = 0.0f;
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        s[e] *= g;
-        if (e & 1)
-          m1 = fmaf(s[e], kk[e], m1);
-        else
-          m0 = fmaf(s[e], kk[e], m0);
-      }
-      const float kv_mem = row_sum(m0 + m1);
-      const float delta = (v_s[tt][r] - kv_mem) * beta;
-      float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        s[e] = fmaf(kk[e], delta, s[e]);
-        if (e & 1)
-          a1 = fmaf(s[e], qq[e], a1);
-        else
-          a0 = fmaf(s[e], qq[e], a0);
-      }
-      const float acc = row_sum(a0 + a1);
+      const float acc = delta_row_token<EPT>(s, kk, qq, g, beta, v_s[tt][r]);
       if (l == 0) o_s[tt][r] = acc;
     }
     __syncthreads();  // every wave is done with this chunk's LDS
@@ -282,19 +305,17 @@ __global__ __launch_bounds__(kThreads) void dn_scan_kernel(DnArgs a) {
   }
 }
 
-// One wave per (token, value head), blocks of 1 or 4 waves; in place on `out`.
-__global__ __launch_bounds__(kThreads) void dn_gate_norm_kernel(DnArgs a) {
-  const uint32_t item = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (item >= a.M * a.value_heads) return;
-  const uint32_t lane = threadIdx.x & 63;
-  float* o = a.out + (size_t)item * a.dv;
-  const float* z = a.z + (size_t)item * a.dv;
+// Gated RMS norm of one (token, value head) output row by one wave: reads
+// o_in[c], writes out[c] = o * rsqrt(mean o^2 + eps) * norm * silu(z).
+// Shared by the prefill path and the fused step.
+__device__ __forceinline__ void gate_norm_row(const DnArgs& a, const float* o_in, const float* z, float* out,
+                                              uint32_t lane) {
   float v[4];  // dv <= 256
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t c = lane + 64 * i;
-    v[i] = c < a.dv ? o[c] : 0.0f;
+    v[i] = c < a.dv ? o_in[c] : 0.0f;
     ss += v[i] * v[i];
   }
   ss = wave_sum(ss);
@@ -302,7 +323,104 @@ __global__ __launch_bounds__(kThreads) void dn_gate_norm_kernel(DnArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t c = lane + 64 * i;
-    if (c < a.dv) o[c] = v[i] * scale * a.norm[c] * silu_f(z[c]);
+    if (c < a.dv) out[c] = v[i] * scale * a.norm[c] * silu_f(z[c]);
+  }
+}
+
+// One wave per (token, value head), blocks of 1 or 4 waves; in place on `out`.
+__global__ __launch_bounds__(kThreads) void dn_gate_norm_kernel(DnArgs a) {
+  const uint32_t item = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (item >= a.M * a.value_heads) return;
+  float* o = a.out + (size_t)item * a.dv;
+  gate_norm_row(a, o, a.z + (size_t)item * a.dv, o, threadIdx.x & 63);
+}
+
+// The whole decode step (M = 1) in one launch: block = value head vh.
+//  wave 0: q^, k^ of key head kh (prep_key_head); wave 1: conv of vh's v
+//  channels; thread 128: g and beta.  Then the 16-lane row groups update the
+//  dv rows of S in DV / 16 passes (delta_row_token), and wave 0 applies the
+//  gated norm (gate_norm_row).  The arithmetic is the three-launch path's,
+//  call for call, so a step equals a one-token prefill bit for bit.
+template <int EPT, int PASSES>
+__global__ __launch_bounds__(kThreads) void dn_step_kernel(DnArgs a) {
+  __shared__ __attribute__((aligned(16))) float qk_s[2][16][EPT];  // [q | k][lane][e]
+  __shared__ float v_s[16 * PASSES], o_s[16 * PASSES];
+  __shared__ float gb_s[2];
+  const uint32_t vh = blockIdx.x;
+  const uint32_t group = a.value_heads / a.key_heads;
+  const uint32_t kh = vh / group;
+  const uint32_t key_el = a.key_heads * a.dk;
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // The first value head of a key group also writes that key head's history.
+  const bool key_hist = vh % group == 0 && a.kernel > 1;
+
+  // S rows of this block: pass p, row 16 p + r, columns l + 16 e.
+  const int r = threadIdx.x / 16, l = threadIdx.x % 16;
+  float s[PASSES][EPT];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const uint32_t row = 16 * p + r;
+    const size_t srow = ((size_t)vh * a.dv + row) * a.dk;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const uint32_t j = l + 16 * e;
+      s[p][e] = row < a.dv && j < a.dk ? a.s_in[srow + j] : 0.0f;
+    }
+  }
+
+  if (wave == 0) {
+    float cq[4], ck[4];
+    prep_key_head(a, 0, kh, lane, cq, ck);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = lane + 64 * i;
+      if (c < 16 * EPT) {
+        qk_s[0][c % 16][c / 16] = c < a.dk ? cq[i] : 0.0f;
+        qk_s[1][c % 16][c / 16] = c < a.dk ? ck[i] : 0.0f;
+      }
+      if (c < a.dk && key_hist) {
+        shift_history(a, kh * a.dk + c);
+        shift_history(a, key_el + kh * a.dk + c);
+      }
+    }
+  } else if (wave == 1) {
+    for (uint32_t c = lane; c < 16 * PASSES; c += 64) {
+      const uint32_t ch = 2 * key_el + vh * a.dv + c;
+      v_s[c] = c < a.dv ? conv_silu(a, ch, 0) : 0.0f;
+      if (c < a.dv && a.kernel > 1) shift_history(a, ch);
+    }
+  } else if (threadIdx.x == 128) {
+    const float neg_a = -expf(a.a_log[vh]);
+    gb_s[0] = expf(neg_a * softplus_f(a.a[vh] + a.dt_bias[vh]));
+    gb_s[1] = sigmoid_f(a.b[vh]);
+  }
+  __syncthreads();
+
+  float kk[EPT], qq[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    kk[e] = qk_s[1][l][e];
+    qq[e] = qk_s[0][l][e];
+  }
+  const float g = gb_s[0], beta = gb_s[1];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const uint32_t row = 16 * p + r;
+    const float o = delta_row_token<EPT>(s[p], kk, qq, g, beta, v_s[row]);
+    if (l == 0) o_s[row] = o;
+    if (row < a.dv) {
+      const size_t srow = ((size_t)vh * a.dv + row) * a.dk;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const uint32_t j = l + 16 * e;
+        if (j < a.dk) a.s_out[srow + j] = s[p][e];
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float* out = a.out + (size_t)vh * a.dv;
+    gate_norm_row(a, o_s, a.z + (size_t)vh * a.dv, out, lane);
   }
 }
 
@@ -316,6 +434,20 @@ void launch_scan(const DnArgs& a, hipStream_t st) {
 
 hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
   if (a.dk == 0 || a.dk > 256 || a.dv == 0 || a.dv > 256 || a.M == 0) return hipErrorInvalidValue;
+  // One token with S rows that fit the fused kernel's registers: one launch.
+  if (a.M == 1 && a.dk <= 128 && a.dv <= 128) {
+    const dim3 grid(a.value_heads), block(kThreads);
+    const uint32_t ept = (a.dk + 15) / 16, passes = (a.dv + 15) / 16;
+    if (ept <= 4 && passes <= 4)
+      hipLaunchKernelGGL((dn_step_kernel<4, 4>), grid, block, 0, st, a);
+    else if (ept <= 4)
+      hipLaunchKernelGGL((dn_step_kernel<4, 8>), grid, block, 0, st, a);
+    else if (passes <= 4)
+      hipLaunchKernelGGL((dn_step_kernel<8, 4>), grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((dn_step_kernel<8, 8>), grid, block, 0, st, a);
+    return hipGetLastError();
+  }
   // Few items (decode): one wave per block so they spread over more CUs.
   const uint32_t prep_items = a.M * (a.key_heads + a.value_heads);
   const uint32_t wpb = prep_items >= 1024 ? kThreads / 64 : 1;
