@@ -63,9 +63,10 @@ struct DecodeArgs {
 };
 
 // DMA entries per tile of the scale/bias table (16 bytes = 8 groups, or one
-// group per 4-byte LDS word), padded to whole 64-lane instructions.
+// group per 4-byte LDS word).  Exact: the last DMA instruction of a table runs
+// with the lanes past its end masked off, so they write no LDS.
 __host__ __device__ constexpr uint32_t sb_tile_entries(bool sb16, uint32_t gps) {
-  return ((16 * (sb16 ? gps / 8 : gps) + 63) / 64) * 64;
+  return 16 * (sb16 ? gps / 8 : gps);
 }
 // LDS bytes per staged activation row of one wave's K slice: the slice's
 // groups (rounded up to whole iterations) plus 16 bytes, so the rows read by
@@ -259,9 +260,9 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const int q = SWIGLU ? t / kHalf : 0;
-        for (uint32_t i = 0; i < pad / 64; ++i) {
-          uint32_t e = i * 64 + lane;
-          e = e < per_tile ? e : per_tile - 1;
+        for (uint32_t i = 0; i < (per_tile + 63) / 64; ++i) {
+          const uint32_t e = i * 64 + lane;
+          if (e >= per_tile) continue;
           const uint32_t row = e / cols;
           const uint32_t col = e - row * cols;
           const uint32_t r = row_base + 16u * (t % kHalf) + row;

@@ -512,17 +512,35 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
     wait_vmcnt<0>();
     __syncthreads();
   }
-  // Page ids are wave-uniform scalar loads (lgkmcnt), never vector loads
-  // whose vmcnt wait would drain the DMA ring.  The table is read through the
-  // constant address space: the only entries this kernel writes are pages
-  // materialised by this call, whose ids page_id() computes without a read.
+  // Physical ids of this wave's first 64 pages, lane j holding page j, read
+  // once before any DMA and taken with v_readlane at issue time.  A scalar
+  // load per refill would leave an SMEM access outstanding, and since SMEM
+  // returns out of order every later LDS read would wait for it (lgkmcnt(0)):
+  // one memory round trip per ring step.  Pages beyond the 64th (splits over
+  // 256 pages) fall back to scalar loads through the constant address space.
+  // The only table entries this kernel writes are pages materialised by this
+  // call, whose ids are computed without a read.
   const __attribute__((address_space(4))) int32_t* pt_s =
       (const __attribute__((address_space(4))) int32_t*)sq.pt;
-  auto issue = [&](uint32_t j, int slot_idx) {
+  auto phys_of = [&](uint32_t p) __attribute__((always_inline)) {
+    return sq.new_page_count > 0 && (int32_t)p >= sq.new_page_first ? sq.new_page_id + ((int32_t)p - sq.new_page_first)
+                                                                     : -1;
+  };
+  int32_t ids_v;
+  {
+    const uint32_t p = first + kWaves * (uint32_t)lane;
+    const int32_t fresh = phys_of(p);
+    ids_v = (uint32_t)lane < n_mine && fresh < 0 ? sq.pt[p] : fresh;
+  }
+  auto issue = [&](uint32_t j, int slot_idx) __attribute__((always_inline)) {
     const uint32_t p = first + kWaves * j;
-    const int32_t phys = sq.new_page_count > 0 && (int32_t)p >= sq.new_page_first
-                             ? sq.new_page_id + ((int32_t)p - sq.new_page_first)
-                             : pt_s[p];
+    int32_t phys;
+    if (j < 64) {
+      phys = __builtin_amdgcn_readlane(ids_v, (int)j);
+    } else {
+      const int32_t fresh = phys_of(p);
+      phys = fresh >= 0 ? fresh : pt_s[p];
+    }
     uint8_t* dst = ring + slot_idx * L::kPage;
     const size_t pbase = (size_t)phys * kv_page_stride;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(sq.k + pbase + (size_t)kvh * 16 * D, 16 * D);
@@ -621,6 +639,16 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   // Pages issued so far land in ring slots in order; a pair (i, i+1) needs
   // every DMA up to page i+1 complete: vmcnt <= (pages issued after it) *
   // kDmaPerPage.
+  // Q rows are loaded before the first page DMAs so that waiting for them
+  // does not wait for the pages (vmcnt retires in order).
+  u32x4 qraw[kKS];
+  {
+    const uint16_t* qp = args.q + ((size_t)b * H + head) * D;
+#pragma unroll
+    for (int jj = 0; jj < kKS; ++jj)
+      qraw[jj] = col_ok ? *(const u32x4*)(qp + D / 4 * kq + 8 * jj) : u32x4{0u, 0u, 0u, 0u};
+  }
+  __builtin_amdgcn_sched_barrier(0);
   const uint32_t pre = min(n_mine, (uint32_t)kRing);
   for (uint32_t i = 0; i < pre; ++i) issue(i, i);
   uint32_t issued = pre;
@@ -629,10 +657,9 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   // unpack of K produces.  bf16 -> fp16 is exact within fp16's range.
   {
     float qsum = 0.0f;
-    const uint16_t* qp = args.q + ((size_t)b * H + head) * D;
 #pragma unroll
     for (int jj = 0; jj < kKS; ++jj) {
-      const u32x4 v = col_ok ? *(const u32x4*)(qp + D / 4 * kq + 8 * jj) : u32x4{0u, 0u, 0u, 0u};
+      const u32x4 v = qraw[jj];
       float f[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {

@@ -235,6 +235,29 @@ def test_decode_ragged_batch(rt, torch_dev, D, H, KVH, pps):
         _check_cache(c, m)
 
 
+@pytest.mark.parametrize("D,H,KVH", [(128, 64, 8), (64, 8, 8)])
+def test_decode_long_split_page_ids(rt, torch_dev, D, H, KVH):
+    """Splits of 320 pages give each wave 80 pages: the first 64 ids come from
+    the per-wave id vector, the rest (including the page this step
+    materialises, page 620 = wave 0's 76th page of split 1) from scalar loads."""
+    rng = np.random.default_rng(D + H)
+    n = 620 * 16
+    cache = rt.create_q8_kv_state(KVH, D, n + 64)
+    mirror = Mirror(KVH, D)
+    _fill(rt, torch_dev, cache, mirror, rng, n, H, KVH, D)
+    os.environ["QM38_ATTN_PPS"] = "320"
+    try:
+        for it in range(2):
+            q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, 1, H, KVH, D, gate=(it == 1))
+            got = _decode(rt, torch_dev, [cache], q_bits, g_bits, k, v, H)
+            mirror.append(k[0], v[0])
+            ref = mirror.reference(q_f, g_f, mirror.k.shape[0] - 1)
+            assert_bf16_close(got, ref, what=f"len {mirror.k.shape[0]} it {it}")
+    finally:
+        os.environ.pop("QM38_ATTN_PPS", None)
+    _check_cache(cache, mirror)
+
+
 @pytest.mark.parametrize("D,H,KVH", [(256, 24, 4), (128, 64, 8), (128, 16, 2), (64, 4, 4), (256, 16, 1)])
 @pytest.mark.parametrize("start,M", [(0, 1), (0, 5), (0, 16), (0, 77), (13, 40), (32, 33), (200, 300)])
 def test_prefill_matches_oracle(rt, torch_dev, D, H, KVH, start, M):
