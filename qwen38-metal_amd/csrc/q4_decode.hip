@@ -35,7 +35,12 @@
 #include "common.h"
 #include "internal.h"
 
+#include <stdio.h>
 #include <stdlib.h>
+
+#include <algorithm>
+#include <cstring>
+#include <mutex>
 
 namespace qm {
 namespace {
@@ -58,6 +63,7 @@ struct DecodeArgs {
   uint32_t G;        // groups per row = K / 64
   uint32_t gps;      // groups per wave slice (multiple of 4)
   uint32_t x_bytes;  // LDS bytes of one wave's staged activations (0: register path)
+  uint32_t rpw;      // rows per workgroup and projection (<= 16 * tiles per projection)
   uint32_t n_jobs;
   Q4Job jobs[kMaxQ4Jobs];  // tile_begin: first tile set (workgroup) of the job
 };
@@ -164,20 +170,25 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
   if (!SWIGLU) {
     while (j + 1 < (int)args.n_jobs && tile >= args.jobs[j + 1].tile_begin) ++j;
   }
-  const uint32_t row_base = (tile - args.jobs[j].tile_begin) * 16u * kHalf;
+  const uint32_t row_base = (tile - args.jobs[j].tile_begin) * args.rpw;
   const uint32_t K = args.K;
   const uint32_t G = args.G;
   const uint32_t row_bytes = K >> 1;
 
+  // The workgroup owns rows [row_base, row_base + n_valid) of each projection
+  // (the gate and up pair share them).  Its buffer resources start at
+  // row_base and end after n_valid rows, so the lanes of the remaining rows of
+  // its 16-row tiles load zeros without touching memory.
   __amdgpu_buffer_rsrc_t rw[kJobs], rs[kJobs], rb[kJobs];
   uint32_t rows_j[kJobs];
+  const uint32_t n_valid = min(args.rpw, args.jobs[SWIGLU ? 0 : j].rows - row_base);
 #pragma unroll
   for (int q = 0; q < kJobs; ++q) {
     const Q4Job& jb = args.jobs[SWIGLU ? q : j];
     rows_j[q] = jb.rows;
-    rw[q] = make_rsrc(jb.w, (uint64_t)jb.rows * row_bytes);
-    rs[q] = make_rsrc(jb.s, (uint64_t)jb.rows * G * 2);
-    rb[q] = make_rsrc(jb.b, (uint64_t)jb.rows * G * 2);
+    rw[q] = make_rsrc(jb.w + (size_t)row_base * (row_bytes / 4), (uint64_t)n_valid * row_bytes);
+    rs[q] = make_rsrc(jb.s + (size_t)row_base * G, (uint64_t)n_valid * G * 2);
+    rb[q] = make_rsrc(jb.b + (size_t)row_base * G, (uint64_t)n_valid * G * 2);
   }
 
   const uint32_t g_begin = wave * gps;
@@ -202,15 +213,10 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
   uint32_t row_of[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    const int q = SWIGLU ? t / kHalf : 0;
-    const uint32_t base = row_base + 16u * (t % kHalf);
+    const uint32_t base = 16u * (t % kHalf);  // local to the workgroup's rows
     row_of[t] = base + nl;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t r = base + 8 * h + lrow;
-      const uint32_t rc = r < rows_j[q] ? r : rows_j[q] - 1;
-      vw[t][h] = rc * row_bytes + 16 * lchunk;
-    }
+    for (int h = 0; h < 2; ++h) vw[t][h] = (base + 8 * h + lrow) * row_bytes + 16 * lchunk;
   }
   const uint32_t wst = lrow * 128 + 16 * (lchunk ^ (lrow & 7));  // transpose-buffer store offset
 
@@ -265,8 +271,7 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
           if (e >= per_tile) continue;
           const uint32_t row = e / cols;
           const uint32_t col = e - row * cols;
-          const uint32_t r = row_base + 16u * (t % kHalf) + row;
-          const uint32_t rc = r < rows_j[q] ? r : rows_j[q] - 1;
+          const uint32_t rc = 16u * (t % kHalf) + row;  // local row; past n_valid loads zeros
           if (SB16) {
             const uint32_t off = (rc * G + g_begin + col * 8) * 2;
             dma16(rs[q], s_tab + (t * pad + i * 64) * 16, off, 0);
@@ -439,15 +444,15 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
     if (SWIGLU) {
 #pragma unroll
       for (int t = 0; t < kHalf; ++t)
-        if (row_of[t] < rows_j[0]) {
+        if (row_of[t] < n_valid) {
           const float h = silu_f(acc[t][rr]) * acc[t + kHalf][rr];
-          args.jobs[0].out[(size_t)m * rows_j[0] + row_of[t]] = f32_to_bf16(h);
+          args.jobs[0].out[(size_t)m * rows_j[0] + row_base + row_of[t]] = f32_to_bf16(h);
         }
     } else {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        if (row_of[t] < rows_j[0])
-          args.jobs[j].out[(size_t)m * rows_j[0] + row_of[t]] = f32_to_bf16(acc[t][rr]);
+        if (row_of[t] < n_valid)
+          args.jobs[j].out[(size_t)m * rows_j[0] + row_base + row_of[t]] = f32_to_bf16(acc[t][rr]);
     }
   }
 }
@@ -457,83 +462,144 @@ int env_int(const char* name, int fallback) {
   return v ? atoi(v) : fallback;
 }
 
+// Kernel instance for the template parameters a plan selects.
+template <int NT, int R, bool SW>
+const void* instance_of(bool sb16, bool xw) {
+  if (xw) return sb16 ? (const void*)q4_decode_kernel<NT, R, SW, true, true>
+                      : (const void*)q4_decode_kernel<NT, R, SW, false, true>;
+  return sb16 ? (const void*)q4_decode_kernel<NT, R, SW, true, false>
+              : (const void*)q4_decode_kernel<NT, R, SW, false, false>;
+}
+template <int NT, bool SW>
+const void* instance_m(uint32_t M, bool sb16, bool xw) {
+  if (M == 1) return instance_of<NT, 1, SW>(sb16, xw);
+  if (M == 2) return instance_of<NT, 2, SW>(sb16, xw);
+  return instance_of<NT, 4, SW>(sb16, xw);
+}
+
 struct Plan {
+  const void* fn;
   int nt;
-  uint32_t tiles, waves, gps, lds, x_bytes;
-  bool sb16;
+  uint32_t tiles, waves, gps, lds, x_bytes, rpw;
 };
 
-// Work decomposition: workgroups own 16*NT rows (a gate/up pair of 16 rows in
-// SwiGLU mode); their waves split K.  HBM throughput here is set by the bytes
-// in flight, so the split aims at about `target` resident waves.
+// Work decomposition.  A workgroup owns `rpw` rows of each projection (at most
+// its 16-row tiles: 16 * NT, or a gate/up pair of 16 in SwiGLU mode); its
+// waves split K.
+//  * HBM throughput is set by the bytes in flight, so the K split aims at
+//    about `target` resident waves.
+//  * All workgroups should be resident at once: a second dispatch round
+//    starts only when the first drains.  The wave count is lowered until the
+//    occupancy query says they fit.
+//  * The busiest CU sets the time.  With whole 16-row tiles, tile counts just
+//    above a multiple of the CU count leave some CUs one workgroup more than
+//    others (320 tiles on 256 CUs: a quarter of the CUs carry twice the rows).
+//    Fewer rows per workgroup can spread the rows more evenly; the masked rows
+//    of a tile cost arithmetic on zeros but no memory traffic.  Each candidate
+//    is scored by the rows on the busiest CU, with rounds past the first
+//    weighted by a quarter.
 Plan make_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M) {
-  Plan p{};
+  Plan best{};
   const uint32_t G = K / 64;
   uint64_t rows = 0;
   for (int i = 0; i < n_jobs; ++i) rows += jobs[i].rows;
   const uint32_t cus = (uint32_t)env_int("QM38_CUS", 256);
-  p.nt = swiglu ? 2 : ((rows / 32 >= (uint64_t)cus * 2) ? 2 : 1);
-  if (!swiglu && env_int("QM38_Q4_NT", 0) > 0) p.nt = env_int("QM38_Q4_NT", 1) >= 2 ? 2 : 1;
-  const uint32_t rows_per_set = swiglu ? 16u : 16u * p.nt;
-  p.tiles = 0;
-  if (swiglu) {
-    p.tiles = (jobs[0].rows + rows_per_set - 1) / rows_per_set;
-  } else {
-    for (int i = 0; i < n_jobs; ++i) p.tiles += (jobs[i].rows + rows_per_set - 1) / rows_per_set;
-  }
+  int nt = swiglu ? 2 : ((rows / 32 >= (uint64_t)cus * 2) ? 2 : 1);
+  if (!swiglu && env_int("QM38_Q4_NT", 0) > 0) nt = env_int("QM38_Q4_NT", 1) >= 2 ? 2 : 1;
   // Staged activations when all M rows fit (each wave holds its K slice).
   const bool xw = M * (K * 2 + 16) <= kXStageMax && env_int("QM38_Q4_XSTAGE", 1) != 0;
   const bool g8 = (G % 8) == 0;
-  const uint32_t step = 4 * ring_depth(p.nt, xw);  // whole ring rounds per slice (also a multiple of 8)
+  const void* fn = swiglu ? instance_m<2, true>(M, g8, xw)
+                          : (nt == 2 ? instance_m<2, false>(M, g8, xw) : instance_m<1, false>(M, g8, xw));
+  const uint32_t step = 4 * ring_depth(nt, xw);  // whole ring rounds per slice (also a multiple of 8)
   const uint32_t lds_cu = 160 * 1024;
   const uint32_t target = (uint32_t)env_int("QM38_Q4_TARGET_WAVES", (int)(cus * 16));
-  uint32_t waves = (target + p.tiles - 1) / p.tiles;
-  if (env_int("QM38_Q4_SPLIT", 0) > 0) waves = (uint32_t)env_int("QM38_Q4_SPLIT", 1);
-  waves = waves < 1 ? 1 : (waves > (uint32_t)kMaxWaves ? (uint32_t)kMaxWaves : waves);
-  // Fewer, longer slices lower the total LDS (fixed per-wave buffers); the
-  // wave count only decreases, so the search ends.
-  for (int guard = 0; guard < 64; ++guard) {
-    uint32_t gps = (G + waves - 1) / waves;
-    gps = (gps + step - 1) / step * step;
-    const uint32_t w = (G + gps - 1) / gps;
-    p.gps = gps;
-    p.waves = w;
-    p.x_bytes = xw ? M * x_slice_pitch(gps) : 0;
-    p.lds = w * wave_layout(p.nt, g8, gps, p.x_bytes).total;
-    if (p.lds <= lds_cu / 2 || w == 1) break;
-    waves = w - 1;
+  const uint32_t r_max = 16u * (swiglu ? 1u : (uint32_t)nt);
+  // Masked rows still cost arithmetic and activation staging: measured on the
+  // BASELINE shapes, workgroups below 13/16 of their tiles lose more than the
+  // balance gains.
+  uint32_t r_hi = r_max, r_lo = (13 * r_max + 15) / 16;
+  if (env_int("QM38_Q4_RPW", 0) > 0) r_hi = r_lo = std::min<uint32_t>(r_max, (uint32_t)env_int("QM38_Q4_RPW", 16));
+  double best_cost = 0.0;
+  for (uint32_t r = r_hi; r >= r_lo && r > 0; --r) {
+    Plan p{};
+    p.fn = fn;
+    p.nt = nt;
+    p.rpw = r;
+    for (int i = 0; i < (swiglu ? 1 : n_jobs); ++i) p.tiles += (jobs[i].rows + r - 1) / r;
+    uint32_t waves = (target + p.tiles - 1) / p.tiles;
+    if (env_int("QM38_Q4_SPLIT", 0) > 0) waves = (uint32_t)env_int("QM38_Q4_SPLIT", 1);
+    waves = std::max<uint32_t>(1, std::min<uint32_t>(waves, kMaxWaves));
+    int occ = 0;
+    for (;;) {
+      uint32_t gps = (G + waves - 1) / waves;
+      gps = (gps + step - 1) / step * step;
+      const uint32_t w = (G + gps - 1) / gps;
+      p.gps = gps;
+      p.waves = w;
+      p.x_bytes = xw ? M * x_slice_pitch(gps) : 0;
+      p.lds = w * wave_layout(nt, g8, gps, p.x_bytes).total;
+      // The final cross-wave reduction reuses the LDS from offset 0.
+      p.lds = std::max<uint32_t>(p.lds, w * nt * 4 * 64 * 4);
+      occ = 0;
+      if (p.lds <= lds_cu &&
+          hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, (int)(64 * w), p.lds) != hipSuccess)
+        occ = 0;
+      if (w == 1 || (occ > 0 && p.tiles <= (uint32_t)occ * cus)) break;
+      waves = w - 1;  // fewer, longer slices: less LDS per workgroup, fewer waves
+    }
+    if (occ <= 0) continue;
+    const uint32_t rounds = (p.tiles + (uint32_t)occ * cus - 1) / ((uint32_t)occ * cus);
+    const double cost = (double)((p.tiles + cus - 1) / cus) * r * (1.0 + 0.25 * (rounds - 1));
+    if (!best.fn || cost < best_cost) {
+      best = p;
+      best_cost = cost;
+    }
   }
-  // The final cross-wave reduction reuses the LDS from offset 0.
-  const uint32_t red_bytes = p.waves * p.nt * 4 * 64 * 4;
-  if (p.lds < red_bytes) p.lds = red_bytes;
-  p.sb16 = g8;
+  return best;
+}
+
+// Plans depend only on the shapes (and the tuning environment), so the last
+// few are kept: a decode loop calls with the same shapes every token.
+struct PlanKey {
+  uint32_t rows[kMaxQ4Jobs];
+  int n_jobs;
+  bool swiglu;
+  uint32_t K, M;
+  int env[6];
+  bool operator==(const PlanKey& o) const {
+    return n_jobs == o.n_jobs && swiglu == o.swiglu && K == o.K && M == o.M &&
+           std::memcmp(rows, o.rows, sizeof(rows)) == 0 && std::memcmp(env, o.env, sizeof(env)) == 0;
+  }
+};
+Plan cached_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M) {
+  static std::mutex mu;
+  static PlanKey keys[8];
+  static Plan plans[8];
+  static int used = 0, next = 0;
+  PlanKey k{};
+  for (int i = 0; i < n_jobs; ++i) k.rows[i] = jobs[i].rows;
+  k.n_jobs = n_jobs;
+  k.swiglu = swiglu;
+  k.K = K;
+  k.M = M;
+  const char* names[6] = {"QM38_CUS", "QM38_Q4_NT", "QM38_Q4_XSTAGE", "QM38_Q4_TARGET_WAVES", "QM38_Q4_RPW",
+                          "QM38_Q4_SPLIT"};
+  for (int i = 0; i < 6; ++i) k.env[i] = env_int(names[i], -1);
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < used; ++i)
+    if (keys[i] == k) return plans[i];
+  const Plan p = make_plan(jobs, n_jobs, swiglu, K, M);
+  if (env_int("QM38_Q4_PLAN_LOG", 0) > 0)
+    fprintf(stderr, "q4 decode plan: K=%u M=%u swiglu=%d rows0=%u -> nt=%d rpw=%u tiles=%u waves=%u gps=%u lds=%u\n", K,
+            M, (int)swiglu, jobs[0].rows, p.nt, p.rpw, p.tiles, p.waves, p.gps, p.lds);
+  if (p.fn) {
+    keys[next] = k;
+    plans[next] = p;
+    next = (next + 1) % 8;
+    used = std::min(used + 1, 8);
+  }
   return p;
-}
-
-template <int NT, int R, bool SW>
-hipError_t launch_one(const DecodeArgs& a, const Plan& p, hipStream_t st) {
-  const dim3 grid(p.tiles), block(64 * p.waves);
-  if (p.x_bytes) {
-    if (p.sb16)
-      hipLaunchKernelGGL((q4_decode_kernel<NT, R, SW, true, true>), grid, block, p.lds, st, a);
-    else
-      hipLaunchKernelGGL((q4_decode_kernel<NT, R, SW, false, true>), grid, block, p.lds, st, a);
-  } else {
-    if (p.sb16)
-      hipLaunchKernelGGL((q4_decode_kernel<NT, R, SW, true, false>), grid, block, p.lds, st, a);
-    else
-      hipLaunchKernelGGL((q4_decode_kernel<NT, R, SW, false, false>), grid, block, p.lds, st, a);
-  }
-  return hipGetLastError();
-}
-
-template <int NT, bool SW>
-hipError_t dispatch_m(const DecodeArgs& a, const Plan& p, hipStream_t st) {
-  switch (a.M) {
-    case 1: return launch_one<NT, 1, SW>(a, p, st);
-    case 2: return launch_one<NT, 2, SW>(a, p, st);
-    default: return launch_one<NT, 4, SW>(a, p, st);
-  }
 }
 
 }  // namespace
@@ -545,8 +611,8 @@ void q4_decode_workspace(const Q4Job*, int, bool, uint32_t, uint32_t, size_t* pa
 
 hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x,
                             uint32_t K, uint32_t M, const Workspace&, hipStream_t stream) {
-  const Plan p = make_plan(jobs, n_jobs, swiglu, K, M);
-  if (p.lds > 160 * 1024) return hipErrorInvalidValue;
+  const Plan p = cached_plan(jobs, n_jobs, swiglu, K, M);
+  if (!p.fn || p.lds > 160 * 1024) return hipErrorInvalidValue;
   DecodeArgs a{};
   a.x = x;
   a.K = K;
@@ -554,16 +620,17 @@ hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const ui
   a.G = K / 64;
   a.gps = p.gps;
   a.x_bytes = p.x_bytes;
+  a.rpw = p.rpw;
   a.n_jobs = (uint32_t)n_jobs;
   uint32_t ts = 0;
-  const uint32_t rows_per_set = swiglu ? 16u : 16u * p.nt;
   for (int i = 0; i < n_jobs; ++i) {
     a.jobs[i] = jobs[i];
     a.jobs[i].tile_begin = ts;
-    if (!swiglu) ts += (jobs[i].rows + rows_per_set - 1) / rows_per_set;
+    if (!swiglu) ts += (jobs[i].rows + p.rpw - 1) / p.rpw;
   }
-  if (swiglu) return dispatch_m<2, true>(a, p, stream);
-  return p.nt == 2 ? dispatch_m<2, false>(a, p, stream) : dispatch_m<1, false>(a, p, stream);
+  void* args[] = {&a};
+  const hipError_t e = hipLaunchKernel(p.fn, dim3(p.tiles), dim3(64 * p.waves), args, p.lds, stream);
+  return e != hipSuccess ? e : hipGetLastError();
 }
 
 }  // namespace qm

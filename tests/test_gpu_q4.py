@@ -161,6 +161,31 @@ def test_decode_set_27b_shapes(rt, torch_dev, M):
     assert_bf16_close(y, oracle.q4_project(hb, *down), what="down")
 
 
+@pytest.mark.parametrize("nt,rpw", [(1, 16), (1, 13), (1, 10), (1, 8), (2, 32), (2, 20), (2, 17)])
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_rows_per_workgroup(rt, torch_dev, monkeypatch, nt, rpw, M):
+    """Workgroups owning fewer rows than their 16-row tiles (the planner's
+    balancing choice) mask the rest; forced here for several row counts that
+    do not divide the projection heights, with several jobs in one launch and
+    a SwiGLU pair."""
+    import qm38
+    monkeypatch.setenv("QM38_Q4_NT", str(nt))
+    monkeypatch.setenv("QM38_Q4_RPW", str(rpw))
+    rng = np.random.default_rng(300 + nt * 50 + rpw + M)
+    K = 1024
+    mats = [synth.q4_matrix(rng, n, K) for n in (200, 37, 512)]
+    xb = synth.bf16_normal(rng, (M, K))
+    for mat, got in zip(mats, _project(rt, torch_dev, mats, xb, M)):
+        assert_bf16_close(got, oracle.q4_project(xb, *mat), what=f"rows {mat[0].shape[0]}")
+    I = 333
+    gate, up = synth.q4_matrix(rng, I, K), synth.q4_matrix(rng, I, K)
+    dg, du = _upload(torch_dev, *gate), _upload(torch_dev, *up)
+    h = empty_bf16((M, I), torch_dev)
+    rt.q4_swiglu(qm38.Runtime.job(*dg, I), qm38.Runtime.job(*du, I), to_dev(xb, torch_dev), K, M, h)
+    h_ref = oracle.swiglu(oracle.q4_project(xb, *gate), oracle.q4_project(xb, *up))
+    assert_bf16_close(bf16_dev_to_f32(h), h_ref, what="swiglu")
+
+
 def test_config1_4096(rt, torch_dev):
     rng = np.random.default_rng(1)
     mat = synth.q4_matrix(rng, 4096, 4096)
