@@ -312,6 +312,11 @@ struct GemmPlan {
 // K slices per tile: when the tiles fill less than one dispatch round of
 // `cus` workgroups, split K so the units fill whole rounds as evenly as
 // possible (at least 8 K steps per slice, at most 8 slices).
+int env_int_gemm(const char* name, int fallback) {
+  const char* v = getenv(name);
+  return v ? atoi(v) : fallback;
+}
+
 GemmPlan gemm_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M) {
   GemmPlan p{};
   p.m_tiles = (M + kBM - 1) / kBM;
@@ -323,18 +328,25 @@ GemmPlan gemm_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint3
   }
   p.tiles = n_tiles * p.m_tiles;
   const uint32_t G = K / 64, cus = 256;
+  // Split-K fills partial dispatch rounds (one workgroup per CU).  Cost in
+  // units of one K group of one tile, fitted to measured BASELINE shapes:
+  // per round the slice's groups plus about 10 for the pipeline fill and the
+  // epilogue, 4 more for writing the fp32 partials when split, and about 10
+  // per slice for the last slice's read-back.  (Down at M = 2048, 160 tiles:
+  // three slices in two rounds beat one long round by 15 %; QKV's 320 tiles
+  // stay unsplit: five rounds of short slices lose to two full rounds.)
   p.splits = 1;
-  if (p.tiles < cus) {
-    double best = (double)p.tiles / cus;
-    for (uint32_t s = 2; s <= 8 && G / s >= 8; ++s) {
-      const uint32_t units = p.tiles * s, rounds = (units + cus - 1) / cus;
-      const double eff = (double)units / (rounds * cus);
-      if (eff > best + 0.05) {
-        best = eff;
-        p.splits = s;
-      }
+  double best = 0.0;
+  for (uint32_t s = 1; s <= 8 && (s == 1 || G / s >= 8); ++s) {
+    const uint32_t gks = (G + s - 1) / s;
+    const uint32_t units = p.tiles * s, rounds = (units + cus - 1) / cus;
+    const double cost = rounds * (gks + 10.0 + (s > 1 ? 4.0 : 0.0)) + (s > 1 ? 10.0 * s : 0.0);
+    if (s == 1 || cost < best) {
+      best = cost;
+      p.splits = s;
     }
   }
+  if (env_int_gemm("QM38_GEMM_SPLITS", 0) > 0) p.splits = std::min<uint32_t>(8, (uint32_t)env_int_gemm("QM38_GEMM_SPLITS", 1));
   p.gks = (G + p.splits - 1) / p.splits;
   p.splits = (G + p.gks - 1) / p.gks;
   return p;
