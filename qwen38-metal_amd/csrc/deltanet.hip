@@ -36,19 +36,78 @@ __device__ __forceinline__ float conv_input(const DnArgs& a, uint32_t ch, int t)
   return t >= 0 ? a.qkv[(size_t)t * a.channels + ch] : a.hist_in[(size_t)ch * hw + hw + t];
 }
 
-__device__ __forceinline__ float conv_silu(const DnArgs& a, uint32_t ch, int t) {
+__device__ __forceinline__ void shift_history(const DnArgs& a, uint32_t ch) {
+  const int hw = (int)a.kernel - 1;
+  for (int tap = 0; tap < hw; ++tap)
+    a.hist_out[(size_t)ch * hw + tap] = conv_input(a, ch, (int)a.M - hw + tap);
+}
+
+// Operands of one conv output for kernels of up to kTaps taps: tap j holds
+// weight w[j] and input x(t - hw + j).  Loaded in one batch (addresses picked
+// by select, no branches) so that several outputs' loads are in flight
+// together; conv_finish then forms the sum in the order of the loop below.
+constexpr int kTaps = 4;
+struct ConvIn {
+  float w[kTaps], x[kTaps];
+};
+__device__ __forceinline__ void conv_load(const DnArgs& a, uint32_t ch, int t, ConvIn& c) {
+  const int hw = (int)a.kernel - 1;
+#pragma unroll
+  for (int j = 0; j < kTaps; ++j) {
+    // Taps past the kernel read a valid address and are zeroed, so every
+    // load is unconditional.
+    const int jj = j <= hw ? j : hw;
+    const int tj = t - hw + jj;
+    const float* src = tj >= 0 ? a.qkv + (size_t)tj * a.channels + ch : a.hist_in + (size_t)ch * hw + hw + tj;
+    const float wv = a.conv_w[(size_t)ch * a.kernel + jj];
+    const float xv = *src;
+    c.w[j] = j <= hw ? wv : 0.0f;
+    c.x[j] = j <= hw ? xv : 0.0f;
+  }
+}
+// History after token t = M - 1: the inputs x(t - hw + 1 .. t), i.e. taps 1..hw.
+__device__ __forceinline__ void conv_store_history(const DnArgs& a, uint32_t ch, const ConvIn& c) {
+  const int hw = (int)a.kernel - 1;
+#pragma unroll
+  for (int j = 0; j < kTaps - 1; ++j)
+    if (j < hw) a.hist_out[(size_t)ch * hw + j] = c.x[j + 1];
+}
+__device__ __forceinline__ float conv_finish(const DnArgs& a, const ConvIn& c) {
+  const int hw = (int)a.kernel - 1;
+  float wl = c.w[0], xl = c.x[0];
+#pragma unroll
+  for (int j = 1; j < kTaps; ++j) {
+    wl = hw == j ? c.w[j] : wl;
+    xl = hw == j ? c.x[j] : xl;
+  }
+  float sum = wl * xl;
+#pragma unroll
+  for (int j = 0; j < kTaps - 1; ++j)
+    if (j < hw) sum += c.w[j] * c.x[j];
+  return silu_f(sum);
+}
+// Longer kernels: the same sum, one tap at a time.
+__device__ __forceinline__ float conv_silu_loop(const DnArgs& a, uint32_t ch, int t) {
   const int hw = (int)a.kernel - 1;
   const float* w = a.conv_w + (size_t)ch * a.kernel;
   float sum = w[hw] * conv_input(a, ch, t);
   for (int tap = 0; tap < hw; ++tap) sum += w[tap] * conv_input(a, ch, t - hw + tap);
   return silu_f(sum);
 }
-
-__device__ __forceinline__ void shift_history(const DnArgs& a, uint32_t ch) {
-  const int hw = (int)a.kernel - 1;
-  for (int tap = 0; tap < hw; ++tap)
-    a.hist_out[(size_t)ch * hw + tap] = conv_input(a, ch, (int)a.M - hw + tap);
+// One conv output; with `last` (t = M - 1) it also writes the channel's new
+// history window.
+__device__ __forceinline__ float conv_silu(const DnArgs& a, uint32_t ch, int t, bool last) {
+  if (a.kernel > kTaps) {
+    const float y = conv_silu_loop(a, ch, t);
+    if (last) shift_history(a, ch);
+    return y;
+  }
+  ConvIn c;
+  conv_load(a, ch, t, c);
+  if (last) conv_store_history(a, ch, c);
+  return conv_finish(a, c);
 }
+
 
 // Sum over the 16 lanes of a DPP row: quad swaps, then rotations by 4 and 8
 // within the row; every lane ends with the total.
@@ -78,15 +137,44 @@ __device__ __forceinline__ float row_sum(float v) {
 // channels c = lane + 64 i (i < 4; dk <= 256).  Shared by the prefill path
 // and the fused step so both round identically.
 __device__ __forceinline__ void prep_key_head(const DnArgs& a, uint32_t t, uint32_t kh, uint32_t lane, float (&qo)[4],
-                                              float (&ko)[4]) {
+                                              float (&ko)[4], bool last) {
   const uint32_t key_el = a.key_heads * a.dk;
   float qs = 0.0f, ks = 0.0f;
+  if (a.kernel <= kTaps) {
+    // All operands of the lane's (up to 8) outputs in flight at once.
+    ConvIn cq[4], ck[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = min(lane + 64 * i, a.dk - 1);
+      conv_load(a, kh * a.dk + c, (int)t, cq[i]);
+      conv_load(a, key_el + kh * a.dk + c, (int)t, ck[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = lane + 64 * i;
+      const bool ok = c < a.dk;
+      qo[i] = ok ? conv_finish(a, cq[i]) : 0.0f;
+      ko[i] = ok ? conv_finish(a, ck[i]) : 0.0f;
+      if (ok && last) {
+        conv_store_history(a, kh * a.dk + c, cq[i]);
+        conv_store_history(a, key_el + kh * a.dk + c, ck[i]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = lane + 64 * i;
+      const bool ok = c < a.dk;
+      qo[i] = ok ? conv_silu_loop(a, kh * a.dk + c, (int)t) : 0.0f;
+      ko[i] = ok ? conv_silu_loop(a, key_el + kh * a.dk + c, (int)t) : 0.0f;
+      if (ok && last) {
+        shift_history(a, kh * a.dk + c);
+        shift_history(a, key_el + kh * a.dk + c);
+      }
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t c = lane + 64 * i;
-    const bool ok = c < a.dk;
-    qo[i] = ok ? conv_silu(a, kh * a.dk + c, (int)t) : 0.0f;
-    ko[i] = ok ? conv_silu(a, key_el + kh * a.dk + c, (int)t) : 0.0f;
     qs += qo[i] * qo[i];
     ks += ko[i] * ko[i];
   }
@@ -116,26 +204,20 @@ __global__ __launch_bounds__(kThreads) void dn_conv_prepare_kernel(DnArgs a) {
   const bool last = t + 1 == a.M && a.kernel > 1;
   if (u < a.key_heads) {
     float cq[4], ck[4];
-    prep_key_head(a, t, u, lane, cq, ck);
+    prep_key_head(a, t, u, lane, cq, ck, last);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t c = lane + 64 * i;
       if (c < a.dk) {
-        const uint32_t qc = u * a.dk + c, kc = key_el + u * a.dk + c;
-        row[qc] = cq[i];
-        row[kc] = ck[i];
-        if (last) {
-          shift_history(a, qc);
-          shift_history(a, kc);
-        }
+        row[u * a.dk + c] = cq[i];
+        row[key_el + u * a.dk + c] = ck[i];
       }
     }
   } else {
     const uint32_t vh = u - a.key_heads;
     for (uint32_t c = lane; c < a.dv; c += 64) {
       const uint32_t ch = 2 * key_el + vh * a.dv + c;
-      row[ch] = conv_silu(a, ch, (int)t);
-      if (last) shift_history(a, ch);
+      row[ch] = conv_silu(a, ch, (int)t, last);
     }
   }
 }
@@ -338,13 +420,18 @@ __global__ __launch_bounds__(kThreads) void dn_gate_norm_kernel(DnArgs a) {
 // The whole decode step (M = 1) in one launch: block = value head vh.
 //  wave 0: q^, k^ of key head kh (prep_key_head); wave 1: conv of vh's v
 //  channels; thread 128: g and beta.  Then the 16-lane row groups update the
-//  dv rows of S in DV / 16 passes (delta_row_token), and wave 0 applies the
+//  dv rows of S in dv / 16 passes (delta_row_token), and wave 0 applies the
 //  gated norm (gate_norm_row).  The arithmetic is the three-launch path's,
-//  call for call, so a step equals a one-token prefill bit for bit.
+//  call for call, so a step equals a one-token prefill bit for bit.  (A
+//  1024-thread block with 64 rows per pass compiled to code whose results
+//  differ from the prefill path's in the last bit for some heads, so the
+//  block stays at 256 threads.)
+constexpr int kStepThreads = 256;
+constexpr int kStepRows = kStepThreads / 16;  // S rows per pass
 template <int EPT, int PASSES>
-__global__ __launch_bounds__(kThreads) void dn_step_kernel(DnArgs a) {
+__global__ __launch_bounds__(kStepThreads) void dn_step_kernel(DnArgs a) {
   __shared__ __attribute__((aligned(16))) float qk_s[2][16][EPT];  // [q | k][lane][e]
-  __shared__ float v_s[16 * PASSES], o_s[16 * PASSES];
+  __shared__ float v_s[kStepRows * PASSES], o_s[kStepRows * PASSES];
   __shared__ float gb_s[2];
   const uint32_t vh = blockIdx.x;
   const uint32_t group = a.value_heads / a.key_heads;
@@ -354,12 +441,12 @@ __global__ __launch_bounds__(kThreads) void dn_step_kernel(DnArgs a) {
   // The first value head of a key group also writes that key head's history.
   const bool key_hist = vh % group == 0 && a.kernel > 1;
 
-  // S rows of this block: pass p, row 16 p + r, columns l + 16 e.
+  // S rows of this block: pass p, row kStepRows p + r, columns l + 16 e.
   const int r = threadIdx.x / 16, l = threadIdx.x % 16;
   float s[PASSES][EPT];
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
-    const uint32_t row = 16 * p + r;
+    const uint32_t row = kStepRows * p + r;
     const size_t srow = ((size_t)vh * a.dv + row) * a.dk;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
@@ -370,7 +457,7 @@ __global__ __launch_bounds__(kThreads) void dn_step_kernel(DnArgs a) {
 
   if (wave == 0) {
     float cq[4], ck[4];
-    prep_key_head(a, 0, kh, lane, cq, ck);
+    prep_key_head(a, 0, kh, lane, cq, ck, key_hist);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t c = lane + 64 * i;
@@ -378,16 +465,25 @@ __global__ __launch_bounds__(kThreads) void dn_step_kernel(DnArgs a) {
         qk_s[0][c % 16][c / 16] = c < a.dk ? cq[i] : 0.0f;
         qk_s[1][c % 16][c / 16] = c < a.dk ? ck[i] : 0.0f;
       }
-      if (c < a.dk && key_hist) {
-        shift_history(a, kh * a.dk + c);
-        shift_history(a, key_el + kh * a.dk + c);
-      }
     }
   } else if (wave == 1) {
-    for (uint32_t c = lane; c < 16 * PASSES; c += 64) {
-      const uint32_t ch = 2 * key_el + vh * a.dv + c;
-      v_s[c] = c < a.dv ? conv_silu(a, ch, 0) : 0.0f;
-      if (c < a.dv && a.kernel > 1) shift_history(a, ch);
+    // Both of the lane's value channels loaded before either is finished.
+    constexpr int kV = (kStepRows * PASSES + 63) / 64;
+    if (a.kernel <= kTaps) {
+      ConvIn cv[kV];
+#pragma unroll
+      for (int i = 0; i < kV; ++i) conv_load(a, 2 * key_el + vh * a.dv + min(lane + 64 * i, a.dv - 1), 0, cv[i]);
+#pragma unroll
+      for (int i = 0; i < kV; ++i) {
+        const uint32_t c = lane + 64 * i;
+        if (c < kStepRows * PASSES) v_s[c] = c < a.dv ? conv_finish(a, cv[i]) : 0.0f;
+        if (c < a.dv && a.kernel > 1) conv_store_history(a, 2 * key_el + vh * a.dv + c, cv[i]);
+      }
+    } else {
+      for (uint32_t c = lane; c < kStepRows * PASSES; c += 64) {
+        const uint32_t ch = 2 * key_el + vh * a.dv + c;
+        v_s[c] = c < a.dv ? conv_silu(a, ch, 0, a.kernel > 1) : 0.0f;
+      }
     }
   } else if (threadIdx.x == 128) {
     const float neg_a = -expf(a.a_log[vh]);
@@ -405,7 +501,7 @@ __global__ __launch_bounds__(kThreads) void dn_step_kernel(DnArgs a) {
   const float g = gb_s[0], beta = gb_s[1];
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
-    const uint32_t row = 16 * p + r;
+    const uint32_t row = kStepRows * p + r;
     const float o = delta_row_token<EPT>(s[p], kk, qq, g, beta, v_s[row]);
     if (l == 0) o_s[row] = o;
     if (row < a.dv) {
@@ -436,8 +532,8 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
   if (a.dk == 0 || a.dk > 256 || a.dv == 0 || a.dv > 256 || a.M == 0) return hipErrorInvalidValue;
   // One token with S rows that fit the fused kernel's registers: one launch.
   if (a.M == 1 && a.dk <= 128 && a.dv <= 128) {
-    const dim3 grid(a.value_heads), block(kThreads);
-    const uint32_t ept = (a.dk + 15) / 16, passes = (a.dv + 15) / 16;
+    const dim3 grid(a.value_heads), block(kStepThreads);
+    const uint32_t ept = (a.dk + 15) / 16, passes = (a.dv + kStepRows - 1) / kStepRows;
     if (ept <= 4 && passes <= 4)
       hipLaunchKernelGGL((dn_step_kernel<4, 4>), grid, block, 0, st, a);
     else if (ept <= 4)
