@@ -253,6 +253,23 @@ def attention_legs(rt, dev, rng, steps, warmup):
     for c in caches:
         c.close()
     torch.cuda.empty_cache()
+    # (d) q/k preparation (RMSNorm + RoPE + query/gate split) for 1 and 2048
+    # rows, rotary_dim = head_dim / 4 (partial_rotary_factor 0.25).
+    import qm38
+    rope = qm38.RopeConfig(ATT_D, ATT_D // 4, 1e7, 0, 0, 0)
+    qn = torch.ones(ATT_D, dtype=torch.float32, device=dev)
+    for R in (1, 2048):
+        qg = dev_array(synth.bf16_normal(rng, (R, ATT_H, 2 * ATT_D)), dev)
+        kin = dev_array(synth.bf16_normal(rng, (R, ATT_KVH, ATT_D)), dev)
+        qo = torch.empty((R, ATT_H, ATT_D), dtype=torch.int16, device=dev)
+        go = torch.empty((R, ATT_H, ATT_D), dtype=torch.int16, device=dev)
+        ko = torch.empty((R, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
+        ms, _ = timed(lambda i, m: rt.attn_prepare(rope, R, ATT_H, ATT_KVH, qg, kin, qn, qn, 1e-6, qo, go, ko,
+                                                   position_base=4096 + i), stream, steps, warmup)
+        nbytes = R * (ATT_H * 2 * ATT_D * 2 + ATT_KVH * ATT_D * 2 + 2 * ATT_H * ATT_D * 2 + ATT_KVH * ATT_D * 4)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[f"attn_prepare_rows{R}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                                        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
     return out
 
 

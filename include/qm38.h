@@ -192,6 +192,41 @@ qm_status qm_attn_decode(qm_runtime* rt, qm_kv* const* seqs, uint32_t B,
                          const float* k, const float* v, uint32_t H,
                          uint16_t* o);
 
+/* Rotary configuration of the full-attention layers (RopeParameters,
+ * native.rs:119-197; MetalGqaDecodeConfig, metal_runtime.rs).
+ * rotary_dim = round(head_dim * partial_rotary_factor), even, <= head_dim.
+ * With has_mrope_sections, RoPE frequency i of the rotary half uses position
+ * axis 1 when i % 3 == 1 and i / 3 < mrope_section1, axis 2 when i % 3 == 2
+ * and i / 3 < mrope_section2, else axis 0 (native.rs:136-148). */
+typedef struct qm_rope_config {
+  uint32_t head_dim;   /* 1..256 */
+  uint32_t rotary_dim;
+  float rope_theta;    /* > 0 */
+  uint32_t mrope_section1, mrope_section2;
+  uint32_t has_mrope_sections;
+} qm_rope_config;
+
+/* Full-attention q/k preparation for M rows, the step between the q/k
+ * projections and qm_attn_decode / qm_attn_prefill:
+ *   q_with_gate bf16 [M][H][2 head_dim]  query | gate per head (the packed
+ *                                        q_proj output)
+ *   k_in        bf16 [M][kv_heads][head_dim]
+ *   q_norm, k_norm fp32 [head_dim]       per-head RMSNorm weights
+ *   positions   uint32 [3][M] (axis-major) or NULL: all axes = position_base + row
+ *   q_out, gate_out bf16 [M][H][head_dim];  k_out fp32 [M][kv_heads][head_dim]
+ * q = rope(rmsnorm(query) * q_norm), gate copied, k = rope(rmsnorm(k) * k_norm).
+ * Replaces qwen38_gqa_prepare_query(_rows) / qwen38_gqa_prepare_key(_rows)
+ * (qwen38.metal:4761-5029; encoders metal_runtime.rs:5171-5420) and the CPU
+ * split_query_and_gate / rms_norm_slice / apply_mrope (native.rs:4917-4942,
+ * 5153-5180).  The rotation angle is evaluated in fp64 (the reference: fp32).
+ * Device pointers, asynchronous on the runtime's stream; when head_dim % 4 == 0
+ * the bf16 buffers must be 8-byte and k_out 16-byte aligned. */
+qm_status qm_attn_prepare(qm_runtime* rt, const qm_rope_config* rope, uint32_t M,
+                          uint32_t H, uint32_t kv_heads, const uint16_t* q_with_gate,
+                          const uint16_t* k_in, const float* q_norm, const float* k_norm,
+                          float epsilon, const uint32_t* positions, uint32_t position_base,
+                          uint16_t* q_out, uint16_t* gate_out, float* k_out);
+
 /* Causal prefill of M new rows: appends them (qwen38_q8_kv_append_prefill,
  * qwen38.metal:5085-5140) and computes, for row i, attention over the first
  * min(start+i+1, total) tokens (qwen38_gqa_q8_prefill_attention,

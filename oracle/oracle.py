@@ -43,6 +43,8 @@ def lib() -> C.CDLL:
         for n in ("qo_dn_prefill_f32", "qo_dn_prefill_f64"):
             getattr(L, n).argtypes = [u32, u32, u32, u32, u32, vp, vp, vp, vp, vp, vp, vp, vp, u32,
                                       C.c_float, vp, vp, vp]
+        L.qo_attn_prepare.argtypes = [vp, vp, vp, vp, u32, u32, u32, u32, u32, C.c_double, u32, u32, u32, vp, u32,
+                                      C.c_float, vp, vp, vp]
         L.qo_num_threads.restype = i32
         _lib = L
     return _lib
@@ -170,3 +172,23 @@ class LogicalPageTable:
         if token >= self.sequence_tokens:
             return None
         return self.pages[token // self.page_tokens]
+
+
+def attn_prepare(q_with_gate, k, q_norm, k_norm, head_dim: int, rotary_dim: int, theta: float, eps: float,
+                 sections=None, positions=None, base: int = 0):
+    """Full-attention q/k preparation (qo_attn_prepare).  q_with_gate fp32
+    [M][H][2 hd], k fp32 [M][KVH][hd]; sections (s1, s2) or None; positions
+    uint32 [3][M] or None (every axis = base + row).  Returns (q, gate, k) fp32."""
+    qg = _c(q_with_gate, np.float32)
+    kk = _c(k, np.float32)
+    M, H = qg.shape[0], qg.shape[1]
+    KVH = kk.shape[1]
+    q = np.zeros((M, H, head_dim), np.float32)
+    g = np.zeros((M, H, head_dim), np.float32)
+    ko = np.zeros((M, KVH, head_dim), np.float32)
+    pos = None if positions is None else _c(positions, np.uint32)
+    s1, s2 = sections if sections is not None else (0, 0)
+    lib().qo_attn_prepare(_p(qg), _p(kk), _p(_c(q_norm, np.float32)), _p(_c(k_norm, np.float32)), M, H, KVH,
+                          head_dim, rotary_dim, float(theta), s1, s2, int(sections is not None), _p(pos), base, eps,
+                          _p(q), _p(g), _p(ko))
+    return q, g, ko

@@ -295,6 +295,61 @@ void qo_dn_prefill_f64(uint32_t KH, uint32_t VH, uint32_t dk, uint32_t dv, uint3
                     b + (size_t)t * VH, a + (size_t)t * VH, eps, hist, S, out + (size_t)t * VH * dv);
 }
 
+// Full-attention q/k preparation for M rows: per-head RMSNorm with a learned
+// weight, partial (M-)RoPE on the first rotary_dim dims, query/gate split.
+//   q_with_gate [M][H][2 hd]  (query | gate per head; split_query_and_gate,
+//                              native.rs:4917-4942)
+//   k_in        [M][KVH][hd]
+//   positions   [3][M] (axis-major) or NULL: every axis = base + row
+// RMSNorm follows rms_norm_slice (native.rs:5153-5161): mean of squares
+// summed in order, scale = 1/sqrt(mean + eps), out = x * scale * w.  RoPE
+// follows apply_mrope (native.rs:5163-5180) with the interleaved axis choice
+// of MropePosition::axis_for_frequency (native.rs:136-148) and the GPU
+// kernels qwen38_gqa_prepare_query(_rows) / _key(_rows) (qwen38.metal:
+// 4761-5029).  One deviation: the reference forms the angle pos /
+// theta^(2i/rd) in fp32, where one ulp of powf moves the angle by ~1e-2 rad
+// at positions near 128K; here (and in the HIP kernel) frequency, angle and
+// sin/cos are evaluated in fp64 and rounded to fp32.
+static void prep_head(const float* x, const float* w, uint32_t hd, uint32_t rd, double theta, uint32_t s1, uint32_t s2,
+                      uint32_t has_sections, const uint32_t pos[3], float eps, float* out) {
+  float sum = 0.0f;
+  for (uint32_t i = 0; i < hd; ++i) sum += x[i] * x[i];
+  const float mean = sum / (float)hd;
+  const float scale = 1.0f / sqrtf(mean + eps);
+  for (uint32_t i = 0; i < hd; ++i) out[i] = x[i] * scale * w[i];
+  const uint32_t half = rd / 2;
+  for (uint32_t i = 0; i < half; ++i) {
+    uint32_t p = pos[0];
+    if (has_sections) {
+      if (i % 3 == 1 && i / 3 < s1) p = pos[1];
+      if (i % 3 == 2 && i / 3 < s2) p = pos[2];
+    }
+    const double angle = (double)p / pow(theta, (double)(2 * i) / (double)rd);
+    const float sn = (float)sin(angle), cs = (float)cos(angle);
+    const float left = out[i], right = out[i + half];
+    out[i] = left * cs - right * sn;
+    out[i + half] = right * cs + left * sn;
+  }
+}
+
+void qo_attn_prepare(const float* q_with_gate, const float* k_in, const float* q_norm, const float* k_norm,
+                     uint32_t M, uint32_t H, uint32_t KVH, uint32_t hd, uint32_t rd, double theta, uint32_t s1,
+                     uint32_t s2, uint32_t has_sections, const uint32_t* positions, uint32_t base, float eps,
+                     float* q_out, float* gate_out, float* k_out) {
+  for (uint32_t r = 0; r < M; ++r) {
+    uint32_t pos[3];
+    for (int a = 0; a < 3; ++a) pos[a] = positions ? positions[(size_t)a * M + r] : base + r;
+    for (uint32_t h = 0; h < H; ++h) {
+      const float* src = q_with_gate + ((size_t)r * H + h) * 2 * hd;
+      prep_head(src, q_norm, hd, rd, theta, s1, s2, has_sections, pos, eps, q_out + ((size_t)r * H + h) * hd);
+      memcpy(gate_out + ((size_t)r * H + h) * hd, src + hd, hd * sizeof(float));
+    }
+    for (uint32_t h = 0; h < KVH; ++h)
+      prep_head(k_in + ((size_t)r * KVH + h) * hd, k_norm, hd, rd, theta, s1, s2, has_sections, pos, eps,
+                k_out + ((size_t)r * KVH + h) * hd);
+  }
+}
+
 int qo_num_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

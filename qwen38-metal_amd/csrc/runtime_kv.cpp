@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "attention.h"
+#include "prepare.h"
 #include "runtime_internal.h"
 
 using namespace qm;
@@ -390,3 +391,44 @@ qm_status qm_attn_prefill(qm_runtime* rt, qm_kv* seq, const uint16_t* q, const u
 }
 
 }  // extern "C"
+
+qm_status qm_attn_prepare(qm_runtime* rt, const qm_rope_config* rope, uint32_t M, uint32_t H, uint32_t kv_heads,
+                          const uint16_t* q_with_gate, const uint16_t* k_in, const float* q_norm, const float* k_norm,
+                          float epsilon, const uint32_t* positions, uint32_t position_base, uint16_t* q_out,
+                          uint16_t* gate_out, float* k_out) {
+  if (!rt || !rope || !q_with_gate || !k_in || !q_norm || !k_norm || !q_out || !gate_out || !k_out)
+    return fail(QM_ERR_NULL_POINTER, "NULL argument");
+  if (M == 0 || H == 0 || kv_heads == 0) return fail(QM_ERR_EMPTY_DIMENSION, "rows, heads and kv_heads must be > 0");
+  const uint32_t hd = rope->head_dim;
+  if (hd == 0 || hd > kPrepMaxHeadDim)
+    return fail(QM_ERR_INVALID_ATTENTION_SHAPE, "head_dim %u must be 1..%u", hd, kPrepMaxHeadDim);
+  if (rope->rotary_dim > hd || rope->rotary_dim % 2 != 0)
+    return fail(QM_ERR_INVALID_ATTENTION_SHAPE, "rotary_dim %u must be even and <= head_dim %u", rope->rotary_dim, hd);
+  if (!(rope->rope_theta > 0.0f)) return fail(QM_ERR_INVALID_ARGUMENT, "rope_theta must be > 0");
+  if (hd % 4 == 0 && (!aligned(q_with_gate, 8) || !aligned(k_in, 8) || !aligned(q_out, 8) || !aligned(gate_out, 8) ||
+                      !aligned(k_out, 16)))
+    return fail(QM_ERR_MISALIGNED, "attention prepare: bf16 buffers must be 8-byte and k_out 16-byte aligned");
+  if ((uint64_t)H + kv_heads > 0x7FFFFFFFull)
+    return fail(QM_ERR_DIMENSION_OVERFLOW, "attention prepare: %u + %u heads overflow", H, kv_heads);
+  PrepArgs a{};
+  a.q_with_gate = q_with_gate;
+  a.k_in = k_in;
+  a.q_norm = q_norm;
+  a.k_norm = k_norm;
+  a.positions = positions;
+  a.base = position_base;
+  a.q_out = q_out;
+  a.gate_out = gate_out;
+  a.k_out = k_out;
+  a.M = M;
+  a.H = H;
+  a.KVH = kv_heads;
+  a.head_dim = hd;
+  a.rotary_dim = rope->rotary_dim;
+  a.section1 = rope->mrope_section1;
+  a.section2 = rope->mrope_section2;
+  a.has_sections = rope->has_mrope_sections ? 1u : 0u;
+  a.theta = rope->rope_theta;
+  a.eps = epsilon;
+  return hip_check(launch_attn_prepare(a, rt->stream), "attention prepare launch");
+}

@@ -37,7 +37,7 @@ EXPORTS = [
     "qm_q4_project", "qm_q4_swiglu", "qm_q4_mlp",
     "qm_kv_create", "qm_kv_destroy", "qm_kv_length", "qm_kv_allocated_pages", "qm_kv_page_for_token",
     "qm_kv_reserve", "qm_kv_truncate", "qm_kv_clone", "qm_kv_read",
-    "qm_attn_decode", "qm_attn_prefill",
+    "qm_attn_decode", "qm_attn_prefill", "qm_attn_prepare",
     "qm_dn_weights_create", "qm_dn_weights_destroy", "qm_dn_state_create", "qm_dn_state_destroy",
     "qm_dn_state_clone", "qm_dn_state_read", "qm_dn_state_write", "qm_dn_step", "qm_dn_prefill",
 ]
@@ -58,6 +58,12 @@ class Q4Job(C.Structure):
 class DnConfig(C.Structure):
     _fields_ = [("key_heads", C.c_uint32), ("value_heads", C.c_uint32), ("key_head_dim", C.c_uint32),
                 ("value_head_dim", C.c_uint32), ("conv_kernel_size", C.c_uint32)]
+
+
+class RopeConfig(C.Structure):
+    """qm_rope_config (RopeParameters, native.rs:119-197)."""
+    _fields_ = [("head_dim", C.c_uint32), ("rotary_dim", C.c_uint32), ("rope_theta", C.c_float),
+                ("mrope_section1", C.c_uint32), ("mrope_section2", C.c_uint32), ("has_mrope_sections", C.c_uint32)]
 
 
 _lib = None
@@ -107,6 +113,8 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "qm_kv_read": ([vp, vp, vp, vp, vp], i32),
         "qm_attn_decode": ([vp, C.POINTER(vp), u32, vp, vp, vp, vp, u32, vp], i32),
         "qm_attn_prefill": ([vp, vp, vp, vp, vp, vp, u32, u32, vp], i32),
+        "qm_attn_prepare": ([vp, C.POINTER(RopeConfig), u32, u32, u32, vp, vp, vp, vp, C.c_float, vp, u32, vp, vp,
+                             vp], i32),
         "qm_dn_weights_create": ([vp, C.POINTER(DnConfig), vp, vp, vp, vp, C.POINTER(vp)], i32),
         "qm_dn_weights_destroy": ([vp], None),
         "qm_dn_state_create": ([vp, vp, C.POINTER(vp)], i32),
@@ -206,6 +214,14 @@ class Runtime:
     def gqa_attention_q8_prefill(self, seq, q, gate, k, v, num_heads: int, rows: int, o) -> None:
         _check(self.lib.qm_attn_prefill(self.handle, seq.handle, _ptr(q), _ptr(gate), _ptr(k), _ptr(v),
                                         num_heads, rows, _ptr(o)))
+
+    def attn_prepare(self, rope: RopeConfig, rows: int, num_heads: int, kv_heads: int, q_with_gate, k, q_norm,
+                     k_norm, epsilon: float, q_out, gate_out, k_out, positions=None, position_base: int = 0) -> None:
+        """Full-attention q/k preparation (qm_attn_prepare): RMSNorm, (M-)RoPE
+        and the query/gate split of qwen38_gqa_prepare_query/_key."""
+        _check(self.lib.qm_attn_prepare(self.handle, C.byref(rope), rows, num_heads, kv_heads, _ptr(q_with_gate),
+                                        _ptr(k), _ptr(q_norm), _ptr(k_norm), epsilon, _ptr(positions),
+                                        position_base, _ptr(q_out), _ptr(gate_out), _ptr(k_out)))
 
     # ---- DeltaNet ---------------------------------------------------------
     def create_deltanet_weights(self, config: DnConfig, conv_weight, a_log, dt_bias, norm) -> "DnWeights":

@@ -385,3 +385,90 @@ def test_page_table_invariants():
         assert t.allocated_pages() == -(-n // 16)
     assert all(t.page_for_token(i) == i // 16 for i in range(n))
     assert t.page_for_token(n) is None
+
+
+# ---------------------------------------------------------------------------
+# Full-attention q/k preparation (RMSNorm + (M-)RoPE + query/gate split)
+# ---------------------------------------------------------------------------
+# metal_runtime.rs:9370-9420 gqa_gpu_prepare_matches_rms_norm_and_mrope inputs.
+PREP_QG = np.array([0.25, -0.5, 0.75, -1.0, 0.1, 0.2, 0.3, 0.4,
+                    -0.3, 0.6, -0.9, 1.2, -0.2, -0.1, 0.0, 0.1], np.float32).reshape(1, 2, 8)
+PREP_K = np.array([0.5, -0.25, 0.75, -1.0], np.float32).reshape(1, 1, 4)
+PREP_QN = np.array([0.9, 1.0, 1.1, 1.2], np.float32)
+PREP_KN = np.array([1.2, 1.1, 1.0, 0.9], np.float32)
+PREP_POS = np.array([[7], [11], [13]], np.uint32)
+
+
+def test_attn_prepare_reference_kat():
+    q, g, k = oracle.attn_prepare(PREP_QG, PREP_K, PREP_QN, PREP_KN, 4, 4, 10000.0, 1e-6, sections=(1, 1),
+                                  positions=PREP_POS)
+    # Key, by hand: mean x^2 = 0.46875, scale = 1/sqrt(0.468751); pair 0 turns
+    # by 7 rad (axis 0), pair 1 by 11/100 rad (frequency 1 -> axis 1 because
+    # 1 % 3 == 1 and 1 / 3 < section1).
+    s = 1.0 / math.sqrt(0.46875 + 1e-6)
+    n = [0.5 * s * 1.2, -0.25 * s * 1.1, 0.75 * s * 1.0, -1.0 * s * 0.9]
+    c0, s0, c1, s1 = math.cos(7), math.sin(7), math.cos(0.11), math.sin(0.11)
+    want = [n[0] * c0 - n[2] * s0, n[1] * c1 - n[3] * s1, n[2] * c0 + n[0] * s0, n[3] * c1 + n[1] * s1]
+    np.testing.assert_allclose(k[0, 0], want, rtol=2e-6, atol=2e-6)
+    assert abs(k[0, 0, 0] - (-0.0590059)) < 1e-5 and abs(k[0, 0, 2] - 1.4016113) < 1e-5
+    # Gates are the second half of each head, copied.
+    np.testing.assert_array_equal(g[0], PREP_QG[0, :, 4:])
+    # Heads 0 and 1 of the query are negatives of each other up to the weight:
+    # head 1 = -1.2 * head 0, and RMSNorm is scale invariant.
+    np.testing.assert_allclose(q[0, 1], -q[0, 0], rtol=1e-5, atol=1e-6)
+
+
+def test_attn_prepare_invariants():
+    rng = np.random.default_rng(5)
+    M, H, KVH, hd, rd = 6, 4, 2, 128, 32
+    qg = rng.standard_normal((M, H, 2 * hd)).astype(np.float32)
+    kin = rng.standard_normal((M, KVH, hd)).astype(np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    zero = np.zeros((3, M), np.uint32)
+    q0, _, k0 = oracle.attn_prepare(qg, kin, qn, kn, hd, rd, 1e6, 1e-6, positions=zero)
+    # Position 0 rotates nothing: plain RMSNorm (rotary_dim 0 gives the same).
+    qr, _, kr = oracle.attn_prepare(qg, kin, qn, kn, hd, 0, 1e6, 1e-6, positions=zero)
+    np.testing.assert_array_equal(q0, qr)
+    np.testing.assert_array_equal(k0, kr)
+    x = qg[..., :hd].astype(np.float64)
+    ref = x / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6) * qn
+    np.testing.assert_allclose(q0, ref, rtol=1e-5, atol=1e-6)
+    # Rotation preserves each pair's norm and leaves dims >= rotary_dim alone.
+    pos = rng.integers(0, 200000, (3, M)).astype(np.uint32)
+    q1, _, k1 = oracle.attn_prepare(qg, kin, qn, kn, hd, rd, 1e6, 1e-6, sections=(5, 5), positions=pos)
+    h = rd // 2
+    for a, b in ((q0, q1), (k0, k1)):
+        np.testing.assert_allclose(a[..., :h] ** 2 + a[..., h:rd] ** 2, b[..., :h] ** 2 + b[..., h:rd] ** 2,
+                                   rtol=1e-4, atol=1e-6)
+        np.testing.assert_array_equal(a[..., rd:], b[..., rd:])
+    # Text rows: q(p1) . k(p2) over the rotary part depends only on p1 - p2.
+    def dot(p1, p2):
+        qa, _, _ = oracle.attn_prepare(qg[:1], kin[:1], qn, kn, hd, rd, 1e4, 1e-6, base=p1)
+        _, _, kb = oracle.attn_prepare(qg[:1], kin[:1], qn, kn, hd, rd, 1e4, 1e-6, base=p2)
+        return float(np.dot(qa[0, 0, :rd].astype(np.float64), kb[0, 0, :rd]))
+    assert abs(dot(9, 4) - dot(1009, 1004)) < 1e-4
+    assert abs(dot(9, 4) - dot(10, 4)) > 1e-3  # and it does depend on the offset
+
+
+def test_attn_prepare_mrope_axis_selection():
+    # Frequency i uses axis 1 iff i % 3 == 1 and i / 3 < s1, axis 2 iff
+    # i % 3 == 2 and i / 3 < s2 (native.rs:136-148): moving only position 1
+    # changes exactly those pairs.
+    rng = np.random.default_rng(8)
+    hd, rd, s1, s2 = 64, 48, 3, 2
+    qg = rng.standard_normal((1, 1, 2 * hd)).astype(np.float32)
+    kin = rng.standard_normal((1, 1, hd)).astype(np.float32)
+    w = np.ones(hd, np.float32)
+    base = np.array([[100], [200], [300]], np.uint32)
+    moved = base.copy()
+    moved[1, 0] = 777
+    _, _, a = oracle.attn_prepare(qg, kin, w, w, hd, rd, 1e4, 1e-6, sections=(s1, s2), positions=base)
+    _, _, b = oracle.attn_prepare(qg, kin, w, w, hd, rd, 1e4, 1e-6, sections=(s1, s2), positions=moved)
+    h = rd // 2
+    changed = {i for i in range(h) if a[0, 0, i] != b[0, 0, i] or a[0, 0, i + h] != b[0, 0, i + h]}
+    assert changed == {i for i in range(h) if i % 3 == 1 and i // 3 < s1}
+    # Without sections every frequency uses axis 0.
+    _, _, c = oracle.attn_prepare(qg, kin, w, w, hd, rd, 1e4, 1e-6, positions=base)
+    _, _, d = oracle.attn_prepare(qg, kin, w, w, hd, rd, 1e4, 1e-6, positions=moved)
+    np.testing.assert_array_equal(c, d)
