@@ -55,7 +55,9 @@ typedef enum qm_status {
   QM_ERR_NULL_POINTER = 15,         /* a required pointer argument is NULL */
   QM_ERR_OUT_OF_MEMORY = 16,        /* device allocation failed */
   QM_ERR_MISALIGNED = 17,           /* a device pointer violates the documented alignment */
-  QM_ERR_INVALID_ARGUMENT = 18      /* any other precondition */
+  QM_ERR_INVALID_ARGUMENT = 18,     /* any other precondition */
+  QM_ERR_INVALID_SNAPSHOT = 19,     /* MetalRuntimeError::InvalidDeltaNetSnapshot */
+  QM_ERR_INVALID_SNAPSHOT_ROW = 20  /* ::InvalidSnapshotRow */
 } qm_status;
 
 /* Human-readable name of a status code (static storage). */
@@ -292,6 +294,34 @@ qm_status qm_dn_prefill(qm_runtime* rt, const qm_dn_weights* w,
                         const qm_dn_state* from, qm_dn_state* to,
                         const float* qkv, const float* z, const float* b,
                         const float* a, uint32_t M, float epsilon, float* out);
+
+/* State images for speculative verification (MTP).  A verification prefill
+ * of M rows can record the state after each of its first M - 1 rows; the
+ * final row's state is the destination state as usual.  Replaces
+ * MetalDeltaNetSnapshots: create_deltanet_snapshots (metal_runtime.rs:
+ * 7201-7232), deltanet_prefill_from_with_snapshots (7998-8024) and
+ * restore_deltanet_snapshot (7239-7281). */
+typedef struct qm_dn_snapshots qm_dn_snapshots;
+
+/* Room for `rows` images (rows > 0) of states of these weights. */
+qm_status qm_dn_snapshots_create(qm_runtime* rt, const qm_dn_weights* w, uint32_t rows,
+                                 qm_dn_snapshots** out);
+void qm_dn_snapshots_destroy(qm_dn_snapshots* snaps);
+
+/* qm_dn_prefill that also writes the state after row r into image r for
+ * r < M - 1 (requires M - 1 <= rows, else QM_ERR_INVALID_SNAPSHOT). */
+qm_status qm_dn_prefill_snapshots(qm_runtime* rt, const qm_dn_weights* w,
+                                  const qm_dn_state* from, qm_dn_state* to,
+                                  qm_dn_snapshots* snaps, const float* qkv,
+                                  const float* z, const float* b, const float* a,
+                                  uint32_t M, float epsilon, float* out);
+
+/* Makes `dst` the state after verification row `row` (row < rows, else
+ * QM_ERR_INVALID_SNAPSHOT_ROW).  A one-row set exchanges its buffers with
+ * dst's instead of copying (the image then holds dst's former state), as the
+ * reference does; otherwise an asynchronous device copy on the runtime's
+ * stream. */
+qm_status qm_dn_snapshot_restore(qm_dn_snapshots* snaps, uint32_t row, qm_dn_state* dst);
 
 #ifdef __cplusplus
 }

@@ -28,6 +28,13 @@ struct DnArgs {
   // workspace / output
   float* conv_out;  // [M][channels]: q^, k^, v after conv + prepare
   float* out;       // [M][VH][dv]
+  // optional state images after tokens 0 .. snap_rows - 1 (speculative
+  // verification; snap_rows <= M - 1): history [row][channels][kernel-1] and
+  // S [row][VH][dv][dk], strides in floats
+  float* snap_hist;
+  float* snap_s;
+  uint32_t snap_rows;
+  uint64_t snap_hist_stride, snap_s_stride;
 };
 
 hipError_t launch_deltanet(const DnArgs& a, hipStream_t st);

@@ -36,10 +36,17 @@ __device__ __forceinline__ float conv_input(const DnArgs& a, uint32_t ch, int t)
   return t >= 0 ? a.qkv[(size_t)t * a.channels + ch] : a.hist_in[(size_t)ch * hw + hw + t];
 }
 
-__device__ __forceinline__ void shift_history(const DnArgs& a, uint32_t ch) {
+// History window after token t (inputs t - hw + 1 .. t) into dst.
+__device__ __forceinline__ void shift_history(const DnArgs& a, uint32_t ch, int t, float* dst) {
   const int hw = (int)a.kernel - 1;
-  for (int tap = 0; tap < hw; ++tap)
-    a.hist_out[(size_t)ch * hw + tap] = conv_input(a, ch, (int)a.M - hw + tap);
+  for (int tap = 0; tap < hw; ++tap) dst[(size_t)ch * hw + tap] = conv_input(a, ch, t - hw + 1 + tap);
+}
+// Where token t's history window goes: the state's new buffer after the last
+// token, a snapshot image after an earlier one, else nowhere.
+__device__ __forceinline__ float* history_target(const DnArgs& a, uint32_t t) {
+  if (a.kernel <= 1) return nullptr;
+  if (t + 1 == a.M) return a.hist_out;
+  return t < a.snap_rows ? a.snap_hist + (size_t)t * a.snap_hist_stride : nullptr;
 }
 
 // Operands of one conv output for kernels of up to kTaps taps: tap j holds
@@ -65,12 +72,12 @@ __device__ __forceinline__ void conv_load(const DnArgs& a, uint32_t ch, int t, C
     c.x[j] = j <= hw ? xv : 0.0f;
   }
 }
-// History after token t = M - 1: the inputs x(t - hw + 1 .. t), i.e. taps 1..hw.
-__device__ __forceinline__ void conv_store_history(const DnArgs& a, uint32_t ch, const ConvIn& c) {
+// History window after the token of c: inputs x(t - hw + 1 .. t), taps 1..hw.
+__device__ __forceinline__ void conv_store_history(const DnArgs& a, uint32_t ch, const ConvIn& c, float* dst) {
   const int hw = (int)a.kernel - 1;
 #pragma unroll
   for (int j = 0; j < kTaps - 1; ++j)
-    if (j < hw) a.hist_out[(size_t)ch * hw + j] = c.x[j + 1];
+    if (j < hw) dst[(size_t)ch * hw + j] = c.x[j + 1];
 }
 __device__ __forceinline__ float conv_finish(const DnArgs& a, const ConvIn& c) {
   const int hw = (int)a.kernel - 1;
@@ -94,17 +101,17 @@ __device__ __forceinline__ float conv_silu_loop(const DnArgs& a, uint32_t ch, in
   for (int tap = 0; tap < hw; ++tap) sum += w[tap] * conv_input(a, ch, t - hw + tap);
   return silu_f(sum);
 }
-// One conv output; with `last` (t = M - 1) it also writes the channel's new
-// history window.
-__device__ __forceinline__ float conv_silu(const DnArgs& a, uint32_t ch, int t, bool last) {
+// One conv output; with a history target it also writes the channel's window
+// after token t there.
+__device__ __forceinline__ float conv_silu(const DnArgs& a, uint32_t ch, int t, float* hist_dst) {
   if (a.kernel > kTaps) {
     const float y = conv_silu_loop(a, ch, t);
-    if (last) shift_history(a, ch);
+    if (hist_dst) shift_history(a, ch, t, hist_dst);
     return y;
   }
   ConvIn c;
   conv_load(a, ch, t, c);
-  if (last) conv_store_history(a, ch, c);
+  if (hist_dst) conv_store_history(a, ch, c, hist_dst);
   return conv_finish(a, c);
 }
 
@@ -137,7 +144,7 @@ __device__ __forceinline__ float row_sum(float v) {
 // channels c = lane + 64 i (i < 4; dk <= 256).  Shared by the prefill path
 // and the fused step so both round identically.
 __device__ __forceinline__ void prep_key_head(const DnArgs& a, uint32_t t, uint32_t kh, uint32_t lane, float (&qo)[4],
-                                              float (&ko)[4], bool last) {
+                                              float (&ko)[4], float* hist_dst) {
   const uint32_t key_el = a.key_heads * a.dk;
   float qs = 0.0f, ks = 0.0f;
   if (a.kernel <= kTaps) {
@@ -155,9 +162,9 @@ __device__ __forceinline__ void prep_key_head(const DnArgs& a, uint32_t t, uint3
       const bool ok = c < a.dk;
       qo[i] = ok ? conv_finish(a, cq[i]) : 0.0f;
       ko[i] = ok ? conv_finish(a, ck[i]) : 0.0f;
-      if (ok && last) {
-        conv_store_history(a, kh * a.dk + c, cq[i]);
-        conv_store_history(a, key_el + kh * a.dk + c, ck[i]);
+      if (ok && hist_dst) {
+        conv_store_history(a, kh * a.dk + c, cq[i], hist_dst);
+        conv_store_history(a, key_el + kh * a.dk + c, ck[i], hist_dst);
       }
     }
   } else {
@@ -167,9 +174,9 @@ __device__ __forceinline__ void prep_key_head(const DnArgs& a, uint32_t t, uint3
       const bool ok = c < a.dk;
       qo[i] = ok ? conv_silu_loop(a, kh * a.dk + c, (int)t) : 0.0f;
       ko[i] = ok ? conv_silu_loop(a, key_el + kh * a.dk + c, (int)t) : 0.0f;
-      if (ok && last) {
-        shift_history(a, kh * a.dk + c);
-        shift_history(a, key_el + kh * a.dk + c);
+      if (ok && hist_dst) {
+        shift_history(a, kh * a.dk + c, (int)t, hist_dst);
+        shift_history(a, key_el + kh * a.dk + c, (int)t, hist_dst);
       }
     }
   }
@@ -201,10 +208,10 @@ __global__ __launch_bounds__(kThreads) void dn_conv_prepare_kernel(DnArgs a) {
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t key_el = a.key_heads * a.dk;
   float* row = a.conv_out + (size_t)t * a.channels;
-  const bool last = t + 1 == a.M && a.kernel > 1;
+  float* hist_dst = history_target(a, t);
   if (u < a.key_heads) {
     float cq[4], ck[4];
-    prep_key_head(a, t, u, lane, cq, ck, last);
+    prep_key_head(a, t, u, lane, cq, ck, hist_dst);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t c = lane + 64 * i;
@@ -217,7 +224,7 @@ __global__ __launch_bounds__(kThreads) void dn_conv_prepare_kernel(DnArgs a) {
     const uint32_t vh = u - a.key_heads;
     for (uint32_t c = lane; c < a.dv; c += 64) {
       const uint32_t ch = 2 * key_el + vh * a.dv + c;
-      row[ch] = conv_silu(a, ch, (int)t, last);
+      row[ch] = conv_silu(a, ch, (int)t, hist_dst);
     }
   }
 }
@@ -365,6 +372,14 @@ __global__ __launch_bounds__(kThreads) void dn_scan_kernel(DnArgs a) {
       }
       const float acc = delta_row_token<EPT>(s, kk, qq, g, beta, v_s[tt][r]);
       if (l == 0) o_s[tt][r] = acc;
+      if (t0 + tt < a.snap_rows && row_ok) {  // state image after this token
+        float* img = a.snap_s + (size_t)(t0 + tt) * a.snap_s_stride + srow;
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          const uint32_t j = l + kLanesPerRow * e;
+          if (j < a.dk) img[j] = s[e];
+        }
+      }
     }
     __syncthreads();  // every wave is done with this chunk's LDS
     for (uint32_t idx = threadIdx.x; idx < nt * kRowsPerWg; idx += kThreads) {
@@ -457,7 +472,7 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_kernel(DnArgs a) {
 
   if (wave == 0) {
     float cq[4], ck[4];
-    prep_key_head(a, 0, kh, lane, cq, ck, key_hist);
+    prep_key_head(a, 0, kh, lane, cq, ck, key_hist ? a.hist_out : nullptr);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t c = lane + 64 * i;
@@ -477,12 +492,12 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_kernel(DnArgs a) {
       for (int i = 0; i < kV; ++i) {
         const uint32_t c = lane + 64 * i;
         if (c < kStepRows * PASSES) v_s[c] = c < a.dv ? conv_finish(a, cv[i]) : 0.0f;
-        if (c < a.dv && a.kernel > 1) conv_store_history(a, 2 * key_el + vh * a.dv + c, cv[i]);
+        if (c < a.dv && a.kernel > 1) conv_store_history(a, 2 * key_el + vh * a.dv + c, cv[i], a.hist_out);
       }
     } else {
       for (uint32_t c = lane; c < kStepRows * PASSES; c += 64) {
         const uint32_t ch = 2 * key_el + vh * a.dv + c;
-        v_s[c] = c < a.dv ? conv_silu(a, ch, 0, a.kernel > 1) : 0.0f;
+        v_s[c] = c < a.dv ? conv_silu(a, ch, 0, a.kernel > 1 && c < a.dv ? a.hist_out : nullptr) : 0.0f;
       }
     }
   } else if (threadIdx.x == 128) {

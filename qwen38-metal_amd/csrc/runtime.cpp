@@ -140,6 +140,8 @@ const char* qm_status_string(qm_status status) {
     case QM_ERR_OUT_OF_MEMORY: return "QM_ERR_OUT_OF_MEMORY";
     case QM_ERR_MISALIGNED: return "QM_ERR_MISALIGNED";
     case QM_ERR_INVALID_ARGUMENT: return "QM_ERR_INVALID_ARGUMENT";
+    case QM_ERR_INVALID_SNAPSHOT: return "QM_ERR_INVALID_SNAPSHOT";
+    case QM_ERR_INVALID_SNAPSHOT_ROW: return "QM_ERR_INVALID_SNAPSHOT_ROW";
   }
   return "QM_ERR_UNKNOWN";
 }

@@ -29,6 +29,16 @@ struct qm_dn_state {
   float* rec = nullptr;
 };
 
+// Verification images: hist [rows][max(hist_elems, 1)], rec [rows][rec_elems].
+struct qm_dn_snapshots {
+  qm_runtime* rt = nullptr;
+  qm_dn_config cfg{};
+  uint32_t rows = 0;
+  size_t hist_elems = 0, hist_stride = 0, rec_elems = 0;
+  float* hist = nullptr;
+  float* rec = nullptr;
+};
+
 namespace {
 
 // validate_deltanet_config (metal_runtime.rs:9151-9168).
@@ -93,7 +103,8 @@ qm_status alloc_state(qm_runtime* rt, const qm_dn_config& cfg, qm_dn_state** out
 }
 
 qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, qm_dn_state* to, const float* qkv,
-              const float* z, const float* b, const float* a, uint32_t M, float eps, float* out) {
+              const float* z, const float* b, const float* a, uint32_t M, float eps, float* out,
+              qm_dn_snapshots* snaps = nullptr) {
   if (!rt || !w || !to || !qkv || !z || !b || !a || !out) return fail(QM_ERR_NULL_POINTER, "NULL argument");
   if (!from) from = to;
   if (M == 0) return fail(QM_ERR_EMPTY_DIMENSION, "DeltaNet prefill needs at least one token");
@@ -101,6 +112,11 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
     return fail(QM_ERR_INVALID_ARGUMENT, "weights and states must belong to this runtime");
   if (memcmp(&from->cfg, &w->cfg, sizeof(qm_dn_config)) != 0 || memcmp(&to->cfg, &w->cfg, sizeof(qm_dn_config)) != 0)
     return fail(QM_ERR_WRONG_LENGTH, "DeltaNet state was created for another configuration");
+  if (snaps) {
+    if (snaps->rt != rt || memcmp(&snaps->cfg, &w->cfg, sizeof(qm_dn_config)) != 0 || M - 1 > snaps->rows)
+      return fail(QM_ERR_INVALID_SNAPSHOT, "snapshot set has %u rows for a %u-row verification (or another model)",
+                  snaps->rows, M);
+  }
   const qm_dn_config& c = w->cfg;
   const size_t conv_bytes = (size_t)M * w->channels * sizeof(float);
   qm_status st = ensure_scratch(rt, conv_bytes);
@@ -130,6 +146,13 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
   d.s_out = to->rec;
   d.conv_out = (float*)rt->scratch;
   d.out = out;
+  if (snaps && M > 1) {
+    d.snap_hist = snaps->hist;
+    d.snap_s = snaps->rec;
+    d.snap_rows = M - 1;
+    d.snap_hist_stride = snaps->hist_stride;
+    d.snap_s_stride = snaps->rec_elems;
+  }
   DeviceGuard g(rt->device);
   hipError_t e = launch_deltanet(d, rt->stream);
   if (e != hipSuccess) return hip_check(e, "DeltaNet launch");
@@ -248,6 +271,78 @@ qm_status qm_dn_prefill(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_stat
                         const float* qkv, const float* z, const float* b, const float* a, uint32_t M, float epsilon,
                         float* out) {
   return run(rt, w, from, to, qkv, z, b, a, M, epsilon, out);
+}
+
+qm_status qm_dn_snapshots_create(qm_runtime* rt, const qm_dn_weights* w, uint32_t rows, qm_dn_snapshots** out) {
+  if (!rt || !w || !out) return fail(QM_ERR_NULL_POINTER, "NULL argument");
+  *out = nullptr;
+  if (rows == 0) return fail(QM_ERR_EMPTY_DIMENSION, "a snapshot set needs at least one row");
+  if (w->rt != rt) return fail(QM_ERR_INVALID_ARGUMENT, "weights belong to another runtime");
+  qm_dn_snapshots* s = new qm_dn_snapshots();
+  s->rt = rt;
+  s->cfg = w->cfg;
+  s->rows = rows;
+  s->hist_elems = (size_t)w->channels * (w->cfg.conv_kernel_size - 1);
+  s->hist_stride = s->hist_elems ? s->hist_elems : 1;  // the state's buffer size, so one-row sets can swap
+  s->rec_elems = (size_t)w->cfg.value_heads * w->cfg.value_head_dim * w->cfg.key_head_dim;
+  DeviceGuard g(rt->device);
+  hipError_t e = hipMalloc(&s->hist, (size_t)rows * s->hist_stride * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&s->rec, (size_t)rows * s->rec_elems * sizeof(float));
+  if (e == hipSuccess) e = hipMemsetAsync(s->hist, 0, (size_t)rows * s->hist_stride * sizeof(float), rt->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(s->rec, 0, (size_t)rows * s->rec_elems * sizeof(float), rt->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
+  if (e != hipSuccess) {
+    hipFree(s->hist);
+    hipFree(s->rec);
+    delete s;
+    return hip_check(e, "DeltaNet snapshot allocation");
+  }
+  *out = s;
+  return QM_OK;
+}
+
+void qm_dn_snapshots_destroy(qm_dn_snapshots* s) {
+  if (!s) return;
+  DeviceGuard g(s->rt->device);
+  hipStreamSynchronize(s->rt->stream);
+  hipFree(s->hist);
+  hipFree(s->rec);
+  delete s;
+}
+
+qm_status qm_dn_prefill_snapshots(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, qm_dn_state* to,
+                                  qm_dn_snapshots* snaps, const float* qkv, const float* z, const float* b,
+                                  const float* a, uint32_t M, float epsilon, float* out) {
+  if (!snaps) return fail(QM_ERR_NULL_POINTER, "snapshot set is NULL");
+  return run(rt, w, from, to, qkv, z, b, a, M, epsilon, out, snaps);
+}
+
+qm_status qm_dn_snapshot_restore(qm_dn_snapshots* s, uint32_t row, qm_dn_state* dst) {
+  if (!s || !dst) return fail(QM_ERR_NULL_POINTER, "NULL argument");
+  if (row >= s->rows) return fail(QM_ERR_INVALID_SNAPSHOT_ROW, "row %u of a %u-row snapshot set", row, s->rows);
+  if (dst->rt != s->rt || memcmp(&dst->cfg, &s->cfg, sizeof(qm_dn_config)) != 0)
+    return fail(QM_ERR_INVALID_SNAPSHOT, "state and snapshot set belong to different models or runtimes");
+  if (s->rows == 1) {
+    // Same buffer sizes as the state's: later work on the stream uses the
+    // exchanged pointers, earlier work already holds its own.
+    float* h = dst->hist[dst->cur];
+    dst->hist[dst->cur] = s->hist;
+    s->hist = h;
+    float* r = dst->rec;
+    dst->rec = s->rec;
+    s->rec = r;
+    return QM_OK;
+  }
+  DeviceGuard g(s->rt->device);
+  hipStream_t stream = s->rt->stream;
+  hipError_t e = hipSuccess;
+  if (s->hist_elems)
+    e = hipMemcpyAsync(dst->hist[dst->cur], s->hist + (size_t)row * s->hist_stride, s->hist_elems * sizeof(float),
+                       hipMemcpyDeviceToDevice, stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(dst->rec, s->rec + (size_t)row * s->rec_elems, s->rec_elems * sizeof(float),
+                       hipMemcpyDeviceToDevice, stream);
+  return hip_check(e, "DeltaNet snapshot restore");
 }
 
 }  // extern "C"

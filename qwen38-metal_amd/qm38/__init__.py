@@ -40,6 +40,7 @@ EXPORTS = [
     "qm_attn_decode", "qm_attn_prefill", "qm_attn_prepare",
     "qm_dn_weights_create", "qm_dn_weights_destroy", "qm_dn_state_create", "qm_dn_state_destroy",
     "qm_dn_state_clone", "qm_dn_state_read", "qm_dn_state_write", "qm_dn_step", "qm_dn_prefill",
+    "qm_dn_snapshots_create", "qm_dn_snapshots_destroy", "qm_dn_prefill_snapshots", "qm_dn_snapshot_restore",
 ]
 
 
@@ -124,6 +125,10 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "qm_dn_state_write": ([vp, vp, vp], i32),
         "qm_dn_step": ([vp, vp, vp, vp, vp, vp, vp, C.c_float, vp], i32),
         "qm_dn_prefill": ([vp, vp, vp, vp, vp, vp, vp, vp, u32, C.c_float, vp], i32),
+        "qm_dn_snapshots_create": ([vp, vp, u32, C.POINTER(vp)], i32),
+        "qm_dn_snapshots_destroy": ([vp], None),
+        "qm_dn_prefill_snapshots": ([vp, vp, vp, vp, vp, vp, vp, vp, vp, u32, C.c_float, vp], i32),
+        "qm_dn_snapshot_restore": ([vp, u32, vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -231,6 +236,14 @@ class Runtime:
         _check(self.lib.qm_dn_step(self.handle, weights.handle, state.handle, _ptr(qkv), _ptr(z), _ptr(b),
                                    _ptr(a), epsilon, _ptr(out)))
 
+    def deltanet_prefill_with_snapshots(self, weights, source, state, snapshots, qkv, z, b, a, rows: int,
+                                        epsilon: float, out) -> None:
+        """deltanet_prefill_from_with_snapshots: also records the state after
+        each of the first rows - 1 rows into `snapshots`."""
+        _check(self.lib.qm_dn_prefill_snapshots(self.handle, weights.handle, source.handle if source else None,
+                                                state.handle, snapshots.handle, _ptr(qkv), _ptr(z), _ptr(b),
+                                                _ptr(a), rows, epsilon, _ptr(out)))
+
     def deltanet_prefill(self, weights, state, qkv, z, b, a, rows: int, epsilon: float, out,
                          source=None) -> None:
         src = source.handle if source is not None else None
@@ -323,6 +336,12 @@ class DnWeights:
         except Exception:
             pass
 
+    def create_snapshots(self, rows: int) -> "DnSnapshots":
+        """create_deltanet_snapshots: room for `rows` verification state images."""
+        h = C.c_void_p()
+        _check(self.rt.lib.qm_dn_snapshots_create(self.rt.handle, self.handle, rows, C.byref(h)))
+        return DnSnapshots(self, h, rows)
+
     def create_state(self) -> "DnState":
         h = C.c_void_p()
         _check(self.rt.lib.qm_dn_state_create(self.rt.handle, self.handle, C.byref(h)))
@@ -372,3 +391,29 @@ class DnState:
         rec = None if rec is None else np.ascontiguousarray(rec, np.float32)
         _check(self.rt.lib.qm_dn_state_write(self.handle, hist.ctypes.data if hist is not None and hist.size else None,
                                              rec.ctypes.data if rec is not None else None))
+
+
+class DnSnapshots:
+    """MetalDeltaNetSnapshots: verification state images."""
+
+    def __init__(self, weights: DnWeights, handle, rows: int):
+        self.weights = weights
+        self.rt = weights.rt
+        self.handle = handle
+        self.rows = rows
+        self.rt._children.add(self)
+
+    def restore(self, row: int, state: DnState) -> None:
+        """restore_deltanet_snapshot: `state` becomes the state after row `row`."""
+        _check(self.rt.lib.qm_dn_snapshot_restore(self.handle, row, state.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            self.rt.lib.qm_dn_snapshots_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

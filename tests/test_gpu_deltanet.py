@@ -264,3 +264,112 @@ def test_rejects_bad_configs(rt, torch_dev):
         with pytest.raises(QmError, match="INVALID_DELTANET_CONFIG"):
             rt.create_deltanet_weights(cfg, np.zeros((ch, max(shape[4], 1)), np.float32), np.zeros(max(shape[1], 1)),
                                        np.zeros(max(shape[1], 1)), np.zeros(max(shape[3], 1)))
+
+
+# ---------------------------------------------------------------------------
+# Verification snapshots (MetalDeltaNetSnapshots; metal_runtime.rs:7201-7281,
+# 7998-8024; reference test at :11398-11570)
+# ---------------------------------------------------------------------------
+def _snap_prefill(rt, dev, w, src, dst, snaps, qkv, z, b, a, eps):
+    import torch
+    M = qkv.shape[0]
+    out = torch.full((M, w.config.value_heads * w.config.value_head_dim), float("nan"), dtype=torch.float32,
+                     device=dev)
+    rt.deltanet_prefill_with_snapshots(w, src, dst, snaps, to_dev(qkv, dev), to_dev(z, dev), to_dev(b, dev),
+                                       to_dev(a, dev), M, eps, out)
+    return from_dev(out)
+
+
+@pytest.mark.parametrize("kh,vh,dk,dv,ks", [(1, 1, 2, 2, 2), (2, 4, 64, 64, 4), (16, 32, 128, 128, 4),
+                                            (2, 2, 32, 32, 1), (1, 2, 16, 16, 6)])
+def test_snapshots_equal_step_states(rt, torch_dev, kh, vh, dk, dv, ks):
+    # Image r equals the state after r + 1 ordinary steps, bit for bit (the
+    # prefill path's arithmetic is the step's), and restoring it continues
+    # exactly as the stepped state does.
+    cfg, c = _cfg(kh, vh, dk, dv, ks)
+    M = 4
+    rng = np.random.default_rng(kh * 100 + dk + ks)
+    wts, acts = _synth(rng, c, M + 1)
+    w = rt.create_deltanet_weights(cfg, *wts)
+    snaps = w.create_snapshots(M - 1)
+    src, dst = w.create_state(), w.create_state()
+    pre = _snap_prefill(rt, torch_dev, w, src, dst, snaps, *(x[:M] for x in acts), 1e-6)
+    stepped = w.create_state()
+    outs = []
+    for r in range(M):
+        outs.append(_step(rt, torch_dev, w, stepped, *(x[r] for x in acts), 1e-6))
+        if r < M - 1:
+            img = w.create_state()
+            snaps.restore(r, img)
+            for x, y in zip(img.read(), stepped.read()):
+                np.testing.assert_array_equal(x, y)
+            # continuing from the restored image = continuing from the steps
+            nxt = _step(rt, torch_dev, w, img, *(x[r + 1] for x in acts), 1e-6)
+            ref = _step(rt, torch_dev, w, stepped.clone(), *(x[r + 1] for x in acts), 1e-6)
+            np.testing.assert_array_equal(nxt, ref)
+            img.close()
+    np.testing.assert_array_equal(pre, np.stack(outs))
+    for x, y in zip(dst.read(), stepped.read()):
+        np.testing.assert_array_equal(x, y)
+    # the source state is untouched
+    for x in src.read():
+        assert not np.any(x)
+
+
+def test_snapshot_reference_flow_and_single_row_swap(rt, torch_dev):
+    # The reference's flow (:11398-11570): 3-row verify with 2 images, restore
+    # rows 0 and 1; then the default one-intermediate-row verifier, whose
+    # restore swaps buffers.
+    cfg, c = _cfg(1, 1, 2, 2, 2)
+    rng = np.random.default_rng(11398)
+    wts, acts = _synth(rng, c, 3)
+    w = rt.create_deltanet_weights(cfg, *wts)
+    one = w.create_snapshots(1)
+    src, shadow = w.create_state(), w.create_state()
+    _snap_prefill(rt, torch_dev, w, src, shadow, one, *(x[:2] for x in acts), 1e-6)
+    expected = w.create_state()
+    _step(rt, torch_dev, w, expected, *(x[0] for x in acts), 1e-6)
+    live = w.create_state()
+    before = live.read()
+    one.restore(0, live)  # exchange
+    for x, y in zip(live.read(), expected.read()):
+        np.testing.assert_array_equal(x, y)
+    np.testing.assert_array_equal(
+        _step(rt, torch_dev, w, live, *(x[1] for x in acts), 1e-6),
+        _step(rt, torch_dev, w, expected, *(x[1] for x in acts), 1e-6))
+    # the set now holds the live state's former buffers, and can be reused
+    img = w.create_state()
+    one.restore(0, img)
+    for x, y in zip(img.read(), before):
+        np.testing.assert_array_equal(x, y)
+    _snap_prefill(rt, torch_dev, w, src, shadow, one, *(x[:2] for x in acts), 1e-6)
+    again = w.create_state()
+    one.restore(0, again)
+    for x, y in zip(again.read(), _step_state(rt, torch_dev, w, acts, 1)):
+        np.testing.assert_array_equal(x, y)
+
+
+def _step_state(rt, dev, w, acts, n):
+    st = w.create_state()
+    for r in range(n):
+        _step(rt, dev, w, st, *(x[r] for x in acts), 1e-6)
+    return st.read()
+
+
+def test_snapshot_errors(rt, torch_dev):
+    cfg, c = _cfg(1, 1, 4, 4, 4)
+    rng = np.random.default_rng(5)
+    wts, acts = _synth(rng, c, 4)
+    w = rt.create_deltanet_weights(cfg, *wts)
+    snaps = w.create_snapshots(2)
+    st = w.create_state()
+    with pytest.raises(QmError):  # 4 rows need 3 images
+        _snap_prefill(rt, torch_dev, w, None, st, snaps, *acts, 1e-6)
+    with pytest.raises(QmError):
+        snaps.restore(2, st)
+    with pytest.raises(QmError):
+        w.create_snapshots(0)
+    other_cfg, oc = _cfg(1, 1, 8, 8, 4)
+    ow = rt.create_deltanet_weights(other_cfg, *_synth(rng, oc, 1)[0])
+    with pytest.raises(QmError):
+        snaps.restore(0, ow.create_state())
