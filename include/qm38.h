@@ -57,7 +57,11 @@ typedef enum qm_status {
   QM_ERR_MISALIGNED = 17,           /* a device pointer violates the documented alignment */
   QM_ERR_INVALID_ARGUMENT = 18,     /* any other precondition */
   QM_ERR_INVALID_SNAPSHOT = 19,     /* MetalRuntimeError::InvalidDeltaNetSnapshot */
-  QM_ERR_INVALID_SNAPSHOT_ROW = 20  /* ::InvalidSnapshotRow */
+  QM_ERR_INVALID_SNAPSHOT_ROW = 20, /* ::InvalidSnapshotRow */
+  QM_ERR_MODEL_FORMAT = 21,         /* model::ModelFormatError (index, shard or header) */
+  QM_ERR_INVALID_TENSOR = 22        /* native::NativeError tensor variants (MissingTensor,
+                                       NotQuantizedWeight, InvalidQuantizedWeight,
+                                       InvalidAffineTensor, TensorByteLength) */
 } qm_status;
 
 /* Human-readable name of a status code (static storage). */
@@ -322,6 +326,50 @@ qm_status qm_dn_prefill_snapshots(qm_runtime* rt, const qm_dn_weights* w,
  * reference does; otherwise an asynchronous device copy on the runtime's
  * stream. */
 qm_status qm_dn_snapshot_restore(qm_dn_snapshots* snaps, uint32_t row, qm_dn_state* dst);
+
+/* ------------------------------------------------------------------ */
+/* MLX safetensors weight store (on-disk format of the Q4 checkpoints)  */
+/* ------------------------------------------------------------------ */
+
+/* Opens a model directory: model.safetensors.index.json (tensor -> shard) and
+ * the shards it names, memory-mapped read-only.  Every indexed tensor must be
+ * present in its shard with a data range inside the file; shard names must be
+ * plain relative paths; headers are at most 128 MiB.  Replaces
+ * open_mlx_safetensors_dir / read_safetensors_header / validate_tensor_range /
+ * resolve_shard (model.rs:136-197, 312-431).  Host only. */
+typedef struct qm_weight_store qm_weight_store;
+qm_status qm_store_open(const char* dir, qm_weight_store** out);
+void qm_store_close(qm_weight_store* store);
+uint32_t qm_store_tensor_count(const qm_weight_store* store);
+
+/* dtype as in the header ("U32", "BF16", ...), up to shape_cap dims. */
+qm_status qm_store_tensor_info(const qm_weight_store* store, const char* name, char* dtype,
+                               size_t dtype_cap, uint32_t* ndim, uint64_t* shape,
+                               uint32_t shape_cap, uint64_t* bytes);
+
+/* Copies one tensor's bytes into a new device allocation (free with
+ * qm_device_free); synchronous. */
+qm_status qm_store_upload(qm_runtime* rt, const qm_weight_store* store, const char* name,
+                          void** device_out, uint64_t* bytes);
+
+/* A Q4 matrix in HBM: weights u32 [out_rows][in_elems/8], scales and biases
+ * bf16 [out_rows][in_elems/64]; each pointer is a separate allocation (free
+ * with qm_device_free).  Use as a qm_q4_job's weights/scales/biases. */
+typedef struct qm_q4_matrix {
+  uint32_t* weights;
+  uint16_t* scales;
+  uint16_t* biases;
+  uint32_t out_rows;
+  uint32_t in_elems;
+} qm_q4_matrix;
+
+/* Validates `<base>.weight` (U32 [rows][K/8], K a non-zero multiple of 64)
+ * with `<base>.scales` / `<base>.biases` (BF16 [rows][K/64], exact byte
+ * lengths) and uploads the three tensors.  Replaces Q4AffineMatrix::
+ * from_store / from_tensors / validate_affine_tensor (native.rs:5384-5516)
+ * and the weight mapping of map_weight_store (metal_runtime.rs:955-984). */
+qm_status qm_store_upload_q4(qm_runtime* rt, const qm_weight_store* store,
+                             const char* weight_name, qm_q4_matrix* out);
 
 #ifdef __cplusplus
 }

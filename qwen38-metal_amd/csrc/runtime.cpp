@@ -142,6 +142,8 @@ const char* qm_status_string(qm_status status) {
     case QM_ERR_INVALID_ARGUMENT: return "QM_ERR_INVALID_ARGUMENT";
     case QM_ERR_INVALID_SNAPSHOT: return "QM_ERR_INVALID_SNAPSHOT";
     case QM_ERR_INVALID_SNAPSHOT_ROW: return "QM_ERR_INVALID_SNAPSHOT_ROW";
+    case QM_ERR_MODEL_FORMAT: return "QM_ERR_MODEL_FORMAT";
+    case QM_ERR_INVALID_TENSOR: return "QM_ERR_INVALID_TENSOR";
   }
   return "QM_ERR_UNKNOWN";
 }

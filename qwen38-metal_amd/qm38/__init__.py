@@ -41,6 +41,8 @@ EXPORTS = [
     "qm_dn_weights_create", "qm_dn_weights_destroy", "qm_dn_state_create", "qm_dn_state_destroy",
     "qm_dn_state_clone", "qm_dn_state_read", "qm_dn_state_write", "qm_dn_step", "qm_dn_prefill",
     "qm_dn_snapshots_create", "qm_dn_snapshots_destroy", "qm_dn_prefill_snapshots", "qm_dn_snapshot_restore",
+    "qm_store_open", "qm_store_close", "qm_store_tensor_count", "qm_store_tensor_info", "qm_store_upload",
+    "qm_store_upload_q4",
 ]
 
 
@@ -59,6 +61,12 @@ class Q4Job(C.Structure):
 class DnConfig(C.Structure):
     _fields_ = [("key_heads", C.c_uint32), ("value_heads", C.c_uint32), ("key_head_dim", C.c_uint32),
                 ("value_head_dim", C.c_uint32), ("conv_kernel_size", C.c_uint32)]
+
+
+class Q4Matrix(C.Structure):
+    """qm_q4_matrix: a Q4 matrix uploaded from a weight store."""
+    _fields_ = [("weights", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p),
+                ("out_rows", C.c_uint32), ("in_elems", C.c_uint32)]
 
 
 class RopeConfig(C.Structure):
@@ -125,6 +133,13 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "qm_dn_state_write": ([vp, vp, vp], i32),
         "qm_dn_step": ([vp, vp, vp, vp, vp, vp, vp, C.c_float, vp], i32),
         "qm_dn_prefill": ([vp, vp, vp, vp, vp, vp, vp, vp, u32, C.c_float, vp], i32),
+        "qm_store_open": ([C.c_char_p, C.POINTER(vp)], i32),
+        "qm_store_close": ([vp], None),
+        "qm_store_tensor_count": ([vp], u32),
+        "qm_store_tensor_info": ([vp, C.c_char_p, C.c_char_p, C.c_size_t, C.POINTER(u32), C.POINTER(C.c_uint64),
+                                  u32, C.POINTER(C.c_uint64)], i32),
+        "qm_store_upload": ([vp, vp, C.c_char_p, C.POINTER(vp), C.POINTER(C.c_uint64)], i32),
+        "qm_store_upload_q4": ([vp, vp, C.c_char_p, C.POINTER(Q4Matrix)], i32),
         "qm_dn_snapshots_create": ([vp, vp, u32, C.POINTER(vp)], i32),
         "qm_dn_snapshots_destroy": ([vp], None),
         "qm_dn_prefill_snapshots": ([vp, vp, vp, vp, vp, vp, vp, vp, vp, u32, C.c_float, vp], i32),
@@ -411,6 +426,82 @@ class DnSnapshots:
         if self.handle:
             self.rt.lib.qm_dn_snapshots_destroy(self.handle)
             self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class WeightStore:
+    """MLX safetensors model directory (qm_store_open; open_mlx_safetensors_dir,
+    model.rs:136-197).  Host-only until a tensor is uploaded."""
+
+    def __init__(self, directory, lib=None):
+        self.lib = lib or load()
+        h = C.c_void_p()
+        _check(self.lib.qm_store_open(os.fsencode(directory), C.byref(h)))
+        self.handle = h
+
+    def __len__(self) -> int:
+        return int(self.lib.qm_store_tensor_count(self.handle))
+
+    def info(self, name: str):
+        """(dtype, shape, bytes) of one tensor."""
+        dt = C.create_string_buffer(16)
+        nd = C.c_uint32()
+        shape = (C.c_uint64 * 8)()
+        nbytes = C.c_uint64()
+        _check(self.lib.qm_store_tensor_info(self.handle, name.encode(), dt, 16, C.byref(nd), shape, 8,
+                                             C.byref(nbytes)))
+        return dt.value.decode(), tuple(int(shape[i]) for i in range(nd.value)), int(nbytes.value)
+
+    def upload(self, rt: "Runtime", name: str) -> "DeviceBuffer":
+        p = C.c_void_p()
+        n = C.c_uint64()
+        _check(self.lib.qm_store_upload(rt.handle, self.handle, name.encode(), C.byref(p), C.byref(n)))
+        return DeviceBuffer(rt, p.value, int(n.value))
+
+    def upload_q4(self, rt: "Runtime", weight_name: str) -> Q4Job:
+        """Validated Q4 upload (Q4AffineMatrix::from_store); returns a job whose
+        device buffers live as long as it does."""
+        m = Q4Matrix()
+        _check(self.lib.qm_store_upload_q4(rt.handle, self.handle, weight_name.encode(), C.byref(m)))
+        bufs = tuple(DeviceBuffer(rt, p, 0) for p in (m.weights, m.scales, m.biases))
+        j = Q4Job(m.weights, m.scales, m.biases, m.out_rows)
+        j._refs = bufs
+        j.in_elems = m.in_elems
+        return j
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.qm_store_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DeviceBuffer:
+    """A device allocation made by the library (freed with qm_device_free)."""
+
+    def __init__(self, rt: "Runtime", ptr: int, nbytes: int):
+        self.rt = rt
+        self.ptr = ptr
+        self.nbytes = nbytes
+        rt._children.add(self)
+
+    def data_ptr(self) -> int:
+        return self.ptr
+
+    def close(self) -> None:
+        if self.ptr:
+            self.rt.lib.qm_device_free(self.rt.handle, self.ptr)
+            self.ptr = None
 
     def __del__(self):
         try:
