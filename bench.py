@@ -22,6 +22,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
 import sys
@@ -401,6 +403,45 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> int:
     return 0
 
 
+def _short_kernel_name(name: str) -> str:
+    n = name.replace("qm::(anonymous namespace)::", "").replace("(anonymous namespace)::", "")
+    return n.replace("(qm::DecodeArgs)", "(DecodeArgs)").replace("(qm::GemmArgs)", "(GemmArgs)")
+
+
+def stats_summary(prof_dir: str) -> int:
+    """profiles/bench_all_legs_kernel_stats.txt from a rocprofv3 --kernel-trace --stats run of bench.py."""
+    files = glob.glob(os.path.join(prof_dir, "**", "*kernel_stats.csv"), recursive=True)
+    if not files:
+        raise FileNotFoundError(f"no *kernel_stats.csv under {prof_dir}")
+    with open(files[0]) as f:
+        rows = list(csv.DictReader(f))
+    lines = [
+        "# rocprofv3 kernel statistics: bench.py (all legs, 20 timed steps)",
+        "#",
+        "# command (repo root, MI355X, one GPU):",
+        "#   rocprofv3 --kernel-trace --stats -d gpurun_out/prof -o bench --output-format csv -- python3 -u bench.py "
+        "--no-cpu --steps 20",
+        "#   python bench.py --stats-from gpurun_out/prof",
+        "#",
+        "# Per-kernel averages mix the legs that launch the same template (q8_attn_kernel<128,true> is the",
+        "# causal prefill, including the 32K/128K cache fills of the attention legs; q4_gemm_kernel serves",
+        "# M = 512 and 2048; q8_decode_kernel<128> serves the 32K single-sequence and ragged batch-8 legs).",
+        "# The gate+up decode kernel (q4_decode_kernel<2, 1, true, true, true>, M = 1) is the bench's",
+        "# roofline kernel: its average here agrees with bench.py's avg_launch_us for that launch.",
+        "",
+        f"{'kernel':<100} {'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'pct':>7}",
+    ]
+    for r in sorted(rows, key=lambda r: -float(r["Percentage"])):
+        lines.append(f"{_short_kernel_name(r['Name'])[:100]:<100} {int(r['Calls']):>6} "
+                     f"{float(r['AverageNs']) / 1e3:>10.2f} {float(r['MinNs']) / 1e3:>10.2f} "
+                     f"{float(r['MaxNs']) / 1e3:>10.2f} {float(r['Percentage']):>7.3f}")
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "bench_all_legs_kernel_stats.txt")
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print(path)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -415,7 +456,12 @@ def main() -> int:
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn the two --traffic-probe counter runs (rocprofv3 csv output directories) "
                          "into profiles/q4_decode_gateup_traffic.json (no GPU needed)")
+    ap.add_argument("--stats-from", metavar="PROF_DIR",
+                    help="turn a rocprofv3 --kernel-trace --stats run of bench.py into "
+                         "profiles/bench_all_legs_kernel_stats.txt (no GPU needed)")
     args = ap.parse_args()
+    if args.stats_from:
+        return stats_summary(args.stats_from)
     if args.traffic_from:
         return traffic_summary(*args.traffic_from)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
