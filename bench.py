@@ -423,7 +423,7 @@ def stats_summary(prof_dir: str) -> int:
         "--no-cpu --steps 20",
         "#   python bench.py --stats-from gpurun_out/prof",
         "#",
-        "# Per-kernel averages mix the legs that launch the same template (q8_attn_kernel<128,true> is the",
+        "# Per-kernel averages mix the legs that launch the same template (q8_prefill_kernel<128,2> is the",
         "# causal prefill, including the 32K/128K cache fills of the attention legs; q4_gemm_kernel serves",
         "# M = 512 and 2048; q8_decode_kernel<128> serves the 32K single-sequence and ragged batch-8 legs).",
         "# The gate+up decode kernel (q4_decode_kernel<2, 1, true, true, true>, M = 1) is the bench's",

@@ -11,9 +11,10 @@
 //    FLT_MIN), q = (int8) round(clamp(x / s, -127, 127)) with IEEE division
 //    and round-half-away-from-zero, and writes page-table entries of pages
 //    materialised by this append.
-//  * q8_attn_kernel: flash-decode over Q8 pages.  A wave owns one KV head and
-//    the GQA group of <= 16 query heads sharing it (decode), or 16 (row, head)
-//    columns (causal prefill).  Per 16-token page:
+//  * q8_prefill_kernel (causal prefill) and q8_decode_kernel (decode):
+//    flash attention over Q8 pages.  A wave owns one KV head and the GQA group
+//    of <= 16 query heads sharing it (decode), or CB blocks of 16 (row, head)
+//    columns (prefill).  Per 16-token page:
 //      S^T = K Q^T on MFMA 16x16x32 (K bytes -> bf16 of k+128 exactly, the
 //      +128 is removed with a per-head correction),
 //      online softmax in fp32 (exp2 domain),
@@ -24,6 +25,7 @@
 //    Decode splits the pages of a sequence over workgroups (4 waves each,
 //    combined in LDS); split partials are merged by q8_combine_kernel.
 #include <float.h>
+#include <stdlib.h>
 
 #include "attention.h"
 #include "common.h"
@@ -110,250 +112,6 @@ __device__ __forceinline__ u32x2 q8x4_to_bf16_biased(uint32_t w) {
   r.x = perm_b32(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
   r.y = perm_b32(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
   return r;
-}
-
-template <int D, bool PREFILL>
-__global__ __launch_bounds__(256) void q8_attn_kernel(AttnArgs args) {
-  constexpr int kWaves = 4;
-  constexpr int kDB = D / 16;   // 16-wide d blocks of O^T
-  constexpr int kKS = D / 32;   // QK k-steps
-  __shared__ float red_o[kWaves][D][16];
-  __shared__ float red_m[kWaves][16], red_l[kWaves][16], red_p[kWaves][16];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int col = lane & 15;   // head column (decode) / (row, head) column (prefill)
-  const int kq = lane >> 4;
-  const uint32_t H = args.heads;
-  const uint32_t KVH = args.kv_heads;
-  const uint32_t gh = H / KVH;  // heads per KV head (<= 16)
-
-  // ---- work unit -------------------------------------------------------------
-  uint32_t b = 0, kvh, p_begin, p_end, row_base = 0;
-  const uint32_t unit = blockIdx.x;
-  if (!PREFILL) {
-    while (b + 1 < args.n_seqs && unit >= args.seqs[b + 1].unit_begin) ++b;
-    const uint32_t u = unit - args.seqs[b].unit_begin;
-    kvh = u % KVH;
-    const uint32_t split = u / KVH;
-    const uint32_t pages = (args.seqs[b].len + 15) / 16;
-    p_begin = split * args.pages_per_split;
-    p_end = min(pages, p_begin + args.pages_per_split);
-  } else {
-    // blockIdx.x = kvh * row_blocks + rb; each wave owns 16/gh rows.
-    const uint32_t rows_per_wave = 16 / gh;
-    const uint32_t row_blocks = (args.rows + rows_per_wave * kWaves - 1) / (rows_per_wave * kWaves);
-    kvh = unit / row_blocks;
-    row_base = ((unit % row_blocks) * kWaves + wave) * rows_per_wave;
-    p_begin = 0;
-    const uint32_t last_row = min(args.rows, row_base + rows_per_wave) - 1;
-    const uint32_t vis_max = min(args.start + last_row + 1, args.seqs[0].len);
-    p_end = row_base < args.rows ? (vis_max + 15) / 16 : 0;
-  }
-  const AttnSeq& sq = args.seqs[b];
-
-  // Column -> (query row, head).
-  const uint32_t cr = PREFILL ? col / gh : 0;        // row within the wave's rows
-  const uint32_t ch = PREFILL ? col % gh : col;      // head within the group
-  const bool col_ok = PREFILL ? (ch < gh && row_base + cr < args.rows && col < (int)((16 / gh) * gh))
-                              : ((uint32_t)col < gh);
-  const uint32_t qrow = PREFILL ? row_base + cr : b;
-  const uint32_t head = kvh * gh + ch;
-  const uint32_t visible = PREFILL ? min(args.start + qrow + 1, sq.len) : sq.len;
-
-  // ---- Q operand (B of QK^T): lane (col, kq) holds q[head][32kq + 8j .. +7]
-  u32x4 qb[kKS];
-  float qsum = 0.0f;
-  {
-    const uint16_t* qp = args.q + ((size_t)qrow * H + head) * D;
-#pragma unroll
-    for (int jj = 0; jj < kKS; ++jj) {
-      u32x4 v = col_ok ? *(const u32x4*)(qp + D / 4 * kq + 8 * jj) : u32x4{0u, 0u, 0u, 0u};
-      qb[jj] = v;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) qsum += bf16_to_f32(v[e] & 0xFFFFu) + bf16_to_f32(v[e] >> 16);
-    }
-    qsum += __shfl_xor(qsum, 16);
-    qsum += __shfl_xor(qsum, 32);
-  }
-  const float qcorr = 128.0f * qsum;
-  const float sm_scale = kLog2e / sqrtf((float)D);
-
-  floatx4 o[kDB];
-#pragma unroll
-  for (int i = 0; i < kDB; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_lane = 0.0f, ps_lane = 0.0f;
-
-  const size_t kv_page_stride = (size_t)KVH * 16 * D;
-  const int tok = lane & 15;  // A-operand row: token of QK^T, d row of PV^T
-
-  // One page's operands in registers: lane (tok, kq) holds K[tok][D/4*kq ..
-  // + D/4) (16 B per two QK k-steps), V^T[16 db + tok][4 kq .. 4 kq + 3] for
-  // every d block, and the scales of tokens 4 kq .. 4 kq + 3.
-  struct PageRegs {
-    u32x4 k[kKS / 2];
-    uint32_t v[kDB];
-    floatx4 ks, vs;
-  };
-  auto load_page = [&](int32_t phys, PageRegs& r) {
-    const size_t pbase = (size_t)phys * kv_page_stride;
-    const int8_t* kr = sq.k + pbase + (size_t)kvh * 16 * D + tok * D + D / 4 * kq;
-#pragma unroll
-    for (int j = 0; j < kKS / 2; ++j) r.k[j] = *(const u32x4*)(kr + 16 * j);
-    const int8_t* vr = sq.v + pbase + (size_t)kvh * D * 16 + tok * 16 + 4 * kq;
-#pragma unroll
-    for (int db = 0; db < kDB; ++db) r.v[db] = *(const uint32_t*)(vr + 256 * db);
-    const size_t sbase = ((size_t)phys * KVH + kvh) * 16 + 4 * kq;
-    r.ks = *(const floatx4*)(sq.ks + sbase);
-    r.vs = *(const floatx4*)(sq.vs + sbase);
-  };
-  auto process_page = [&](uint32_t p, const PageRegs& r) {
-    // S^T[token][col] over D in kKS steps of 32.
-    floatx4 s4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < kKS / 2; ++j) {
-      const u32x4 kb = r.k[j];
-      const u32x2 l0 = q8x4_to_bf16_biased(kb.x), h0 = q8x4_to_bf16_biased(kb.y);
-      const u32x2 l1 = q8x4_to_bf16_biased(kb.z), h1 = q8x4_to_bf16_biased(kb.w);
-      s4 = mfma16x16x32(u32x4{l0.x, l0.y, h0.x, h0.y}, qb[2 * j], s4);
-      s4 = mfma16x16x32(u32x4{l1.x, l1.y, h1.x, h1.y}, qb[2 * j + 1], s4);
-    }
-    float sc[4];
-    float bmax = -INFINITY;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const uint32_t t = p * 16 + 4 * kq + rr;
-      const bool ok = col_ok && t < visible;
-      sc[rr] = ok ? (s4[rr] - qcorr) * r.ks[rr] * sm_scale : -INFINITY;
-      bmax = fmaxf(bmax, sc[rr]);
-    }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-    const float m_new = fmaxf(m_run, bmax);
-    const float corr = m_new == -INFINITY ? 1.0f : exp2f(m_run - m_new);
-    m_run = m_new;
-    float pw[4];
-    float psum = 0.0f, pvsum = 0.0f;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const float e = sc[rr] == -INFINITY ? 0.0f : exp2f(sc[rr] - m_new);
-      psum += e;
-      pw[rr] = sc[rr] == -INFINITY ? 0.0f : e * r.vs[rr];  // fold the V scale (never NaN for masked rows)
-      pvsum += pw[rr];
-    }
-    l_lane = l_lane * corr + psum;
-    ps_lane = ps_lane * corr + pvsum;
-    // P'^T as bf16 hi + lo (B operand: k = tokens 4kq..4kq+3, column col).
-    uint32_t hi[4], lo[4];
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      hi[rr] = __float_as_uint(pw[rr]) & 0xFFFF0000u;
-      lo[rr] = f32_to_bf16(pw[rr] - __uint_as_float(hi[rr]));
-    }
-    const u32x2 phi = {(hi[0] >> 16) | hi[1], (hi[2] >> 16) | hi[3]};
-    const u32x2 plo = {lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
-#pragma unroll
-    for (int db = 0; db < kDB; ++db) {
-      const u32x2 va = q8x4_to_bf16_biased(r.v[db]);
-      floatx4 od = o[db] * corr;
-      od = mfma16x16x16(va, phi, od);
-      o[db] = mfma16x16x16(va, plo, od);
-    }
-  };
-
-  // Pages of this wave, two register sets deep: the loads of the next page
-  // are in flight while the current one is reduced, and the page-table entry
-  // of the page after that is fetched one step earlier still.
-  const uint32_t step = PREFILL ? 1 : kWaves;
-  uint32_t p = p_begin + (PREFILL ? 0 : wave);
-  PageRegs ra, rb;
-  int32_t phys_next = 0;
-  if (p < p_end) load_page(sq.pt[p], ra);
-  if (p + step < p_end) phys_next = sq.pt[p + step];
-  while (p < p_end) {
-    if (p + step < p_end) {
-      load_page(phys_next, rb);
-      if (p + 2 * step < p_end) phys_next = sq.pt[p + 2 * step];
-    }
-    process_page(p, ra);
-    p += step;
-    if (p >= p_end) break;
-    if (p + step < p_end) {
-      load_page(phys_next, ra);
-      if (p + 2 * step < p_end) phys_next = sq.pt[p + 2 * step];
-    }
-    process_page(p, rb);
-    p += step;
-  }
-
-  // ---- combine the waves of the workgroup (decode) / finish (prefill) ------
-  float l_tot = l_lane + __shfl_xor(l_lane, 16);
-  l_tot += __shfl_xor(l_tot, 32);
-  float ps_tot = ps_lane + __shfl_xor(ps_lane, 16);
-  ps_tot += __shfl_xor(ps_tot, 32);
-
-  if (PREFILL) {
-    // O^T lane layout: column col, rows d = 16 db + 4 kq + r.
-    if (col_ok) {
-      const float inv = 1.0f / fmaxf(l_tot, FLT_MIN);
-      const size_t obase = ((size_t)qrow * H + head) * D;
-#pragma unroll
-      for (int db = 0; db < kDB; ++db)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t d = 16 * db + 4 * kq + r;
-          float v = (o[db][r] - 128.0f * ps_tot) * inv;
-          if (args.gate) v *= sigmoid_f(bf16_to_f32(args.gate[obase + d]));
-          args.o[obase + d] = f32_to_bf16(v);
-        }
-    }
-    return;
-  }
-
-#pragma unroll
-  for (int db = 0; db < kDB; ++db)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) red_o[wave][16 * db + 4 * kq + r][col] = o[db][r];
-  if (kq == 0) {
-    red_m[wave][col] = m_run;
-    red_l[wave][col] = l_tot;
-    red_p[wave][col] = ps_tot;
-  }
-  __syncthreads();
-
-  const uint32_t nsplit = sq.nsplit;
-  const uint32_t split = (unit - sq.unit_begin) / KVH;
-  for (uint32_t e = threadIdx.x; e < (uint32_t)D * 16; e += 256) {
-    const uint32_t c = e % 16, d = e / 16;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, red_m[w][c]);
-    float L = 0.0f, P = 0.0f, O = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float f = red_m[w][c] == -INFINITY ? 0.0f : exp2f(red_m[w][c] - mx);
-      L += f * red_l[w][c];
-      P += f * red_p[w][c];
-      O += f * red_o[w][d][c];
-    }
-    O -= 128.0f * P;  // V was accumulated as v + 128
-    if (c >= gh) continue;
-    const uint32_t hh = kvh * gh + c;
-    if (nsplit == 1) {
-      float v = O / fmaxf(L, FLT_MIN);
-      const size_t oi = ((size_t)b * H + hh) * D + d;
-      if (args.gate) v *= sigmoid_f(bf16_to_f32(args.gate[oi]));
-      args.o[oi] = f32_to_bf16(v);
-    } else {
-      // partial[(seq split row)][head][D + 2]: O (unnormalised), then m, l.
-      float* part = args.partials + ((size_t)(sq.part_begin + split) * H + hh) * (D + 2);
-      part[d] = O;
-      if (d == 0) {
-        part[D] = mx;
-        part[D + 1] = L;
-      }
-    }
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -845,11 +603,252 @@ __global__ __launch_bounds__(256) void q8_combine_kernel(AttnArgs args) {
   }
 }
 
+// Causal prefill: blockIdx.x = rb * KVH + kvh.  A wave owns CB column
+// blocks of 16 (row, head) columns, i.e. CB * 16 / gh query rows of one KV
+// head, and streams the pages its last row can see through two register
+// sets.  Each page's K and V are unpacked once into MFMA A operands and serve
+// all CB blocks: K/V traffic per column falls by CB.
+template <int D, int CB>
+__global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
+  constexpr int kWaves = 4;
+  constexpr int kDB = D / 16;  // 16-wide d blocks of O^T
+  constexpr int kKS = D / 32;  // QK k-steps
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15;  // (row, head) column within a block
+  const int kq = lane >> 4;
+  const uint32_t H = args.heads, KVH = args.kv_heads, gh = H / KVH;  // gh <= 16
+
+  const uint32_t rows_per_block = 16 / gh, rows_per_wave = CB * rows_per_block;
+  const uint32_t row_blocks = (args.rows + rows_per_wave * kWaves - 1) / (rows_per_wave * kWaves);
+  // KV head = blockIdx % KVH: workgroups are dealt round-robin to the 8 XCDs,
+  // so every row block of one KV head runs on the same XCD(s) and its pages
+  // (1.5 MiB per head at 6K tokens, d = 128) stay in that XCD's L2.
+  const uint32_t kvh = blockIdx.x % KVH;
+  const uint32_t row_base = ((blockIdx.x / KVH) * kWaves + wave) * rows_per_wave;
+  const AttnSeq& sq = args.seqs[0];
+  const uint32_t last_row = min(args.rows, row_base + rows_per_wave) - 1;
+  const uint32_t vis_max = min(args.start + last_row + 1, sq.len);
+  const uint32_t p_end = row_base < args.rows ? (vis_max + 15) / 16 : 0;
+
+  const uint32_t ch = col % gh, cr = col / gh;
+  const uint32_t head = kvh * gh + ch;
+  bool col_ok[CB];
+  uint32_t qrow[CB], visible[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    qrow[cb] = row_base + cb * rows_per_block + cr;
+    col_ok[cb] = (uint32_t)col < rows_per_block * gh && qrow[cb] < args.rows;
+    visible[cb] = min(args.start + qrow[cb] + 1, sq.len);
+  }
+
+  // Q operands (B of QK^T) in fp16: lane (col, kq) of block cb holds
+  // q[qrow][head][D/4 kq + 8 j .. + 7] in the element order d0,d2,d1,d3,
+  // d4,d6,d5,d7 that the int8 -> fp16 unpack of K produces.  bf16 -> fp16 is
+  // exact within fp16's range.  K enters as 1024 + (k + 128): 1152 * sum(q)
+  // is subtracted from every score.
+  u32x4 qb[CB][kKS];
+  float qcorr[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    const uint16_t* qp = args.q + ((size_t)qrow[cb] * H + head) * D;
+    float qsum = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < kKS; ++jj) {
+      const u32x4 v = col_ok[cb] ? *(const u32x4*)(qp + D / 4 * kq + 8 * jj) : u32x4{0u, 0u, 0u, 0u};
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f[2 * e] = bf16_to_f32(v[e] & 0xFFFFu);
+        f[2 * e + 1] = bf16_to_f32(v[e] >> 16);
+      }
+      const int order[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+      uint32_t h[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const _Float16 x = (_Float16)f[order[e]];
+        qsum += (float)x;
+        h[e] = __builtin_bit_cast(uint16_t, x);
+      }
+      qb[cb][jj] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    }
+    qsum += __shfl_xor(qsum, 16);
+    qsum += __shfl_xor(qsum, 32);
+    qcorr[cb] = 1152.0f * qsum;
+  }
+  const float sm_scale = kLog2e / sqrtf((float)D);
+
+  floatx4 o[CB][kDB];
+  float m_run[CB], l_lane[CB], ps_lane[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+    for (int i = 0; i < kDB; ++i) o[cb][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    m_run[cb] = -INFINITY;
+    l_lane[cb] = 0.0f;
+    ps_lane[cb] = 0.0f;
+  }
+
+  const size_t kv_page_stride = (size_t)KVH * 16 * D;
+  const int tok = lane & 15;  // A-operand row: token of QK^T, d row of PV^T
+
+  // One page's operands in registers: lane (tok, kq) holds K[tok][D/4*kq ..
+  // + D/4) (16 B per two QK k-steps), V^T[16 db + tok][4 kq .. 4 kq + 3] for
+  // every d block, and the scales of tokens 4 kq .. 4 kq + 3.
+  struct PageRegs {
+    u32x4 k[kKS / 2];
+    uint32_t v[kDB];
+    floatx4 ks, vs;
+  };
+  auto load_page = [&](int32_t phys, PageRegs& r) __attribute__((always_inline)) {
+    const size_t pbase = (size_t)phys * kv_page_stride;
+    const int8_t* kr = sq.k + pbase + (size_t)kvh * 16 * D + tok * D + D / 4 * kq;
+#pragma unroll
+    for (int j = 0; j < kKS / 2; ++j) r.k[j] = *(const u32x4*)(kr + 16 * j);
+    const int8_t* vr = sq.v + pbase + (size_t)kvh * D * 16 + tok * 16 + 4 * kq;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) r.v[db] = *(const uint32_t*)(vr + 256 * db);
+    const size_t sbase = ((size_t)phys * KVH + kvh) * 16 + 4 * kq;
+    r.ks = *(const floatx4*)(sq.ks + sbase);
+    r.vs = *(const floatx4*)(sq.vs + sbase);
+  };
+  auto process_page = [&](uint32_t p, const PageRegs& r) __attribute__((always_inline)) {
+    // K as fp16 of 1024 + (k + 128) (one AND-OR per pair), unpacked once for
+    // every block.
+    u32x4 ka[kKS];
+#pragma unroll
+    for (int j = 0; j < kKS / 2; ++j) {
+      const u32x4 kb = r.k[j];
+      const u32x2 l0 = q8x4_to_f16_biased(kb.x), h0 = q8x4_to_f16_biased(kb.y);
+      const u32x2 l1 = q8x4_to_f16_biased(kb.z), h1 = q8x4_to_f16_biased(kb.w);
+      ka[2 * j] = u32x4{l0.x, l0.y, h0.x, h0.y};
+      ka[2 * j + 1] = u32x4{l1.x, l1.y, h1.x, h1.y};
+    }
+    u32x2 va[kDB];
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) va[db] = q8x4_to_bf16_biased(r.v[db]);
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      // S^T[token][col] over D in kKS steps of 32.
+      floatx4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < kKS; ++j) s4 = mfma16x16x32_f16(ka[j], qb[cb][j], s4);
+      float sc[4];
+      float bmax = -INFINITY;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const uint32_t t = p * 16 + 4 * kq + rr;
+        const bool ok = col_ok[cb] && t < visible[cb];
+        sc[rr] = ok ? (s4[rr] - qcorr[cb]) * r.ks[rr] * sm_scale : -INFINITY;
+        bmax = fmaxf(bmax, sc[rr]);
+      }
+      bmax = max4_across_kq(bmax);
+      // Lazy rescaling: the reference maximum moves only when a score exceeds
+      // it by more than 2^8, so exp2(s - m) <= 256 stays exact in fp32 and the
+      // pass over every accumulator is rare; the final division by l removes
+      // the choice of reference.
+      const float m_new = bmax > m_run[cb] + 8.0f ? bmax : m_run[cb];
+      const bool moved = m_new != m_run[cb];
+      const float corr = moved ? exp2f(m_run[cb] - m_new) : 1.0f;
+      m_run[cb] = m_new;
+      float pw[4];
+      float psum = 0.0f, pvsum = 0.0f;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const float e = sc[rr] == -INFINITY ? 0.0f : exp2f(sc[rr] - m_new);
+        psum += e;
+        pw[rr] = sc[rr] == -INFINITY ? 0.0f : e * r.vs[rr];  // fold the V scale (never NaN for masked rows)
+        pvsum += pw[rr];
+      }
+      l_lane[cb] = l_lane[cb] * corr + psum;
+      ps_lane[cb] = ps_lane[cb] * corr + pvsum;
+      // P'^T as bf16 hi + lo (B operand: k = tokens 4kq..4kq+3, column col).
+      uint32_t hi[4], lo[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        hi[rr] = __float_as_uint(pw[rr]) & 0xFFFF0000u;
+        lo[rr] = f32_to_bf16(pw[rr] - __uint_as_float(hi[rr]));
+      }
+      const u32x2 phi = {(hi[0] >> 16) | hi[1], (hi[2] >> 16) | hi[3]};
+      const u32x2 plo = {lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
+      if (__builtin_amdgcn_ballot_w64(moved)) {
+#pragma unroll
+        for (int db = 0; db < kDB; ++db) o[cb][db] *= corr;
+      }
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) {
+        const floatx4 od = mfma16x16x16(va[db], phi, o[cb][db]);
+        o[cb][db] = mfma16x16x16(va[db], plo, od);
+      }
+    }
+  };
+
+  // Two register sets deep: the next page's loads are in flight while the
+  // current one is reduced; its page-table entry is read a step earlier.
+  uint32_t p = 0;
+  PageRegs ra, rb;
+  int32_t phys_next = 0;
+  if (p < p_end) load_page(sq.pt[p], ra);
+  if (p + 1 < p_end) phys_next = sq.pt[p + 1];
+  while (p < p_end) {
+    if (p + 1 < p_end) {
+      load_page(phys_next, rb);
+      if (p + 2 < p_end) phys_next = sq.pt[p + 2];
+    }
+    process_page(p, ra);
+    ++p;
+    if (p >= p_end) break;
+    if (p + 1 < p_end) {
+      load_page(phys_next, ra);
+      if (p + 2 < p_end) phys_next = sq.pt[p + 2];
+    }
+    process_page(p, rb);
+    ++p;
+  }
+
+  // O^T lane layout: column col, rows d = 16 db + 4 kq + r.
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    float l_tot = l_lane[cb] + __shfl_xor(l_lane[cb], 16);
+    l_tot += __shfl_xor(l_tot, 32);
+    float ps_tot = ps_lane[cb] + __shfl_xor(ps_lane[cb], 16);
+    ps_tot += __shfl_xor(ps_tot, 32);
+    if (!col_ok[cb]) continue;
+    const float inv = 1.0f / fmaxf(l_tot, FLT_MIN);
+    const size_t obase = ((size_t)qrow[cb] * H + head) * D;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t d = 16 * db + 4 * kq + r;
+        float v = (o[cb][db][r] - 128.0f * ps_tot) * inv;  // V was accumulated as v + 128
+        if (args.gate) v *= sigmoid_f(bf16_to_f32(args.gate[obase + d]));
+        args.o[obase + d] = f32_to_bf16(v);
+      }
+  }
+}
+
+template <int D, int CB>
+hipError_t launch_prefill(const AttnArgs& a, hipStream_t st) {
+  const uint32_t gh = a.heads / a.kv_heads;
+  const uint32_t rows_per_wg = CB * (16 / gh) * 4;
+  const uint32_t units = a.kv_heads * ((a.rows + rows_per_wg - 1) / rows_per_wg);
+  hipLaunchKernelGGL((q8_prefill_kernel<D, CB>), dim3(units), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
 template <int D>
 hipError_t launch_attn_d(const AttnArgs& a, uint32_t units, bool need_combine, hipStream_t st) {
   if (a.prefill) {
-    hipLaunchKernelGGL((q8_attn_kernel<D, true>), dim3(units), dim3(256), 0, st, a);
-    return hipGetLastError();
+    // Column blocks per wave: two up to D = 128 (registers for both blocks'
+    // accumulators), one above; QM38_PREFILL_CB overrides (1, 2, 4).
+    const char* env = getenv("QM38_PREFILL_CB");
+    int cb = env ? atoi(env) : (D <= 128 ? 2 : 1);
+    if (D > 128 && cb > 2) cb = 2;
+    if (cb >= 4 && D <= 128) return launch_prefill<D, (D <= 128 ? 4 : 2)>(a, st);
+    if (cb >= 2) return launch_prefill<D, 2>(a, st);
+    return launch_prefill<D, 1>(a, st);
   }
   hipLaunchKernelGGL(q8_decode_kernel<D>, dim3(units), dim3(256), 0, st, a);
   if (need_combine)
