@@ -382,11 +382,10 @@ qm_status qm_attn_prefill(qm_runtime* rt, qm_kv* seq, const uint16_t* q, const u
   at.rows = M;
   at.start = start;
   at.seqs[0] = sd;
-  const uint32_t gh = H / KVH;
-  const uint32_t rows_per_wg = (16 / gh) * 4;
-  const uint32_t units = KVH * ((M + rows_per_wg - 1) / rows_per_wg);
   hipError_t e = launch_q8_append(ap, M, rt->stream);
-  if (e == hipSuccess) e = launch_q8_attention(at, units, false, rt->stream);
+  // The prefill launcher sizes its own grid (rows per workgroup depend on the
+  // kernel's column blocks).
+  if (e == hipSuccess) e = launch_q8_attention(at, 0, false, rt->stream);
   return hip_check(e, "attention prefill launch");
 }
 

@@ -75,3 +75,20 @@ def test_store_rejects_malformed_q4_groups(rt, torch_dev, tmp_path):
         st.upload_q4(rt, "y")
     j = st.upload_q4(rt, "x.weight")
     assert (j.out_rows, j.in_elems) == (16, 128)
+
+
+def test_reference_layout_cases(rt, torch_dev, tmp_path):
+    # native.rs:5731 accepts_an_mlx_q4_affine_matrix_layout and :5745
+    # rejects_a_wrong_scale_layout: U32 [3, 16] with BF16 [3, 2] scales and
+    # biases is a 3 x 128 matrix; BF16 [3, 3] scales are rejected.
+    w = np.arange(48, dtype=np.uint32).reshape(3, 16)
+    s2 = np.full((3, 2), 0x3F80, np.uint16)
+    s3 = np.full((3, 3), 0x3F80, np.uint16)
+    ok = WeightStore(write_model(tmp_path / "ok", {"s.safetensors": {"layer.weight": w, "layer.scales": s2,
+                                                                     "layer.biases": s2}}))
+    j = ok.upload_q4(rt, "layer.weight")
+    assert (j.out_rows, j.in_elems) == (3, 128)
+    bad = WeightStore(write_model(tmp_path / "bad", {"s.safetensors": {"layer.weight": w, "layer.scales": s3,
+                                                                       "layer.biases": s2}}))
+    with pytest.raises(QmError, match="INVALID_TENSOR"):
+        bad.upload_q4(rt, "layer.weight")
