@@ -528,6 +528,11 @@ Plan make_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t 
     p.rpw = r;
     for (int i = 0; i < (swiglu ? 1 : n_jobs); ++i) p.tiles += (jobs[i].rows + r - 1) / r;
     uint32_t waves = (target + p.tiles - 1) / p.tiles;
+    // With several activation rows a ring slot costs several times the
+    // arithmetic (per-row FMAs, more registers): at most 4 waves per tile, so
+    // each wave's longer slice overlaps its own loads with that work over
+    // several ring rounds (measured: M = 4 / 8 sets +7 % / +9 %; slower at M = 1).
+    if (M > 1) waves = std::min<uint32_t>(waves, 4);
     if (env_int("QM38_Q4_SPLIT", 0) > 0) waves = (uint32_t)env_int("QM38_Q4_SPLIT", 1);
     waves = std::max<uint32_t>(1, std::min<uint32_t>(waves, kMaxWaves));
     int occ = 0;
