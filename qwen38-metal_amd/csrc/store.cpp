@@ -15,8 +15,8 @@
 //     `<base>.scales` / `<base>.biases` are BF16 [rows][K/64], with K a
 //     non-zero multiple of 64 and exact byte lengths.
 //
-// Shards are memory-mapped read-only; uploads copy a tensor's bytes into a
-// fresh 256-byte-aligned device allocation through a pinned staging buffer.
+// Shards are memory-mapped read-only; uploads copy a tensor's bytes from the
+// mapping into a fresh 256-byte-aligned device allocation.
 #include <errno.h>
 #include <fcntl.h>
 #include <stdint.h>
@@ -371,18 +371,10 @@ qm_status upload_bytes(qm_runtime* rt, const uint8_t* src, uint64_t bytes, void*
   void* dev = nullptr;
   hipError_t e = hipMalloc(&dev, bytes ? bytes : 1);
   if (e != hipSuccess) return hip_check(e, "weight upload allocation");
-  // Pinned staging in 64 MiB pieces: the mapped file pages are pageable.
-  constexpr size_t kStage = 64u << 20;
-  void* stage = nullptr;
-  e = hipHostMalloc(&stage, (size_t)std::min<uint64_t>(bytes ? bytes : 1, kStage));
-  for (uint64_t done = 0; e == hipSuccess && done < bytes;) {
-    const size_t n = (size_t)std::min<uint64_t>(kStage, bytes - done);
-    memcpy(stage, src + done, n);
-    e = hipMemcpyAsync((uint8_t*)dev + done, stage, n, hipMemcpyHostToDevice, rt->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);  // the staging buffer is reused
-    done += n;
-  }
-  if (stage) (void)hipHostFree(stage);
+  // Straight from the mapped file pages (pageable; the HIP runtime stages
+  // them), ordered on the runtime's stream.
+  if (bytes) e = hipMemcpyAsync(dev, src, bytes, hipMemcpyHostToDevice, rt->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
   if (e != hipSuccess) {
     (void)hipFree(dev);
     return hip_check(e, "weight upload");
