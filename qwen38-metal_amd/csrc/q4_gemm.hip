@@ -49,10 +49,24 @@ struct GemmArgs {
   const uint16_t* xh;  // fp16 bits [M][K], chunk-permuted
   uint32_t K, M;
   uint32_t m_tiles, total_tiles;
-  uint32_t splits, gks;  // K slices per tile, groups per slice
-  float* partials;       // [tile][slice][kThreads * 128] fp32 (splits > 1)
+  // Work assignment over the flattened K steps (step L G + g is group g of
+  // tile L).  splits == 1: worker w runs steps [w Q, (w + 1) Q) (Q = G: one
+  // tile each; Q > G: stream-K, ranges crossing tile boundaries).  splits > 1:
+  // worker w runs slice w % splits (Q steps) of tile w / splits.
+  uint32_t q_steps, splits;
+  uint32_t workers;
+  float* partials;       // fp32 pieces, kThreads * 128 floats per slot
+
   unsigned* counters;    // [tile], zero between launches
 };
+
+constexpr uint32_t kPieceFloats = kThreads * 128;  // one 256 x 256 fp32 tile
+
+// Piece slot of worker w in tile L (splits == 1): 2w for the first tile of
+// w's range, 2w + 1 for the last one (a range cuts at most two tiles).
+__device__ __forceinline__ uint32_t piece_slot(uint32_t w, uint32_t L, uint32_t Q, uint32_t G) {
+  return 2 * w + (L != (w * Q) / G ? 1u : 0u);
+}
 
 // s_waitcnt vmcnt(0) (gfx9 encoding; expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
@@ -104,83 +118,32 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const uint16_t* __restric
 template <bool SWIGLU>
 __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmArgs args) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][kTileBytes];  // [stage][X | W]
+  __shared__ unsigned last;
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t wm = wave & 3, wn = wave >> 2;
-  const uint32_t K = args.K, M = args.M, G = K / 64;
+  const uint32_t K = args.K, M = args.M, G = K / 64, Q = args.q_steps, S = args.splits;
+  const uint32_t total = args.total_tiles * G;
 
-  // ---- XCD-aware tile remap (over tile x K-slice units) -------------------
-  const uint32_t S = args.splits;
-  const uint32_t T = args.total_tiles * S;
+  // ---- XCD-aware worker remap ---------------------------------------------
+  // Workgroups are dealt round-robin to the XCDs; each XCD gets a contiguous
+  // run of workers, so the tiles it covers are contiguous (n-major, m inner)
+  // and every W tile is read from HBM once per XCD, then from its L2.
+  const uint32_t W = args.workers;
   const uint32_t xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds;
-  const uint32_t q = T / kXcds, rem = T % kXcds;
-  const uint32_t LS = xcd * q + min(xcd, rem) + local;
-  const uint32_t L = LS / S, split = LS - L * S;
-  const uint32_t n_tile = L / args.m_tiles, m_tile = L % args.m_tiles;
-  const uint32_t g0 = split * args.gks;
-  const uint32_t NG = min(G, g0 + args.gks) - g0;  // K steps of this slice (>= 1)
-  const uint32_t m0 = m_tile * kBM;
-
-  // ---- this thread's W row and the tile's job ------------------------------
-  int jt = 0;
-  if (!SWIGLU) {
-    while (jt + 1 < args.n_jobs && n_tile >= args.jobs[jt + 1].tile_begin) ++jt;
-  }
-  const uint32_t srow = tid >> 1, shalf = tid & 1;  // staging: row of the tiles, chunk half
-  const Q4Job& wj = args.jobs[SWIGLU ? (srow >= 128 ? 1 : 0) : jt];
-  uint32_t n_first, wrow;
-  if (SWIGLU) {
-    n_first = n_tile * 128;
-    wrow = n_first + (srow & 127);
+  const uint32_t wq = W / kXcds, wrem = W % kXcds;
+  const uint32_t lw = xcd * wq + min(xcd, wrem) + local;
+  uint32_t step0, s_end;
+  if (S > 1) {
+    const uint32_t L = lw / S;
+    step0 = L * G + (lw - L * S) * Q;
+    s_end = min(step0 + Q, (L + 1) * G);
   } else {
-    n_first = (n_tile - wj.tile_begin) * kBN;
-    wrow = n_first + srow;
+    step0 = lw * Q;
+    s_end = min(total, step0 + Q);
   }
-  wrow = min(wrow, wj.rows - 1);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(wj.w, (uint64_t)wj.rows * (K / 2));
-  const uint16_t* s_row = wj.s + (size_t)wrow * G;
-  const uint16_t* b_row = wj.b + (size_t)wrow * G;
-  const uint32_t w_voff = wrow * (K / 2) + shalf * 16;
-  const uint32_t xrow = min(m0 + srow, M - 1);
-  const uint16_t* x_src = args.xh + (size_t)xrow * K + shalf * 32;
-
-  // ---- staging registers ---------------------------------------------------
-  u32x4 xr[4];
-  u32x4 wr;
-  uint16_t sr, br;
-  auto load = [&](uint32_t g) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) xr[i] = *(const u32x4*)(x_src + g * 64 + 8 * i);
-    wr = __builtin_amdgcn_raw_buffer_load_b128(rw, w_voff, g * 32, 0);
-    sr = s_row[g];
-    br = b_row[g];
-  };
-  auto store = [&](int stage) {
-    uint8_t* xt = lds[stage][0];
-    uint8_t* wt = lds[stage][1];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *(u32x4*)(xt + swz(srow, shalf * 4 + i)) = xr[i];
-    const _Float16 s = (_Float16)bf16_to_f32(sr), b = (_Float16)bf16_to_f32(br);
-    const half2v s2 = {s, s}, b2 = {b, b};
-    const uint32_t wv[4] = {wr.x, wr.y, wr.z, wr.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      u32x4 d;
-      d.x = dq_pair(wv[i], 0, s2, b2);
-      d.y = dq_pair(wv[i], 1, s2, b2);
-      d.z = dq_pair(wv[i], 2, s2, b2);
-      d.w = dq_pair(wv[i], 3, s2, b2);
-      *(u32x4*)(wt + swz(srow, shalf * 4 + i)) = d;
-    }
-  };
-
-  floatx16 acc[2][4];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = floatx16{};
 
   // B-tile row bases of this wave's four 32-column blocks.
   uint32_t brow[4];
@@ -189,72 +152,121 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmArgs args) {
     brow[j] = SWIGLU ? (j < 2 ? 64 * wn + 32 * j : 128 + 64 * wn + 32 * (j - 2)) : 128 * wn + 32 * j;
   const uint32_t arow0 = 64 * wm + (lane & 31);
   const uint32_t kh = lane >> 5;
+  const uint32_t srow = tid >> 1, shalf = tid & 1;  // staging: row of the tiles, chunk half
 
-  load(g0);
-  store(0);
-  if (NG > 1) load(g0 + 1);
-  __syncthreads();
+  for (uint32_t step = step0; step < s_end;) {
+    // Uniform values: readfirstlane keeps them (and the buffer offsets built
+    // from them) in SGPRs; a VGPR offset would turn every partial-piece store
+    // and load into a waterfall loop.
+    const uint32_t L = __builtin_amdgcn_readfirstlane(step / G), g0 = step - L * G;
+    const uint32_t NG = min(G - g0, s_end - step);  // K steps of this piece (>= 1)
+    step += NG;
+    const uint32_t n_tile = L / args.m_tiles, m_tile = L % args.m_tiles;
+    const uint32_t m0 = m_tile * kBM;
 
-  for (uint32_t i = 0; i < NG; ++i) {
-    const int st = i & 1;
-    const uint8_t* xt = lds[st][0];
-    const uint8_t* wt = lds[st][1];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const uint32_t c = 2 * s + kh;
-      u32x4 a[2], b[4];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) a[i] = *(const u32x4*)(xt + swz(arow0 + 32 * i, c));
-#pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = *(const u32x4*)(wt + swz(brow[j] + (lane & 31), c));
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_f16(a[i], b[j], acc[i][j]);
+    // ---- this thread's W row and the tile's job ----------------------------
+    int jt = 0;
+    if (!SWIGLU) {
+      while (jt + 1 < args.n_jobs && n_tile >= args.jobs[jt + 1].tile_begin) ++jt;
     }
-    if (i + 1 < NG) {
-      store(st ^ 1);
-      if (i + 2 < NG) load(g0 + i + 2);
+    const Q4Job& wj = args.jobs[SWIGLU ? (wave >= 4 ? 1 : 0) : jt];  // srow >= 128 <=> wave >= 4
+    uint32_t n_first, wrow;
+    if (SWIGLU) {
+      n_first = n_tile * 128;
+      wrow = n_first + (srow & 127);
+    } else {
+      n_first = (n_tile - wj.tile_begin) * kBN;
+      wrow = n_first + srow;
     }
-    __syncthreads();
-  }
+    wrow = min(wrow, wj.rows - 1);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(wj.w, (uint64_t)wj.rows * (K / 2));
+    const uint16_t* s_row = wj.s + (size_t)wrow * G;
+    const uint16_t* b_row = wj.b + (size_t)wrow * G;
+    const uint32_t w_voff = wrow * (K / 2) + shalf * 16;
+    const uint32_t xrow = min(m0 + srow, M - 1);
+    const uint16_t* x_src = args.xh + (size_t)xrow * K + shalf * 32;
 
-  // ---- split-K: publish this slice, the last one of the tile adds them -----
-  if (S > 1) {
-    // Thread-major float4 layout: element (k4, tid) at (k4 * kThreads + tid) * 4.
-    // Stores and loads carry sc0 sc1 (system coherence: written through to
-    // memory, read past the caches), so publishing them needs only their
-    // completion before the count, not a cache write-back.
-    constexpr int kSys = 0x11;  // buffer cache policy: sc0 | sc1
-    const __amdgpu_buffer_rsrc_t rp =
-        make_rsrc(args.partials + (size_t)L * S * (kThreads * 128), (uint64_t)S * kThreads * 128 * 4);
+    // ---- staging registers -------------------------------------------------
+    u32x4 xr[4];
+    u32x4 wr;
+    uint16_t sr, br;
+    auto load = [&](uint32_t g) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 4; ++i) xr[i] = *(const u32x4*)(x_src + g * 64 + 8 * i);
+      wr = __builtin_amdgcn_raw_buffer_load_b128(rw, w_voff, g * 32, 0);
+      sr = s_row[g];
+      br = b_row[g];
+    };
+    auto store = [&](int stage) {
+      uint8_t* xt = lds[stage][0];
+      uint8_t* wt = lds[stage][1];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int i = 0; i < 4; ++i) *(u32x4*)(xt + swz(srow, shalf * 4 + i)) = xr[i];
+      const _Float16 s = (_Float16)bf16_to_f32(sr), b = (_Float16)bf16_to_f32(br);
+      const half2v s2 = {s, s}, b2 = {b, b};
+      const uint32_t wv[4] = {wr.x, wr.y, wr.z, wr.w};
 #pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4) {
-          const int k4 = (i * 4 + j) * 4 + e4;
-          const u32x4 v = {__float_as_uint(acc[i][j][4 * e4]), __float_as_uint(acc[i][j][4 * e4 + 1]),
-                           __float_as_uint(acc[i][j][4 * e4 + 2]), __float_as_uint(acc[i][j][4 * e4 + 3])};
-          __builtin_amdgcn_raw_buffer_store_b128(v, rp, (k4 * kThreads + tid) * 16, split * (kThreads * 128 * 4),
-                                                 kSys);
-        }
-    wait_vmcnt0();
-    __shared__ unsigned last;
-    __syncthreads();
-    if (tid == 0) {
-      const unsigned prev = __hip_atomic_fetch_add(&args.counters[L], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last = prev == S - 1;
-      if (last) __hip_atomic_store(&args.counters[L], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!last) return;
+      for (int i = 0; i < 4; ++i) {
+        u32x4 d;
+        d.x = dq_pair(wv[i], 0, s2, b2);
+        d.y = dq_pair(wv[i], 1, s2, b2);
+        d.z = dq_pair(wv[i], 2, s2, b2);
+        d.w = dq_pair(wv[i], 3, s2, b2);
+        *(u32x4*)(wt + swz(srow, shalf * 4 + i)) = d;
+      }
+    };
+
+    floatx16 acc[2][4];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = floatx16{};
-    for (uint32_t sl = 0; sl < S; ++sl) {
+
+    // The previous piece's last step ended on a barrier: both stages are free.
+    load(g0);
+    store(0);
+    load(g0 + min(1u, NG - 1));
+    __syncthreads();
+
+    for (uint32_t i = 0; i < NG; ++i) {
+      const int st = i & 1;
+      const uint8_t* xt = lds[st][0];
+      const uint8_t* wt = lds[st][1];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t c = 2 * s + kh;
+        u32x4 a[2], b[4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) a[i] = *(const u32x4*)(xt + swz(arow0 + 32 * i, c));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[j] = *(const u32x4*)(wt + swz(brow[j] + (lane & 31), c));
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = mfma_f16(a[i], b[j], acc[i][j]);
+      }
+      // Branch-free body: the last step stages an unused tile and the last
+      // two reload group g0 + NG - 1.
+      store(st ^ 1);
+      load(g0 + min(i + 2, NG - 1));
+      __syncthreads();
+    }
+
+    // ---- a partial piece: publish it; the tile's last piece adds them ------
+    if (NG < G) {
+      // Thread-major float4 layout: element (k4, tid) at (k4 * kThreads + tid) * 4.
+      // Stores and loads carry sc0 sc1 (system coherence: written through to
+      // memory, read past the caches), so publishing them needs only their
+      // completion before the count, not a cache write-back.
+      constexpr int kSys = 0x11;  // buffer cache policy: sc0 | sc1
+      constexpr uint32_t kPieceBytes = kPieceFloats * 4;
+      const uint64_t pbase = (uint64_t)args.partials;
+      // readfirstlane returns int: convert through uint32_t (no sign extension).
+      const uint32_t p_hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(pbase >> 32));
+      const uint32_t p_lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)pbase);
+      const uint64_t pb = ((uint64_t)p_hi << 32) | p_lo;
+      const __amdgpu_buffer_rsrc_t rp = make_rsrc((const void*)pb, (uint64_t)(S > 1 ? 1 : 2) * W * kPieceBytes);
+      const uint32_t own = __builtin_amdgcn_readfirstlane((S > 1 ? lw : piece_slot(lw, L, Q, G)) * kPieceBytes);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -262,39 +274,81 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmArgs args) {
 #pragma unroll
           for (int e4 = 0; e4 < 4; ++e4) {
             const int k4 = (i * 4 + j) * 4 + e4;
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rp, (k4 * kThreads + tid) * 16,
-                                                                  sl * (kThreads * 128 * 4), kSys);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[i][j][4 * e4 + e] += __uint_as_float(v[e]);
+            const u32x4 v = {__float_as_uint(acc[i][j][4 * e4]), __float_as_uint(acc[i][j][4 * e4 + 1]),
+                             __float_as_uint(acc[i][j][4 * e4 + 2]), __float_as_uint(acc[i][j][4 * e4 + 3])};
+            __builtin_amdgcn_raw_buffer_store_b128(v, rp, (k4 * kThreads + tid) * 16, own, kSys);
           }
+      wait_vmcnt0();
+      // Workers covering tile L: fw .. lwl, one piece each.
+      const uint32_t fw = S > 1 ? L * S : (L * G) / Q;
+      const uint32_t lwl = S > 1 ? fw + S - 1 : ((L + 1) * G - 1) / Q;
+      __syncthreads();
+      if (tid == 0) {
+        const unsigned prev =
+            __hip_atomic_fetch_add(&args.counters[L], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = prev == lwl - fw;
+        if (last) __hip_atomic_store(&args.counters[L], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (!__builtin_amdgcn_readfirstlane(last)) continue;  // uniform branch
+      // The sum does not depend on which piece arrives last: two pieces are
+      // added as own + other (fp32 addition commutes); more are re-read and
+      // added in worker order.
+      const bool two = lwl == fw + 1;
+      if (!two) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = floatx16{};
+      }
+      for (uint32_t w = two ? (lw == fw ? lwl : fw) : fw; w <= lwl; ++w) {
+        const uint32_t off = __builtin_amdgcn_readfirstlane((S > 1 ? w : piece_slot(w, L, Q, G)) * kPieceBytes);
+        // Eight loads in flight per batch (issued before any is used).
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int jp = 0; jp < 4; jp += 2) {
+            u32x4 v[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+              const int k4 = (i * 4 + jp + (t >> 2)) * 4 + (t & 3);
+              v[t] = __builtin_amdgcn_raw_buffer_load_b128(rp, (k4 * kThreads + tid) * 16, off, kSys);
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[i][jp + (t >> 2)][4 * (t & 3) + e] += __uint_as_float(v[t][e]);
+          }
+        if (two) break;
+      }
     }
-  }
 
-  // ---- epilogue ------------------------------------------------------------
-  // acc[i][j] element e: row 32 i + 8 (e >> 2) + 4 kh + (e & 3) of the wave's
-  // 64 rows, column (lane & 31) of block j.
+    // ---- epilogue ----------------------------------------------------------
+    // acc[i][j] element e: row 32 i + 8 (e >> 2) + 4 kh + (e & 3) of the wave's
+    // 64 rows, column (lane & 31) of block j.
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 2; ++i) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const uint32_t m = m0 + 64 * wm + 32 * i + 8 * (e >> 2) + 4 * kh + (e & 3);
-      if (m >= M) continue;
-      if (SWIGLU) {
-        const Q4Job& gj = args.jobs[0];
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t m = m0 + 64 * wm + 32 * i + 8 * (e >> 2) + 4 * kh + (e & 3);
+        if (m >= M) continue;
+        if (SWIGLU) {
+          const Q4Job& gj = args.jobs[0];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const uint32_t n = n_tile * 128 + 64 * wn + 32 * j + (lane & 31);
-          if (n < gj.rows) {
-            const float gv = acc[i][j][e], uv = acc[i][j + 2][e];
-            gj.out[(size_t)m * gj.rows + n] = f32_to_bf16(silu_f(gv) * uv);
+          for (int j = 0; j < 2; ++j) {
+            const uint32_t n = n_tile * 128 + 64 * wn + 32 * j + (lane & 31);
+            if (n < gj.rows) {
+              const float gv = acc[i][j][e], uv = acc[i][j + 2][e];
+              gj.out[(size_t)m * gj.rows + n] = f32_to_bf16(silu_f(gv) * uv);
+            }
           }
-        }
-      } else {
-        const Q4Job& oj = args.jobs[jt];
+        } else {
+          const Q4Job& oj = args.jobs[jt];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t n = n_first + brow[j] + (lane & 31);
-          if (n < oj.rows) oj.out[(size_t)m * oj.rows + n] = f32_to_bf16(acc[i][j][e]);
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t n = n_first + brow[j] + (lane & 31);
+            if (n < oj.rows) oj.out[(size_t)m * oj.rows + n] = f32_to_bf16(acc[i][j][e]);
+          }
         }
       }
     }
@@ -307,14 +361,32 @@ size_t q4_gemm_xh_bytes(uint32_t K, uint32_t M) { return (size_t)M * K * 2; }
 
 namespace {
 struct GemmPlan {
-  uint32_t m_tiles, tiles, splits, gks;
+  uint32_t m_tiles, tiles, q, splits, workers;
+  size_t partial_bytes;  // 0 when every worker's range is whole tiles
 };
-// K slices per tile: when the tiles fill less than one dispatch round of
-// `cus` workgroups, split K so the units fill whole rounds as evenly as
-// possible (at least 8 K steps per slice, at most 8 slices).
+
 int env_int_gemm(const char* name, int fallback) {
   const char* v = getenv(name);
   return v ? atoi(v) : fallback;
+}
+
+// Plan cost in units of one K step of one 256 x 256 tile (about 1.9 us on
+// MI355X), fitted to the measured BASELINE prefill shapes (M = 512, 2048).
+// Workers run in rounds of `cus` (one workgroup per CU).  A K slice costs its
+// steps plus about 10 (pipeline fill, epilogue) and 12 for writing its fp32
+// piece, and the tile's last slice reads the others back at about 5 per
+// piece (one read for two pieces).  A stream-K worker pays about 20 per tile
+// it touches, 12 for writing a piece and 5 per piece of the tiles it sums.
+double split_cost(uint32_t tiles, uint32_t G, uint32_t S, uint32_t cus) {
+  const uint32_t gs = (G + S - 1) / S;
+  const uint64_t rounds = ((uint64_t)tiles * S + cus - 1) / cus;
+  return rounds * (gs + 10.0 + (S > 1 ? 12.0 : 0.0)) + (S > 1 ? 5.0 * (S == 2 ? 1 : S) : 0.0);
+}
+double stream_cost(uint32_t tiles, uint32_t G, uint32_t Q, uint32_t cus) {
+  const uint64_t workers = ((uint64_t)tiles * G + Q - 1) / Q;
+  const uint64_t rounds = (workers + cus - 1) / cus;
+  const double pieces = Q >= G ? 1.0 : (double)G / Q + 1.0;
+  return rounds * (Q + 20.0 * ((double)Q / G + 1.0) + 12.0 + 5.0 * pieces);
 }
 
 GemmPlan gemm_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M) {
@@ -328,27 +400,43 @@ GemmPlan gemm_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint3
   }
   p.tiles = n_tiles * p.m_tiles;
   const uint32_t G = K / 64, cus = 256;
-  // Split-K fills partial dispatch rounds (one workgroup per CU).  Cost in
-  // units of one K group of one tile, fitted to measured BASELINE shapes:
-  // per round the slice's groups plus about 10 for the pipeline fill and the
-  // epilogue, 4 more for writing the fp32 partials when split, and about 10
-  // per slice for the last slice's read-back.  (Down at M = 2048, 160 tiles:
-  // three slices in two rounds beat one long round by 15 %; QKV's 320 tiles
-  // stay unsplit: five rounds of short slices lose to two full rounds.)
+  const uint64_t total = (uint64_t)p.tiles * G;
+  // Candidates: K split into S equal slices per tile (S = 1: whole tiles;
+  // S <= 8, slices of at least 8 steps), and stream-K with the steps dealt
+  // evenly over one or two rounds of workers.
   p.splits = 1;
-  double best = 0.0;
-  for (uint32_t s = 1; s <= 8 && (s == 1 || G / s >= 8); ++s) {
-    const uint32_t gks = (G + s - 1) / s;
-    const uint32_t units = p.tiles * s, rounds = (units + cus - 1) / cus;
-    const double cost = rounds * (gks + 10.0 + (s > 1 ? 4.0 : 0.0)) + (s > 1 ? 10.0 * s : 0.0);
-    if (s == 1 || cost < best) {
-      best = cost;
+  p.q = G;
+  double best = split_cost(p.tiles, G, 1, cus);
+  for (uint32_t s = 2; s <= 8 && G / s >= 8; ++s) {
+    const double c = split_cost(p.tiles, G, s, cus);
+    if (c < best) {
+      best = c;
       p.splits = s;
+      p.q = (G + s - 1) / s;
     }
   }
-  if (env_int_gemm("QM38_GEMM_SPLITS", 0) > 0) p.splits = std::min<uint32_t>(8, (uint32_t)env_int_gemm("QM38_GEMM_SPLITS", 1));
-  p.gks = (G + p.splits - 1) / p.splits;
-  p.splits = (G + p.gks - 1) / p.gks;
+  for (uint32_t r = 1; r <= 2; ++r) {
+    const uint64_t q = (total + r * cus - 1) / (r * cus);
+    if (q < 8 || q % G == 0 || q >= (1ull << 31)) continue;
+    const double c = stream_cost(p.tiles, G, (uint32_t)q, cus);
+    if (c < best) {
+      best = c;
+      p.splits = 1;
+      p.q = (uint32_t)q;
+    }
+  }
+  const int fs = env_int_gemm("QM38_GEMM_SPLITS", 0), fq = env_int_gemm("QM38_GEMM_Q", 0);
+  if (fs > 0) {
+    p.splits = std::min<uint32_t>((uint32_t)fs, G);
+    p.q = (G + p.splits - 1) / p.splits;
+  } else if (fq > 0) {
+    p.splits = 1;
+    p.q = (uint32_t)fq;
+  }
+  p.splits = p.splits > 1 ? (G + p.q - 1) / p.q : 1;  // slices actually used
+  p.workers = p.splits > 1 ? p.tiles * p.splits : (uint32_t)((total + p.q - 1) / p.q);
+  const bool pieces = p.splits > 1 || p.q % G != 0;
+  p.partial_bytes = pieces ? (size_t)(p.splits > 1 ? 1 : 2) * p.workers * kPieceFloats * sizeof(float) : 0;
   return p;
 }
 }  // namespace
@@ -356,8 +444,8 @@ GemmPlan gemm_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint3
 void q4_gemm_workspace(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M, size_t* partial_bytes,
                        size_t* counters) {
   const GemmPlan p = gemm_plan(jobs, n_jobs, swiglu, K, M);
-  *partial_bytes = p.splits > 1 ? (size_t)p.tiles * p.splits * kThreads * 128 * sizeof(float) : 0;
-  *counters = p.splits > 1 ? p.tiles : 0;
+  *partial_bytes = p.partial_bytes;
+  *counters = p.partial_bytes ? p.tiles : 0;
 }
 
 hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x, uint32_t K, uint32_t M,
@@ -365,12 +453,18 @@ hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint
   if (n_jobs < 1 || n_jobs > kMaxQ4Jobs || K % 64 != 0 || M == 0) return hipErrorInvalidValue;
   if (!ws.xh || ws.xh_bytes < q4_gemm_xh_bytes(K, M)) return hipErrorInvalidValue;
   const GemmPlan plan = gemm_plan(jobs, n_jobs, swiglu, K, M);
-  if (plan.splits > 1 && (ws.partial_bytes < (size_t)plan.tiles * plan.splits * kThreads * 128 * sizeof(float) ||
-                          ws.counter_count < plan.tiles))
+  static const bool log_plan = env_int_gemm("QM38_GEMM_PLAN_LOG", 0) != 0;
+  static uint64_t logged = 0;  // debug aid: print each new shape's plan once
+  const uint64_t key = ((uint64_t)M << 40) ^ ((uint64_t)K << 16) ^ plan.tiles ^ ((uint64_t)plan.q << 56);
+  if (log_plan && key != logged && (logged = key))
+    fprintf(stderr, "q4_gemm plan: M=%u K=%u tiles=%u splits=%u Q=%u workers=%u\n", M, K, plan.tiles, plan.splits,
+            plan.q, plan.workers);
+  if (plan.partial_bytes && (ws.partial_bytes < plan.partial_bytes || ws.counter_count < plan.tiles))
     return hipErrorInvalidValue;
   GemmArgs a{};
+  a.q_steps = plan.q;
   a.splits = plan.splits;
-  a.gks = plan.gks;
+  a.workers = plan.workers;
   a.partials = ws.partials;
   a.counters = ws.counters;
   a.n_jobs = n_jobs;
@@ -389,7 +483,7 @@ hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint
 
   const size_t chunks = (size_t)M * K / 8;
   hipLaunchKernelGGL(x_to_f16_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream, x, ws.xh, chunks);
-  const dim3 grid(a.total_tiles * a.splits);
+  const dim3 grid(plan.workers);
   if (swiglu)
     hipLaunchKernelGGL(q4_gemm_kernel<true>, grid, dim3(kThreads), 0, stream, a);
   else
