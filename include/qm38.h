@@ -59,9 +59,10 @@ typedef enum qm_status {
   QM_ERR_INVALID_SNAPSHOT = 19,     /* MetalRuntimeError::InvalidDeltaNetSnapshot */
   QM_ERR_INVALID_SNAPSHOT_ROW = 20, /* ::InvalidSnapshotRow */
   QM_ERR_MODEL_FORMAT = 21,         /* model::ModelFormatError (index, shard or header) */
-  QM_ERR_INVALID_TENSOR = 22        /* native::NativeError tensor variants (MissingTensor,
+  QM_ERR_INVALID_TENSOR = 22,       /* native::NativeError tensor variants (MissingTensor,
                                        NotQuantizedWeight, InvalidQuantizedWeight,
                                        InvalidAffineTensor, TensorByteLength) */
+  QM_ERR_GRAPH_STALE = 23           /* a decode graph's captured buffers or state parity changed */
 } qm_status;
 
 /* Human-readable name of a status code (static storage). */
@@ -370,6 +371,91 @@ typedef struct qm_q4_matrix {
  * and the weight mapping of map_weight_store (metal_runtime.rs:955-984). */
 qm_status qm_store_upload_q4(qm_runtime* rt, const qm_weight_store* store,
                              const char* weight_name, qm_q4_matrix* out);
+
+/* ------------------------------------------------------------------ */
+/* Residual stream and per-token decode graph                          */
+/* ------------------------------------------------------------------ */
+
+/* hidden fp32 [M][n] += delta (bf16 [M][n], skipped when NULL), then
+ * out = bf16((hidden * rsqrt(mean(hidden^2) + epsilon)) * weights) per row
+ * (weights fp32 [n], used as given).  Replaces qwen38_add_in_place /
+ * _add_rows followed by qwen38_rms_norm / _rms_norm_rows (qwen38.metal:
+ * 4250-4333; encoders metal_runtime.rs encode_add_in_place / encode_rms_norm).
+ * Device pointers; asynchronous. */
+qm_status qm_residual_rmsnorm(qm_runtime* rt, float* hidden, const uint16_t* delta,
+                              const float* weights, uint32_t M, uint32_t n, float epsilon,
+                              uint16_t* out);
+/* hidden fp32 [count] += delta bf16 [count] (qwen38_add_in_place). */
+qm_status qm_residual_add(qm_runtime* rt, float* hidden, const uint16_t* delta, size_t count);
+
+/* A Gated DeltaNet decoder layer (MetalDecodeLinearLayer,
+ * metal_runtime.rs:304-318; encoder encode_decode_linear_layer, :3301-3521):
+ *   x = rmsnorm(hidden) * input_norm;  qkv, z, b, a = Q4(x)
+ *   d = deltanet_step(qkv, z, b, a);   hidden += Q4_out(d)
+ *   x = rmsnorm(hidden) * post_attention_norm
+ *   hidden += down(silu(gate(x)) * up(x))
+ * Jobs take K = hidden for qkv/z/b/a/gate/up, value_heads*value_head_dim for
+ * out_proj and gate.out_rows for down. */
+typedef struct qm_decode_linear_layer {
+  const float* input_norm;           /* fp32 [hidden] */
+  const float* post_attention_norm;  /* fp32 [hidden] */
+  qm_q4_job qkv, z, b, a, out_proj;
+  const qm_dn_weights* dn_weights;
+  qm_dn_state* dn_state;
+  qm_q4_job gate, up, down;
+} qm_decode_linear_layer;
+
+/* A full-attention decoder layer (MetalDecodeFullLayer, :385-399; encoder
+ * encode_decode_full_layer, :1567-2020): q_proj gives [H][2 head_dim]
+ * (query | gate per head), then qm_attn_prepare, qm_attn_decode on `kv`
+ * (appends this token), o_proj, and the MLP as above. */
+typedef struct qm_decode_full_layer {
+  const float* input_norm;
+  const float* post_attention_norm;
+  qm_q4_job q_proj, k_proj, v_proj, o_proj;
+  const float* q_norm;  /* fp32 [head_dim] */
+  const float* k_norm;  /* fp32 [head_dim] */
+  uint32_t num_heads;
+  qm_rope_config rope;  /* rope.head_dim must equal kv's head_dim */
+  qm_kv* kv;
+  qm_q4_job gate, up, down;
+} qm_decode_full_layer;
+
+/* One layer: exactly one of linear / full is non-NULL (MetalDecodeLayer). */
+typedef struct qm_decode_layer {
+  const qm_decode_linear_layer* linear;
+  const qm_decode_full_layer* full;
+} qm_decode_layer;
+
+/* Activation state of single-token decode (MetalDecodeState,
+ * metal_runtime.rs:246-268): the fp32 residual row `hidden` [hidden_elems]
+ * (device memory owned by the state) and grow-only intermediate buffers. */
+typedef struct qm_decode_state qm_decode_state;
+qm_status qm_decode_state_create(qm_runtime* rt, uint32_t hidden_elems, qm_decode_state** out);
+void qm_decode_state_destroy(qm_decode_state* st);
+float* qm_decode_state_hidden(qm_decode_state* st);
+
+/* Runs one token through `layers` in order, updating hidden in place
+ * (decode_layers, metal_runtime.rs:2022-2084).  position: the three M-RoPE
+ * axes of this token (all equal for text).  Asynchronous. */
+qm_status qm_decode_layers(qm_runtime* rt, qm_decode_state* st, const qm_decode_layer* layers,
+                           uint32_t n_layers, const uint32_t position[3], float epsilon);
+
+/* The same token as HIP graphs: every launch between two attention calls is
+ * captured once (two variants, for the parity of the DeltaNet history
+ * buffers); a run sets the position, then replays the segments with each
+ * layer's qm_attn_decode launched between them (its grid depends on the cache
+ * length).  Results equal qm_decode_layers bit for bit.  The graph holds the
+ * layer descriptors' pointers: a run fails with QM_ERR_GRAPH_STALE when a
+ * DeltaNet state's buffers or history parity, or the decode state's buffers,
+ * changed since capture (qm_dn_snapshot_restore of a one-row set exchanges
+ * buffers; an eager qm_dn_step in between flips the parity only, which the
+ * second variant covers).  Creation captures only; it runs nothing. */
+typedef struct qm_decode_graph qm_decode_graph;
+qm_status qm_decode_graph_create(qm_runtime* rt, qm_decode_state* st, const qm_decode_layer* layers,
+                                 uint32_t n_layers, float epsilon, qm_decode_graph** out);
+qm_status qm_decode_graph_run(qm_decode_graph* g, const uint32_t position[3]);
+void qm_decode_graph_destroy(qm_decode_graph* g);
 
 #ifdef __cplusplus
 }

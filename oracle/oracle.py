@@ -45,6 +45,7 @@ def lib() -> C.CDLL:
                                       C.c_float, vp, vp, vp]
         L.qo_attn_prepare.argtypes = [vp, vp, vp, vp, u32, u32, u32, u32, u32, C.c_double, u32, u32, u32, vp, u32,
                                       C.c_float, vp, vp, vp]
+        L.qo_residual_rmsnorm.argtypes = [vp, vp, vp, u32, u32, C.c_float, vp]
         L.qo_num_threads.restype = i32
         _lib = L
     return _lib
@@ -192,3 +193,16 @@ def attn_prepare(q_with_gate, k, q_norm, k_norm, head_dim: int, rotary_dim: int,
                           head_dim, rotary_dim, float(theta), s1, s2, int(sections is not None), _p(pos), base, eps,
                           _p(q), _p(g), _p(ko))
     return q, g, ko
+
+
+def residual_rmsnorm(hidden, w, eps: float, delta=None):
+    """qo_residual_rmsnorm: returns (hidden + delta in fp32, fp64 RMSNorm(hidden) * w).
+    hidden fp32 [M][n] (not modified), delta fp32 [M][n] or None, w fp32 [n]."""
+    h = np.array(hidden, dtype=np.float32, copy=True)
+    if h.ndim == 1:
+        h = h[None]
+    M, n = h.shape
+    out = np.zeros((M, n), np.float64)
+    d = _c(np.reshape(delta, (M, n)), np.float32) if delta is not None else None
+    lib().qo_residual_rmsnorm(_p(h), _p(d), _p(_c(w, np.float32)), M, n, eps, _p(out))
+    return h, out

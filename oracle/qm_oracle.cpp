@@ -350,6 +350,25 @@ void qo_attn_prepare(const float* q_with_gate, const float* k_in, const float* q
   }
 }
 
+// Residual add + RMSNorm of M rows (qwen38_add_in_place followed by
+// qwen38_rms_norm / qwen38_rms_norm_rows, shaders/qwen38.metal:4253-4333):
+// hidden += delta (when delta != NULL), then
+// out = hidden * (1 / sqrt(mean(hidden^2) + eps)) * w, the weights used as
+// given.  hidden is updated in fp32 (the reference's type); the norm is
+// evaluated in fp64 and returned unrounded.
+void qo_residual_rmsnorm(float* hidden, const float* delta, const float* w, uint32_t M, uint32_t n, float eps,
+                         double* out) {
+  for (uint32_t r = 0; r < M; ++r) {
+    float* h = hidden + (size_t)r * n;
+    if (delta)
+      for (uint32_t i = 0; i < n; ++i) h[i] = h[i] + delta[(size_t)r * n + i];
+    double ss = 0.0;
+    for (uint32_t i = 0; i < n; ++i) ss += (double)h[i] * h[i];
+    const double scale = 1.0 / std::sqrt(ss / n + (double)eps);
+    for (uint32_t i = 0; i < n; ++i) out[(size_t)r * n + i] = (double)h[i] * scale * (double)w[i];
+  }
+}
+
 int qo_num_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

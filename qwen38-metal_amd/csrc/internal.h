@@ -45,4 +45,19 @@ void q4_gemm_workspace(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, u
 hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x,
                           uint32_t K, uint32_t M, const Workspace& ws, hipStream_t stream);
 
+// Residual stream helpers of the decode graph (residual.hip).
+// hidden fp32 [M][n] (+= delta bf16 when delta != NULL), out = bf16 RMSNorm(hidden) * w.
+hipError_t launch_residual_rmsnorm(float* hidden, const uint16_t* delta, const float* w, uint16_t* out, uint32_t M,
+                                   uint32_t n, float eps, hipStream_t stream);
+hipError_t launch_residual_add(float* hidden, const uint16_t* delta, size_t count, hipStream_t stream);
+constexpr int kMaxConvSegs = 6;
+struct ConvSeg {
+  const void* src;
+  void* dst;
+  uint32_t n;       // elements
+  uint32_t to_f32;  // 1: bf16 -> fp32, 0: fp32 -> bf16
+};
+hipError_t launch_convert(const ConvSeg* segs, int nseg, hipStream_t stream);
+hipError_t launch_set_u32x3(uint32_t* dst, uint32_t a, uint32_t b, uint32_t c, hipStream_t stream);
+
 }  // namespace qm

@@ -112,6 +112,16 @@ qm_status qm::ensure_counters(qm_runtime* rt, size_t count) {
   return QM_OK;
 }
 
+void qm::release_buffers(qm_runtime* rt) {
+  if (rt->scratch) hipFree(rt->scratch);
+  if (rt->counters) hipFree(rt->counters);
+  if (rt->partials) hipFree(rt->partials);
+  if (rt->xh) hipFree(rt->xh);
+  rt->scratch = rt->counters = nullptr;
+  rt->partials = rt->xh = nullptr;
+  rt->scratch_bytes = rt->counter_count = rt->partial_bytes = rt->xh_bytes = 0;
+}
+
 qm::Workspace qm::workspace(qm_runtime* rt) {
   return Workspace{(float*)rt->partials, rt->partial_bytes, rt->counters, rt->counter_count, (uint16_t*)rt->xh,
                    rt->xh_bytes};
@@ -144,6 +154,7 @@ const char* qm_status_string(qm_status status) {
     case QM_ERR_INVALID_SNAPSHOT_ROW: return "QM_ERR_INVALID_SNAPSHOT_ROW";
     case QM_ERR_MODEL_FORMAT: return "QM_ERR_MODEL_FORMAT";
     case QM_ERR_INVALID_TENSOR: return "QM_ERR_INVALID_TENSOR";
+    case QM_ERR_GRAPH_STALE: return "QM_ERR_GRAPH_STALE";
   }
   return "QM_ERR_UNKNOWN";
 }
@@ -171,10 +182,7 @@ void qm_runtime_destroy(qm_runtime* rt) {
   if (!rt) return;
   DeviceGuard g(rt->device);
   hipStreamSynchronize(rt->stream);
-  if (rt->scratch) hipFree(rt->scratch);
-  if (rt->counters) hipFree(rt->counters);
-  if (rt->partials) hipFree(rt->partials);
-  if (rt->xh) hipFree(rt->xh);
+  qm::release_buffers(rt);
   delete rt;
 }
 

@@ -108,8 +108,9 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
   if (!rt || !w || !to || !qkv || !z || !b || !a || !out) return fail(QM_ERR_NULL_POINTER, "NULL argument");
   if (!from) from = to;
   if (M == 0) return fail(QM_ERR_EMPTY_DIMENSION, "DeltaNet prefill needs at least one token");
-  if (w->rt != rt || from->rt != rt || to->rt != rt)
-    return fail(QM_ERR_INVALID_ARGUMENT, "weights and states must belong to this runtime");
+  // Weights and states are device memory: any runtime on their device may use them.
+  if (w->rt->device != rt->device || from->rt->device != rt->device || to->rt->device != rt->device)
+    return fail(QM_ERR_INVALID_ARGUMENT, "weights and states must live on this runtime's device");
   if (memcmp(&from->cfg, &w->cfg, sizeof(qm_dn_config)) != 0 || memcmp(&to->cfg, &w->cfg, sizeof(qm_dn_config)) != 0)
     return fail(QM_ERR_WRONG_LENGTH, "DeltaNet state was created for another configuration");
   if (snaps) {
@@ -161,6 +162,13 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
 }
 
 }  // namespace
+
+const qm_dn_config& qm::dn_weights_config(const qm_dn_weights* w) { return w->cfg; }
+const qm_runtime* qm::dn_weights_runtime(const qm_dn_weights* w) { return w->rt; }
+qm::DnStateView qm::dn_state_view(const qm_dn_state* s) {
+  return DnStateView{s->hist[0], s->hist[1], s->rec, s->cur, s->rt, s->cfg};
+}
+void qm::dn_state_set_cur(qm_dn_state* s, int cur) { s->cur = cur; }
 
 extern "C" {
 

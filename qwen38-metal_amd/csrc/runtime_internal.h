@@ -40,6 +40,25 @@ qm_status ensure_counters(qm_runtime* rt, size_t count);
 qm_status ensure_xh(qm_runtime* rt, size_t bytes);
 // Workspace handed to kernels that split work across workgroups.
 Workspace workspace(qm_runtime* rt);
+// Frees a runtime's grow-only buffers (not the runtime itself).
+void release_buffers(qm_runtime* rt);
+
+// Views of the opaque state objects for the decode graph (runtime_decode.cpp).
+const qm_dn_config& dn_weights_config(const qm_dn_weights* w);
+const qm_runtime* dn_weights_runtime(const qm_dn_weights* w);
+struct DnStateView {
+  const void* hist0;
+  const void* hist1;
+  const void* rec;
+  int cur;
+  const qm_runtime* rt;
+  qm_dn_config cfg;
+};
+DnStateView dn_state_view(const qm_dn_state* s);
+void dn_state_set_cur(qm_dn_state* s, int cur);
+uint32_t kv_heads_of(const qm_kv* kv);
+uint32_t kv_head_dim_of(const qm_kv* kv);
+const qm_runtime* kv_runtime_of(const qm_kv* kv);
 
 class DeviceGuard {
  public:

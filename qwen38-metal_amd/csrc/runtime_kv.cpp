@@ -98,6 +98,10 @@ bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0;
 
 }  // namespace
 
+uint32_t qm::kv_heads_of(const qm_kv* kv) { return kv->kv_heads; }
+uint32_t qm::kv_head_dim_of(const qm_kv* kv) { return kv->head_dim; }
+const qm_runtime* qm::kv_runtime_of(const qm_kv* kv) { return kv->rt; }
+
 extern "C" {
 
 qm_status qm_kv_create(qm_runtime* rt, uint32_t kv_heads, uint32_t head_dim, uint32_t page_tokens,

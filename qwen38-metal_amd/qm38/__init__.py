@@ -27,6 +27,8 @@ QM_STATUS = [
     "QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE", "QM_ERR_DIMENSION_OVERFLOW", "QM_ERR_COMMAND_FAILED",
     "QM_ERR_ZERO_CAPACITY", "QM_ERR_EMPTY_APPEND", "QM_ERR_CAPACITY_EXCEEDED",
     "QM_ERR_NULL_POINTER", "QM_ERR_OUT_OF_MEMORY", "QM_ERR_MISALIGNED", "QM_ERR_INVALID_ARGUMENT",
+    "QM_ERR_INVALID_SNAPSHOT", "QM_ERR_INVALID_SNAPSHOT_ROW", "QM_ERR_MODEL_FORMAT", "QM_ERR_INVALID_TENSOR",
+    "QM_ERR_GRAPH_STALE",
 ]
 
 # Every symbol include/qm38.h declares (checked by tests/test_abi.py).
@@ -43,6 +45,9 @@ EXPORTS = [
     "qm_dn_snapshots_create", "qm_dn_snapshots_destroy", "qm_dn_prefill_snapshots", "qm_dn_snapshot_restore",
     "qm_store_open", "qm_store_close", "qm_store_tensor_count", "qm_store_tensor_info", "qm_store_upload",
     "qm_store_upload_q4",
+    "qm_residual_rmsnorm", "qm_residual_add", "qm_decode_state_create", "qm_decode_state_destroy",
+    "qm_decode_state_hidden", "qm_decode_layers", "qm_decode_graph_create", "qm_decode_graph_run",
+    "qm_decode_graph_destroy",
 ]
 
 
@@ -73,6 +78,27 @@ class RopeConfig(C.Structure):
     """qm_rope_config (RopeParameters, native.rs:119-197)."""
     _fields_ = [("head_dim", C.c_uint32), ("rotary_dim", C.c_uint32), ("rope_theta", C.c_float),
                 ("mrope_section1", C.c_uint32), ("mrope_section2", C.c_uint32), ("has_mrope_sections", C.c_uint32)]
+
+
+class DecodeLinearLayer(C.Structure):
+    """qm_decode_linear_layer (MetalDecodeLinearLayer, metal_runtime.rs:304-318)."""
+    _fields_ = [("input_norm", C.c_void_p), ("post_attention_norm", C.c_void_p),
+                ("qkv", Q4Job), ("z", Q4Job), ("b", Q4Job), ("a", Q4Job), ("out_proj", Q4Job),
+                ("dn_weights", C.c_void_p), ("dn_state", C.c_void_p),
+                ("gate", Q4Job), ("up", Q4Job), ("down", Q4Job)]
+
+
+class DecodeFullLayer(C.Structure):
+    """qm_decode_full_layer (MetalDecodeFullLayer, metal_runtime.rs:385-399)."""
+    _fields_ = [("input_norm", C.c_void_p), ("post_attention_norm", C.c_void_p),
+                ("q_proj", Q4Job), ("k_proj", Q4Job), ("v_proj", Q4Job), ("o_proj", Q4Job),
+                ("q_norm", C.c_void_p), ("k_norm", C.c_void_p), ("num_heads", C.c_uint32),
+                ("rope", RopeConfig), ("kv", C.c_void_p),
+                ("gate", Q4Job), ("up", Q4Job), ("down", Q4Job)]
+
+
+class DecodeLayer(C.Structure):
+    _fields_ = [("linear", C.POINTER(DecodeLinearLayer)), ("full", C.POINTER(DecodeFullLayer))]
 
 
 _lib = None
@@ -144,6 +170,15 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "qm_dn_snapshots_destroy": ([vp], None),
         "qm_dn_prefill_snapshots": ([vp, vp, vp, vp, vp, vp, vp, vp, vp, u32, C.c_float, vp], i32),
         "qm_dn_snapshot_restore": ([vp, u32, vp], i32),
+        "qm_residual_rmsnorm": ([vp, vp, vp, vp, u32, u32, C.c_float, vp], i32),
+        "qm_residual_add": ([vp, vp, vp, C.c_size_t], i32),
+        "qm_decode_state_create": ([vp, u32, C.POINTER(vp)], i32),
+        "qm_decode_state_destroy": ([vp], None),
+        "qm_decode_state_hidden": ([vp], vp),
+        "qm_decode_layers": ([vp, vp, C.POINTER(DecodeLayer), u32, C.POINTER(u32), C.c_float], i32),
+        "qm_decode_graph_create": ([vp, vp, C.POINTER(DecodeLayer), u32, C.c_float, C.POINTER(vp)], i32),
+        "qm_decode_graph_run": ([vp, C.POINTER(u32)], i32),
+        "qm_decode_graph_destroy": ([vp], None),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -264,6 +299,103 @@ class Runtime:
         src = source.handle if source is not None else None
         _check(self.lib.qm_dn_prefill(self.handle, weights.handle, src, state.handle, _ptr(qkv), _ptr(z),
                                       _ptr(b), _ptr(a), rows, epsilon, _ptr(out)))
+
+
+    # ---- residual stream and decode graph ----------------------------------
+    def residual_rmsnorm(self, hidden, delta, weights, rows: int, elements: int, epsilon: float, out) -> None:
+        """hidden += delta (when given), out = bf16(rms_norm(hidden) * weights)
+        (qwen38_add_in_place + qwen38_rms_norm(_rows))."""
+        _check(self.lib.qm_residual_rmsnorm(self.handle, _ptr(hidden), _ptr(delta), _ptr(weights), rows, elements,
+                                            epsilon, _ptr(out)))
+
+    def residual_add(self, hidden, delta, count: int) -> None:
+        _check(self.lib.qm_residual_add(self.handle, _ptr(hidden), _ptr(delta), count))
+
+    def create_decode_state(self, hidden_elements: int) -> "DecodeState":
+        return DecodeState(self, hidden_elements)
+
+    def decode_layers(self, state: "DecodeState", layers, position, epsilon: float) -> None:
+        """One token through `layers` (decode_layers, metal_runtime.rs:2022)."""
+        arr, _keep = _layer_array(layers)
+        pos = (C.c_uint32 * 3)(*_position3(position))
+        _check(self.lib.qm_decode_layers(self.handle, state.handle, arr, len(layers), pos, epsilon))
+
+
+def _position3(position):
+    if isinstance(position, int):
+        return (position, position, position)
+    p = tuple(int(v) for v in position)
+    assert len(p) == 3
+    return p
+
+
+def _layer_array(layers):
+    """DecodeLinearLayer / DecodeFullLayer list -> qm_decode_layer array (and the
+    objects it points at, which must stay alive for the call)."""
+    arr = (DecodeLayer * len(layers))()
+    for i, L in enumerate(layers):
+        if isinstance(L, DecodeLinearLayer):
+            arr[i].linear = C.pointer(L)
+        elif isinstance(L, DecodeFullLayer):
+            arr[i].full = C.pointer(L)
+        else:
+            raise TypeError(f"layer {i}: {type(L).__name__}")
+    return arr, list(layers)
+
+
+class DecodeState:
+    """qm_decode_state: the fp32 residual row of one decoding request and its
+    intermediates (MetalDecodeState, metal_runtime.rs:246)."""
+
+    def __init__(self, rt: Runtime, hidden_elements: int):
+        self.rt = rt
+        self.hidden_elements = hidden_elements
+        h = C.c_void_p()
+        _check(rt.lib.qm_decode_state_create(rt.handle, hidden_elements, C.byref(h)))
+        self.handle = h
+        rt._children.add(self)
+
+    @property
+    def hidden_ptr(self) -> int:
+        return self.rt.lib.qm_decode_state_hidden(self.handle)
+
+    def close(self) -> None:
+        if self.handle:
+            self.rt.lib.qm_decode_state_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DecodeGraph:
+    """qm_decode_graph: one token's launches captured as HIP graph segments."""
+
+    def __init__(self, rt: Runtime, state: DecodeState, layers, epsilon: float):
+        self.rt = rt
+        arr, self._keep = _layer_array(layers)
+        h = C.c_void_p()
+        _check(rt.lib.qm_decode_graph_create(rt.handle, state.handle, arr, len(layers), epsilon, C.byref(h)))
+        self.handle = h
+        rt._children.add(self)
+
+    def run(self, position) -> None:
+        pos = (C.c_uint32 * 3)(*_position3(position))
+        _check(self.rt.lib.qm_decode_graph_run(self.handle, pos))
+
+    def close(self) -> None:
+        if self.handle:
+            self.rt.lib.qm_decode_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class KvCache:

@@ -1,0 +1,371 @@
+"""Residual stream kernels and the per-token decode graph on the GPU.
+
+* qm_residual_rmsnorm / qm_residual_add against the oracle's
+  qo_residual_rmsnorm (qwen38_add_in_place + qwen38_rms_norm(_rows),
+  qwen38.metal:4250-4333): the fp32 residual add bit for bit, the bf16 norm
+  within 2e-3 of max|ref| beyond the final rounding.
+* qm_decode_layers (decode_layers, metal_runtime.rs:2022-2084) on a small
+  model of DeltaNet and full-attention layers: bit-equal to the same token
+  issued as separate entry-point calls (each parity-tested on its own), and
+  within 2e-2 of max|hidden| of an oracle composition (fp64/fp32 CPU
+  functions with the GPU's bf16 rounding points) after three tokens.
+* qm_decode_graph: bit-equal to qm_decode_layers over five tokens (both
+  history-parity variants), and QM_ERR_GRAPH_STALE once a captured buffer
+  changes.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from gpu_util import assert_bf16_close, bf16_dev_to_f32, empty_bf16, from_dev, to_dev
+from qm38 import (DecodeFullLayer, DecodeGraph, DecodeLinearLayer, DnConfig, QmError, RopeConfig, Runtime,
+                  synth)
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-6
+
+
+# ---------------------------------------------------------------- RMSNorm --
+@pytest.mark.parametrize("M,n", [(1, 5120), (3, 256), (2, 1002), (1, 6), (4, 64)])
+@pytest.mark.parametrize("with_delta", [False, True])
+def test_residual_rmsnorm_matches_oracle(rt, torch_dev, M, n, with_delta):
+    rng = np.random.default_rng(M * 1000 + n + with_delta)
+    h = (rng.standard_normal((M, n)) * 3).astype(np.float32)
+    w = (1 + 0.2 * rng.standard_normal(n)).astype(np.float32)
+    d_bits = synth.bf16_normal(rng, (M, n)) if with_delta else None
+    hd = to_dev(h, torch_dev)
+    out = empty_bf16((M, n), torch_dev)
+    rt.residual_rmsnorm(hd, None if d_bits is None else to_dev(d_bits, torch_dev), to_dev(w, torch_dev), M, n,
+                        EPS, out)
+    h_ref, o_ref = oracle.residual_rmsnorm(h, w, EPS, None if d_bits is None else synth.bf16_to_f32(d_bits))
+    np.testing.assert_array_equal(from_dev(hd), h_ref)
+    assert_bf16_close(bf16_dev_to_f32(out), o_ref, what=f"rmsnorm M{M} n{n}")
+
+
+def test_residual_add_exact(rt, torch_dev):
+    rng = np.random.default_rng(5)
+    h = rng.standard_normal(3000).astype(np.float32)
+    d = synth.bf16_normal(rng, (3000,))
+    hd = to_dev(h, torch_dev)
+    rt.residual_add(hd, to_dev(d, torch_dev), 3000)
+    np.testing.assert_array_equal(from_dev(hd), h + synth.bf16_to_f32(d))
+
+
+def test_rmsnorm_rejects_bad_arguments(rt, torch_dev):
+    import torch
+    h = torch.zeros(64, dtype=torch.float32, device=torch_dev)
+    w = torch.ones(64, dtype=torch.float32, device=torch_dev)
+    o = torch.zeros(64, dtype=torch.int16, device=torch_dev)
+    with pytest.raises(QmError, match="EMPTY"):
+        rt.residual_rmsnorm(h, None, w, 0, 64, EPS, o)
+    with pytest.raises(QmError):
+        rt.residual_rmsnorm(h, None, None, 1, 64, EPS, o)
+    with pytest.raises(QmError):
+        rt.residual_rmsnorm(h, None, w, 1, 64, -1.0, o)
+
+
+# ------------------------------------------------------------ toy model --
+HID, INTER = 256, 512
+DN = dict(key_heads=2, value_heads=4, key_head_dim=32, value_head_dim=32, conv_kernel_size=4)
+FULL = dict(heads=4, kv_heads=2, head_dim=64, rotary_dim=16, theta=1e7)
+
+
+def _q4(rng, rows, K):
+    return synth.q4_matrix(rng, rows, K)
+
+
+class Model:
+    """Host copies of a small [linear, full, linear] model's weights plus their
+    device uploads (shared by every state built from it)."""
+
+    def __init__(self, rt, dev, seed=0, kinds=("linear", "full", "linear")):
+        rng = np.random.default_rng(seed)
+        self.kinds = kinds
+        self.rt, self.dev = rt, dev
+        c = DN
+        self.channels = 2 * c["key_heads"] * c["key_head_dim"] + c["value_heads"] * c["value_head_dim"]
+        self.value = c["value_heads"] * c["value_head_dim"]
+        self.layers = []
+        for kind in kinds:
+            L = dict(kind=kind,
+                     in_norm=(1 + 0.1 * rng.standard_normal(HID)).astype(np.float32),
+                     post_norm=(1 + 0.1 * rng.standard_normal(HID)).astype(np.float32),
+                     gate=_q4(rng, INTER, HID), up=_q4(rng, INTER, HID), down=_q4(rng, HID, INTER))
+            if kind == "linear":
+                L.update(qkv=_q4(rng, self.channels, HID), z=_q4(rng, self.value, HID),
+                         b=_q4(rng, c["value_heads"], HID), a=_q4(rng, c["value_heads"], HID),
+                         out=_q4(rng, HID, self.value),
+                         conv=(0.3 * rng.standard_normal((self.channels, c["conv_kernel_size"]))).astype(np.float32),
+                         a_log=(0.1 * rng.standard_normal(c["value_heads"])).astype(np.float32),
+                         dt_bias=(0.1 * rng.standard_normal(c["value_heads"])).astype(np.float32),
+                         norm=(1 + 0.1 * rng.standard_normal(c["value_head_dim"])).astype(np.float32))
+            else:
+                H, KVH, D = FULL["heads"], FULL["kv_heads"], FULL["head_dim"]
+                L.update(q=_q4(rng, 2 * H * D, HID), k=_q4(rng, KVH * D, HID), v=_q4(rng, KVH * D, HID),
+                         o=_q4(rng, HID, H * D),
+                         q_norm=(1 + 0.1 * rng.standard_normal(D)).astype(np.float32),
+                         k_norm=(1 + 0.1 * rng.standard_normal(D)).astype(np.float32))
+            self.layers.append(L)
+        self._dev = []  # device tensors kept alive
+        self._alive = []  # states and caches of every request
+        self.jobs = []
+        self.dn_weights = []
+        for L in self.layers:
+            J = {}
+            for key in ("gate", "up", "down", "qkv", "z", "b", "a", "out", "q", "k", "v", "o"):
+                if key in L:
+                    w, s, b = (to_dev(t, dev) for t in L[key])
+                    self._dev += [w, s, b]
+                    J[key] = Runtime.job(w, s, b, L[key][0].shape[0])
+            for key in ("in_norm", "post_norm", "q_norm", "k_norm"):
+                if key in L:
+                    t = to_dev(L[key], dev)
+                    self._dev.append(t)
+                    J[key] = t
+            self.jobs.append(J)
+            if L["kind"] == "linear":
+                cfg = DnConfig(c["key_heads"], c["value_heads"], c["key_head_dim"], c["value_head_dim"],
+                               c["conv_kernel_size"])
+                self.dn_weights.append(rt.create_deltanet_weights(cfg, L["conv"], L["a_log"], L["dt_bias"], L["norm"]))
+            else:
+                self.dn_weights.append(None)
+
+    def rope(self):
+        return RopeConfig(FULL["head_dim"], FULL["rotary_dim"], FULL["theta"], 2, 2, 1)  # M-RoPE sections (2, 2)
+
+    def new_request(self, max_tokens=64):
+        """Fresh DeltaNet states / KV caches and the layer descriptors over them."""
+        states, caches, descs = [], [], []
+        for L, J, W in zip(self.layers, self.jobs, self.dn_weights):
+            if L["kind"] == "linear":
+                st = W.create_state()
+                states.append(st)
+                caches.append(None)
+                descs.append(DecodeLinearLayer(J["in_norm"].data_ptr(), J["post_norm"].data_ptr(), J["qkv"], J["z"],
+                                               J["b"], J["a"], J["out"], W.handle.value, st.handle.value, J["gate"],
+                                               J["up"],
+                                               J["down"]))
+            else:
+                kv = self.rt.create_q8_kv_state(FULL["kv_heads"], FULL["head_dim"], max_tokens)
+                states.append(None)
+                caches.append(kv)
+                descs.append(DecodeFullLayer(J["in_norm"].data_ptr(), J["post_norm"].data_ptr(), J["q"], J["k"],
+                                             J["v"], J["o"], J["q_norm"].data_ptr(), J["k_norm"].data_ptr(),
+                                             FULL["heads"], self.rope(), kv.handle.value, J["gate"], J["up"],
+                                             J["down"]))
+        # The descriptors hold raw handles: keep the objects alive with the model.
+        self._alive.append((states, caches))
+        return states, caches, descs
+
+
+def _hidden0(seed):
+    return (np.random.default_rng(seed).standard_normal(HID) * 2).astype(np.float32)
+
+
+def _state_with(rt, dev, h):
+    st = rt.create_decode_state(HID)
+    rt.lib.qm_copy_to_device(rt.handle, st.hidden_ptr, h.ctypes.data, h.nbytes)
+    return st
+
+
+def _hidden(rt, st):
+    out = np.zeros(HID, np.float32)
+    rt.synchronize()
+    rt.lib.qm_copy_to_host(rt.handle, out.ctypes.data, st.hidden_ptr, out.nbytes)
+    return out
+
+
+def _positions(t):
+    return (t, t + 3, t + 7)  # distinct M-RoPE axes
+
+
+def _manual_token(rt, dev, model, states, caches, hidden, pos):
+    """The same token as separate entry-point calls (torch for the exact
+    bf16 <-> fp32 conversions)."""
+    import torch
+    bf = lambda n: torch.empty(n, dtype=torch.int16, device=dev)  # noqa: E731
+
+    def f32(t):
+        return (t.to(torch.int32) & 0xFFFF).bitwise_left_shift(16).view(torch.float32)
+
+    def to_bf(t):
+        return t.to(torch.bfloat16).view(torch.int16)
+
+    x = bf(HID)
+    delta2 = None
+    posd = torch.tensor(np.array(pos, np.uint32).view(np.int32), device=dev)
+    for i, (L, J) in enumerate(zip(model.layers, model.jobs)):
+        rt.residual_rmsnorm(hidden, delta2, J["in_norm"], 1, HID, EPS, x)
+        delta = bf(HID)
+        if L["kind"] == "linear":
+            outs = [bf(model.channels), bf(model.value), bf(DN["value_heads"]), bf(DN["value_heads"])]
+            rt.q4_project([J["qkv"], J["z"], J["b"], J["a"]], x, HID, 1, outs)
+            dn_out = torch.empty(model.value, dtype=torch.float32, device=dev)
+            rt.deltanet_step(model.dn_weights[i], states[i], *(f32(o) for o in outs), EPS, dn_out)
+            rt.q4_project([J["out"]], to_bf(dn_out), model.value, 1, [delta])
+        else:
+            H, KVH, D = FULL["heads"], FULL["kv_heads"], FULL["head_dim"]
+            qg, kb, vb = bf(2 * H * D), bf(KVH * D), bf(KVH * D)
+            rt.q4_project([J["q"], J["k"], J["v"]], x, HID, 1, [qg, kb, vb])
+            q, g = bf(H * D), bf(H * D)
+            k = torch.empty(KVH * D, dtype=torch.float32, device=dev)
+            rt.attn_prepare(model.rope(), 1, H, KVH, qg, kb, J["q_norm"], J["k_norm"], EPS, q, g, k, positions=posd)
+            att = bf(H * D)
+            rt.gqa_attention_q8([caches[i]], q, g, k, f32(vb), H, att)
+            rt.q4_project([J["o"]], att, H * D, 1, [delta])
+        rt.residual_rmsnorm(hidden, delta, J["post_norm"], 1, HID, EPS, x)
+        h = bf(INTER)
+        rt.q4_swiglu(J["gate"], J["up"], x, HID, 1, h)
+        delta2 = bf(HID)
+        rt.q4_project([J["down"]], h, INTER, 1, [delta2])
+    rt.residual_add(hidden, delta2, HID)
+
+
+def test_decode_layers_match_separate_calls(rt, torch_dev):
+    import torch
+    model = Model(rt, torch_dev, seed=11)
+    h0 = _hidden0(1)
+    states_a, caches_a, descs = model.new_request()
+    st = _state_with(rt, torch_dev, h0)
+    states_b, caches_b, _ = model.new_request()
+    hidden_b = torch.from_numpy(h0.copy()).to(torch_dev)
+    for t in range(3):
+        rt.decode_layers(st, descs, _positions(t), EPS)
+        _manual_token(rt, torch_dev, model, states_b, caches_b, hidden_b, _positions(t))
+        np.testing.assert_array_equal(_hidden(rt, st), from_dev(hidden_b), err_msg=f"token {t}")
+    for sa, sb in zip(states_a, states_b):
+        if sa is not None:
+            for x, y in zip(sa.read(), sb.read()):
+                np.testing.assert_array_equal(x, y)
+    for ca, cb in zip(caches_a, caches_b):
+        if ca is not None:
+            assert ca.sequence_length == cb.sequence_length == 3
+            for x, y in zip(ca.read(), cb.read()):
+                np.testing.assert_array_equal(x, y)
+
+
+def _bf(v):
+    return synth.bf16_to_f32(synth.f32_to_bf16(np.asarray(v, np.float32)))
+
+
+def _oracle_tokens(model, h0, n_tokens):
+    """The decode layers composed from oracle functions, rounding to bf16 where
+    the GPU path stores bf16."""
+    c = DN
+    h = h0.copy()[None]
+    hist = {i: np.zeros((model.channels, c["conv_kernel_size"] - 1), np.float64) for i, L in
+            enumerate(model.layers) if L["kind"] == "linear"}
+    S = {i: np.zeros((c["value_heads"], c["value_head_dim"], c["key_head_dim"]), np.float64) for i in hist}
+    kcache = {i: [] for i, L in enumerate(model.layers) if L["kind"] == "full"}
+    vcache = {i: [] for i in kcache}
+    H, KVH, D = FULL["heads"], FULL["kv_heads"], FULL["head_dim"]
+    for t in range(n_tokens):
+        pos = np.array(_positions(t), np.uint32).reshape(3, 1)
+        pending = None
+        for i, L in enumerate(model.layers):
+            h, xn = oracle.residual_rmsnorm(h, L["in_norm"], EPS, pending)
+            xb = synth.f32_to_bf16(xn.astype(np.float32))
+            proj = lambda key, xbits: _bf(oracle.q4_project(xbits, *L[key]))  # noqa: E731
+            if L["kind"] == "linear":
+                qkv, z, b, a = (proj(k, xb) for k in ("qkv", "z", "b", "a"))
+                out, hist[i], S[i] = oracle.deltanet_prefill(c, L["conv"], L["a_log"], L["dt_bias"], L["norm"], qkv,
+                                                              z, b, a, EPS, hist[i], S[i], f64=True)
+                delta = proj("out", synth.f32_to_bf16(out))
+            else:
+                qg, kk, vv = proj("q", xb), proj("k", xb), proj("v", xb)
+                q, g, k = oracle.attn_prepare(qg.reshape(1, H, 2 * D), kk.reshape(1, KVH, D), L["q_norm"],
+                                              L["k_norm"], D, FULL["rotary_dim"], FULL["theta"], EPS,
+                                              sections=(2, 2), positions=pos)
+                kcache[i].append(k.reshape(KVH, D))
+                vcache[i].append(vv.reshape(KVH, D))
+                kq, ks = oracle.q8_quantize_rows(np.stack(kcache[i]))
+                vq, vs = oracle.q8_quantize_rows(np.stack(vcache[i]))
+                att = oracle.attention(_bf(q), _bf(g), kq, ks, vq, vs, len(kcache[i]) - 1)
+                delta = proj("o", synth.f32_to_bf16(att.reshape(1, H * D)))
+            h, xn = oracle.residual_rmsnorm(h, L["post_norm"], EPS, delta)
+            xb = synth.f32_to_bf16(xn.astype(np.float32))
+            hmid = _bf(oracle.swiglu(oracle.q4_project(xb, *L["gate"]), oracle.q4_project(xb, *L["up"])))
+            pending = proj("down", synth.f32_to_bf16(hmid))
+        h = h + pending
+    return h[0]
+
+
+def test_decode_layers_match_oracle(rt, torch_dev):
+    model = Model(rt, torch_dev, seed=12)
+    h0 = _hidden0(2)
+    _, _, descs = model.new_request()
+    st = _state_with(rt, torch_dev, h0)
+    for t in range(3):
+        rt.decode_layers(st, descs, _positions(t), EPS)
+    got = _hidden(rt, st)
+    ref = _oracle_tokens(model, h0, 3)
+    err = np.max(np.abs(got - ref)) / np.max(np.abs(ref))
+    assert err < 2e-2, f"hidden after 3 tokens: rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("kinds", [("linear", "full", "linear"), ("full", "full"), ("linear", "linear")])
+def test_graph_matches_eager(rt, torch_dev, kinds):
+    model = Model(rt, torch_dev, seed=13, kinds=kinds)
+    h0 = _hidden0(3)
+    states_a, caches_a, descs_a = model.new_request()
+    states_b, caches_b, descs_b = model.new_request()
+    st_a = _state_with(rt, torch_dev, h0)
+    st_b = _state_with(rt, torch_dev, h0)
+    g = DecodeGraph(rt, st_b, descs_b, EPS)
+    for t in range(5):
+        rt.decode_layers(st_a, descs_a, _positions(t), EPS)
+        g.run(_positions(t))
+        np.testing.assert_array_equal(_hidden(rt, st_b), _hidden(rt, st_a), err_msg=f"token {t}")
+    for sa, sb in zip(states_a, states_b):
+        if sa is not None:
+            for x, y in zip(sa.read(), sb.read()):
+                np.testing.assert_array_equal(x, y)
+    for ca, cb in zip(caches_a, caches_b):
+        if ca is not None:
+            assert cb.sequence_length == 5
+            for x, y in zip(ca.read(), cb.read()):
+                np.testing.assert_array_equal(x, y)
+    g.close()
+
+
+def test_graph_stale_after_buffer_exchange(rt, torch_dev):
+    model = Model(rt, torch_dev, seed=14, kinds=("linear", "full"))
+    states, _, descs = model.new_request()
+    st = _state_with(rt, torch_dev, _hidden0(4))
+    g = DecodeGraph(rt, st, descs, EPS)
+    g.run(_positions(0))
+    # An eager token flips the history parity: the other variant still runs.
+    rt.decode_layers(st, descs, _positions(1), EPS)
+    g.run(_positions(2))
+    # A one-row snapshot restore exchanges the state's buffers.
+    snaps = model.dn_weights[0].create_snapshots(1)
+    snaps.restore(0, states[0])
+    with pytest.raises(QmError, match="changed after capture"):
+        g.run(_positions(3))
+    g.close()
+    # Recapturing picks up the new buffers.
+    g2 = DecodeGraph(rt, st, descs, EPS)
+    g2.run(_positions(3))
+    rt.synchronize()
+    g2.close()
+
+
+def test_decode_layers_reject_bad_layers(rt, torch_dev):
+    model = Model(rt, torch_dev, seed=15, kinds=("linear", "full"))
+    _, _, descs = model.new_request()
+    st = _state_with(rt, torch_dev, _hidden0(5))
+    bad = DecodeLinearLayer.from_buffer_copy(descs[0])
+    bad.out_proj = bad.b  # wrong output rows
+    with pytest.raises(QmError, match="WRONG_LENGTH|output rows"):
+        rt.decode_layers(st, [bad, descs[1]], 0, EPS)
+    badf = DecodeFullLayer.from_buffer_copy(descs[1])
+    badf.num_heads = 3  # not a multiple of kv_heads
+    with pytest.raises(QmError):
+        rt.decode_layers(st, [descs[0], badf], 0, EPS)
+    with pytest.raises(QmError):
+        rt.decode_layers(st, [], 0, EPS)
+    with pytest.raises(QmError):
+        DecodeGraph(rt, st, [bad], EPS)
