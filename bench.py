@@ -313,6 +313,115 @@ def deltanet_legs(rt, dev, rng, steps, warmup):
     return out
 
 
+def _dev_q4(rows: int, cols: int, gen, dev):
+    """A random Q4 matrix made on the device (packed words, bf16 scales in
+    [0.002, 0.012), biases -8 * scale)."""
+    import torch
+    import qm38
+    w = torch.randint(-2 ** 31, 2 ** 31 - 1, (rows, cols // 8), dtype=torch.int32, device=dev, generator=gen)
+    s = (torch.rand((rows, cols // 64), device=dev, generator=gen) * 0.01 + 0.002).to(torch.bfloat16)
+    b = (-8 * s.float()).to(torch.bfloat16)
+    return qm38.Runtime.job(w, s.view(torch.int16), b.view(torch.int16), rows)
+
+
+def decode_graph_legs(rt, dev, rng, steps, warmup):
+    """One token through a 4-layer block (3 DeltaNet + 1 full-attention layer,
+    the 3:1 pattern of the hybrid model) at the BASELINE dimensions, eager
+    (qm_decode_layers) and as HIP graph segments (qm_decode_graph)."""
+    import torch
+    import qm38
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    c = DN
+    ch = 2 * c["key_heads"] * c["key_head_dim"] + c["value_heads"] * c["value_head_dim"]
+    val = c["value_heads"] * c["value_head_dim"]
+    keep, weight_bytes = [], 0
+    kinds = ("linear", "linear", "linear", "full")
+
+    def job(rows, cols):
+        nonlocal weight_bytes
+        weight_bytes += q4_bytes(rows, cols)
+        return _dev_q4(rows, cols, gen, dev)
+
+    def norm(n):
+        t = (1 + 0.1 * torch.randn(n, device=dev, generator=gen)).float()
+        keep.append(t)
+        return t.data_ptr()
+
+    layers = []
+    for kind in kinds:
+        L = dict(kind=kind, in_norm=norm(H), post_norm=norm(H), gate=job(I, H), up=job(I, H), down=job(H, I))
+        if kind == "linear":
+            L.update(qkv=job(ch, H), z=job(val, H), b=job(c["value_heads"], H), a=job(c["value_heads"], H),
+                     out=job(H, val))
+            cfg = qm38.DnConfig(c["key_heads"], c["value_heads"], c["key_head_dim"], c["value_head_dim"],
+                                c["conv_kernel_size"])
+            L["w"] = rt.create_deltanet_weights(cfg, (rng.standard_normal((ch, 4)) * 0.3).astype(np.float32),
+                                                np.zeros(c["value_heads"], np.float32),
+                                                np.zeros(c["value_heads"], np.float32),
+                                                np.ones(c["value_head_dim"], np.float32))
+        else:
+            L.update(q=job(2 * ATT_H * ATT_D, H), k=job(ATT_KVH * ATT_D, H), v=job(ATT_KVH * ATT_D, H),
+                     o=job(H, ATT_H * ATT_D), q_norm=norm(ATT_D), k_norm=norm(ATT_D))
+        layers.append(L)
+    rope = qm38.RopeConfig(ATT_D, 64, 1e7, 0, 0, 0)
+
+    def request():
+        alive, descs = [], []
+        for L in layers:
+            if L["kind"] == "linear":
+                st = L["w"].create_state()
+                alive.append(st)
+                descs.append(qm38.DecodeLinearLayer(L["in_norm"], L["post_norm"], L["qkv"], L["z"], L["b"], L["a"],
+                                                    L["out"], L["w"].handle.value, st.handle.value, L["gate"],
+                                                    L["up"], L["down"]))
+            else:
+                kv = rt.create_q8_kv_state(ATT_KVH, ATT_D, 4096)
+                alive.append(kv)
+                descs.append(qm38.DecodeFullLayer(L["in_norm"], L["post_norm"], L["q"], L["k"], L["v"], L["o"],
+                                                  L["q_norm"], L["k_norm"], ATT_H, rope, kv.handle.value, L["gate"],
+                                                  L["up"], L["down"]))
+        st = rt.create_decode_state(H)
+        h0 = (rng.standard_normal(H) * 2).astype(np.float32)
+        rt.lib.qm_copy_to_device(rt.handle, st.hidden_ptr, h0.ctypes.data, h0.nbytes)
+        alive.append(st)
+        return st, descs, alive
+
+    stream = torch.cuda.current_stream()
+    out = {}
+
+    def host_us(fn, n=20):
+        """Host time to enqueue one token (the GPU drains behind it)."""
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(n):
+            fn(10_000 + i, None)
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        return (t1 - t0) / n * 1e6
+
+    st_e, descs_e, alive_e = request()
+    eager = lambda i, m: rt.decode_layers(st_e, descs_e, (i, i, i), 1e-6)  # noqa: E731
+    ms_e, _ = timed(eager, stream, steps, warmup)
+    host_e = host_us(eager)
+    st_g, descs_g, alive_g = request()
+    graph = qm38.DecodeGraph(rt, st_g, descs_g, 1e-6)
+    replay = lambda i, m: graph.run((i, i, i))  # noqa: E731
+    ms_g, _ = timed(replay, stream, steps, warmup)
+    host_g = host_us(replay)
+    for key, ms, hu in (("decode_block4_eager", ms_e, host_e), ("decode_block4_graph", ms_g, host_g)):
+        gbs = weight_bytes / (ms * 1e-3) / 1e9
+        out[key] = {"us_per_token": round(ms * 1e3, 1), "host_enqueue_us_per_token": round(hu, 1),
+                    "weight_bytes": weight_bytes, "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    graph.close()
+    for obj in alive_e + alive_g:
+        obj.close()
+    for L in layers:
+        if "w" in L:
+            L["w"].close()
+    return out
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline
 # ---------------------------------------------------------------------------
@@ -449,7 +558,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="headline only: no extra legs, no CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--legs", default="decode,prefill,attn,deltanet",
+    ap.add_argument("--legs", default="decode,prefill,attn,deltanet,graph",
                     help="comma list of extra legs to run (the M=1 headline always runs)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc: 5 launches of a 256 MiB copy, then 5 gate+up M=1 launches")
@@ -526,6 +635,9 @@ def main() -> int:
     if "deltanet" in legs:
         log("[bench] deltanet")
         extras.update(deltanet_legs(rt, dev, rng, args.steps, args.warmup))
+    if "graph" in legs:
+        log("[bench] decode graph")
+        extras.update(decode_graph_legs(rt, dev, rng, args.steps, args.warmup))
 
     gbs, ms, step_bytes, gu_bytes, gu_ms = head
     gu_achieved = gu_bytes / (gu_ms * 1e-3) / 1e9

@@ -28,6 +28,7 @@ struct DnArgs {
   // workspace / output
   float* conv_out;  // [M][channels]: q^, k^, v after conv + prepare
   float* out;       // [M][VH][dv]
+  uint16_t* out_bf16;  // single-token step only: the output rounded to bf16 as well (or NULL)
   // optional state images after tokens 0 .. snap_rows - 1 (speculative
   // verification; snap_rows <= M - 1): history [row][channels][kernel-1] and
   // S [row][VH][dv][dk], strides in floats

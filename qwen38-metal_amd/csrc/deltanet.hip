@@ -406,7 +406,7 @@ __global__ __launch_bounds__(kThreads) void dn_scan_kernel(DnArgs a) {
 // o_in[c], writes out[c] = o * rsqrt(mean o^2 + eps) * norm * silu(z).
 // Shared by the prefill path and the fused step.
 __device__ __forceinline__ void gate_norm_row(const DnArgs& a, const float* o_in, const float* z, float* out,
-                                              uint32_t lane) {
+                                              uint32_t lane, uint16_t* out_bf16 = nullptr) {
   float v[4];  // dv <= 256
   float ss = 0.0f;
 #pragma unroll
@@ -420,7 +420,11 @@ __device__ __forceinline__ void gate_norm_row(const DnArgs& a, const float* o_in
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t c = lane + 64 * i;
-    if (c < a.dv) out[c] = v[i] * scale * a.norm[c] * silu_f(z[c]);
+    if (c < a.dv) {
+      const float r = v[i] * scale * a.norm[c] * silu_f(z[c]);
+      out[c] = r;
+      if (out_bf16) out_bf16[c] = f32_to_bf16(r);
+    }
   }
 }
 
@@ -531,7 +535,7 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_kernel(DnArgs a) {
   __syncthreads();
   if (wave == 0) {
     float* out = a.out + (size_t)vh * a.dv;
-    gate_norm_row(a, o_s, a.z + (size_t)vh * a.dv, out, lane);
+    gate_norm_row(a, o_s, a.z + (size_t)vh * a.dv, out, lane, a.out_bf16 ? a.out_bf16 + (size_t)vh * a.dv : nullptr);
   }
 }
 

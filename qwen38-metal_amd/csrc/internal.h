@@ -15,7 +15,12 @@ struct Q4Job {
   uint16_t* out;
   uint32_t rows;
   uint32_t tile_begin;  // filled by the launcher
+  // Output of a decode (M <= 16) projection: 0 bf16; 1 fp32 holding the bf16-
+  // rounded value (as if converted afterwards); 2 fp32 += the bf16-rounded
+  // value (a residual add).  `out` then points at fp32.  The GEMM takes 0 only.
+  uint32_t mode;
 };
+constexpr uint32_t kQ4OutBf16 = 0, kQ4OutF32 = 1, kQ4OutAddF32 = 2;
 
 // Device workspace for kernels whose workgroups combine partial results:
 // `counters` are zero between launches (each kernel leaves them at zero).

@@ -449,10 +449,19 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
           args.jobs[0].out[(size_t)m * rows_j[0] + row_base + row_of[t]] = f32_to_bf16(h);
         }
     } else {
+      const uint32_t mode = args.jobs[j].mode;
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        if (row_of[t] < n_valid)
-          args.jobs[j].out[(size_t)m * rows_j[0] + row_base + row_of[t]] = f32_to_bf16(acc[t][rr]);
+        if (row_of[t] < n_valid) {
+          const size_t idx = (size_t)m * rows_j[0] + row_base + row_of[t];
+          const uint16_t v = f32_to_bf16(acc[t][rr]);
+          if (mode == kQ4OutBf16)
+            args.jobs[j].out[idx] = v;
+          else if (mode == kQ4OutF32)
+            ((float*)args.jobs[j].out)[idx] = bf16_to_f32(v);
+          else
+            ((float*)args.jobs[j].out)[idx] += bf16_to_f32(v);
+        }
     }
   }
 }

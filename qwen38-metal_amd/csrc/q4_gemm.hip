@@ -451,6 +451,8 @@ void q4_gemm_workspace(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, u
 hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x, uint32_t K, uint32_t M,
                           const Workspace& ws, hipStream_t stream) {
   if (n_jobs < 1 || n_jobs > kMaxQ4Jobs || K % 64 != 0 || M == 0) return hipErrorInvalidValue;
+  for (int i = 0; i < n_jobs; ++i)
+    if (jobs[i].mode != kQ4OutBf16) return hipErrorInvalidValue;
   if (!ws.xh || ws.xh_bytes < q4_gemm_xh_bytes(K, M)) return hipErrorInvalidValue;
   const GemmPlan plan = gemm_plan(jobs, n_jobs, swiglu, K, M);
   static const bool log_plan = env_int_gemm("QM38_GEMM_PLAN_LOG", 0) != 0;

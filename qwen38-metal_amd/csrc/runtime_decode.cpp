@@ -4,10 +4,10 @@
 // 3301-3521, 1567-2020) composed from this library's entry points.
 //
 // Activations between the kernels are bf16 where a Q4 projection reads them
-// and fp32 where the DeltaNet step or attention does (small conversion
-// launches join them); the residual row stays fp32.  The residual add that
-// ends a layer is fused into the next layer's input RMSNorm (and done alone
-// after the last layer).
+// and fp32 where the DeltaNet step or attention does; the residual row stays
+// fp32.  Conversions and residual adds are folded into the producing
+// kernels' epilogues (see encode_pre), so a DeltaNet layer is seven launches
+// and a full-attention layer seven plus its attention.
 //
 // Graph mode captures every launch between two attention calls into one HIP
 // graph segment.  The attention decode is launched eagerly between segments:
@@ -45,10 +45,8 @@ struct qm_decode_state {
   } cap;
   // Views into the arena.
   uint16_t* x = nullptr;       // bf16 [hidden] normalised row
-  uint16_t* delta = nullptr;   // bf16 [hidden] mixer output
-  uint16_t* delta2 = nullptr;  // bf16 [hidden] MLP output (added by the next layer)
-  uint16_t* p[4] = {};         // bf16 projection outputs
-  float* f[4] = {};            // fp32 copies of p[0..3]
+  uint16_t* p[2] = {};         // bf16 projection outputs (query | gate, key)
+  float* f[4] = {};            // fp32 projection outputs (DeltaNet qkv, z, b, a; value)
   float* dn_out = nullptr;     // fp32 [value]
   uint16_t* dn_out_bf = nullptr;
   uint16_t* q = nullptr;       // bf16 [qh]
@@ -151,11 +149,9 @@ size_t layout(qm_decode_state* st, const qm_decode_state::Sizes& s, uint8_t* bas
   };
   const size_t H = st->hidden;
   void* x = take(H * 2);
-  void* d1 = take(H * 2);
-  void* d2 = take(H * 2);
-  void* p[4];
+  void* p[2];
   void* f[4];
-  for (int i = 0; i < 4; ++i) p[i] = take((size_t)s.p[i] * 2);
+  for (int i = 0; i < 2; ++i) p[i] = take((size_t)s.p[i] * 2);
   for (int i = 0; i < 4; ++i) f[i] = take((size_t)s.p[i] * 4);
   void* dn = take((size_t)s.value * 4);
   void* dnb = take((size_t)s.value * 2);
@@ -166,12 +162,8 @@ size_t layout(qm_decode_state* st, const qm_decode_state::Sizes& s, uint8_t* bas
   void* h = take((size_t)s.inter * 2);
   if (base) {
     st->x = (uint16_t*)x;
-    st->delta = (uint16_t*)d1;
-    st->delta2 = (uint16_t*)d2;
-    for (int i = 0; i < 4; ++i) {
-      st->p[i] = (uint16_t*)p[i];
-      st->f[i] = (float*)f[i];
-    }
+    for (int i = 0; i < 2; ++i) st->p[i] = (uint16_t*)p[i];
+    for (int i = 0; i < 4; ++i) st->f[i] = (float*)f[i];
     st->dn_out = (float*)dn;
     st->dn_out_bf = (uint16_t*)dnb;
     st->q = (uint16_t*)q;
@@ -210,48 +202,41 @@ qm_status ensure_arena(qm_decode_state* st, const qm_decode_state::Sizes& need) 
   return QM_OK;
 }
 
-qm_status convert(qm_runtime* rt, std::initializer_list<ConvSeg> segs) {
-  std::vector<ConvSeg> v(segs);
-  return hip_check(launch_convert(v.data(), (int)v.size(), rt->stream), "conversion launch");
-}
-
-// The launches of one layer up to (attention == false) or after (true) its
-// attention call; linear layers are one piece.  `rt` carries the stream and
-// the workspace of the captured or eager launches.
-qm_status encode_pre(qm_runtime* rt, qm_decode_state* st, const qm_decode_layer& L, bool first, float eps) {
+// The launches of one layer before its attention call (all of a DeltaNet
+// layer's mixer) and after it.  `rt` carries the stream and the workspace of
+// the captured or eager launches.  Projections that feed fp32 consumers
+// write fp32 copies of their bf16-rounded outputs, and the mixer and MLP
+// outputs are added into the fp32 residual row by the projections' own
+// epilogues (hidden += bf16(y), the reference's add_in_place after a bf16
+// projection), so no conversion or add launches remain.
+qm_status encode_pre(qm_runtime* rt, qm_decode_state* st, const qm_decode_layer& L, float eps) {
   const uint32_t H = st->hidden;
   const float* in_norm = L.linear ? L.linear->input_norm : L.full->input_norm;
-  qm_status s = qm_residual_rmsnorm(rt, st->hid, first ? nullptr : st->delta2, in_norm, 1, H, eps, st->x);
+  qm_status s = qm_residual_rmsnorm(rt, st->hid, nullptr, in_norm, 1, H, eps, st->x);
   if (s != QM_OK) return s;
   if (L.linear) {
     const qm_decode_linear_layer& l = *L.linear;
     const qm_dn_config& c = dn_weights_config(l.dn_weights);
-    const uint32_t channels = 2 * c.key_heads * c.key_head_dim + c.value_heads * c.value_head_dim;
     const uint32_t value = c.value_heads * c.value_head_dim;
     const qm_q4_job jobs[4] = {l.qkv, l.z, l.b, l.a};
-    uint16_t* const outs[4] = {st->p[0], st->p[1], st->p[2], st->p[3]};
-    if ((s = qm_q4_project(rt, jobs, 4, st->x, H, 1, outs)) != QM_OK) return s;
-    if ((s = convert(rt, {{st->p[0], st->f[0], channels, 1},
-                          {st->p[1], st->f[1], value, 1},
-                          {st->p[2], st->f[2], c.value_heads, 1},
-                          {st->p[3], st->f[3], c.value_heads, 1}})) != QM_OK)
+    void* const outs[4] = {st->f[0], st->f[1], st->f[2], st->f[3]};
+    const uint32_t modes[4] = {kQ4OutF32, kQ4OutF32, kQ4OutF32, kQ4OutF32};
+    if ((s = q4_project_modes(rt, jobs, outs, modes, 4, st->x, H, 1)) != QM_OK) return s;
+    if ((s = dn_step_bf16(rt, l.dn_weights, l.dn_state, st->f[0], st->f[1], st->f[2], st->f[3], eps, st->dn_out,
+                          st->dn_out_bf)) != QM_OK)
       return s;
-    if ((s = qm_dn_step(rt, l.dn_weights, l.dn_state, st->f[0], st->f[1], st->f[2], st->f[3], eps, st->dn_out)) !=
-        QM_OK)
-      return s;
-    if ((s = convert(rt, {{st->dn_out, st->dn_out_bf, value, 0}})) != QM_OK) return s;
-    uint16_t* o = st->delta;
-    return qm_q4_project(rt, &l.out_proj, 1, st->dn_out_bf, value, 1, &o);
+    void* const o[1] = {st->hid};
+    const uint32_t add[1] = {kQ4OutAddF32};
+    return q4_project_modes(rt, &l.out_proj, o, add, 1, st->dn_out_bf, value, 1);
   }
   const qm_decode_full_layer& l = *L.full;
-  const uint32_t KVH = kv_heads_of(l.kv), D = l.rope.head_dim;
+  const uint32_t KVH = kv_heads_of(l.kv);
   const qm_q4_job jobs[3] = {l.q_proj, l.k_proj, l.v_proj};
-  uint16_t* const outs[3] = {st->p[0], st->p[1], st->p[2]};
-  if ((s = qm_q4_project(rt, jobs, 3, st->x, H, 1, outs)) != QM_OK) return s;
-  if ((s = qm_attn_prepare(rt, &l.rope, 1, l.num_heads, KVH, st->p[0], st->p[1], l.q_norm, l.k_norm, eps, st->pos,
-                           0, st->q, st->gate, st->k)) != QM_OK)
-    return s;
-  return convert(rt, {{st->p[2], st->f[2], KVH * D, 1}});
+  void* const outs[3] = {st->p[0], st->p[1], st->f[2]};
+  const uint32_t modes[3] = {kQ4OutBf16, kQ4OutBf16, kQ4OutF32};
+  if ((s = q4_project_modes(rt, jobs, outs, modes, 3, st->x, H, 1)) != QM_OK) return s;
+  return qm_attn_prepare(rt, &l.rope, 1, l.num_heads, KVH, st->p[0], st->p[1], l.q_norm, l.k_norm, eps, st->pos, 0,
+                         st->q, st->gate, st->k);
 }
 
 qm_status encode_attention(qm_runtime* rt, qm_decode_state* st, const qm_decode_full_layer& l) {
@@ -262,19 +247,19 @@ qm_status encode_attention(qm_runtime* rt, qm_decode_state* st, const qm_decode_
 qm_status encode_post(qm_runtime* rt, qm_decode_state* st, const qm_decode_layer& L, float eps) {
   const uint32_t H = st->hidden;
   qm_status s;
+  void* const o[1] = {st->hid};
+  const uint32_t add[1] = {kQ4OutAddF32};
   if (L.full) {
-    uint16_t* o = st->delta;
     const uint32_t qh = L.full->num_heads * L.full->rope.head_dim;
-    if ((s = qm_q4_project(rt, &L.full->o_proj, 1, st->attn, qh, 1, &o)) != QM_OK) return s;
+    if ((s = q4_project_modes(rt, &L.full->o_proj, o, add, 1, st->attn, qh, 1)) != QM_OK) return s;
   }
   const float* post_norm = L.linear ? L.linear->post_attention_norm : L.full->post_attention_norm;
   const qm_q4_job& gate = L.linear ? L.linear->gate : L.full->gate;
   const qm_q4_job& up = L.linear ? L.linear->up : L.full->up;
   const qm_q4_job& down = L.linear ? L.linear->down : L.full->down;
-  if ((s = qm_residual_rmsnorm(rt, st->hid, st->delta, post_norm, 1, H, eps, st->x)) != QM_OK) return s;
+  if ((s = qm_residual_rmsnorm(rt, st->hid, nullptr, post_norm, 1, H, eps, st->x)) != QM_OK) return s;
   if ((s = qm_q4_swiglu(rt, &gate, &up, st->x, H, 1, st->h)) != QM_OK) return s;
-  uint16_t* o = st->delta2;
-  return qm_q4_project(rt, &down, 1, st->h, gate.out_rows, 1, &o);
+  return q4_project_modes(rt, &down, o, add, 1, st->h, gate.out_rows, 1);
 }
 
 }  // namespace
@@ -332,7 +317,7 @@ qm_status capture_variant(qm_decode_graph* g, float eps, qm_decode_graph::Varian
   qm_status s = QM_OK;
   for (size_t i = 0; i < g->layers.size() && s == QM_OK; ++i) {
     const qm_decode_layer& L = g->layers[i];
-    s = encode_pre(&g->cap, g->st, L, i == 0, eps);
+    s = encode_pre(&g->cap, g->st, L, eps);
     if (s != QM_OK) break;
     if (L.full) {
       if ((s = end_segment(g, v)) != QM_OK) return s;
@@ -341,7 +326,6 @@ qm_status capture_variant(qm_decode_graph* g, float eps, qm_decode_graph::Varian
     }
     s = encode_post(&g->cap, g->st, L, eps);
   }
-  if (s == QM_OK) s = qm_residual_add(&g->cap, g->st->hid, g->st->delta2, g->st->hidden);
   if (s != QM_OK) {
     hipGraph_t graph = nullptr;
     hipStreamEndCapture(g->cap_stream, &graph);
@@ -422,11 +406,11 @@ qm_status qm_decode_layers(qm_runtime* rt, qm_decode_state* st, const qm_decode_
     return s;
   for (uint32_t i = 0; i < n_layers; ++i) {
     const qm_decode_layer& L = layers[i];
-    if ((s = encode_pre(rt, st, L, i == 0, epsilon)) != QM_OK) return s;
+    if ((s = encode_pre(rt, st, L, epsilon)) != QM_OK) return s;
     if (L.full && (s = encode_attention(rt, st, *L.full)) != QM_OK) return s;
     if ((s = encode_post(rt, st, L, epsilon)) != QM_OK) return s;
   }
-  return qm_residual_add(rt, st->hid, st->delta2, st->hidden);
+  return QM_OK;
 }
 
 qm_status qm_decode_graph_create(qm_runtime* rt, qm_decode_state* st, const qm_decode_layer* layers,

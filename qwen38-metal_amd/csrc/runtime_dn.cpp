@@ -104,7 +104,7 @@ qm_status alloc_state(qm_runtime* rt, const qm_dn_config& cfg, qm_dn_state** out
 
 qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, qm_dn_state* to, const float* qkv,
               const float* z, const float* b, const float* a, uint32_t M, float eps, float* out,
-              qm_dn_snapshots* snaps = nullptr) {
+              qm_dn_snapshots* snaps = nullptr, uint16_t* out_bf16 = nullptr) {
   if (!rt || !w || !to || !qkv || !z || !b || !a || !out) return fail(QM_ERR_NULL_POINTER, "NULL argument");
   if (!from) from = to;
   if (M == 0) return fail(QM_ERR_EMPTY_DIMENSION, "DeltaNet prefill needs at least one token");
@@ -147,6 +147,10 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
   d.s_out = to->rec;
   d.conv_out = (float*)rt->scratch;
   d.out = out;
+  // The fused single-token kernel also writes the bf16 copy; other paths
+  // convert afterwards.
+  const bool fused_bf16 = out_bf16 && M == 1 && c.key_head_dim <= 128 && c.value_head_dim <= 128;
+  if (fused_bf16) d.out_bf16 = out_bf16;
   if (snaps && M > 1) {
     d.snap_hist = snaps->hist;
     d.snap_s = snaps->rec;
@@ -157,11 +161,21 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
   DeviceGuard g(rt->device);
   hipError_t e = launch_deltanet(d, rt->stream);
   if (e != hipSuccess) return hip_check(e, "DeltaNet launch");
+  if (out_bf16 && !fused_bf16) {
+    const ConvSeg seg{out, out_bf16, M * c.value_heads * c.value_head_dim, 0};
+    if ((e = launch_convert(&seg, 1, rt->stream)) != hipSuccess) return hip_check(e, "DeltaNet bf16 output");
+  }
   if (c.conv_kernel_size > 1) to->cur = next;
   return QM_OK;
 }
 
 }  // namespace
+
+qm_status qm::dn_step_bf16(qm_runtime* rt, const qm_dn_weights* w, qm_dn_state* st, const float* qkv, const float* z,
+                           const float* b, const float* a, float eps, float* out, uint16_t* out_bf16) {
+  if (!out_bf16) return fail(QM_ERR_NULL_POINTER, "bf16 output is NULL");
+  return run(rt, w, st, st, qkv, z, b, a, 1, eps, out, nullptr, out_bf16);
+}
 
 const qm_dn_config& qm::dn_weights_config(const qm_dn_weights* w) { return w->cfg; }
 const qm_runtime* qm::dn_weights_runtime(const qm_dn_weights* w) { return w->rt; }

@@ -40,6 +40,12 @@ qm_status ensure_counters(qm_runtime* rt, size_t count);
 qm_status ensure_xh(qm_runtime* rt, size_t bytes);
 // Workspace handed to kernels that split work across workgroups.
 Workspace workspace(qm_runtime* rt);
+// qm_q4_project with a per-job output mode (kQ4Out*; fp32 modes need M <= 16).
+qm_status q4_project_modes(qm_runtime* rt, const qm_q4_job* jobs, void* const* outs, const uint32_t* modes,
+                           int n_jobs, const uint16_t* x, uint32_t in_elems, uint32_t M);
+// qm_dn_step that also writes the output rounded to bf16 into out_bf16.
+qm_status dn_step_bf16(qm_runtime* rt, const qm_dn_weights* w, qm_dn_state* st, const float* qkv, const float* z,
+                       const float* b, const float* a, float eps, float* out, uint16_t* out_bf16);
 // Frees a runtime's grow-only buffers (not the runtime itself).
 void release_buffers(qm_runtime* rt);
 

@@ -66,6 +66,26 @@ qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const ui
 
 }  // namespace
 
+qm_status qm::q4_project_modes(qm_runtime* rt, const qm_q4_job* jobs, void* const* outs, const uint32_t* modes,
+                               int n_jobs, const uint16_t* x, uint32_t in_elems, uint32_t M) {
+  if (!rt || !jobs || !outs || !modes) return fail(QM_ERR_NULL_POINTER, "NULL argument");
+  if (n_jobs <= 0 || n_jobs > kMaxQ4Jobs) return fail(QM_ERR_INVALID_ARGUMENT, "1..%d jobs per call", kMaxQ4Jobs);
+  qm_status st = validate_x(x, M);
+  if (st != QM_OK) return st;
+  Q4Job q[kMaxQ4Jobs];
+  for (int i = 0; i < n_jobs; ++i) {
+    if ((st = validate_job(&jobs[i], in_elems, "Q4 projection")) != QM_OK) return st;
+    if (!outs[i]) return fail(QM_ERR_NULL_POINTER, "output %d is NULL", i);
+    if (modes[i] > kQ4OutAddF32 || (modes[i] != kQ4OutBf16 && M > kDecodeMaxRows))
+      return fail(QM_ERR_INVALID_ARGUMENT, "output mode %u needs the decode path (M <= %u)", modes[i],
+                  kDecodeMaxRows);
+    q[i] = to_job(jobs[i], (uint16_t*)outs[i]);
+    q[i].mode = modes[i];
+  }
+  DeviceGuard g(rt->device);
+  return launch(rt, q, n_jobs, false, x, in_elems, M, "Q4 projection launch");
+}
+
 extern "C" {
 
 qm_status qm_q4_project(qm_runtime* rt, const qm_q4_job* jobs, int n_jobs, const uint16_t* x,

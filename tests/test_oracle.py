@@ -472,3 +472,37 @@ def test_attn_prepare_mrope_axis_selection():
     _, _, c = oracle.attn_prepare(qg, kin, w, w, hd, rd, 1e4, 1e-6, positions=base)
     _, _, d = oracle.attn_prepare(qg, kin, w, w, hd, rd, 1e4, 1e-6, positions=moved)
     np.testing.assert_array_equal(c, d)
+
+
+# ---- residual add + RMSNorm (qo_residual_rmsnorm; qwen38.metal:4253-4333) --
+def test_rmsnorm_known_answers():
+    # [3, 4]: mean square 12.5, scale 1/sqrt(12.5); weights [1, 2] as given.
+    _, out = oracle.residual_rmsnorm(np.array([[3.0, 4.0]], np.float32), np.array([1.0, 2.0], np.float32), 0.0)
+    s = 1 / np.sqrt(12.5)
+    np.testing.assert_allclose(out[0], [3 * s, 8 * s], rtol=1e-15)
+    # A constant row normalises to its sign times the weights.
+    _, out = oracle.residual_rmsnorm(np.full((2, 7), -2.5, np.float32), np.full(7, 0.5, np.float32), 0.0)
+    np.testing.assert_allclose(out, np.full((2, 7), -0.5), rtol=1e-15)
+
+
+def test_rmsnorm_invariants():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((3, 40)).astype(np.float32)
+    w = rng.standard_normal(40).astype(np.float32)
+    _, a = oracle.residual_rmsnorm(x, w, 0.0)
+    _, b = oracle.residual_rmsnorm(4 * x, w, 0.0)  # scale invariance (exact power-of-two scaling)
+    np.testing.assert_allclose(a, b, rtol=1e-14)
+    # Unit-RMS output with unit weights; zero weights give zero (weights are not 1 + w).
+    _, u = oracle.residual_rmsnorm(x, np.ones(40, np.float32), 0.0)
+    np.testing.assert_allclose(np.sqrt(np.mean(u ** 2, axis=1)), 1.0, rtol=1e-12)
+    _, z = oracle.residual_rmsnorm(x, np.zeros(40, np.float32), 1e-6)
+    assert not np.any(z)
+    # eps keeps an all-zero row finite.
+    _, e = oracle.residual_rmsnorm(np.zeros((1, 8), np.float32), np.ones(8, np.float32), 1e-6)
+    assert np.all(e == 0)
+    # The residual add is plain fp32 addition, row by row.
+    d = rng.standard_normal((3, 40)).astype(np.float32)
+    h, r = oracle.residual_rmsnorm(x, w, 1e-6, d)
+    np.testing.assert_array_equal(h, x + d)
+    _, r2 = oracle.residual_rmsnorm(x + d, w, 1e-6)
+    np.testing.assert_array_equal(r, r2)
