@@ -116,6 +116,24 @@ def timed(step, stream, steps: int, warmup: int):
     return t0.elapsed_time(t1) / steps, marks_all
 
 
+def step_distribution(step, stream, steps: int, warmup: int = 2):
+    """Per-step times (us) from one event after each step: (p10, median, p90).
+    The events sit between steps, so the set's own kernels stay back to back."""
+    import torch
+    ev = Events(stream)
+    for i in range(warmup):
+        step(i, None)
+    torch.cuda.synchronize()
+    gpu_blocker()
+    marks = [ev.mark()]
+    for i in range(steps):
+        step(warmup + i, None)
+        marks.append(ev.mark())
+    torch.cuda.synchronize()
+    d = np.array([a.elapsed_time(b) * 1e3 for a, b in zip(marks[:-1], marks[1:])])
+    return tuple(round(float(v), 2) for v in np.percentile(d, [10, 50, 90]))
+
+
 # ---------------------------------------------------------------------------
 # Q4 projections
 # ---------------------------------------------------------------------------
@@ -167,7 +185,27 @@ def q4_leg(rt, dev, sets, M: int, rng, steps, warmup):
     abytes = {"qkv": 2 * M * (H + QKV), "gateup": 2 * M * (H + I), "down": 2 * M * (I + H)}
     flops = {"qkv": 2 * M * QKV * H, "gateup": 4 * M * I * H, "down": 2 * M * H * I}
     kern = dict(zip(("qkv", "gateup", "down"), per))
+    q4_leg.last_step = step
     return ms, kern, wbytes, abytes, flops
+
+
+def matvec_4096_leg(rt, dev, rng, steps, warmup):
+    """one 4096 x 4096 Q4 matvec (M = 1), launch-bound."""
+    import torch
+    import qm38
+    from qm38 import synth
+    N = K = 4096
+    jobs = []
+    for _ in range(NCOPY):
+        w, sc, b = synth.q4_matrix(rng, N, K)
+        jobs.append((qm38.Runtime.job(dev_array(w, dev), dev_array(sc, dev), dev_array(b, dev), N)))
+    x = dev_array(synth_bf16(rng, (1, K)), dev)
+    y = torch.empty((1, N), dtype=torch.int16, device=dev)
+    ms, _ = timed(lambda i, m: rt.q4_project([jobs[i % NCOPY]], x, K, 1, [y]), torch.cuda.current_stream(), steps,
+                  warmup)
+    nbytes = q4_bytes(N, K) + 2 * K + 2 * N  # 9,453,568 B
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 # ---------------------------------------------------------------------------
@@ -512,6 +550,56 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> int:
     return 0
 
 
+def gemm_counter_summary(d: str) -> int:
+    """profiles/q4_gemm_gateup_m2048_counters.txt from a rocprofv3 --pmc run of
+    bench.py --gemm-probe (per-dispatch SQ/GRBM counters of q4_gemm_kernel)."""
+    rows = []
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        with open(f) as fh:
+            rows += list(csv.DictReader(fh))
+    per = {}
+    for r in rows:
+        if "q4_gemm_kernel" not in r["Kernel_Name"]:
+            continue
+        e = per.setdefault(int(r["Dispatch_Id"]), {"ns": int(r["End_Timestamp"]) - int(r["Start_Timestamp"])})
+        e[r["Counter_Name"]] = float(r["Counter_Value"])
+    if not per:
+        print("no q4_gemm_kernel dispatches found", file=sys.stderr)
+        return 1
+    simds, cus, xcds = 1024, 256, 8
+    lines = [
+        "# rocprofv3 counters: q4_gemm_kernel, gate/up with SwiGLU, M = 2048 (BASELINE config 3)",
+        "#",
+        "# command (repo root, MI355X, one GPU):",
+        "#   rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_BUSY_CU_CYCLES SQ_LDS_BANK_CONFLICT \\",
+        "#     SQ_LDS_IDX_ACTIVE SQ_INSTS_LDS SQ_INSTS_MFMA SQ_WAIT_INST_LDS GRBM_GUI_ACTIVE --kernel-trace \\",
+        "#     -d gpurun_out/gemm_pmc -o gemm --output-format csv -- python3 bench.py --gemm-probe",
+        "#   python bench.py --gemm-counters-from gpurun_out/gemm_pmc",
+        "#",
+        "# GRBM_GUI_ACTIVE is summed over the 8 XCDs, so the kernel's GPU cycles are GRBM_GUI_ACTIVE / 8.",
+        "# MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (cycles x 1024 SIMDs); each v_mfma_f32_32x32x16_f16 is",
+        "# 32 busy cycles (SQ_INSTS_MFMA x 32 = SQ_VALU_MFMA_BUSY_CYCLES).  LDS active = SQ_LDS_IDX_ACTIVE /",
+        "# (cycles x 256 CUs).  Durations run longer under counter collection than in the bench.",
+        "",
+        f"{'dispatch':>8} {'us':>9} {'GHz':>6} {'MFMA busy':>10} {'MFMA instr':>12} {'LDS active':>11} "
+        f"{'LDS instr':>11} {'bank confl':>11}",
+    ]
+    for k in sorted(per):
+        e = per[k]
+        cyc = e.get("GRBM_GUI_ACTIVE", 0.0) / xcds
+        if cyc <= 0:
+            continue
+        lines.append(f"{k:>8} {e['ns'] / 1e3:>9.1f} {cyc / e['ns']:>6.2f} "
+                     f"{e.get('SQ_VALU_MFMA_BUSY_CYCLES', 0) / (cyc * simds):>10.1%} {e.get('SQ_INSTS_MFMA', 0):>12.0f} "
+                     f"{e.get('SQ_LDS_IDX_ACTIVE', 0) / (cyc * cus):>11.1%} {e.get('SQ_INSTS_LDS', 0):>11.0f} "
+                     f"{e.get('SQ_LDS_BANK_CONFLICT', 0):>11.0f}")
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "q4_gemm_gateup_m2048_counters.txt")
+    with open(path, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print(path)
+    return 0
+
+
 def _short_kernel_name(name: str) -> str:
     n = name.replace("qm::(anonymous namespace)::", "").replace("(anonymous namespace)::", "")
     return n.replace("(qm::DecodeArgs)", "(DecodeArgs)").replace("(qm::GemmArgs)", "(GemmArgs)")
@@ -560,6 +648,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--legs", default="decode,prefill,attn,deltanet,graph",
                     help="comma list of extra legs to run (the M=1 headline always runs)")
+    ap.add_argument("--gemm-counters-from", metavar="PMC_DIR",
+                    help="write profiles/q4_gemm_gateup_m2048_counters.txt from a --gemm-probe counter run")
+    ap.add_argument("--gemm-probe", action="store_true",
+                    help="only run six M=2048 gate/up GEMMs (for rocprofv3 --pmc passes)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc: 5 launches of a 256 MiB copy, then 5 gate+up M=1 launches")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -571,6 +663,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.stats_from:
         return stats_summary(args.stats_from)
+    if args.gemm_counters_from:
+        return gemm_counter_summary(args.gemm_counters_from)
     if args.traffic_from:
         return traffic_summary(*args.traffic_from)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -590,6 +684,17 @@ def main() -> int:
 
     log("[bench] uploading 3 weight copies")
     sets = q4_sets(rng, dev)
+    if args.gemm_probe:
+        # Six gate/up SwiGLU GEMMs at M = 2048, for
+        # rocprofv3 --pmc passes over the prefill kernel.
+        x = dev_array(synth_bf16(rng, (2048, H)), dev)
+        h = torch.empty((2048, I), dtype=torch.int16, device=dev)
+        for i in range(6):
+            j = sets[i % NCOPY]
+            rt.q4_swiglu(j["gate"][0], j["up"][0], x, H, 2048, h)
+        torch.cuda.synchronize()
+        rt.close()
+        return 0
     if args.traffic_probe:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -617,6 +722,11 @@ def main() -> int:
             "kernel_hbm_frac": {k: round((wb[k] + ab[k]) / (kern[k] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) for k in kern}}
         if M == 1:
             head = (gbs, ms, step_bytes, wb["gateup"] + ab["gateup"], kern["gateup"])
+            p10, p50, p90 = step_distribution(q4_leg.last_step, torch.cuda.current_stream(), max(args.steps, 100))
+            extras["q4_decode_set_M1"]["step_us_p10_p50_p90"] = [p10, p50, p90]
+    if "decode" in legs:
+        log("[bench] q4 matvec 4096x4096 (config 1)")
+        extras["q4_matvec_4096_M1"] = matvec_4096_leg(rt, dev, rng, args.steps, args.warmup)
     if "prefill" in legs:
         for M in (512, 2048):
             log(f"[bench] q4 prefill GEMM set M={M}")
