@@ -536,11 +536,11 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> int:
                 "algorithmic_bytes": alg,
                 "traffic_over_algorithmic": round((per["FETCH_SIZE"] + per["WRITE_SIZE"]) / alg, 4),
                 "commands": [
-                    "rocprofv3 --pmc FETCH_SIZE --kernel-trace -d gpurun_out/pmc_fetch -o fetch --output-format csv "
+                    "rocprofv3 --pmc FETCH_SIZE --kernel-trace -d prof_out/pmc_fetch -o fetch --output-format csv "
                     "-- python -u bench.py --traffic-probe",
-                    "rocprofv3 --pmc WRITE_SIZE --kernel-trace -d gpurun_out/pmc_write -o write --output-format csv "
+                    "rocprofv3 --pmc WRITE_SIZE --kernel-trace -d prof_out/pmc_write -o write --output-format csv "
                     "-- python -u bench.py --traffic-probe",
-                    "python bench.py --traffic-from gpurun_out/pmc_fetch gpurun_out/pmc_write"],
+                    "python bench.py --traffic-from prof_out/pmc_fetch prof_out/pmc_write"],
                 "method": "per-dispatch counter (KiB) x (known copy bytes / the counter's reading for a 256 MiB "
                           "device copy); small copies excluded from the calibration mean"})
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "q4_decode_gateup_traffic.json")
@@ -573,8 +573,8 @@ def gemm_counter_summary(d: str) -> int:
         "# command (repo root, MI355X, one GPU):",
         "#   rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_BUSY_CU_CYCLES SQ_LDS_BANK_CONFLICT \\",
         "#     SQ_LDS_IDX_ACTIVE SQ_INSTS_LDS SQ_INSTS_MFMA SQ_WAIT_INST_LDS GRBM_GUI_ACTIVE --kernel-trace \\",
-        "#     -d gpurun_out/gemm_pmc -o gemm --output-format csv -- python3 bench.py --gemm-probe",
-        "#   python bench.py --gemm-counters-from gpurun_out/gemm_pmc",
+        "#     -d prof_out/gemm_pmc -o gemm --output-format csv -- python3 bench.py --gemm-probe",
+        "#   python bench.py --gemm-counters-from prof_out/gemm_pmc",
         "#",
         "# GRBM_GUI_ACTIVE is summed over the 8 XCDs, so the kernel's GPU cycles are GRBM_GUI_ACTIVE / 8.",
         "# MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (cycles x 1024 SIMDs); each v_mfma_f32_32x32x16_f16 is",
@@ -616,9 +616,9 @@ def stats_summary(prof_dir: str) -> int:
         "# rocprofv3 kernel statistics: bench.py (all legs, 20 timed steps)",
         "#",
         "# command (repo root, MI355X, one GPU):",
-        "#   rocprofv3 --kernel-trace --stats -d gpurun_out/prof -o bench --output-format csv -- python3 -u bench.py "
+        "#   rocprofv3 --kernel-trace --stats -d prof_out/prof -o bench --output-format csv -- python3 -u bench.py "
         "--no-cpu --steps 20",
-        "#   python bench.py --stats-from gpurun_out/prof",
+        "#   python bench.py --stats-from prof_out/prof",
         "#",
         "# Per-kernel averages mix the legs that launch the same template (q8_prefill_kernel<128,2> is the",
         "# causal prefill, including the 32K/128K cache fills of the attention legs; q4_gemm_kernel serves",
