@@ -369,3 +369,23 @@ def test_decode_layers_reject_bad_layers(rt, torch_dev):
         rt.decode_layers(st, [], 0, EPS)
     with pytest.raises(QmError):
         DecodeGraph(rt, st, [bad], EPS)
+
+
+def test_graph_and_eager_report_kv_capacity(rt, torch_dev):
+    # A full-attention layer whose cache holds two tokens: the third token's
+    # attention call fails with CAPACITY_EXCEEDED (reserve_q8_kv_tokens's
+    # check), eagerly and from a graph replay, without launching past it.
+    model = Model(rt, torch_dev, seed=16, kinds=("full",))
+    _, caches, descs = model.new_request(max_tokens=2)
+    st = _state_with(rt, torch_dev, _hidden0(6))
+    rt.decode_layers(st, descs, _positions(0), EPS)
+    g = DecodeGraph(rt, st, descs, EPS)
+    g.run(_positions(1))
+    assert caches[0].sequence_length == 2
+    with pytest.raises(QmError, match="CAPACITY|capacity"):
+        g.run(_positions(2))
+    with pytest.raises(QmError, match="CAPACITY|capacity"):
+        rt.decode_layers(st, descs, _positions(2), EPS)
+    rt.synchronize()
+    assert caches[0].sequence_length == 2
+    g.close()
