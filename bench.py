@@ -227,6 +227,14 @@ def kv_fill(rt, dev, cache, rng, tokens: int, chunk: int = 8192):
     torch.cuda.synchronize()
 
 
+def kv_cache(rt, tokens: int):
+    """A cache grown to hold `tokens` tokens up front (no growth in timed calls)."""
+    c = rt.create_q8_kv_state(ATT_KVH, ATT_D)
+    c.reserve(tokens)
+    c.truncate(0)
+    return c
+
+
 def attn_bytes(T: int) -> int:
     return T * ATT_KVH * ATT_D * 2 + T * ATT_KVH * 2 * 4
 
@@ -236,28 +244,33 @@ def attention_legs(rt, dev, rng, steps, warmup):
     from qm38 import synth
     out = {}
     stream = torch.cuda.current_stream()
-    # (a) one sequence at 32K: us per decode token.
-    T0 = 32768
-    cache = rt.create_q8_kv_state(ATT_KVH, ATT_D, T0 + steps + warmup + 8)
-    kv_fill(rt, dev, cache, rng, T0)
+    # (a) one sequence at 32K: us per decode token.  Six caches (415 MB) take
+    # turns so the 256 MB MALL cannot hold the one being read.
+    T0, NC = 32768, 6
+    caches = []
+    for _ in range(NC):
+        c = kv_cache(rt, T0 + steps + warmup + 8)
+        kv_fill(rt, dev, c, rng, T0)
+        caches.append(c)
     q = dev_array(synth.bf16_normal(rng, (1, ATT_H, ATT_D)), dev)
     g = dev_array(synth.bf16_normal(rng, (1, ATT_H, ATT_D)), dev)
     k = torch.randn((1, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
     v = torch.randn((1, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
     o = torch.empty((1, ATT_H, ATT_D), dtype=torch.int16, device=dev)
-    ms, _ = timed(lambda i, m: rt.gqa_attention_q8([cache], q, g, k, v, ATT_H, o), stream, steps, warmup)
-    T_avg = T0 + warmup + (steps + 1) / 2
+    ms, _ = timed(lambda i, m: rt.gqa_attention_q8([caches[i % NC]], q, g, k, v, ATT_H, o), stream, steps, warmup)
+    T_avg = T0 + (warmup + steps) / NC / 2
     gbs = attn_bytes(int(T_avg)) / (ms * 1e-3) / 1e9
     out["attn_decode_32k"] = {"us_per_token": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                               "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-                              "shape": "H=64 KVH=8 d=128, 1 sequence at 32K"}
-    cache.close()
+                              "shape": f"H=64 KVH=8 d=128, 1 sequence at 32K, {NC} caches in turn"}
+    for c in caches:
+        c.close()
     torch.cuda.empty_cache()
     # (b) ragged batch of 8 over {4K, 32K, 128K}.
     lens = list(np.random.default_rng(4).choice([4096, 32768, 131072], 8))
     caches = []
     for n in lens:
-        c = rt.create_q8_kv_state(ATT_KVH, ATT_D, int(n) + steps + warmup + 8)
+        c = kv_cache(rt, int(n) + steps + warmup + 8)
         kv_fill(rt, dev, c, rng, int(n))
         caches.append(c)
     B = len(caches)
@@ -278,7 +291,7 @@ def attention_legs(rt, dev, rng, steps, warmup):
     # (c) causal prefill: 2048 rows onto a 4096-token cache.
     P, T = 2048, 4096
     reps = max(2, min(steps, 5))
-    caches = [rt.create_q8_kv_state(ATT_KVH, ATT_D, T + P) for _ in range(reps + 1)]
+    caches = [kv_cache(rt, T + P) for _ in range(reps + 1)]
     for c in caches:
         kv_fill(rt, dev, c, rng, T)
     q = dev_array(synth.bf16_normal(rng, (P, ATT_H, ATT_D)), dev)
@@ -483,6 +496,49 @@ def cpu_baseline_q4(seconds: float = 12.0):
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"QKV projection 5120->10240 (M=1) repeated {n}x over {dt:.1f}s, fp32 per-group "
                       f"accumulation (oracle qo_q4_project_f32)"}
+
+
+def cpu_baseline_legs(seconds: float = 4.0):
+    """The attention and DeltaNet legs' math on host cores (oracle/, OpenMP),
+    each over a bounded sample, reported beside the GPU legs."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    rng = np.random.default_rng(98)
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
+    out = {}
+
+    def rate(fn):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            fn()
+            n += 1
+        return (time.perf_counter() - t0) / n, n
+
+    # Decode attention, one sequence at 32K (fp64-accumulated oracle, heads in parallel).
+    T = 32768
+    kq, ks = oracle.q8_quantize_rows(rng.standard_normal((T, ATT_KVH, ATT_D)).astype(np.float32))
+    vq, vs = oracle.q8_quantize_rows(rng.standard_normal((T, ATT_KVH, ATT_D)).astype(np.float32))
+    q = rng.standard_normal((1, ATT_H, ATT_D)).astype(np.float32)
+    sec, n = rate(lambda: oracle.attention(q, q, kq, ks, vq, vs, T - 1, threads=threads))
+    out["attn_decode_32k"] = {"us_per_token": round(sec * 1e6, 1),
+                              "GB/s": round(attn_bytes(T) / sec / 1e9, 2), "cores": threads,
+                              "sample": f"{n} decode tokens at T=32768, H=64 KVH=8 d=128 (qo_attention)"}
+    # DeltaNet step and 2048-token prefill (fp32 oracle, value heads in parallel).
+    c = DN
+    ch = 2 * c["key_heads"] * c["key_head_dim"] + c["value_heads"] * c["value_head_dim"]
+    VH, dv, dk = c["value_heads"], c["value_head_dim"], c["key_head_dim"]
+    conv = (rng.standard_normal((ch, 4)) * 0.5).astype(np.float32)
+    zero = np.zeros(VH, np.float32)
+    norm = np.ones(dv, np.float32)
+    for M, key in ((1, "deltanet_step"), (2048, "deltanet_prefill_2048")):
+        acts = [rng.standard_normal(sh).astype(np.float32) for sh in ((M, ch), (M, VH * dv), (M, VH), (M, VH))]
+        hist = np.zeros((ch, 3), np.float32)
+        S = np.zeros((VH, dv, dk), np.float32)
+        sec, n = rate(lambda: oracle.deltanet_prefill(c, conv, zero, zero, norm, *acts, 1e-6, hist, S))
+        out[key] = {"us": round(sec * 1e6, 1), "tokens_per_s": round(M / sec, 1), "cores": threads,
+                    "sample": f"{n} runs of {M} token(s), 16/32 heads, d=128 (qo_dn_prefill_f32)"}
+    return out
 
 
 def traffic_from_profiles():
@@ -776,6 +832,9 @@ def main() -> int:
     if not args.no_cpu and not args.quick:
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline_q4()
+        if legs & {"attn", "deltanet"}:
+            log("[bench] cpu baselines of the attention / DeltaNet legs")
+            result["extras"]["cpu_legs"] = cpu_baseline_legs()
     else:
         result["cpu_baseline"] = None
     rt.close()

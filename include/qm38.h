@@ -153,26 +153,35 @@ typedef struct qm_kv qm_kv;
 /* Replaces create_q8_kv_state (metal_runtime.rs:7298) and
  * LogicalPageTable::new (paged_kv.rs:22-35).  K/V are int8 with one fp32
  * scale per token and KV head.  Physical layout (HBM), per page of
- * `page_tokens` tokens:
- *   K pages  int8 [page][kv_head][page_tokens][head_dim]
- *   V pages  int8 [page][kv_head][head_dim][page_tokens]   (d-major)
+ * `page_tokens` tokens, with Dp = 64, 128 or 256 the smallest of these
+ * >= head_dim (dimensions past head_dim hold zero):
+ *   K pages  int8 [page][kv_head][page_tokens][Dp]
+ *   V pages  int8 [page][kv_head][Dp][page_tokens]   (d-major)
  *   scales   fp32 [page][kv_head][page_tokens]  (one array for K, one for V)
  * Pages materialise lazily as tokens arrive and receive sequential page ids
- * (paged_kv.rs:89-97).  page_tokens must be 16; head_dim must be 64, 128 or 256
- * (multiple of 32, <= 256 in the reference's validate_attention_shape,
- * metal_runtime.rs:9186-9193).  max_tokens bounds the sequence length. */
+ * (paged_kv.rs:89-97).  head_dim 1..256 and kv_heads > 0
+ * (validate_attention_shape, metal_runtime.rs:9186-9193); page_tokens must
+ * be 16.  Capacity starts at 16 tokens and grows on demand to the next power
+ * of two of the required length, copying the cache (ensure_q8_kv_capacity,
+ * metal_runtime.rs:7406-7421).  max_tokens = 0 grows without limit, as the
+ * reference does; otherwise appends past max_tokens fail with
+ * QM_ERR_CAPACITY_EXCEEDED (LogicalPageTable's capacity, paged_kv.rs:54-62). */
 qm_status qm_kv_create(qm_runtime* rt, uint32_t kv_heads, uint32_t head_dim,
                        uint32_t page_tokens, uint32_t max_tokens, qm_kv** out);
 void qm_kv_destroy(qm_kv* kv);
 /* Active sequence length (Q8KvState::sequence_length, metal_runtime.rs:595). */
 uint32_t qm_kv_length(const qm_kv* kv);
+/* Tokens the cache holds without growing (Q8KvState::capacity_tokens,
+ * metal_runtime.rs:578-593). */
+uint32_t qm_kv_capacity(const qm_kv* kv);
 /* Number of materialised pages (LogicalPageTable::allocated_pages). */
 uint32_t qm_kv_allocated_pages(const qm_kv* kv);
 /* Physical page id backing `token`, or -1 if token >= length
  * (LogicalPageTable::page_for_token, paged_kv.rs:77-85). */
 int64_t qm_kv_page_for_token(const qm_kv* kv, uint32_t token);
 /* Ensures capacity for `additional` more tokens (reserve_q8_kv_tokens,
- * metal_runtime.rs:7307-7317): materialises the pages they will need. */
+ * metal_runtime.rs:7307-7317): grows the cache if needed and materialises
+ * the pages they will need. */
 qm_status qm_kv_reserve(qm_kv* kv, uint32_t additional);
 /* Moves the logical end backwards (truncate_q8_kv_tokens, :7323-7333). */
 qm_status qm_kv_truncate(qm_kv* kv, uint32_t length);
@@ -193,7 +202,9 @@ qm_status qm_kv_read(const qm_kv* kv, int8_t* keys, int8_t* values,
  *   o    bf16 [B][H][head_dim] = softmax(q K^T / sqrt(d)) V * sigmoid(gate)
  * Replaces gqa_attention_q8 (metal_runtime.rs:8230-8425; kernels
  * qwen38_gqa_q8_scores/values, qwen38.metal:5240-5323).  All sequences must
- * share kv_heads/head_dim; H % kv_heads == 0. */
+ * share kv_heads/head_dim; H % kv_heads == 0 with at most 16 query heads per
+ * KV head.  q/gate must be 16-byte aligned when head_dim % 8 == 0.  Caches
+ * grow as needed before anything is launched. */
 qm_status qm_attn_decode(qm_runtime* rt, qm_kv* const* seqs, uint32_t B,
                          const uint16_t* q, const uint16_t* gate,
                          const float* k, const float* v, uint32_t H,

@@ -39,6 +39,7 @@ def lib() -> C.CDLL:
             getattr(L, n).restype = None
         L.qo_swiglu.argtypes = [vp, vp, C.c_size_t, vp]
         L.qo_q8_quantize.argtypes = [vp, u32, vp, vp]
+        L.qo_q8_quantize_rows.argtypes = [vp, C.c_uint64, u32, vp, vp]
         L.qo_attention.argtypes = [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, vp, i32]
         for n in ("qo_dn_prefill_f32", "qo_dn_prefill_f64"):
             getattr(L, n).argtypes = [u32, u32, u32, u32, u32, vp, vp, vp, vp, vp, vp, vp, vp, u32,
@@ -97,8 +98,8 @@ def q8_quantize_rows(x) -> tuple[np.ndarray, np.ndarray]:
     flat = x.reshape(-1, x.shape[-1])
     q = np.zeros(flat.shape, np.int8)
     s = np.zeros(flat.shape[0], np.float32)
-    for i in range(flat.shape[0]):
-        q[i], s[i] = q8_quantize(flat[i])
+    if flat.shape[0]:
+        lib().qo_q8_quantize_rows(_p(flat), flat.shape[0], flat.shape[1], _p(q), _p(s))
     return q.reshape(x.shape), s.reshape(x.shape[:-1])
 
 

@@ -136,6 +136,14 @@ void qo_q8_quantize(const float* x, uint32_t d, int8_t* q, float* scale) {
   }
 }
 
+// Row-wise qo_q8_quantize of n rows of d elements (scales [n]).
+void qo_q8_quantize_rows(const float* x, uint64_t n, uint32_t d, int8_t* q, float* scale) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+  for (int64_t r = 0; r < (int64_t)n; ++r) qo_q8_quantize(x + (size_t)r * d, d, q + (size_t)r * d, scale + r);
+}
+
 // GQA attention of `rows` query rows over a token-major Q8 cache
 // (Q8KvState layout, metal_runtime.rs:578-593):
 //   keys/values int8 [T][KVH][d], key/value scales fp32 [T][KVH].
@@ -175,10 +183,16 @@ void qo_attention(const float* q, const float* gate, const int8_t* keys, const f
       den += sc[t];
     }
     float* orow = o + ((size_t)r * H + h) * d;
+    // Token-outer so each V row is read once; every acc[i] still sums its
+    // terms sc_t * v_ti * vs_t in token order.
+    std::vector<double> accv(d, 0.0);
+    for (uint32_t t = 0; t < visible; ++t) {
+      const int8_t* vr = values + ((size_t)t * KVH + kvh) * d;
+      const double w = sc[t], vs = (double)vscale[(size_t)t * KVH + kvh];
+      for (uint32_t i = 0; i < d; ++i) accv[i] += w * (double)vr[i] * vs;
+    }
     for (uint32_t i = 0; i < d; ++i) {
-      double acc = 0.0;
-      for (uint32_t t = 0; t < visible; ++t)
-        acc += sc[t] * (double)values[((size_t)t * KVH + kvh) * d + i] * (double)vscale[(size_t)t * KVH + kvh];
+      double acc = accv[i];
       acc /= den;
       if (gate) acc *= 1.0 / (1.0 + exp(-(double)gate[((size_t)r * H + h) * d + i]));
       orow[i] = (float)acc;
@@ -237,8 +251,13 @@ static void dn_step(uint32_t KH, uint32_t VH, uint32_t dk, uint32_t dv, uint32_t
     }
   }
   const uint32_t rep = VH / KH;
-  std::vector<T> o(dv);
+  // Value heads are independent: they run on OpenMP threads (each head's
+  // arithmetic is unchanged).
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if (VH > 1)
+#endif
   for (uint32_t vh = 0; vh < VH; ++vh) {
+    std::vector<T> o(dv);
     const uint32_t kh = vh / rep;
     const T* qv = &c[kh * dk];
     const T* kv = &c[key_el + kh * dk];

@@ -6,8 +6,12 @@
 namespace qm {
 
 constexpr int kMaxAttnSeqs = 16;  // sequences per launch (kernel-argument table)
-constexpr int kMaxSplits = 2048;         // page splits per sequence (combine kernel's LDS table)
-constexpr int kMaxPagesPerSplit = 1024;  // pages per decode workgroup (its LDS page-id table)
+constexpr int kMaxSplits = 2048;         // page splits per sequence
+constexpr int kMaxPagesPerSplit = 1024;  // pages per decode workgroup
+
+// Storage dimension of a cache with head dimension d (1..256): pages hold
+// the next kernel width, the extra dimensions are zero.
+inline uint32_t attn_padded_dim(uint32_t d) { return d <= 64 ? 64 : d <= 128 ? 128 : 256; }
 
 struct AttnSeq {
   int8_t* k;          // K pages   [page][kv_head][16][D]
@@ -28,7 +32,8 @@ struct AppendArgs {
   const float* k;  // [items][kv_heads][D]
   const float* v;
   uint32_t kv_heads;
-  uint32_t head_dim;
+  uint32_t head_dim;      // real head dimension (strides of k and v)
+  uint32_t head_dim_pad;  // storage dimension of the cache pages (64, 128 or 256)
   uint32_t decode;  // 1: item = sequence (one token each); 0: item = row of seqs[0]
   uint32_t start;   // prefill: cache position of row 0
   AttnSeq seqs[kMaxAttnSeqs];
@@ -38,12 +43,14 @@ struct AttnArgs {
   const uint16_t* q;     // bf16 [rows][H][D]
   const uint16_t* gate;  // bf16 [rows][H][D] or null
   uint16_t* o;           // bf16 [rows][H][D]
-  float* partials;       // [split rows][H][D + 2]
+  float* partials;       // decode split partials: O [split rows][H][Dp], then (m, l) [split rows][H][2]
   const float* k_new;    // decode: fp32 [n_seqs][kv_heads][D] rows appended by the kernel
   const float* v_new;
   uint32_t heads;
   uint32_t kv_heads;
-  uint32_t head_dim;
+  uint32_t head_dim;      // real head dimension (strides of q, gate, o, k_new, v_new)
+  uint32_t head_dim_pad;  // storage dimension Dp of the cache pages (64, 128 or 256)
+  uint32_t part_rows;     // decode: split rows in `partials` (offset of the (m, l) table)
   uint32_t n_seqs;
   uint32_t pages_per_split;  // decode
   uint32_t prefill;
@@ -53,6 +60,8 @@ struct AttnArgs {
 };
 
 hipError_t launch_q8_append(const AppendArgs& a, uint32_t items, hipStream_t st);
+// Decode: `units` workgroups; when need_combine, q8_combine_kernel merges the
+// split partials (which must be set) in a second launch.
 hipError_t launch_q8_attention(const AttnArgs& a, uint32_t units, bool need_combine, hipStream_t st);
 
 }  // namespace qm

@@ -24,6 +24,9 @@
 //    softmax statistics never move between lanes except for the 4-way max.
 //    Decode splits the pages of a sequence over workgroups (4 waves each,
 //    combined in LDS); split partials are merged by q8_combine_kernel.
+//  Head dimensions 1..256 run on pages of the next storage width Dp (64,
+//  128 or 256) whose extra dimensions hold zero; queries, gates, outputs and
+//  the appended K/V rows keep the caller's real head dimension.
 #include <float.h>
 #include <stdlib.h>
 
@@ -38,16 +41,17 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Quantises one (token, kv_head) row of K (kind 0) or V (kind 1) with one
 // 64-lane wave and stores it into page `page` slot `slot`.  Matches
 // qwen38_q8_kv_append: s = max(absmax / 127, FLT_MIN), q = round-half-away
-// (clamp(x / s, -127, 127)), IEEE division.
+// (clamp(x / s, -127, 127)), IEEE division.  `src` holds the dr real
+// dimensions; the page row has Dp, and dimensions dr..Dp-1 store zero.
 __device__ __forceinline__ void q8_store_row(const AttnSeq& sq, const float* src, uint32_t kind, int32_t page,
-                                             uint32_t slot, uint32_t kvh, uint32_t kvh_count, uint32_t D,
-                                             int lane) {
+                                             uint32_t slot, uint32_t kvh, uint32_t kvh_count, uint32_t dr,
+                                             uint32_t Dp, int lane) {
   float vals[4];
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t d = lane * 4 + i;
-    vals[i] = d < D ? src[d] : 0.0f;
+    vals[i] = d < dr ? src[d] : 0.0f;
     amax = fmaxf(amax, fabsf(vals[i]));
   }
 #pragma unroll
@@ -57,17 +61,27 @@ __device__ __forceinline__ void q8_store_row(const AttnSeq& sq, const float* src
 #pragma unroll
   for (int i = 0; i < 4; ++i) qv[i] = (int8_t)roundf(fminf(fmaxf(vals[i] / s, -127.0f), 127.0f));
   const size_t pkv = (size_t)page * kvh_count + kvh;
-  if ((uint32_t)lane * 4 < D) {
+  if ((uint32_t)lane * 4 < Dp) {
     if (kind == 0) {
       const uint32_t packed = (uint32_t)(uint8_t)qv[0] | ((uint32_t)(uint8_t)qv[1] << 8) |
                               ((uint32_t)(uint8_t)qv[2] << 16) | ((uint32_t)(uint8_t)qv[3] << 24);
-      *(uint32_t*)(sq.k + (pkv * 16 + slot) * D + lane * 4) = packed;
+      *(uint32_t*)(sq.k + (pkv * 16 + slot) * Dp + lane * 4) = packed;
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sq.v[(pkv * D + lane * 4 + i) * 16 + slot] = qv[i];
+      for (int i = 0; i < 4; ++i) sq.v[(pkv * Dp + lane * 4 + i) * 16 + slot] = qv[i];
     }
   }
   if (lane == 0) (kind == 0 ? sq.ks : sq.vs)[pkv * 16 + slot] = s;
+}
+
+// Eight bf16 of a query/gate row starting at element d0, zero past the real
+// dimension dr; `full` (dr == Dp) takes one 16-byte load.
+__device__ __forceinline__ u32x4 load_bf16x8(const uint16_t* row, uint32_t d0, uint32_t dr, bool full) {
+  if (full) return *(const u32x4*)(row + d0);
+  uint32_t h[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) h[e] = d0 + e < dr ? (uint32_t)row[d0 + e] : 0u;
+  return u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
 }
 
 // Physical page of logical page p: pages materialised by this call are not
@@ -87,7 +101,7 @@ __global__ __launch_bounds__(64) void q8_append_kernel(AppendArgs args) {
   const uint32_t kvh = (blockIdx.x / 2) % kvh_count;
   const uint32_t item = blockIdx.x / (2 * kvh_count);
   const int lane = threadIdx.x;
-  const uint32_t D = args.head_dim;
+  const uint32_t D = args.head_dim, Dp = args.head_dim_pad;
   const AttnSeq& sq = args.seqs[args.decode ? item : 0];
   const uint32_t token = args.decode ? sq.len - 1 : args.start + item;
   // Page-table entries of newly materialised pages (written once per call).
@@ -95,7 +109,7 @@ __global__ __launch_bounds__(64) void q8_append_kernel(AppendArgs args) {
     for (int32_t i = 0; i < sq.new_page_count; ++i) sq.pt[sq.new_page_first + i] = sq.new_page_id + i;
   }
   const float* src = (kind == 0 ? args.k : args.v) + ((size_t)item * kvh_count + kvh) * D;
-  q8_store_row(sq, src, kind, page_id(sq, token / 16), token % 16, kvh, kvh_count, D, lane);
+  q8_store_row(sq, src, kind, page_id(sq, token / 16), token % 16, kvh, kvh_count, D, Dp, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -199,7 +213,8 @@ struct DecodeLds {
   static constexpr int kK = 16 * D, kV = 16 * D, kS = 512;  // K, V, scales (K 256 B + V 256 B)
   static constexpr int kPage = kK + kV + kS;
   static constexpr int kWaveRing = kRing * kPage;
-  static constexpr int kRed = 4 * D * 16 * 4 + (3 * 4 + 2) * 16 * 4;  // O, m, l, weights, max, sums
+  static constexpr int kPad = 17;  // floats per (wave, d) row of the O reduction (16 columns + 1)
+  static constexpr int kRed = 4 * D * kPad * 4 + (3 * 4 + 2) * 16 * 4;  // O, m, l, weights, max, sums
   static constexpr int kBytes = 4 * kWaveRing > kRed ? 4 * kWaveRing : kRed;
 };
 
@@ -234,7 +249,9 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   // Q operand (B of QK^T), filled after the first page DMAs are in flight.
   u32x4 qb[kKS];
   float qcorr = 0.0f;
-  const float sm_scale = kLog2e / sqrtf((float)D);
+  const uint32_t dr = args.head_dim;  // real head dimension; D is the page storage width
+  const bool full_d = dr == (uint32_t)D;
+  const float sm_scale = kLog2e / sqrtf((float)dr);
 
   floatx4 o[kDB];
 #pragma unroll
@@ -262,8 +279,8 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   if (split + 1 == sq.nsplit) {
     const uint32_t token = sq.len - 1;
     if (wave < 2) {
-      const float* src = (wave == 0 ? args.k_new : args.v_new) + ((size_t)b * KVH + kvh) * D;
-      q8_store_row(sq, src, wave, page_id(sq, token / 16), token % 16, kvh, KVH, D, lane);
+      const float* src = (wave == 0 ? args.k_new : args.v_new) + ((size_t)b * KVH + kvh) * dr;
+      q8_store_row(sq, src, wave, page_id(sq, token / 16), token % 16, kvh, KVH, dr, D, lane);
     } else if (wave == 2 && kvh == 0 && lane == 0) {
       for (int32_t i = 0; i < sq.new_page_count; ++i) sq.pt[sq.new_page_first + i] = sq.new_page_id + i;
     }
@@ -401,10 +418,10 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   // does not wait for the pages (vmcnt retires in order).
   u32x4 qraw[kKS];
   {
-    const uint16_t* qp = args.q + ((size_t)b * H + head) * D;
+    const uint16_t* qp = args.q + ((size_t)b * H + head) * dr;
 #pragma unroll
     for (int jj = 0; jj < kKS; ++jj)
-      qraw[jj] = col_ok ? *(const u32x4*)(qp + D / 4 * kq + 8 * jj) : u32x4{0u, 0u, 0u, 0u};
+      qraw[jj] = col_ok ? load_bf16x8(qp, D / 4 * kq + 8 * jj, dr, full_d) : u32x4{0u, 0u, 0u, 0u};
   }
   __builtin_amdgcn_sched_barrier(0);
   const uint32_t pre = min(n_mine, (uint32_t)kRing);
@@ -458,13 +475,14 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   float l_tot = l_lane + __shfl_xor(l_lane, 16);
   l_tot += __shfl_xor(l_tot, 32);
   __syncthreads();  // the rings are reused for the reduction
-  float(*red_o)[D][16] = reinterpret_cast<float(*)[D][16]>(lds);
-  float(*red_m)[16] = reinterpret_cast<float(*)[16]>(lds + 4 * D * 16 * 4);
+  constexpr int kPad = L::kPad;
+  float* red_o = reinterpret_cast<float*>(lds);  // [wave][d][kPad]
+  float(*red_m)[16] = reinterpret_cast<float(*)[16]>(lds + 4 * D * kPad * 4);
   float(*red_l)[16] = red_m + 4;
 #pragma unroll
   for (int db = 0; db < kDB; ++db)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red_o[wave][16 * db + 4 * kq + r][col] = o[db][r];
+    for (int r = 0; r < 4; ++r) red_o[(wave * D + 16 * db + 4 * kq + r) * kPad + col] = o[db][r];
   if (kq == 0) {
     red_m[wave][col] = m_run;
     red_l[wave][col] = l_tot;
@@ -492,26 +510,34 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   }
   __syncthreads();
   const uint32_t nsplit = sq.nsplit;
-  for (uint32_t e = threadIdx.x; e < (uint32_t)D * 16; e += 256) {
-    const uint32_t c = e % 16, d = e / 16;
-    if (c >= gh) continue;
-    const float mx = red_mx[c], Ls = red_L[c];
-    float O = 0.0f;
+  // Split partials: O [split row][H][D], then (m, l) [split row][H][2];
+  // q8_combine_kernel merges them after this launch.
+  const size_t o_rows = (size_t)args.part_rows * H;
+  float* po = args.partials;
+  float* pm = args.partials + o_rows * D;
+  constexpr uint32_t kD4 = D / 4;
+  for (uint32_t e = threadIdx.x; e < gh * kD4; e += 256) {
+    const uint32_t c = e / kD4, d0 = 4 * (e % kD4);
+    floatx4 O = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) O += red_f[w][c] * red_o[w][d][c];
+    for (int w = 0; w < kWaves; ++w)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) O[i] += red_f[w][c] * red_o[(w * D + d0 + i) * kPad + c];
     const uint32_t hh = kvh * gh + c;
     if (nsplit == 1) {
-      float v = O / fmaxf(Ls, FLT_MIN);
-      const size_t oi = ((size_t)b * H + hh) * D + d;
-      if (args.gate) v *= sigmoid_f(bf16_to_f32(args.gate[oi]));
-      args.o[oi] = f32_to_bf16(v);
-    } else {
-      float* part = args.partials + ((size_t)(sq.part_begin + split) * H + hh) * (D + 2);
-      part[d] = O;
-      if (d == 0) {
-        part[D] = mx;
-        part[D + 1] = Ls;
+      const float inv = 1.0f / fmaxf(red_L[c], FLT_MIN);
+      const size_t oi = ((size_t)b * H + hh) * dr + d0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (d0 + i >= dr) break;
+        float v = O[i] * inv;
+        if (args.gate) v *= sigmoid_f(bf16_to_f32(args.gate[oi + i]));
+        args.o[oi + i] = f32_to_bf16(v);
       }
+    } else {
+      const size_t row = (size_t)(sq.part_begin + split) * H + hh;
+      *(floatx4*)(po + row * D + d0) = O;
+      if (d0 == 0) *(float2*)(pm + row * 2) = float2{red_mx[c], red_L[c]};
     }
   }
 }
@@ -530,15 +556,16 @@ __global__ __launch_bounds__(256) void q8_combine_kernel(AttnArgs args) {
   __shared__ float red_m[256];
   __shared__ floatx4 red_o[256];
   __shared__ float red_l[256];
-  const uint32_t H = args.heads;
+  const uint32_t H = args.heads, dr = args.head_dim;
   const uint32_t wq = blockIdx.x % kWgPerHead;
   const uint32_t bh = blockIdx.x / kWgPerHead;
   const uint32_t b = bh / H, hh = bh % H;
   const AttnSeq& sq = args.seqs[b];
   const uint32_t ns = sq.nsplit;
-  if (ns <= 1) return;
-  const size_t stride = (size_t)H * (D + 2);
-  const float* base = args.partials + ((size_t)sq.part_begin * H + hh) * (D + 2);
+  if (ns <= 1 || 32 * wq >= dr) return;
+  const size_t o_rows = (size_t)args.part_rows * H;
+  const float* obase = args.partials + ((size_t)sq.part_begin * H + hh) * D;
+  const float* mbase = args.partials + o_rows * D + ((size_t)sq.part_begin * H + hh) * 2;
   const uint32_t t = threadIdx.x, c = t % 8, g = t / 8;
   const uint32_t d0 = 32 * wq + 4 * c;
 
@@ -547,20 +574,19 @@ __global__ __launch_bounds__(256) void q8_combine_kernel(AttnArgs args) {
   float lacc = 0.0f;
   for (uint32_t s0 = 0; s0 < ns; s0 += kGroups * kMaxPer) {
     floatx4 ov[kMaxPer];
-    float mv[kMaxPer], lv[kMaxPer];
+    float2 ml[kMaxPer];
     // Unconditional loads (index clamped, weight masked) so all of them are
     // in flight together.
 #pragma unroll
     for (int k = 0; k < kMaxPer; ++k) {
       const uint32_t s = s0 + g + k * kGroups;
-      const float* row = base + (s < ns ? s : ns - 1) * stride;
-      ov[k] = *(const floatx4*)(row + d0);
-      mv[k] = row[D];
-      lv[k] = row[D + 1];
+      const size_t row = s < ns ? s : ns - 1;
+      ov[k] = *(const floatx4*)(obase + row * H * D + d0);
+      ml[k] = *(const float2*)(mbase + row * H * 2);
     }
+    float mv[kMaxPer];
 #pragma unroll
-    for (int k = 0; k < kMaxPer; ++k)
-      if (s0 + g + k * kGroups >= ns) mv[k] = -INFINITY;
+    for (int k = 0; k < kMaxPer; ++k) mv[k] = s0 + g + k * kGroups < ns ? ml[k].x : -INFINITY;
     float mnew = mloc;
 #pragma unroll
     for (int k = 0; k < kMaxPer; ++k) mnew = fmaxf(mnew, mv[k]);
@@ -572,7 +598,7 @@ __global__ __launch_bounds__(256) void q8_combine_kernel(AttnArgs args) {
       for (int k = 0; k < kMaxPer; ++k) {
         const float f = mv[k] == -INFINITY ? 0.0f : exp2f(mv[k] - mnew);
         acc += ov[k] * f;
-        lacc += lv[k] * f;
+        lacc += ml[k].y * f;
       }
       mloc = mnew;
     }
@@ -593,9 +619,10 @@ __global__ __launch_bounds__(256) void q8_combine_kernel(AttnArgs args) {
       L += red_l[c + 8 * k];
     }
     const float inv = 1.0f / fmaxf(L, FLT_MIN);
-    const size_t oi = ((size_t)b * H + hh) * D + d0;
+    const size_t oi = ((size_t)b * H + hh) * dr + d0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
+      if (d0 + e >= dr) break;
       float v = o[e] * inv;
       if (args.gate) v *= sigmoid_f(bf16_to_f32(args.gate[oi + e]));
       args.o[oi + e] = f32_to_bf16(v);
@@ -648,15 +675,17 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
   // d4,d6,d5,d7 that the int8 -> fp16 unpack of K produces.  bf16 -> fp16 is
   // exact within fp16's range.  K enters as 1024 + (k + 128): 1152 * sum(q)
   // is subtracted from every score.
+  const uint32_t dr = args.head_dim;  // real head dimension; D is the page storage width
+  const bool full_d = dr == (uint32_t)D;
   u32x4 qb[CB][kKS];
   float qcorr[CB];
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
-    const uint16_t* qp = args.q + ((size_t)qrow[cb] * H + head) * D;
+    const uint16_t* qp = args.q + ((size_t)qrow[cb] * H + head) * dr;
     float qsum = 0.0f;
 #pragma unroll
     for (int jj = 0; jj < kKS; ++jj) {
-      const u32x4 v = col_ok[cb] ? *(const u32x4*)(qp + D / 4 * kq + 8 * jj) : u32x4{0u, 0u, 0u, 0u};
+      const u32x4 v = col_ok[cb] ? load_bf16x8(qp, D / 4 * kq + 8 * jj, dr, full_d) : u32x4{0u, 0u, 0u, 0u};
       float f[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -677,7 +706,7 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
     qsum += __shfl_xor(qsum, 32);
     qcorr[cb] = 1152.0f * qsum;
   }
-  const float sm_scale = kLog2e / sqrtf((float)D);
+  const float sm_scale = kLog2e / sqrtf((float)dr);
 
   floatx4 o[CB][kDB];
   float m_run[CB], l_lane[CB], ps_lane[CB];
@@ -816,12 +845,13 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
     ps_tot += __shfl_xor(ps_tot, 32);
     if (!col_ok[cb]) continue;
     const float inv = 1.0f / fmaxf(l_tot, FLT_MIN);
-    const size_t obase = ((size_t)qrow[cb] * H + head) * D;
+    const size_t obase = ((size_t)qrow[cb] * H + head) * dr;
 #pragma unroll
     for (int db = 0; db < kDB; ++db)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const uint32_t d = 16 * db + 4 * kq + r;
+        if (d >= dr) continue;
         float v = (o[cb][db][r] - 128.0f * ps_tot) * inv;  // V was accumulated as v + 128
         if (args.gate) v *= sigmoid_f(bf16_to_f32(args.gate[obase + d]));
         args.o[obase + d] = f32_to_bf16(v);
@@ -850,6 +880,7 @@ hipError_t launch_attn_d(const AttnArgs& a, uint32_t units, bool need_combine, h
     if (cb >= 2) return launch_prefill<D, 2>(a, st);
     return launch_prefill<D, 1>(a, st);
   }
+  if (need_combine && !a.partials) return hipErrorInvalidValue;
   hipLaunchKernelGGL(q8_decode_kernel<D>, dim3(units), dim3(256), 0, st, a);
   if (need_combine)
     hipLaunchKernelGGL(q8_combine_kernel<D>, dim3(a.n_seqs * a.heads * (D / 32)), dim3(256), 0, st, a);
@@ -864,7 +895,7 @@ hipError_t launch_q8_append(const AppendArgs& a, uint32_t items, hipStream_t st)
 }
 
 hipError_t launch_q8_attention(const AttnArgs& a, uint32_t units, bool need_combine, hipStream_t st) {
-  switch (a.head_dim) {
+  switch (a.head_dim_pad) {
     case 64: return launch_attn_d<64>(a, units, need_combine, st);
     case 128: return launch_attn_d<128>(a, units, need_combine, st);
     case 256: return launch_attn_d<256>(a, units, need_combine, st);
@@ -873,3 +904,4 @@ hipError_t launch_q8_attention(const AttnArgs& a, uint32_t units, bool need_comb
 }
 
 }  // namespace qm
+

@@ -41,8 +41,18 @@ qm::DeviceGuard::~DeviceGuard() {
   if (prev_ != dev_) hipSetDevice(prev_);
 }
 
+// Growing a buffer allocates and synchronises, which a stream under graph
+// capture cannot do: such a call fails instead of corrupting the capture.
+static qm_status capture_guard(qm_runtime* rt, const char* what) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(rt->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+    return qm::fail(QM_ERR_INVALID_ARGUMENT, "%s: workspace must grow while the stream is being captured", what);
+  return QM_OK;
+}
+
 qm_status qm::ensure_scratch(qm_runtime* rt, size_t bytes) {
   if (rt->scratch_bytes >= bytes) return QM_OK;
+  if (qm_status st_cap = capture_guard(rt, "ensure_scratch"); st_cap != QM_OK) return st_cap;
   if (rt->scratch) {
     // Work already enqueued may still use the old buffer.
     hipError_t e = hipStreamSynchronize(rt->stream);
@@ -61,6 +71,7 @@ qm_status qm::ensure_scratch(qm_runtime* rt, size_t bytes) {
 
 qm_status qm::ensure_partials(qm_runtime* rt, size_t bytes) {
   if (rt->partial_bytes >= bytes) return QM_OK;
+  if (qm_status st_cap = capture_guard(rt, "ensure_partials"); st_cap != QM_OK) return st_cap;
   if (rt->partials) {
     hipError_t e = hipStreamSynchronize(rt->stream);
     if (e != hipSuccess) return hip_check(e, "partials resize sync");
@@ -78,6 +89,7 @@ qm_status qm::ensure_partials(qm_runtime* rt, size_t bytes) {
 
 qm_status qm::ensure_xh(qm_runtime* rt, size_t bytes) {
   if (rt->xh_bytes >= bytes) return QM_OK;
+  if (qm_status st_cap = capture_guard(rt, "ensure_xh"); st_cap != QM_OK) return st_cap;
   if (rt->xh) {
     hipError_t e = hipStreamSynchronize(rt->stream);
     if (e != hipSuccess) return hip_check(e, "xh resize sync");
@@ -94,6 +106,7 @@ qm_status qm::ensure_xh(qm_runtime* rt, size_t bytes) {
 
 qm_status qm::ensure_counters(qm_runtime* rt, size_t count) {
   if (rt->counter_count >= count) return QM_OK;
+  if (qm_status st_cap = capture_guard(rt, "ensure_counters"); st_cap != QM_OK) return st_cap;
   if (rt->counters) {
     hipError_t e = hipStreamSynchronize(rt->stream);
     if (e != hipSuccess) return hip_check(e, "counters resize sync");

@@ -239,6 +239,18 @@ qm_status encode_pre(qm_runtime* rt, qm_decode_state* st, const qm_decode_layer&
                          st->q, st->gate, st->k);
 }
 
+// Grows every full-attention layer's cache for this token and sizes the
+// attention workspace; fails before anything is launched.
+qm_status prepare_attention(qm_runtime* rt, const qm_decode_layer* layers, uint32_t n_layers) {
+  for (uint32_t i = 0; i < n_layers; ++i)
+    if (layers[i].full) {
+      qm_kv* kv = layers[i].full->kv;
+      qm_status s = attn_decode_prepare(rt, &kv, 1, layers[i].full->num_heads);
+      if (s != QM_OK) return s;
+    }
+  return QM_OK;
+}
+
 qm_status encode_attention(qm_runtime* rt, qm_decode_state* st, const qm_decode_full_layer& l) {
   qm_kv* kv = l.kv;
   return qm_attn_decode(rt, &kv, 1, st->q, st->gate, st->k, st->f[2], l.num_heads, st->attn);
@@ -401,6 +413,11 @@ qm_status qm_decode_layers(qm_runtime* rt, qm_decode_state* st, const qm_decode_
   if (s != QM_OK) return s;
   if ((s = ensure_arena(st, need)) != QM_OK) return s;
   DeviceGuard g(rt->device);
+  // Everything the attention calls could fail on is settled before the first
+  // launch, so a failed token leaves hidden, the DeltaNet states and the
+  // caches as they were (decode_layers encodes the whole token before it
+  // commits, metal_runtime.rs:2022-2084).
+  if ((s = prepare_attention(rt, layers, n_layers)) != QM_OK) return s;
   if ((s = hip_check(launch_set_u32x3(st->pos, position[0], position[1], position[2], rt->stream),
                      "position launch")) != QM_OK)
     return s;
@@ -498,7 +515,9 @@ qm_status qm_decode_graph_run(qm_decode_graph* g, const uint32_t position[3]) {
   qm_decode_graph::Variant& v = g->var[pick];
   qm_runtime* rt = g->rt;
   DeviceGuard dg(rt->device);
-  qm_status s = hip_check(launch_set_u32x3(g->st->pos, position[0], position[1], position[2], rt->stream),
+  qm_status s = prepare_attention(rt, g->layers.data(), (uint32_t)g->layers.size());
+  if (s != QM_OK) return s;
+  s = hip_check(launch_set_u32x3(g->st->pos, position[0], position[1], position[2], rt->stream),
                           "position launch");
   for (size_t i = 0; i < v.segs.size() && s == QM_OK; ++i) {
     s = hip_check(hipGraphLaunch(v.segs[i], rt->stream), "decode graph launch");

@@ -62,6 +62,9 @@ struct DnStateView {
 };
 DnStateView dn_state_view(const qm_dn_state* s);
 void dn_state_set_cur(qm_dn_state* s, int cur);
+// Validates a decode step of one more token for these caches, grows their
+// capacity and sizes the runtime's attention workspace (may allocate).
+qm_status attn_decode_prepare(qm_runtime* rt, qm_kv* const* seqs, uint32_t B, uint32_t H);
 uint32_t kv_heads_of(const qm_kv* kv);
 uint32_t kv_head_dim_of(const qm_kv* kv);
 const qm_runtime* kv_runtime_of(const qm_kv* kv);

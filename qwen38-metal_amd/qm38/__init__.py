@@ -37,7 +37,7 @@ EXPORTS = [
     "qm_runtime_create", "qm_runtime_destroy", "qm_runtime_set_stream", "qm_runtime_synchronize",
     "qm_device_alloc", "qm_device_free", "qm_upload", "qm_copy_to_device", "qm_copy_to_host",
     "qm_q4_project", "qm_q4_swiglu", "qm_q4_mlp",
-    "qm_kv_create", "qm_kv_destroy", "qm_kv_length", "qm_kv_allocated_pages", "qm_kv_page_for_token",
+    "qm_kv_create", "qm_kv_destroy", "qm_kv_length", "qm_kv_capacity", "qm_kv_allocated_pages", "qm_kv_page_for_token",
     "qm_kv_reserve", "qm_kv_truncate", "qm_kv_clone", "qm_kv_read",
     "qm_attn_decode", "qm_attn_prefill", "qm_attn_prepare",
     "qm_dn_weights_create", "qm_dn_weights_destroy", "qm_dn_state_create", "qm_dn_state_destroy",
@@ -140,6 +140,7 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "qm_kv_create": ([vp, u32, u32, u32, u32, C.POINTER(vp)], i32),
         "qm_kv_destroy": ([vp], None),
         "qm_kv_length": ([vp], u32),
+        "qm_kv_capacity": ([vp], u32),
         "qm_kv_allocated_pages": ([vp], u32),
         "qm_kv_page_for_token": ([vp, u32], C.c_int64),
         "qm_kv_reserve": ([vp, u32], i32),
@@ -257,8 +258,9 @@ class Runtime:
                                   in_elems, M, _ptr(y)))
 
     # ---- Q8 KV + attention -------------------------------------------------
-    def create_q8_kv_state(self, kv_heads: int, head_dim: int, max_tokens: int,
+    def create_q8_kv_state(self, kv_heads: int, head_dim: int, max_tokens: int = 0,
                            page_tokens: int = 16) -> "KvCache":
+        """create_q8_kv_state; max_tokens = 0 grows without limit (the reference's policy)."""
         return KvCache(self, kv_heads, head_dim, page_tokens, max_tokens)
 
     def gqa_attention_q8(self, seqs, q, gate, k, v, num_heads: int, o) -> None:
@@ -427,6 +429,10 @@ class KvCache:
     @property
     def sequence_length(self) -> int:
         return self.rt.lib.qm_kv_length(self.handle)
+
+    @property
+    def capacity_tokens(self) -> int:
+        return self.rt.lib.qm_kv_capacity(self.handle)
 
     @property
     def allocated_pages(self) -> int:

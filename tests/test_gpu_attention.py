@@ -2,15 +2,12 @@
 
 Ports metal_runtime.rs tests q8_gqa_attention_keeps_kv_on_the_gpu (:11587),
 q8_gqa_prefill_matches_steps_and_keeps_kv_state (:11608) and
-q8_gqa_prefill_matches_steps_when_kv_capacity_grows (:11683), plus seeded
-cases at the model's shapes (head_dim 256, GQA groups up to 16, ragged
-batches, split-K decode up to 32K tokens).
-
-The reference tests use head_dim 2; this build's kernels take head_dim 64,
-128 or 256.  The reference vectors are embedded by zero-padding q, k and v
-to 64 and scaling q by sqrt(64/2): zero lanes change neither the absmax of
-a row (so the int8 bytes and scales are the reference's) nor any dot
-product, and the scaling keeps q.k/sqrt(d) identical.
+q8_gqa_prefill_matches_steps_when_kv_capacity_grows (:11683) at their own
+head_dim 2 and with the reference's capacity growth, plus seeded cases at
+the model's shapes (head_dim 256, GQA groups up to 16, ragged batches,
+split-K decode), odd head dimensions, and BASELINE config 4 at 64 query /
+8 KV heads, d = 128: decode at 128K, a ragged batch of 8 over
+{4K, 32K, 128K} and a 2048-row causal prefill onto a 4096-token cache.
 
 Bars: quantised cache bytes and scales bit-exact against the oracle's
 quantiser; page tables identical to LogicalPageTable; outputs (bf16) within
@@ -26,6 +23,7 @@ import numpy as np
 import pytest
 
 import oracle
+import torch
 from gpu_util import assert_bf16_close, bf16_dev_to_f32, empty_bf16, to_dev
 from qm38 import QmError, synth
 
@@ -36,15 +34,27 @@ class Mirror:
     """Host copy of one sequence's appended fp32 K/V rows."""
 
     def __init__(self, kvh, d):
-        self.k = np.zeros((0, kvh, d), np.float32)
-        self.v = np.zeros((0, kvh, d), np.float32)
+        self.kvh, self.d = kvh, d
+        self._k, self._v = [np.zeros((0, kvh, d), np.float32)], [np.zeros((0, kvh, d), np.float32)]
 
     def append(self, k, v):
-        self.k = np.concatenate([self.k, k.reshape(-1, *self.k.shape[1:])])
-        self.v = np.concatenate([self.v, v.reshape(-1, *self.v.shape[1:])])
+        self._k.append(np.asarray(k, np.float32).reshape(-1, self.kvh, self.d))
+        self._v.append(np.asarray(v, np.float32).reshape(-1, self.kvh, self.d))
+
+    @property
+    def k(self):
+        if len(self._k) > 1:
+            self._k = [np.concatenate(self._k)]
+        return self._k[0]
+
+    @property
+    def v(self):
+        if len(self._v) > 1:
+            self._v = [np.concatenate(self._v)]
+        return self._v[0]
 
     def truncate(self, n):
-        self.k, self.v = self.k[:n], self.v[:n]
+        self._k, self._v = [self.k[:n]], [self.v[:n]]
 
     def quantised(self):
         kq, ks = oracle.q8_quantize_rows(self.k)
@@ -87,30 +97,24 @@ def _check_cache(cache, mirror):
 
 
 # ---------------------------------------------------------------------------
-# Reference known-answer tests (head_dim 2 embedded in 64)
+# Reference known-answer tests (head_dim 2, as the reference runs them)
 # ---------------------------------------------------------------------------
-PAD_D = 64
-QSCALE = math.sqrt(PAD_D / 2)
+KAT_D = 2
 
 
 def _pad(a, heads):
-    a = np.asarray(a, np.float32).reshape(-1, heads, 2)
-    out = np.zeros((a.shape[0], heads, PAD_D), np.float32)
-    out[..., :2] = a
-    return out
+    return np.asarray(a, np.float32).reshape(-1, heads, KAT_D)
 
 
 def test_reference_kat_single_token(rt, torch_dev):
     # metal_runtime.rs:11587-11605
-    cache = rt.create_q8_kv_state(1, PAD_D, 64)
-    q_bits, _ = _bf16(_pad([1.0, 0.0], 1) * QSCALE)
+    cache = rt.create_q8_kv_state(1, KAT_D, 64)
+    q_bits, _ = _bf16(_pad([1.0, 0.0], 1))
     g_bits, _ = _bf16(_pad([0.0, 0.0], 1))
     out = _decode(rt, torch_dev, [cache], q_bits, g_bits, _pad([1.0, 0.0], 1), _pad([2.0, -1.0], 1), 1)
     assert cache.sequence_length == 1
     assert abs(out[0, 0, 0] - 1.0) < 0.001, out[0, 0, :2]
     assert abs(out[0, 0, 1] + 0.5) < 0.005, out[0, 0, :2]
-    # zero-padded dimensions: only the rounding residual of the fp16 hi+lo P'V split remains
-    assert np.max(np.abs(out[0, 0, 2:])) < 1e-3
     keys, values, ks, vs = cache.read()
     assert list(values[0, 0, :2]) == [127, -64] and ks[0, 0] == np.float32(1.0) / np.float32(127.0)
     assert vs[0, 0] == np.float32(2.0) / np.float32(127.0)
@@ -122,23 +126,23 @@ def test_reference_kat_prefill_matches_steps(rt, torch_dev):
     gates = [0.0, 0.0, 0.1, -0.1, -0.2, 0.2, 0.0, 0.0, 0.3, -0.3, 0.15, 0.05]
     keys = [1.0, 0.0, 0.4, 0.9, -0.7, 0.2]
     values = [2.0, -1.0, 0.75, 1.25, -0.5, 0.4]
-    q_bits, q_f = _bf16(_pad(queries, 2) * QSCALE)
+    q_bits, q_f = _bf16(_pad(queries, 2))
     g_bits, g_f = _bf16(_pad(gates, 2))
     k, v = _pad(keys, 1), _pad(values, 1)
-    step = rt.create_q8_kv_state(1, PAD_D, 64)
-    pre = rt.create_q8_kv_state(1, PAD_D, 64)
+    step = rt.create_q8_kv_state(1, KAT_D, 64)
+    pre = rt.create_q8_kv_state(1, KAT_D, 64)
     expected = np.concatenate([_decode(rt, torch_dev, [step], q_bits[t:t + 1], g_bits[t:t + 1], k[t], v[t], 2)
                                for t in range(3)])
     actual = _prefill(rt, torch_dev, pre, q_bits, g_bits, k, v, 2)
     assert pre.sequence_length == 3
     assert np.max(np.abs(actual - expected)) < 0.005
-    mirror = Mirror(1, PAD_D)
+    mirror = Mirror(1, KAT_D)
     mirror.append(k, v)
     assert_bf16_close(actual, mirror.reference(q_f, g_f, 0), what="kat prefill")
     _check_cache(pre, mirror)
     _check_cache(step, mirror)
 
-    nq_bits, nq_f = _bf16(_pad([0.9, -0.1, -0.3, 0.7], 2) * QSCALE)
+    nq_bits, nq_f = _bf16(_pad([0.9, -0.1, -0.3, 0.7], 2))
     ng_bits, ng_f = _bf16(_pad([0.05, -0.05, 0.2, -0.2], 2))
     nk, nv = _pad([0.2, -0.6], 1), _pad([1.1, -0.8], 1)
     e_next = _decode(rt, torch_dev, [step], nq_bits, ng_bits, nk, nv, 2)
@@ -157,21 +161,25 @@ def test_reference_kat_capacity_grows(rt, torch_dev):
                 [0.5 + t * 0.01, -0.7 + t * 0.005], [0.8 - t * 0.02, -0.2 + t * 0.01])
 
     rows = [row(t) for t in range(19)]
-    q_bits, q_f = _bf16(_pad([x for r in rows for x in r[0]], 2) * QSCALE)
+    q_bits, q_f = _bf16(_pad([x for r in rows for x in r[0]], 2))
     g_bits, g_f = _bf16(_pad([x for r in rows for x in r[1]], 2))
     k = _pad([x for r in rows for x in r[2]], 1)
     v = _pad([x for r in rows for x in r[3]], 1)
-    step = rt.create_q8_kv_state(1, PAD_D, 19)
-    pre = rt.create_q8_kv_state(1, PAD_D, 19)
+    step = rt.create_q8_kv_state(1, KAT_D)
+    pre = rt.create_q8_kv_state(1, KAT_D)
+    assert step.capacity_tokens == pre.capacity_tokens == 16
     for t in range(16):
         _decode(rt, torch_dev, [step], q_bits[t:t + 1], g_bits[t:t + 1], k[t], v[t], 2)
     _prefill(rt, torch_dev, pre, q_bits[:16], g_bits[:16], k[:16], v[:16], 2)
-    mirror = Mirror(1, PAD_D)
+    mirror = Mirror(1, KAT_D)
     mirror.append(k[:16], v[:16])
     _check_cache(step, mirror)
     _check_cache(pre, mirror)
+    assert step.capacity_tokens == pre.capacity_tokens == 16
     step.reserve(3)
     pre.reserve(3)
+    # ensure_q8_kv_capacity: next power of two of 19 tokens, pages copied
+    assert step.capacity_tokens == pre.capacity_tokens == 32
     assert step.allocated_pages == pre.allocated_pages == 2
     _check_cache(pre, mirror)
     expected = np.concatenate([_decode(rt, torch_dev, [step], q_bits[t:t + 1], g_bits[t:t + 1], k[t], v[t], 2)
@@ -183,9 +191,37 @@ def test_reference_kat_capacity_grows(rt, torch_dev):
     _check_cache(pre, mirror)
     assert np.max(np.abs(actual - expected)) < 0.005
     assert_bf16_close(actual, mirror.reference(q_f[16:], g_f[16:], 16), what="grown prefill")
+
+
+def test_capacity_grows_on_append_and_respects_hard_limit(rt, torch_dev):
+    """Appends past the capacity grow the cache without a reserve (decode and
+    prefill); a cache created with a hard token limit (LogicalPageTable's
+    capacity) refuses to pass it and leaves its state unchanged."""
+    D, H, KVH = 128, 8, 2
+    rng = np.random.default_rng(21)
+    cache = rt.create_q8_kv_state(KVH, D)
+    mirror = Mirror(KVH, D)
+    for n in (15, 1, 1, 40):  # 16 -> 32 (decode) -> 64 (prefill of 40)
+        if n == 1:
+            q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, 1, H, KVH, D)
+            got = _decode(rt, torch_dev, [cache], q_bits, g_bits, k, v, H)
+        else:
+            q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, n, H, KVH, D)
+            got = _prefill(rt, torch_dev, cache, q_bits, g_bits, k, v, H)
+        start = mirror.k.shape[0]
+        mirror.append(k, v)
+        assert_bf16_close(got, mirror.reference(q_f, g_f, start), what=f"after growth to {cache.capacity_tokens}")
+    assert cache.capacity_tokens == 64 and cache.sequence_length == 57
+    _check_cache(cache, mirror)
+    lim = rt.create_q8_kv_state(KVH, D, 20)
+    q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, 20, H, KVH, D)
+    _prefill(rt, torch_dev, lim, q_bits, g_bits, k, v, H)
+    assert lim.capacity_tokens == 20
     with pytest.raises(QmError, match="CAPACITY_EXCEEDED"):
-        _decode(rt, torch_dev, [step], q_bits[:1], g_bits[:1], k[0], v[0], 2)
-    assert step.sequence_length == 19
+        _decode(rt, torch_dev, [lim], q_bits[:1], g_bits[:1], k[0], v[0], H)
+    with pytest.raises(QmError, match="CAPACITY_EXCEEDED"):
+        lim.reserve(1)
+    assert lim.sequence_length == 20 and lim.allocated_pages == 2
 
 
 # ---------------------------------------------------------------------------
@@ -362,14 +398,128 @@ def test_long_context_decode(rt, torch_dev, T):
 
 
 def test_rejects_bad_shapes(rt, torch_dev):
+    # validate_attention_shape (metal_runtime.rs:9186-9193): 1 <= head_dim <= 256, kv_heads > 0
     with pytest.raises(QmError, match="INVALID_ATTENTION_SHAPE"):
-        rt.create_q8_kv_state(2, 96, 16)
+        rt.create_q8_kv_state(2, 257)
+    with pytest.raises(QmError, match="INVALID_ATTENTION_SHAPE"):
+        rt.create_q8_kv_state(2, 0)
     with pytest.raises(QmError, match="INVALID_ATTENTION_SHAPE"):
         rt.create_q8_kv_state(0, 128, 16)
-    with pytest.raises(QmError, match="ZERO_CAPACITY"):
-        rt.create_q8_kv_state(2, 128, 0)
     cache = rt.create_q8_kv_state(4, 64, 16)
     q_bits, _, _, _, k, v = _rand_qkv(np.random.default_rng(1), 1, 6, 4, 64, gate=False)
     with pytest.raises(QmError, match="INVALID_ATTENTION_SHAPE"):
         _decode(rt, torch_dev, [cache], q_bits, None, k, v, 6)
     assert cache.sequence_length == 0
+
+
+# ---------------------------------------------------------------------------
+# Head dimensions other than the kernel widths (pages padded with zeros)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("D,H,KVH", [(1, 2, 1), (2, 4, 2), (33, 6, 3), (80, 16, 2), (96, 8, 4), (200, 8, 1),
+                                      (255, 4, 4)])
+def test_odd_head_dims(rt, torch_dev, D, H, KVH):
+    rng = np.random.default_rng(D * 31 + H)
+    lens = [0, 17, 300]
+    caches = [rt.create_q8_kv_state(KVH, D) for _ in lens]
+    mirrors = [Mirror(KVH, D) for _ in lens]
+    for c, m, n in zip(caches, mirrors, lens):
+        if n:
+            q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, n, H, KVH, D)
+            got = _prefill(rt, torch_dev, c, q_bits, g_bits, k, v, H)
+            m.append(k, v)
+            assert_bf16_close(got, m.reference(q_f, g_f, 0), what=f"prefill d={D} n={n}")
+    os.environ["QM38_ATTN_PPS"] = "4"  # split the 300-token cache: the merge runs
+    try:
+        q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, len(lens), H, KVH, D)
+        got = _decode(rt, torch_dev, caches, q_bits, g_bits, k, v, H)
+    finally:
+        os.environ.pop("QM38_ATTN_PPS", None)
+    for b, (c, m) in enumerate(zip(caches, mirrors)):
+        m.append(k[b], v[b])
+        ref = m.reference(q_f[b:b + 1], g_f[b:b + 1], m.k.shape[0] - 1)
+        assert_bf16_close(got[b:b + 1], ref, what=f"decode d={D} seq {b}")
+        _check_cache(c, m)
+
+
+# ---------------------------------------------------------------------------
+# 64 query heads, 8 KV heads, head_dim 128
+# ---------------------------------------------------------------------------
+C4_H, C4_KVH, C4_D = 64, 8, 128
+
+
+def _fill_device(rt, dev, cache, mirror, gen, n, KVH, D, chunk=8192):
+    """Appends n N(0,1) K/V rows drawn on the GPU (prefill with one query head
+    per KV head, outputs unused), mirrored on the host."""
+    done = 0
+    while done < n:
+        m = min(chunk, n - done)
+        k = torch.randn((m, KVH, D), generator=gen, device=dev, dtype=torch.float32)
+        v = torch.randn((m, KVH, D), generator=gen, device=dev, dtype=torch.float32)
+        q = torch.zeros((m, KVH, D), dtype=torch.int16, device=dev)
+        o = torch.empty((m, KVH, D), dtype=torch.int16, device=dev)
+        rt.gqa_attention_q8_prefill(cache, q, None, k, v, KVH, m, o)
+        mirror.append(k.cpu().numpy(), v.cpu().numpy())
+        done += m
+
+
+def test_config4_decode_128k(rt, torch_dev):
+    gen = torch.Generator(device=torch_dev)
+    gen.manual_seed(4128)
+    rng = np.random.default_rng(4128)
+    T = 131072
+    cache = rt.create_q8_kv_state(C4_KVH, C4_D)
+    mirror = Mirror(C4_KVH, C4_D)
+    _fill_device(rt, torch_dev, cache, mirror, gen, T - 1, C4_KVH, C4_D)
+    for it in range(2):
+        q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, 1, C4_H, C4_KVH, C4_D)
+        got = _decode(rt, torch_dev, [cache], q_bits, g_bits, k, v, C4_H)
+        mirror.append(k, v)
+        assert_bf16_close(got, mirror.reference(q_f, g_f, mirror.k.shape[0] - 1), what=f"128K decode it {it}")
+    assert cache.sequence_length == T + 1
+
+
+def test_config4_ragged_batch(rt, torch_dev):
+    """B = 8 sequences whose lengths are drawn (seeded) from {4K, 32K, 128K}."""
+    gen = torch.Generator(device=torch_dev)
+    gen.manual_seed(48)
+    rng = np.random.default_rng(48)
+    lens = [int(x) for x in rng.choice([4096, 32768, 131072], size=8)]
+    lens[0], lens[1], lens[2] = 4096, 32768, 131072  # every length present
+    caches = [rt.create_q8_kv_state(C4_KVH, C4_D) for _ in lens]
+    mirrors = [Mirror(C4_KVH, C4_D) for _ in lens]
+    for c, m, n in zip(caches, mirrors, lens):
+        _fill_device(rt, torch_dev, c, m, gen, n - 1, C4_KVH, C4_D)
+    q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, len(lens), C4_H, C4_KVH, C4_D)
+    got = _decode(rt, torch_dev, caches, q_bits, g_bits, k, v, C4_H)
+    for b, (c, m) in enumerate(zip(caches, mirrors)):
+        m.append(k[b], v[b])
+        assert c.sequence_length == lens[b]
+        ref = m.reference(q_f[b:b + 1], g_f[b:b + 1], lens[b] - 1)
+        assert_bf16_close(got[b:b + 1], ref, what=f"ragged seq {b} len {lens[b]}")
+        keys, values, ks, vs = c.read()
+        kq, kss, vq, vss = m.quantised()
+        assert np.array_equal(keys[-1], kq[-1]) and np.array_equal(values[-1], vq[-1])
+        assert np.array_equal(ks[-1], kss[-1]) and np.array_equal(vs[-1], vss[-1])
+        mirrors[b] = None  # free host memory early
+
+
+def test_config4_prefill_2048_on_4k(rt, torch_dev):
+    """2048 new rows appended to a 4096-token cache; every cache byte checked,
+    outputs of 40 rows (the first, last and a seeded sample) against the oracle."""
+    gen = torch.Generator(device=torch_dev)
+    gen.manual_seed(2048)
+    rng = np.random.default_rng(2048)
+    cache = rt.create_q8_kv_state(C4_KVH, C4_D)
+    mirror = Mirror(C4_KVH, C4_D)
+    _fill_device(rt, torch_dev, cache, mirror, gen, 4096, C4_KVH, C4_D)
+    M = 2048
+    q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, M, C4_H, C4_KVH, C4_D)
+    got = _prefill(rt, torch_dev, cache, q_bits, g_bits, k, v, C4_H)
+    mirror.append(k, v)
+    assert cache.sequence_length == 4096 + M
+    _check_cache(cache, mirror)
+    kq, ks, vq, vs = mirror.quantised()
+    rows = sorted(set([0, 1, 15, 16, M - 1] + [int(r) for r in rng.choice(M, size=35, replace=False)]))
+    for r in rows:
+        ref = oracle.attention(q_f[r:r + 1], g_f[r:r + 1], kq, ks, vq, vs, 4096 + r)
+        assert_bf16_close(got[r:r + 1], ref, what=f"prefill row {r}")

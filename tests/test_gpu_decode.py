@@ -372,20 +372,41 @@ def test_decode_layers_reject_bad_layers(rt, torch_dev):
 
 
 def test_graph_and_eager_report_kv_capacity(rt, torch_dev):
-    # A full-attention layer whose cache holds two tokens: the third token's
-    # attention call fails with CAPACITY_EXCEEDED (reserve_q8_kv_tokens's
-    # check), eagerly and from a graph replay, without launching past it.
-    model = Model(rt, torch_dev, seed=16, kinds=("full",))
-    _, caches, descs = model.new_request(max_tokens=2)
+    # A (linear, full) model whose cache has a hard limit of two tokens: the
+    # third token fails with CAPACITY_EXCEEDED, eagerly and from a graph
+    # replay, before anything is launched, so the residual row, the DeltaNet
+    # state (history, recurrence and history parity) and the cache are as
+    # they were (decode_layers commits nothing on an encode error,
+    # metal_runtime.rs:2022-2084).
+    model = Model(rt, torch_dev, seed=16, kinds=("linear", "full"))
+    states, caches, descs = model.new_request(max_tokens=2)
     st = _state_with(rt, torch_dev, _hidden0(6))
     rt.decode_layers(st, descs, _positions(0), EPS)
     g = DecodeGraph(rt, st, descs, EPS)
     g.run(_positions(1))
-    assert caches[0].sequence_length == 2
+    rt.synchronize()
+    assert caches[1].sequence_length == 2
+
+    def snapshot():
+        rt.synchronize()
+        hist, rec = states[0].read()
+        return _hidden(rt, st), hist.copy(), rec.copy(), caches[1].read()
+
+    before = snapshot()
     with pytest.raises(QmError, match="CAPACITY|capacity"):
         g.run(_positions(2))
     with pytest.raises(QmError, match="CAPACITY|capacity"):
         rt.decode_layers(st, descs, _positions(2), EPS)
+    after = snapshot()
+    for x, y in zip(before[:3], after[:3]):
+        np.testing.assert_array_equal(x, y)
+    for x, y in zip(before[3], after[3]):
+        np.testing.assert_array_equal(x, y)
+    assert caches[1].sequence_length == 2
+    # The history parity did not move: the graph's variant for it still runs
+    # once the cache may grow again (a truncation makes room).
+    caches[1].truncate(1)
+    g.run(_positions(2))
     rt.synchronize()
-    assert caches[0].sequence_length == 2
+    assert caches[1].sequence_length == 2
     g.close()
