@@ -210,6 +210,21 @@ qm_status qm_attn_decode(qm_runtime* rt, qm_kv* const* seqs, uint32_t B,
                          const float* k, const float* v, uint32_t H,
                          uint16_t* o);
 
+/* qm_attn_decode that allocates nothing: no counterpart in the reference.
+ * For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The split
+ * partials live in a fixed 16 MiB device array of the library, one per GPU,
+ * held until the process ends.  The caches are not grown: every sequence
+ * must have room for its token (qm_kv_reserve beforehand), else
+ * QM_ERR_CAPACITY_EXCEEDED; a split plan needing more than 16 MiB of
+ * partials (H * (head_dim_pad + 2) * 4 bytes per split) fails with
+ * QM_ERR_CAPACITY_EXCEEDED as well.  All calls on one GPU share the array:
+ * calls that overlap on that GPU (other streams or threads) race. */
+qm_status qm_attn_decode_noalloc(qm_runtime* rt, qm_kv* const* seqs, uint32_t B,
+                                 const uint16_t* q, const uint16_t* gate,
+                                 const float* k, const float* v, uint32_t H,
+                                 uint16_t* o);
+
 /* Rotary configuration of the full-attention layers (RopeParameters,
  * native.rs:119-197; MetalGqaDecodeConfig, metal_runtime.rs).
  * rotary_dim = round(head_dim * partial_rotary_factor), even, <= head_dim.

@@ -59,6 +59,15 @@ struct AttnArgs {
   AttnSeq seqs[kMaxAttnSeqs];
 };
 
+// Split partials of qm_attn_decode_noalloc: a file-scope device array of the
+// attention source (one copy per GPU, held until the process ends) whose
+// address is looked up once per device with that device current.
+struct AttnScratch {
+  float* partials;
+  size_t partial_bytes;
+};
+hipError_t attn_noalloc_scratch(int device, AttnScratch* out);
+
 hipError_t launch_q8_append(const AppendArgs& a, uint32_t items, hipStream_t st);
 // Decode: `units` workgroups; when need_combine, q8_combine_kernel merges the
 // split partials (which must be set) in a second launch.

@@ -30,6 +30,8 @@
 #include <float.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "attention.h"
 #include "common.h"
 
@@ -905,3 +907,38 @@ hipError_t launch_q8_attention(const AttnArgs& a, uint32_t units, bool need_comb
 
 }  // namespace qm
 
+// ---------------------------------------------------------------------------
+// No-allocation workspace (qm_attn_decode_noalloc)
+// ---------------------------------------------------------------------------
+namespace qm {
+namespace {
+
+// Split partials (O, then (m, l)) of one decode call.  Every slot is written
+// before it is read, so nothing needs clearing.
+constexpr size_t kScratchPartialBytes = 16u << 20;
+// One copy per GPU, held until the process ends.  In host code this name is
+// not a device address: kernels get the address hipGetSymbolAddress returns.
+static __device__ __align__(256) uint8_t scratch[kScratchPartialBytes];
+
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+std::once_flag g_scratch_once[kMaxDevices];
+
+}  // namespace
+
+hipError_t attn_noalloc_scratch(int device, AttnScratch* out) {
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  // Once per device, with that device current (the caller holds a DeviceGuard).
+  std::call_once(g_scratch_once[device], [device] {
+    void* ptr = nullptr;
+    g_scratch_err[device] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    g_scratch_ptr[device] = ptr;
+  });
+  if (g_scratch_err[device] != hipSuccess) return g_scratch_err[device];
+  out->partials = (float*)g_scratch_ptr[device];
+  out->partial_bytes = kScratchPartialBytes;
+  return hipSuccess;
+}
+
+}  // namespace qm

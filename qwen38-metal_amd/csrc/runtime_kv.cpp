@@ -546,6 +546,28 @@ qm_status qm_attn_decode(qm_runtime* rt, qm_kv* const* seqs, uint32_t B, const u
   return launch_decode(rt, seqs, B, q, gate, k, v, H, o, chunks, (float*)rt->partials, rt->partial_bytes);
 }
 
+qm_status qm_attn_decode_noalloc(qm_runtime* rt, qm_kv* const* seqs, uint32_t B, const uint16_t* q,
+                                 const uint16_t* gate, const float* k, const float* v, uint32_t H, uint16_t* o) {
+  qm_status st = check_decode_args(rt, seqs, B, q, gate, k, v, H, o);
+  if (st != QM_OK) return st;
+  for (uint32_t b = 0; b < B; ++b) {
+    const qm_kv* kv = seqs[b];
+    if ((uint64_t)kv->length + 1 > qm_kv_capacity(kv))
+      return fail(QM_ERR_CAPACITY_EXCEEDED,
+                  "sequence %u: no room for another token without allocating (reserve capacity first)", b);
+  }
+  DeviceGuard g(rt->device);
+  AttnScratch ws{};
+  if ((st = hip_check(attn_noalloc_scratch(rt->device, &ws), "attention scratch")) != QM_OK) return st;
+  std::vector<DecodeChunk> chunks;
+  size_t pb = 0;
+  if ((st = plan_decode(rt, seqs, B, H, &chunks, &pb)) != QM_OK) return st;
+  if (pb > ws.partial_bytes)
+    return fail(QM_ERR_CAPACITY_EXCEEDED, "split partials of %zu bytes exceed the %zu-byte no-allocation scratch", pb,
+                ws.partial_bytes);
+  return launch_decode(rt, seqs, B, q, gate, k, v, H, o, chunks, ws.partials, ws.partial_bytes);
+}
+
 qm_status qm_attn_prefill(qm_runtime* rt, qm_kv* seq, const uint16_t* q, const uint16_t* gate, const float* k,
                           const float* v, uint32_t H, uint32_t M, uint16_t* o) {
   if (!rt || !seq || !q || !k || !v || !o) return fail(QM_ERR_NULL_POINTER, "NULL argument");

@@ -39,7 +39,7 @@ EXPORTS = [
     "qm_q4_project", "qm_q4_swiglu", "qm_q4_mlp",
     "qm_kv_create", "qm_kv_destroy", "qm_kv_length", "qm_kv_capacity", "qm_kv_allocated_pages", "qm_kv_page_for_token",
     "qm_kv_reserve", "qm_kv_truncate", "qm_kv_clone", "qm_kv_read",
-    "qm_attn_decode", "qm_attn_prefill", "qm_attn_prepare",
+    "qm_attn_decode", "qm_attn_decode_noalloc", "qm_attn_prefill", "qm_attn_prepare",
     "qm_dn_weights_create", "qm_dn_weights_destroy", "qm_dn_state_create", "qm_dn_state_destroy",
     "qm_dn_state_clone", "qm_dn_state_read", "qm_dn_state_write", "qm_dn_step", "qm_dn_prefill",
     "qm_dn_snapshots_create", "qm_dn_snapshots_destroy", "qm_dn_prefill_snapshots", "qm_dn_snapshot_restore",
@@ -148,6 +148,7 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "qm_kv_clone": ([vp, C.POINTER(vp)], i32),
         "qm_kv_read": ([vp, vp, vp, vp, vp], i32),
         "qm_attn_decode": ([vp, C.POINTER(vp), u32, vp, vp, vp, vp, u32, vp], i32),
+        "qm_attn_decode_noalloc": ([vp, C.POINTER(vp), u32, vp, vp, vp, vp, u32, vp], i32),
         "qm_attn_prefill": ([vp, vp, vp, vp, vp, vp, u32, u32, vp], i32),
         "qm_attn_prepare": ([vp, C.POINTER(RopeConfig), u32, u32, u32, vp, vp, vp, vp, C.c_float, vp, u32, vp, vp,
                              vp], i32),
@@ -267,6 +268,12 @@ class Runtime:
         arr = (C.c_void_p * len(seqs))(*[s.handle for s in seqs])
         _check(self.lib.qm_attn_decode(self.handle, arr, len(seqs), _ptr(q), _ptr(gate), _ptr(k), _ptr(v),
                                        num_heads, _ptr(o)))
+
+    def gqa_attention_q8_noalloc(self, seqs, q, gate, k, v, num_heads: int, o) -> None:
+        """qm_attn_decode_noalloc: no device allocation (caches must have room)."""
+        arr = (C.c_void_p * len(seqs))(*[s.handle for s in seqs])
+        _check(self.lib.qm_attn_decode_noalloc(self.handle, arr, len(seqs), _ptr(q), _ptr(gate), _ptr(k), _ptr(v),
+                                               num_heads, _ptr(o)))
 
     def gqa_attention_q8_prefill(self, seq, q, gate, k, v, num_heads: int, rows: int, o) -> None:
         _check(self.lib.qm_attn_prefill(self.handle, seq.handle, _ptr(q), _ptr(gate), _ptr(k), _ptr(v),
