@@ -95,4 +95,14 @@ __device__ __forceinline__ float wave_allsum(float v) {
   return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
+// Workgroup barrier that orders LDS only: waits for the wave's own LDS
+// operations (lgkmcnt) but leaves its global loads and stores in flight,
+// unlike __syncthreads(), whose workgroup fence also drains vmcnt.  Use it
+// where only LDS data passes between the waves.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 }  // namespace qm

@@ -27,6 +27,7 @@ struct DnArgs {
   float* s_out;          // may equal s_in
   // workspace / output
   float* conv_out;  // [M][channels]: q^, k^, v after conv + prepare
+  float* chunk_ws;  // chunked prefill: per (chunk, value head) dn_chunk_floats() floats
   float* out;       // [M][VH][dv]
   uint16_t* out_bf16;  // single-token step only: the output rounded to bf16 as well (or NULL)
   // optional state images after tokens 0 .. snap_rows - 1 (speculative
@@ -37,6 +38,17 @@ struct DnArgs {
   uint32_t snap_rows;
   uint64_t snap_hist_stride, snap_s_stride;
 };
+
+// Chunked prefill (WY / UT form over chunks of kDnChunk tokens): used for
+// long prefills without state images at head dims 128 / 128 (or when
+// QM38_DN_CHUNKED forces it on or off).  Its workspace per (chunk, value
+// head): W [64][128], U~ [64][128], P [64][64], G [64].
+constexpr uint32_t kDnChunk = 64;
+constexpr size_t kDnChunkFloats = 64 * 128 * 2 + 64 * 64 + 64;
+bool dn_use_chunked(const DnArgs& a);
+inline size_t dn_chunk_ws_bytes(uint32_t M, uint32_t value_heads) {
+  return (size_t)((M + kDnChunk - 1) / kDnChunk) * value_heads * kDnChunkFloats * sizeof(float);
+}
 
 hipError_t launch_deltanet(const DnArgs& a, hipStream_t st);
 

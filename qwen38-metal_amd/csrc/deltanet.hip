@@ -19,6 +19,10 @@
 //     recurrence itself, applied token by token, so prefill equals M steps.
 //  3. dn_gate_norm_kernel  (qwen38_deltanet_gate_norm, :4497-4527):
 //     o <- o * rsqrt(mean o^2 + eps) * norm * silu(z).
+#include <stdlib.h>
+
+#include <algorithm>
+
 #include "common.h"
 #include "deltanet.h"
 
@@ -87,18 +91,20 @@ __device__ __forceinline__ float conv_finish(const DnArgs& a, const ConvIn& c) {
     wl = hw == j ? c.w[j] : wl;
     xl = hw == j ? c.x[j] : xl;
   }
-  float sum = wl * xl;
+  // Roundings spelled out (one product, then fused multiply-adds) so that
+  // every kernel computing a conv output rounds it identically.
+  float sum = __fmul_rn(wl, xl);
 #pragma unroll
   for (int j = 0; j < kTaps - 1; ++j)
-    if (j < hw) sum += c.w[j] * c.x[j];
+    if (j < hw) sum = fmaf(c.w[j], c.x[j], sum);
   return silu_f(sum);
 }
 // Longer kernels: the same sum, one tap at a time.
 __device__ __forceinline__ float conv_silu_loop(const DnArgs& a, uint32_t ch, int t) {
   const int hw = (int)a.kernel - 1;
   const float* w = a.conv_w + (size_t)ch * a.kernel;
-  float sum = w[hw] * conv_input(a, ch, t);
-  for (int tap = 0; tap < hw; ++tap) sum += w[tap] * conv_input(a, ch, t - hw + tap);
+  float sum = __fmul_rn(w[hw], conv_input(a, ch, t));
+  for (int tap = 0; tap < hw; ++tap) sum = fmaf(w[tap], conv_input(a, ch, t - hw + tap), sum);
   return silu_f(sum);
 }
 // One conv output; with a history target it also writes the channel's window
@@ -182,8 +188,8 @@ __device__ __forceinline__ void prep_key_head(const DnArgs& a, uint32_t t, uint3
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    qs += qo[i] * qo[i];
-    ks += ko[i] * ko[i];
+    qs = fmaf(qo[i], qo[i], qs);
+    ks = fmaf(ko[i], ko[i], ks);
   }
   qs = wave_sum(qs);
   ks = wave_sum(ks);
@@ -539,6 +545,479 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_kernel(DnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill conv + prepare over token tiles
+// ---------------------------------------------------------------------------
+// One wave per (tile of kConvTile tokens, unit); 4 waves per block.  A lane
+// keeps its channels' last kernel-1 inputs in registers and walks the tile,
+// so every input is loaded once (the per-token kernel loads each kernel
+// times), four tokens' inputs at a time.  The arithmetic is conv_finish /
+// prep_key_head's, operation for operation, so the outputs equal the
+// per-token kernel's bit for bit.  NS = channel slots per lane and class
+// (ceil(head dim / 64)); kernels of up to kTaps taps.
+constexpr int kConvTile = 16;
+template <int NS>
+__global__ __launch_bounds__(kThreads) void dn_conv_tiled_kernel(DnArgs a) {
+  constexpr int S2 = 2 * NS;  // q slots 0..NS-1, k slots NS..2NS-1 (value units use the first NS)
+  const uint32_t units = a.key_heads + a.value_heads;
+  const uint32_t tiles = (a.M + kConvTile - 1) / kConvTile;
+  const uint32_t item = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (item >= tiles * units) return;
+  // Units of one tile are consecutive: a block's waves share token rows.
+  const uint32_t tile = item / units, u = item % units;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t key_el = a.key_heads * a.dk;
+  const int hw = (int)a.kernel - 1;
+  const bool key = u < a.key_heads;
+  const int ns = key ? S2 : NS;  // live slots (wave-uniform)
+  const uint32_t width = key ? a.dk : a.dv;
+  uint32_t ch[S2];
+  bool ok[S2];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const uint32_t c = lane + 64 * i;
+    ok[i] = c < width;
+    ok[NS + i] = key && c < width;
+    const uint32_t cc = ok[i] ? c : 0;
+    ch[i] = key ? u * a.dk + cc : 2 * key_el + (u - a.key_heads) * a.dv + cc;
+    ch[NS + i] = key ? key_el + u * a.dk + cc : ch[i];
+  }
+  float w[S2][kTaps], win[S2][kTaps];  // win[s][j] = x(t - hw + j) for j < hw
+  const int t0 = (int)(tile * kConvTile);
+  const int t1 = min((int)a.M, t0 + kConvTile);
+#pragma unroll
+  for (int s = 0; s < S2; ++s) {
+    if (s >= ns) break;
+#pragma unroll
+    for (int j = 0; j < kTaps; ++j) {
+      const int jj = j <= hw ? j : hw;
+      w[s][j] = j <= hw ? a.conv_w[(size_t)ch[s] * a.kernel + jj] : 0.0f;
+      win[s][j] = j < hw ? conv_input(a, ch[s], t0 - hw + j) : 0.0f;
+    }
+  }
+  const float inv = 1.0f / sqrtf((float)a.dk);
+  for (int tb = t0; tb < t1; tb += 4) {
+    float xs[4][S2];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int s = 0; s < S2; ++s) {
+        const int t = min(tb + k, t1 - 1);
+        xs[k][s] = s < ns ? a.qkv[(size_t)t * a.channels + ch[s]] : 0.0f;
+      }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int t = tb + k;
+      if (t >= t1) break;
+      float* row = a.conv_out + (size_t)t * a.channels;
+      float* hist_dst = history_target(a, (uint32_t)t);
+      float y[S2];
+#pragma unroll
+      for (int s = 0; s < S2; ++s) {
+        const float x = xs[k][s];
+        // conv_finish: w[hw] * x(t), then taps 0 .. hw - 1 in order.
+        float wl = w[s][0];
+#pragma unroll
+        for (int jx = 1; jx < kTaps; ++jx) wl = hw == jx ? w[s][jx] : wl;
+        float sum = __fmul_rn(wl, x);  // conv_finish's roundings
+#pragma unroll
+        for (int jx = 0; jx < kTaps - 1; ++jx)
+          if (jx < hw) sum = fmaf(w[s][jx], win[s][jx], sum);
+        y[s] = silu_f(sum);
+        // Slide the window: x(t - hw + 1 .. t).
+#pragma unroll
+        for (int jx = 0; jx < kTaps - 1; ++jx) {
+          if (jx + 1 < hw) win[s][jx] = win[s][jx + 1];
+          else if (jx + 1 == hw) win[s][jx] = x;
+        }
+        if (hist_dst && s < ns && ok[s]) {
+#pragma unroll
+          for (int jx = 0; jx < kTaps - 1; ++jx)
+            if (jx < hw) hist_dst[(size_t)ch[s] * hw + jx] = win[s][jx];
+        }
+      }
+      if (key) {
+        float qs = 0.0f, ks = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+          const float yq = ok[i] ? y[i] : 0.0f, yk = ok[NS + i] ? y[NS + i] : 0.0f;
+          qs = fmaf(yq, yq, qs);
+          ks = fmaf(yk, yk, ks);
+        }
+        qs = wave_sum(qs);
+        ks = wave_sum(ks);
+        const float qscale = 1.0f / sqrtf(qs / (float)a.dk + a.eps);
+        const float kscale = 1.0f / sqrtf(ks / (float)a.dk + a.eps);
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+          if (ok[i]) {
+            row[ch[i]] = y[i] * qscale * inv * inv;
+            row[ch[NS + i]] = y[NS + i] * kscale * inv;
+          }
+      } else {
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+          if (ok[i]) row[ch[i]] = y[i];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Chunked scan (WY / UT form), head dims 128 / 128
+// ---------------------------------------------------------------------------
+// Within a chunk of C = 64 tokens (t = 0..63 from the chunk start), with
+// per-token log decay lg_t = -e^{A_log} softplus(a_t + dt_bias), cumulative
+// G_t = sum_{i<=t} lg_i, Gamma_t = e^{G_t}, the step recurrence
+//   S_t = g_t S_{t-1} + u_t k_t^T,  u_t = beta_t (v_t - g_t S_{t-1} k_t)
+// unrolls to S_t = Gamma_t S_0 + sum_{i<=t} e^{G_t - G_i} u_i k_i^T.  The
+// pseudo-values u solve the unit lower-triangular system
+//   (I + A) U = diag(beta) V - diag(beta Gamma) K S_0^T,
+//   A_ti = beta_t e^{G_t - G_i} k_t.k_i  (i < t),
+// so U = U~ - W S_0^T with W = (I+A)^{-1} diag(beta Gamma) K and
+// U~ = (I+A)^{-1} diag(beta) V, which do not depend on S.  Per chunk then
+//   O   = diag(Gamma) Q S_0^T + P U,   P_ti = e^{G_t - G_i} q_t.k_i (i <= t)
+//   S_C = Gamma_C S_0 + U^T diag(e^{G_C - G_i}) K.
+// dn_chunk_prep_kernel forms W, U~, P and G for every (chunk, value head) in
+// parallel (fp32 MFMA for K K^T and Q K^T, forward substitution for the
+// solve); dn_chunk_scan_kernel then walks the chunks in order.  Rows of S
+// stay independent (row j of S only meets column j of U), so each workgroup
+// owns 16 rows of one head in the same way as the token scan.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ floatx4 mfma_f32_4(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+constexpr int kCD = 128;        // head dims of the chunked path
+constexpr int kCStride = 132;   // LDS row stride (floats) of [64][128] tiles: conflict-free 16-byte reads
+constexpr int kAStride = 68;    // LDS row stride of the 64 x 64 triangular matrix
+
+__global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
+  __shared__ __attribute__((aligned(16))) float ks_s[64 * kCStride];
+  __shared__ __attribute__((aligned(16))) float a_s[64 * kAStride];
+  __shared__ float g_s[64], beta_s[64];
+  const uint32_t VH = a.value_heads;
+  const uint32_t h = blockIdx.x % VH, c = blockIdx.x / VH;
+  const uint32_t kh = h / (VH / a.key_heads);
+  const uint32_t key_el = a.key_heads * kCD;
+  const uint32_t t0 = c * kDnChunk;
+  const uint32_t nt = min(kDnChunk, a.M - t0);
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float* ws = a.chunk_ws + ((size_t)c * VH + h) * kDnChunkFloats;
+  float* Wg = ws;
+  float* Ug = ws + 64 * kCD;
+  float* Pg = Ug + 64 * kCD;
+  float* Gg = Pg + 64 * 64;
+
+  // k^ rows of the chunk (zero past the last token) into LDS.
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const uint32_t idx = tid + 256 * p;  // float4 index over [64][32]
+    const uint32_t t = idx / 32, j4 = idx % 32;
+    f32x4 kv = {0.f, 0.f, 0.f, 0.f};
+    if (t < nt) kv = *(const f32x4*)(a.conv_out + (size_t)(t0 + t) * a.channels + key_el + kh * kCD + 4 * j4);
+    *(f32x4*)(ks_s + t * kCStride + 4 * j4) = kv;
+  }
+  // Log decays, their running sum and beta (wave 0; padding tokens: lg = 0,
+  // beta = 0, so they change nothing).
+  if (wave == 0) {
+    float lg = 0.0f, beta = 0.0f;
+    if (lane < nt) {
+      const size_t ti = (size_t)(t0 + lane) * VH + h;
+      lg = -expf(a.a_log[h]) * softplus_f(a.a[ti] + a.dt_bias[h]);
+      beta = sigmoid_f(a.b[ti]);
+    }
+    float G = lg;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float o = __shfl_up(G, off);
+      if (lane >= (uint32_t)off) G += o;
+    }
+    g_s[lane] = G;
+    beta_s[lane] = beta;
+    Gg[lane] = G;
+  }
+  __syncthreads();
+
+  // K K^T and Q K^T on the lower-triangular 16 x 16 tiles (tn <= tm): 20
+  // tiles, 5 per wave.  The MFMA reduction index is permuted (lane group g of
+  // step (m, e) carries k = 16 m + 4 g + e), so every operand is one 16-byte
+  // read per lane and step group (q^ rows straight from memory).
+  const uint32_t j = lane & 15, grp = lane >> 4;
+  for (int tix = wave; tix < 20; tix += 4) {
+    const bool is_q = tix >= 10;
+    int rem = is_q ? tix - 10 : tix, tm = 0;
+    while (rem > tm) rem -= ++tm;
+    const int tn = rem;  // tile (tm, tn), tn <= tm
+    const uint32_t ta = 16 * tm + j;
+    const float* qa = a.conv_out + (size_t)(t0 + (ta < nt ? ta : 0)) * a.channels + kh * kCD + 4 * grp;
+    const float* xa = ks_s + ta * kCStride + 4 * grp;
+    const float* xb = ks_s + (16 * tn + j) * kCStride + 4 * grp;
+    f32x4 av[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+      av[m] = is_q ? (ta < nt ? *(const f32x4*)(qa + 16 * m) : f32x4{0.f, 0.f, 0.f, 0.f}) : *(const f32x4*)(xa + 16 * m);
+    floatx4 ac[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const f32x4 bv = *(const f32x4*)(xb + 16 * m);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ac[e] = mfma_f32_4(av[m][e], bv[e], ac[e]);
+    }
+    const floatx4 acc = (ac[0] + ac[1]) + (ac[2] + ac[3]);
+    // acc[r]: row t = 16 tm + 4 grp + r, column i = 16 tn + j.
+    const uint32_t i = 16 * tn + j;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t t = 16 * tm + 4 * grp + r;
+      const float dec = expf(g_s[t] - g_s[i]);
+      if (is_q) {
+        Pg[t * 64 + i] = i <= t ? dec * acc[r] : 0.0f;
+      } else {
+        a_s[t * kAStride + i] = i < t ? beta_s[t] * dec * acc[r] : 0.0f;
+      }
+    }
+  }
+  // P is zero above the diagonal blocks too, so its readers need no bounds.
+  for (uint32_t idx = tid; idx < 6 * 256; idx += 256) {
+    const uint32_t tile = idx / 256, e = idx % 256;
+    const uint32_t tm = tile < 3 ? 0 : tile < 5 ? 1 : 2;  // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+    const uint32_t tn = tile < 3 ? tile + 1 : tile < 5 ? tile - 1 : 3;
+    Pg[(16 * tm + e / 16) * 64 + 16 * tn + e % 16] = 0.0f;
+  }
+  __syncthreads();
+
+  // Forward substitution (I + A) X = R, one column per thread: columns
+  // 0..127 are R = beta Gamma k (giving W), 128..255 R = beta v (giving U~).
+  // Four partial sums per row keep four independent FMA chains.
+  float x[64];
+  if (tid < kCD) {
+#pragma unroll
+    for (int t = 0; t < 64; ++t) x[t] = beta_s[t] * expf(g_s[t]) * ks_s[t * kCStride + tid];
+  } else {
+    const uint32_t col = tid - kCD;
+    const float* vsrc = a.conv_out + 2 * key_el + h * kCD + col;
+#pragma unroll
+    for (int t = 0; t < 64; ++t) x[t] = (uint32_t)t < nt ? beta_s[t] * vsrc[(size_t)(t0 + t) * a.channels] : 0.0f;
+  }
+#pragma unroll
+  for (int t = 1; t < 64; ++t) {
+    const float* arow = a_s + t * kAStride;
+    float p[4] = {x[t], 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i4 = 0; i4 < t; i4 += 4) {
+      const f32x4 av = *(const f32x4*)(arow + i4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (i4 + e < t) p[e] -= av[e] * x[i4 + e];
+    }
+    x[t] = (p[0] + p[1]) + (p[2] + p[3]);
+  }
+  float* dst = tid < kCD ? Wg + tid : Ug + (tid - kCD);
+#pragma unroll
+  for (int t = 0; t < 64; ++t) dst[t * kCD] = x[t];
+}
+
+// grid: VH * 8 blocks (block = rg * VH + h: the 8 row groups of a head share
+// blockIdx mod 8, i.e. one XCD and its L2, where they read the same chunk
+// operands), 256 threads.  Every wave keeps the group's 16 rows of S in
+// registers (MFMA A layout).  Per chunk, wave w owns tokens 16 w .. 16 w + 15:
+//   U_w^T = U~_w^T - S W_w^T                      (its 16 tokens)
+//   O_w^T = S (Gamma Q_w)^T + sum_{i <= t} U^T P   (after the exchange)
+//   D_w   = U_w^T diag(e^{G_C - G_i}) K_w          (its share of the S update)
+// then one barrier: U^T and the four shares D_w meet in LDS (two buffers,
+// alternating by chunk, so the next chunk never overwrites what a slower wave
+// still reads), and every wave forms S <- Gamma_C S + sum_w D_w itself.  The
+// next chunk's operands are loaded into registers while the current chunk
+// is computed (each register set is refilled right after its last use).
+__global__ __launch_bounds__(256) void dn_chunk_scan_kernel(DnArgs a) {
+  __shared__ __attribute__((aligned(16))) float u_s[2][16 * kAStride];      // U^T [row][token]
+  __shared__ __attribute__((aligned(16))) float d_s[2][4][16 * kCStride];   // D_w [row][col]
+  __shared__ __attribute__((aligned(16))) float k_s[4][16 * kCStride];      // each wave's 16 k^ rows
+  const uint32_t VH = a.value_heads;
+  const uint32_t h = blockIdx.x % VH, rg = blockIdx.x / VH;
+  const uint32_t kh = h / (VH / a.key_heads);
+  const uint32_t key_el = a.key_heads * kCD;
+  const uint32_t row0 = rg * 16;
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t j = lane & 15, grp = lane >> 4;
+  const uint32_t nchunks = (a.M + kDnChunk - 1) / kDnChunk;
+  const uint32_t tok = 16 * wave + j;        // this lane's token column in U and O
+  const uint32_t ktok = 16 * wave + 4 * grp;  // first of the 4 tokens this lane carries in D_w
+
+  f32x4 Wv[8], qv[8], Uv, Pv[4];
+  bool q_ok;  // this lane's token exists in the loaded chunk
+  f32x4 kr[8];     // the wave's 16 k^ rows as loaded: row 16 w + 2 p + grp / 2, float4 (grp % 2) * 16 + j
+  uint32_t k_rows;  // tokens in the chunk kr was loaded for
+  float G_tok, G_last, Gk[4];
+  auto ws_of = [&](uint32_t c) { return a.chunk_ws + ((size_t)c * VH + h) * kDnChunkFloats; };
+  // Rows past the last token read a valid row and are weighted by zero.
+  // Issue order follows first use in the next chunk: the decays, then W, q
+  // and U~ (first phase), then k^ and P (after the exchange), so the waits
+  // at the top of a chunk leave the later loads in flight.
+  auto load_wqu = [&](uint32_t c) __attribute__((always_inline)) {
+    const float* ws = ws_of(c);
+    const uint32_t t0 = c * kDnChunk, nt = min(kDnChunk, a.M - t0);
+    const float* Gg = ws + 2 * 64 * kCD + 64 * 64;
+    G_tok = Gg[tok];
+    G_last = Gg[63];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Gk[e] = Gg[ktok + e];
+    // (Masks are applied where the values are used, not here, so that the
+    // loads stay in flight.)
+    const float* qrow = a.conv_out + (size_t)(t0 + (tok < nt ? tok : 0)) * a.channels + kh * kCD;
+    q_ok = tok < nt;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      Wv[m] = *(const f32x4*)(ws + tok * kCD + 16 * m + 4 * grp);
+      qv[m] = *(const f32x4*)(qrow + 16 * m + 4 * grp);
+    }
+    Uv = *(const f32x4*)(ws + 64 * kCD + tok * kCD + row0 + 4 * grp);
+  };
+  // The wave's 16 k^ rows, 16-byte loads (lane: row 16 w + 2 p + grp / 2,
+  // float4 column (grp % 2) * 16 + j); they reach the MFMA operand layout
+  // through the wave's own LDS rows.
+  auto load_k = [&](uint32_t c) __attribute__((always_inline)) {
+    const uint32_t t0 = c * kDnChunk, nt = min(kDnChunk, a.M - t0);
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const uint32_t t = 16 * wave + 2 * p + grp / 2;
+      const float* krow = a.conv_out + (size_t)(t0 + (t < nt ? t : 0)) * a.channels + key_el + kh * kCD;
+      kr[p] = *(const f32x4*)(krow + 4 * ((grp % 2) * 16 + j));
+    }
+    k_rows = nt;
+  };
+  auto load_p = [&](uint32_t c) __attribute__((always_inline)) {
+    const float* Pg = ws_of(c) + 2 * 64 * kCD;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) Pv[m] = *(const f32x4*)(Pg + tok * 64 + 16 * m + 4 * grp);
+  };
+
+  // Initial rows of S in A layout: sa[m][e] = S[row0 + j][16 m + 4 grp + e].
+  f32x4 sa[8];
+  {
+    const float* sin = a.s_in + ((size_t)h * kCD + row0 + j) * kCD + 4 * grp;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) sa[m] = *(const f32x4*)(sin + 16 * m);
+  }
+
+  // First half of chunk c: U^T (exchanged through u_s), O^T's S Q^T term,
+  // the wave's share D_w of the S update (to d_s).  The next chunk's W, q,
+  // U~, decays and k^ rows are loaded once this chunk's are consumed.
+  auto head = [&](uint32_t c, floatx4& acc_o) __attribute__((always_inline)) {
+    const uint32_t pb = c & 1;
+    const uint32_t cn = min(c + 1, nchunks - 1);  // the last chunk reloads itself (unused)
+    const float gam = q_ok ? expf(G_tok) : 0.0f, gam_l = G_last;
+    float dk4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dk4[e] = expf(gam_l - Gk[e]);
+    // (a) U^T[row][tok] = U~[tok][row] - sum_k S[row][k] W[tok][k]
+    // (b1) O^T[row][tok] = sum_k S[row][k] Gamma_tok q[tok][k]
+    // The MFMA reduction index is permuted: lane group grp of step (m, e)
+    // carries k = 16 m + 4 grp + e, so each operand is one 16-byte read.
+    floatx4 au[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    floatx4 ao[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        au[m & 1] = mfma_f32_4(sa[m][e], Wv[m][e], au[m & 1]);
+        ao[m & 1] = mfma_f32_4(sa[m][e], gam * qv[m][e], ao[m & 1]);
+      }
+    const floatx4 acc_u = au[0] + au[1];
+    acc_o = ao[0] + ao[1];
+    float* us = u_s[pb];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) us[(4 * grp + r) * kAStride + tok] = Uv[r] - acc_u[r];
+    // k^ rows of the wave's tokens: registers -> the wave's LDS rows -> the
+    // operand layout (k^[ktok + e][16 n + j]).  Same wave: no barrier.
+    float* ksw = k_s[wave];
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+      *(f32x4*)(ksw + (2 * p + grp / 2) * kCStride + 4 * ((grp % 2) * 16 + j)) =
+          kr[p] * (16 * wave + 2 * p + grp / 2 < k_rows ? 1.0f : 0.0f);
+    load_wqu(cn);
+    load_k(cn);
+    // D_w[row][col] = sum_{i in w} U^T[row][i] e^{G_C - G_i} k[i][col]
+    const f32x4 uw = *(const f32x4*)(us + j * kAStride + ktok);
+    float kv[4][8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int n = 0; n < 8; ++n) kv[e][n] = ksw[(4 * grp + e) * kCStride + 16 * n + j];
+    floatx4 d[8];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) d[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int n = 0; n < 8; ++n) d[n] = mfma_f32_4(uw[e], dk4[e] * kv[e][n], d[n]);
+    float* ds = d_s[pb][wave];
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ds[(4 * grp + r) * kCStride + 16 * n + j] = d[n][r];
+  };
+  // Second half of chunk c (after the barrier): O^T's P U^T term and its
+  // store, then S <- Gamma_C S + sum_w D_w.
+  auto tail = [&](uint32_t c, floatx4 acc_o, float gam_c) __attribute__((always_inline)) {
+    const uint32_t pb = c & 1;
+    const uint32_t t0 = c * kDnChunk, nt = min(kDnChunk, a.M - t0);
+    const float* us = u_s[pb];
+    // (b2) O^T[row][tok] += sum_{i <= tok} U^T[row][i] P[tok][i]; all four
+    // token blocks (P is zero past the diagonal block), so no branch.
+    floatx4 ap[2] = {acc_o, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const f32x4 ua = *(const f32x4*)(us + j * kAStride + 16 * m + 4 * grp);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ap[e & 1] = mfma_f32_4(ua[e], Pv[m][e], ap[e & 1]);
+    }
+    load_p(min(c + 1, nchunks - 1));
+    acc_o = ap[0] + ap[1];
+    // A buffer store bounded to the chunk's nt rows: tokens past the end are
+    // dropped by the hardware, so the store needs no branch.
+    const uint32_t row_bytes = VH * kCD * 4;
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+        a.out + (size_t)t0 * VH * kCD, (short)0, (int)(nt * row_bytes), 0x00020000);
+    __builtin_amdgcn_raw_buffer_store_b128(
+        u32x4{__float_as_uint(acc_o[0]), __float_as_uint(acc_o[1]), __float_as_uint(acc_o[2]),
+              __float_as_uint(acc_o[3])},
+        ro, tok * row_bytes + (h * kCD + row0 + 4 * grp) * 4, 0, 0);
+    // S <- Gamma_C S + sum_w D_w (A layout, fixed order of w).
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      f32x4 acc = sa[m] * gam_c;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) acc += *(const f32x4*)(d_s[pb][w] + j * kCStride + 16 * m + 4 * grp);
+      sa[m] = acc;
+    }
+  };
+
+  load_wqu(0);
+  load_k(0);
+  load_p(0);
+  floatx4 acc_o;
+  float gam_c = expf(G_last);
+  head(0, acc_o);
+  lds_barrier();  // U^T and every D_w of chunk 0 complete
+  // Iteration c finishes chunk c - 1 and starts chunk c: its loop-carried
+  // loads were all issued a full phase before the loop boundary.
+  for (uint32_t c = 1; c < nchunks; ++c) {
+    tail(c - 1, acc_o, gam_c);
+    gam_c = expf(G_last);
+    head(c, acc_o);
+    lds_barrier();
+  }
+  tail(nchunks - 1, acc_o, gam_c);
+  float* sout = a.s_out + ((size_t)h * kCD + row0 + j) * kCD + 4 * grp;
+  if (wave == 0) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) *(f32x4*)(sout + 16 * m) = sa[m];
+  }
+}
+
 template <int EPT>
 void launch_scan(const DnArgs& a, hipStream_t st) {
   const uint32_t groups = (a.dv + kRowsPerWg - 1) / kRowsPerWg;
@@ -546,6 +1025,13 @@ void launch_scan(const DnArgs& a, hipStream_t st) {
 }
 
 }  // namespace
+
+bool dn_use_chunked(const DnArgs& a) {
+  if (a.dk != kCD || a.dv != kCD || a.snap_rows > 0 || a.M <= 1 || a.value_heads % a.key_heads != 0) return false;
+  const char* env = getenv("QM38_DN_CHUNKED");
+  if (env) return atoi(env) != 0;
+  return a.M >= 2 * kDnChunk;
+}
 
 hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
   if (a.dk == 0 || a.dk > 256 || a.dv == 0 || a.dv > 256 || a.M == 0) return hipErrorInvalidValue;
@@ -563,21 +1049,40 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
       hipLaunchKernelGGL((dn_step_kernel<8, 8>), grid, block, 0, st, a);
     return hipGetLastError();
   }
-  // Few items (decode): one wave per block so they spread over more CUs.
-  const uint32_t prep_items = a.M * (a.key_heads + a.value_heads);
-  const uint32_t wpb = prep_items >= 1024 ? kThreads / 64 : 1;
-  hipLaunchKernelGGL(dn_conv_prepare_kernel, dim3((prep_items + wpb - 1) / wpb), dim3(64 * wpb), 0, st, a);
-  const uint32_t ept = (a.dk + kLanesPerRow - 1) / kLanesPerRow;
-  if (ept <= 1)
-    launch_scan<1>(a, st);
-  else if (ept <= 2)
-    launch_scan<2>(a, st);
-  else if (ept <= 4)
-    launch_scan<4>(a, st);
-  else if (ept <= 8)
-    launch_scan<8>(a, st);
-  else
-    launch_scan<16>(a, st);
+  const uint32_t units = a.key_heads + a.value_heads;
+  if (a.kernel <= kTaps) {
+    const uint32_t items = ((a.M + kConvTile - 1) / kConvTile) * units;
+    const dim3 grid((items + 3) / 4), block(kThreads);
+    const uint32_t ns = (std::max(a.dk, a.dv) + 63) / 64;
+    if (ns <= 1)
+      hipLaunchKernelGGL(dn_conv_tiled_kernel<1>, grid, block, 0, st, a);
+    else if (ns <= 2)
+      hipLaunchKernelGGL(dn_conv_tiled_kernel<2>, grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL(dn_conv_tiled_kernel<4>, grid, block, 0, st, a);
+  } else {
+    const uint32_t prep_items = a.M * units;
+    hipLaunchKernelGGL(dn_conv_prepare_kernel, dim3((prep_items + 3) / 4), dim3(kThreads), 0, st, a);
+  }
+  if (dn_use_chunked(a)) {
+    if (!a.chunk_ws) return hipErrorInvalidValue;
+    const uint32_t nchunks = (a.M + kDnChunk - 1) / kDnChunk;
+    hipLaunchKernelGGL(dn_chunk_prep_kernel, dim3(nchunks * a.value_heads), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(dn_chunk_scan_kernel, dim3(a.value_heads * (kCD / 16)), dim3(256), 0, st, a);
+  } else {
+    const uint32_t ept = (a.dk + kLanesPerRow - 1) / kLanesPerRow;
+    if (ept <= 1)
+      launch_scan<1>(a, st);
+    else if (ept <= 2)
+      launch_scan<2>(a, st);
+    else if (ept <= 4)
+      launch_scan<4>(a, st);
+    else if (ept <= 8)
+      launch_scan<8>(a, st);
+    else
+      launch_scan<16>(a, st);
+  }
+  const uint32_t wpb = a.M * a.value_heads >= 1024 ? kThreads / 64 : 1;
   const uint32_t norm_items = a.M * a.value_heads;
   hipLaunchKernelGGL(dn_gate_norm_kernel, dim3((norm_items + wpb - 1) / wpb), dim3(64 * wpb), 0, st, a);
   return hipGetLastError();

@@ -119,9 +119,7 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
                   snaps->rows, M);
   }
   const qm_dn_config& c = w->cfg;
-  const size_t conv_bytes = (size_t)M * w->channels * sizeof(float);
-  qm_status st = ensure_scratch(rt, conv_bytes);
-  if (st != QM_OK) return st;
+  const size_t conv_bytes = ((size_t)M * w->channels * sizeof(float) + 255) & ~size_t(255);
   DnArgs d{};
   d.key_heads = c.key_heads;
   d.value_heads = c.value_heads;
@@ -145,7 +143,12 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
   d.hist_out = to->hist[next];
   d.s_in = from->rec;
   d.s_out = to->rec;
+  if (snaps && M > 1) d.snap_rows = M - 1;  // decides the path below
+  const size_t chunk_bytes = dn_use_chunked(d) ? dn_chunk_ws_bytes(M, c.value_heads) : 0;
+  qm_status st = ensure_scratch(rt, conv_bytes + chunk_bytes);
+  if (st != QM_OK) return st;
   d.conv_out = (float*)rt->scratch;
+  d.chunk_ws = chunk_bytes ? (float*)((char*)rt->scratch + conv_bytes) : nullptr;
   d.out = out;
   // The fused single-token kernel also writes the bf16 copy; other paths
   // convert afterwards.

@@ -8,11 +8,19 @@ and two closed forms of the recurrence:
   * beta = 0 leaves S <- g S;
   * g = 1, beta = 1 makes S k^ = v after the update (delta rule), since k^
     has unit norm up to eps.
+Long prefills take the chunked (WY / UT) scan; the chunked cases below pin
+it against the fp64 oracle at chunk boundaries, partial chunks, strong
+decays and shadow states, and force the token scan where a test asserts
+bit-identity with token-by-token steps.
+
 Bars: outputs and state within 1e-4 of max|ref| against the fp64 oracle
-(the reference's own tests use 1e-3 absolute); prefill bit-identical to
-token-by-token steps (both run the same recurrence).
+(the reference's own tests use 1e-3 absolute); the token-scan prefill
+bit-identical to token-by-token steps (both run the same recurrence).
 """
 from __future__ import annotations
+
+import os
+from contextlib import contextmanager
 
 import numpy as np
 import pytest
@@ -61,6 +69,16 @@ def _close(got, ref, tol=TOL, what=""):
     err = np.max(np.abs(got - ref)) / scale
     assert err <= tol, f"{what}: rel err {err:.3e} > {tol:.1e}"
     return err
+
+
+@contextmanager
+def _chunked(on: bool):
+    """Forces the chunked scan on or off for long and short prefills alike."""
+    os.environ["QM38_DN_CHUNKED"] = "1" if on else "0"
+    try:
+        yield
+    finally:
+        os.environ.pop("QM38_DN_CHUNKED", None)
 
 
 def _zero_state(c):
@@ -196,7 +214,8 @@ def test_long_prefill_equals_steps(rt, torch_dev):
     wts, acts = _synth(rng, c, M)
     w = rt.create_deltanet_weights(cfg, *wts)
     pre, step = w.create_state(), w.create_state()
-    got = _run(rt, torch_dev, w, pre, *acts, 1e-6)
+    with _chunked(False):
+        got = _run(rt, torch_dev, w, pre, *acts, 1e-6)
     steps = np.stack([_step(rt, torch_dev, w, step, *(x[t] for x in acts), 1e-6) for t in range(M)])
     assert np.array_equal(got, steps)
     for x, y in zip(pre.read(), step.read()):
@@ -205,6 +224,13 @@ def test_long_prefill_equals_steps(rt, torch_dev):
     ref, _, S_ref = oracle.deltanet_prefill(c, *wts, *acts, 1e-6, hist, S, f64=True)
     _close(got, ref, what="long prefill")
     _close(pre.read()[1], S_ref, what="long state")
+    # The default (chunked) path: same oracle bar, steps within it too.
+    ch = w.create_state()
+    got_c = _run(rt, torch_dev, w, ch, *acts, 1e-6)
+    _close(got_c, ref, what="long prefill, chunked")
+    _close(ch.read()[1], S_ref, what="long state, chunked")
+    _close(got_c, steps, what="chunked vs steps")
+    assert np.array_equal(ch.read()[0], pre.read()[0]), "conv history is path independent"
 
 
 def test_prefill_2048_tokens(rt, torch_dev):
@@ -373,3 +399,59 @@ def test_snapshot_errors(rt, torch_dev):
     ow = rt.create_deltanet_weights(other_cfg, *_synth(rng, oc, 1)[0])
     with pytest.raises(QmError):
         snaps.restore(0, ow.create_state())
+
+
+# ---------------------------------------------------------------------------
+# Chunked scan (WY / UT form)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape", [(16, 32, 128, 128, 4), (2, 8, 128, 128, 3)])
+@pytest.mark.parametrize("M", [2, 63, 64, 65, 130, 200])
+@pytest.mark.parametrize("decay", ["baseline", "strong"])
+def test_chunked_matches_oracle(rt, torch_dev, shape, M, decay):
+    """Warm start (9 token-scan tokens), then M tokens through the chunked
+    scan.  "strong": A_log ~ 1.5 N(0,1), dt_bias ~ N(0,1), so cumulative
+    decays across a chunk underflow fp32 for some heads."""
+    cfg, c = _cfg(*shape)
+    rng = np.random.default_rng(sum(shape) * 1000 + M * 7 + (decay == "strong"))
+    (conv, a_log, dt_bias, norm), acts = _synth(rng, c, M + 9)
+    if decay == "strong":
+        a_log = (1.5 * rng.standard_normal(c["value_heads"])).astype(np.float32)
+        dt_bias = rng.standard_normal(c["value_heads"]).astype(np.float32)
+    wts = (conv, a_log, dt_bias, norm)
+    w = rt.create_deltanet_weights(cfg, *wts)
+    st = w.create_state()
+    warm = [x[:9] for x in acts]
+    rest = [x[9:] for x in acts]
+    with _chunked(False):
+        _run(rt, torch_dev, w, st, *warm, 1e-6)
+    with _chunked(True):
+        got = _run(rt, torch_dev, w, st, *rest, 1e-6)
+    hist, S = _zero_state(c)
+    _, hist, S = oracle.deltanet_prefill(c, *wts, *warm, 1e-6, hist, S, f64=True)
+    ref, h_ref, S_ref = oracle.deltanet_prefill(c, *wts, *rest, 1e-6, hist, S, f64=True)
+    _close(got, ref, what=f"chunked out M={M} {decay}")
+    h, S_got = st.read()
+    _close(S_got, S_ref, what=f"chunked state M={M} {decay}")
+    _close(h, h_ref, tol=0, what="history")
+
+
+def test_chunked_shadow_prefill_leaves_source(rt, torch_dev):
+    """deltanet_prefill_from with the chunked scan: the source state is read,
+    never written; the shadow gets the result."""
+    cfg, c = _cfg(16, 32, 128, 128, 4)
+    rng = np.random.default_rng(515)
+    wts, acts = _synth(rng, c, 137)
+    w = rt.create_deltanet_weights(cfg, *wts)
+    src = w.create_state()
+    _run(rt, torch_dev, w, src, *[x[:9] for x in acts], 1e-6)
+    before = [x.copy() for x in src.read()]
+    shadow = w.create_state()
+    with _chunked(True):
+        got = _run(rt, torch_dev, w, shadow, *[x[9:] for x in acts], 1e-6, source=src)
+    after = src.read()
+    assert np.array_equal(before[0], after[0]) and np.array_equal(before[1], after[1])
+    hist, S = _zero_state(c)
+    _, hist, S = oracle.deltanet_prefill(c, *wts, *[x[:9] for x in acts], 1e-6, hist, S, f64=True)
+    ref, _, S_ref = oracle.deltanet_prefill(c, *wts, *[x[9:] for x in acts], 1e-6, hist, S, f64=True)
+    _close(got, ref, what="shadow chunked out")
+    _close(shadow.read()[1], S_ref, what="shadow chunked state")
