@@ -77,7 +77,12 @@ typedef struct qm_runtime qm_runtime;
 
 /* Replaces MetalRuntime::new (metal_runtime.rs:641-927): binds HIP device
  * `device`, creates the runtime's scratch pools.  The default stream is the
- * device's null stream. */
+ * device's null stream.  device = QM_DEVICE_NONE makes a runtime without a
+ * device (no counterpart in the reference): every entry point still checks
+ * its arguments and returns their error, and returns QM_ERR_NO_DEVICE where
+ * it would touch a device.  It lets argument validation run on a host with
+ * no GPU (tests, dry runs). */
+#define QM_DEVICE_NONE (-1)
 qm_status qm_runtime_create(int device, qm_runtime** out);
 void qm_runtime_destroy(qm_runtime* rt);
 /* Enqueue all later work of `rt` on `hip_stream` (a hipStream_t; NULL selects

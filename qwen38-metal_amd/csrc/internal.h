@@ -35,9 +35,6 @@ struct Workspace {
 
 // Decode (weight-streaming) Q4 projection: M <= 16 activation rows.
 // swiglu: jobs[0] = gate, jobs[1] = up, result written to jobs[0].out.
-// q4_decode_workspace reports the partial bytes / counters a launch needs.
-void q4_decode_workspace(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M,
-                         size_t* partial_bytes, size_t* counters);
 hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x,
                             uint32_t K, uint32_t M, const Workspace& ws, hipStream_t stream);
 

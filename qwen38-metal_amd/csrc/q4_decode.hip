@@ -516,7 +516,8 @@ Plan make_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t 
   int nt = swiglu ? 2 : ((rows / 32 >= (uint64_t)cus * 2) ? 2 : 1);
   if (!swiglu && env_int("QM38_Q4_NT", 0) > 0) nt = env_int("QM38_Q4_NT", 1) >= 2 ? 2 : 1;
   // Staged activations when all M rows fit (each wave holds its K slice).
-  const bool xw = M * (K * 2 + 16) <= kXStageMax && env_int("QM38_Q4_XSTAGE", 1) != 0;
+  const uint32_t x_max = (uint32_t)env_int("QM38_Q4_XSTAGE_MAX", (int)kXStageMax);
+  const bool xw = M * (K * 2 + 16) <= x_max && env_int("QM38_Q4_XSTAGE", 1) != 0;
   const bool g8 = (G % 8) == 0;
   const void* fn = swiglu ? instance_m<2, true>(M, g8, xw)
                           : (nt == 2 ? instance_m<2, false>(M, g8, xw) : instance_m<1, false>(M, g8, xw));
@@ -580,7 +581,7 @@ struct PlanKey {
   int n_jobs;
   bool swiglu;
   uint32_t K, M;
-  int env[6];
+  int env[7];
   bool operator==(const PlanKey& o) const {
     return n_jobs == o.n_jobs && swiglu == o.swiglu && K == o.K && M == o.M &&
            std::memcmp(rows, o.rows, sizeof(rows)) == 0 && std::memcmp(env, o.env, sizeof(env)) == 0;
@@ -597,9 +598,9 @@ Plan cached_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_
   k.swiglu = swiglu;
   k.K = K;
   k.M = M;
-  const char* names[6] = {"QM38_CUS", "QM38_Q4_NT", "QM38_Q4_XSTAGE", "QM38_Q4_TARGET_WAVES", "QM38_Q4_RPW",
-                          "QM38_Q4_SPLIT"};
-  for (int i = 0; i < 6; ++i) k.env[i] = env_int(names[i], -1);
+  const char* names[7] = {"QM38_CUS", "QM38_Q4_NT", "QM38_Q4_XSTAGE", "QM38_Q4_TARGET_WAVES", "QM38_Q4_RPW",
+                          "QM38_Q4_SPLIT", "QM38_Q4_XSTAGE_MAX"};
+  for (int i = 0; i < 7; ++i) k.env[i] = env_int(names[i], -1);
   std::lock_guard<std::mutex> lock(mu);
   for (int i = 0; i < used; ++i)
     if (keys[i] == k) return plans[i];
@@ -617,11 +618,6 @@ Plan cached_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_
 }
 
 }  // namespace
-
-void q4_decode_workspace(const Q4Job*, int, bool, uint32_t, uint32_t, size_t* partial_bytes, size_t* counters) {
-  *partial_bytes = 0;
-  *counters = 0;
-}
 
 hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x,
                             uint32_t K, uint32_t M, const Workspace&, hipStream_t stream) {

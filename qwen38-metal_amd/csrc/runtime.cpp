@@ -28,17 +28,28 @@ qm_status qm::fail(qm_status status, const char* fmt, ...) {
 
 qm_status qm::hip_check(hipError_t err, const char* what) {
   if (err == hipSuccess) return QM_OK;
+  // Reported here; cleared so that a later launch's hipGetLastError() does
+  // not see it again.
+  (void)hipGetLastError();
   if (err == hipErrorOutOfMemory) return fail(QM_ERR_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(err));
   return fail(QM_ERR_COMMAND_FAILED, "%s: %s", what, hipGetErrorString(err));
 }
 
 qm::DeviceGuard::DeviceGuard(int device) {
+  dev_ = device;
+  if (device < 0) {  // a runtime without a device (argument checks only)
+    prev_ = device;
+    return;
+  }
   hipGetDevice(&prev_);
   if (prev_ != device) hipSetDevice(device);
-  dev_ = device;
 }
 qm::DeviceGuard::~DeviceGuard() {
-  if (prev_ != dev_) hipSetDevice(prev_);
+  if (dev_ >= 0 && prev_ != dev_) hipSetDevice(prev_);
+}
+
+qm_status qm::no_device() {
+  return fail(QM_ERR_NO_DEVICE, "this runtime has no device (created with device %d)", QM_DEVICE_NONE);
 }
 
 // Growing a buffer allocates and synchronises, which a stream under graph
@@ -52,6 +63,7 @@ static qm_status capture_guard(qm_runtime* rt, const char* what) {
 
 qm_status qm::ensure_scratch(qm_runtime* rt, size_t bytes) {
   if (rt->scratch_bytes >= bytes) return QM_OK;
+  if (rt->device < 0) return no_device();
   if (qm_status st_cap = capture_guard(rt, "ensure_scratch"); st_cap != QM_OK) return st_cap;
   if (rt->scratch) {
     // Work already enqueued may still use the old buffer.
@@ -71,6 +83,7 @@ qm_status qm::ensure_scratch(qm_runtime* rt, size_t bytes) {
 
 qm_status qm::ensure_partials(qm_runtime* rt, size_t bytes) {
   if (rt->partial_bytes >= bytes) return QM_OK;
+  if (rt->device < 0) return no_device();
   if (qm_status st_cap = capture_guard(rt, "ensure_partials"); st_cap != QM_OK) return st_cap;
   if (rt->partials) {
     hipError_t e = hipStreamSynchronize(rt->stream);
@@ -89,6 +102,7 @@ qm_status qm::ensure_partials(qm_runtime* rt, size_t bytes) {
 
 qm_status qm::ensure_xh(qm_runtime* rt, size_t bytes) {
   if (rt->xh_bytes >= bytes) return QM_OK;
+  if (rt->device < 0) return no_device();
   if (qm_status st_cap = capture_guard(rt, "ensure_xh"); st_cap != QM_OK) return st_cap;
   if (rt->xh) {
     hipError_t e = hipStreamSynchronize(rt->stream);
@@ -106,6 +120,7 @@ qm_status qm::ensure_xh(qm_runtime* rt, size_t bytes) {
 
 qm_status qm::ensure_counters(qm_runtime* rt, size_t count) {
   if (rt->counter_count >= count) return QM_OK;
+  if (rt->device < 0) return no_device();
   if (qm_status st_cap = capture_guard(rt, "ensure_counters"); st_cap != QM_OK) return st_cap;
   if (rt->counters) {
     hipError_t e = hipStreamSynchronize(rt->stream);
@@ -177,6 +192,12 @@ const char* qm_last_error_message(void) { return g_last_error.c_str(); }
 qm_status qm_runtime_create(int device, qm_runtime** out) {
   if (!out) return fail(QM_ERR_NULL_POINTER, "out is NULL");
   *out = nullptr;
+  if (device == QM_DEVICE_NONE) {
+    qm_runtime* rt = new qm_runtime();
+    rt->device = QM_DEVICE_NONE;
+    *out = rt;
+    return QM_OK;
+  }
   int count = 0;
   if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
     return fail(QM_ERR_NO_DEVICE, "no HIP device is available");
@@ -185,6 +206,7 @@ qm_status qm_runtime_create(int device, qm_runtime** out) {
   qm_runtime* rt = new qm_runtime();
   rt->device = device;
   DeviceGuard g(device);
+  if (!g.ok()) return no_device();
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) == hipSuccess) rt->cu_count = prop.multiProcessorCount;
   *out = rt;
@@ -193,6 +215,10 @@ qm_status qm_runtime_create(int device, qm_runtime** out) {
 
 void qm_runtime_destroy(qm_runtime* rt) {
   if (!rt) return;
+  if (rt->device < 0) {
+    delete rt;
+    return;
+  }
   DeviceGuard g(rt->device);
   hipStreamSynchronize(rt->stream);
   qm::release_buffers(rt);
@@ -208,6 +234,7 @@ qm_status qm_runtime_set_stream(qm_runtime* rt, void* hip_stream) {
 qm_status qm_runtime_synchronize(qm_runtime* rt) {
   if (!rt) return fail(QM_ERR_NULL_POINTER, "runtime is NULL");
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   return hip_check(hipStreamSynchronize(rt->stream), "stream synchronize");
 }
 
@@ -215,6 +242,7 @@ qm_status qm_device_alloc(qm_runtime* rt, size_t bytes, void** out) {
   if (!rt || !out) return fail(QM_ERR_NULL_POINTER, "runtime/out is NULL");
   if (bytes == 0) return fail(QM_ERR_EMPTY_DIMENSION, "zero-byte allocation");
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   return hip_check(hipMalloc(out, bytes), "hipMalloc");
 }
 
@@ -222,6 +250,7 @@ qm_status qm_device_free(qm_runtime* rt, void* ptr) {
   if (!rt) return fail(QM_ERR_NULL_POINTER, "runtime is NULL");
   if (!ptr) return QM_OK;
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   return hip_check(hipFree(ptr), "hipFree");
 }
 
@@ -235,6 +264,7 @@ qm_status qm_upload(qm_runtime* rt, const void* host, size_t bytes, void** out) 
 qm_status qm_copy_to_device(qm_runtime* rt, void* dst, const void* host, size_t bytes) {
   if (!rt || !dst || !host) return fail(QM_ERR_NULL_POINTER, "NULL argument");
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   qm_status st = hip_check(hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, rt->stream), "H2D copy");
   if (st != QM_OK) return st;
   return hip_check(hipStreamSynchronize(rt->stream), "H2D sync");
@@ -243,6 +273,7 @@ qm_status qm_copy_to_device(qm_runtime* rt, void* dst, const void* host, size_t 
 qm_status qm_copy_to_host(qm_runtime* rt, void* host, const void* src, size_t bytes) {
   if (!rt || !src || !host) return fail(QM_ERR_NULL_POINTER, "NULL argument");
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   qm_status st = hip_check(hipMemcpyAsync(host, src, bytes, hipMemcpyDeviceToHost, rt->stream), "D2H copy");
   if (st != QM_OK) return st;
   return hip_check(hipStreamSynchronize(rt->stream), "D2H sync");

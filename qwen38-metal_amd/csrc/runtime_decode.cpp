@@ -187,6 +187,7 @@ qm_status ensure_arena(qm_decode_state* st, const qm_decode_state::Sizes& need) 
   if (!grow && st->arena) return QM_OK;
   const size_t bytes = layout(st, s, nullptr);
   DeviceGuard g(st->rt->device);
+  if (!g.ok()) return no_device();
   if (st->arena) {
     hipError_t e = hipStreamSynchronize(st->rt->stream);
     if (e != hipSuccess) return hip_check(e, "decode state resize sync");
@@ -359,6 +360,7 @@ qm_status qm_residual_rmsnorm(qm_runtime* rt, float* hidden, const uint16_t* del
   if (M == 0 || n == 0) return fail(QM_ERR_EMPTY_DIMENSION, "RMSNorm of an empty row");
   if (!(epsilon >= 0.0f)) return fail(QM_ERR_INVALID_ARGUMENT, "epsilon must be >= 0");
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   return hip_check(launch_residual_rmsnorm(hidden, delta, weights, out, M, n, epsilon, rt->stream),
                    "RMSNorm launch");
 }
@@ -366,6 +368,7 @@ qm_status qm_residual_rmsnorm(qm_runtime* rt, float* hidden, const uint16_t* del
 qm_status qm_residual_add(qm_runtime* rt, float* hidden, const uint16_t* delta, size_t count) {
   if (!rt || !hidden || !delta) return fail(QM_ERR_NULL_POINTER, "NULL argument");
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   return hip_check(launch_residual_add(hidden, delta, count, rt->stream), "residual add launch");
 }
 
@@ -378,6 +381,10 @@ qm_status qm_decode_state_create(qm_runtime* rt, uint32_t hidden_elems, qm_decod
   st->rt = rt;
   st->hidden = hidden_elems;
   DeviceGuard g(rt->device);
+  if (!g.ok()) {
+    delete st;
+    return no_device();
+  }
   hipError_t e = hipMalloc(&st->hid, (size_t)hidden_elems * 4);
   if (e == hipSuccess) e = hipMalloc(&st->pos, 256);
   if (e == hipSuccess) e = hipMemsetAsync(st->hid, 0, (size_t)hidden_elems * 4, rt->stream);
@@ -413,6 +420,7 @@ qm_status qm_decode_layers(qm_runtime* rt, qm_decode_state* st, const qm_decode_
   if (s != QM_OK) return s;
   if ((s = ensure_arena(st, need)) != QM_OK) return s;
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   // Everything the attention calls could fail on is settled before the first
   // launch, so a failed token leaves hidden, the DeltaNet states and the
   // caches as they were (decode_layers encodes the whole token before it
@@ -461,6 +469,10 @@ qm_status qm_decode_graph_create(qm_runtime* rt, qm_decode_state* st, const qm_d
     g->layers.push_back(L);
   }
   DeviceGuard dg(rt->device);
+  if (!dg.ok()) {
+    delete g;
+    return no_device();
+  }
   hipError_t e = hipStreamCreate(&g->cap_stream);
   if (e != hipSuccess) {
     delete g;
@@ -515,6 +527,7 @@ qm_status qm_decode_graph_run(qm_decode_graph* g, const uint32_t position[3]) {
   qm_decode_graph::Variant& v = g->var[pick];
   qm_runtime* rt = g->rt;
   DeviceGuard dg(rt->device);
+  if (!dg.ok()) return no_device();
   qm_status s = prepare_attention(rt, g->layers.data(), (uint32_t)g->layers.size());
   if (s != QM_OK) return s;
   s = hip_check(launch_set_u32x3(g->st->pos, position[0], position[1], position[2], rt->stream),

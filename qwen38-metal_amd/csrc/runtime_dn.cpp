@@ -87,6 +87,10 @@ qm_status alloc_state(qm_runtime* rt, const qm_dn_config& cfg, qm_dn_state** out
   // A one-element history keeps the pointers valid for a kernel-size-one model.
   const size_t hb = (s->hist_elems ? s->hist_elems : 1) * sizeof(float);
   DeviceGuard g(rt->device);
+  if (!g.ok()) {
+    delete s;
+    return no_device();
+  }
   hipError_t e = hipMalloc(&s->hist[0], hb);
   if (e == hipSuccess) e = hipMalloc(&s->hist[1], hb);
   if (e == hipSuccess) e = hipMalloc(&s->rec, s->rec_elems * sizeof(float));
@@ -162,6 +166,7 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
     d.snap_s_stride = snaps->rec_elems;
   }
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   hipError_t e = launch_deltanet(d, rt->stream);
   if (e != hipSuccess) return hip_check(e, "DeltaNet launch");
   if (out_bf16 && !fused_bf16) {
@@ -202,6 +207,10 @@ qm_status qm_dn_weights_create(qm_runtime* rt, const qm_dn_config* cfg, const fl
   w->channels = channels_of(*cfg);
   const size_t nconv = (size_t)w->channels * cfg->conv_kernel_size;
   DeviceGuard g(rt->device);
+  if (!g.ok()) {
+    delete w;
+    return no_device();
+  }
   hipError_t e = hipMalloc(&w->conv_w, nconv * 4);
   if (e == hipSuccess) e = hipMalloc(&w->a_log, cfg->value_heads * 4);
   if (e == hipSuccess) e = hipMalloc(&w->dt_bias, cfg->value_heads * 4);
@@ -247,6 +256,7 @@ qm_status qm_dn_state_clone(const qm_dn_state* src, qm_dn_state** out) {
   qm_status st = alloc_state(src->rt, src->cfg, &s);
   if (st != QM_OK) return st;
   DeviceGuard g(src->rt->device);
+  if (!g.ok()) return no_device();
   hipStream_t stream = src->rt->stream;
   hipError_t e = hipSuccess;
   if (src->hist_elems)
@@ -264,6 +274,7 @@ qm_status qm_dn_state_clone(const qm_dn_state* src, qm_dn_state** out) {
 qm_status qm_dn_state_read(const qm_dn_state* s, float* conv_history, float* recurrent) {
   if (!s) return fail(QM_ERR_NULL_POINTER, "state is NULL");
   DeviceGuard g(s->rt->device);
+  if (!g.ok()) return no_device();
   hipStream_t stream = s->rt->stream;
   hipError_t e = hipSuccess;
   if (conv_history && s->hist_elems)
@@ -277,6 +288,7 @@ qm_status qm_dn_state_read(const qm_dn_state* s, float* conv_history, float* rec
 qm_status qm_dn_state_write(qm_dn_state* s, const float* conv_history, const float* recurrent) {
   if (!s) return fail(QM_ERR_NULL_POINTER, "state is NULL");
   DeviceGuard g(s->rt->device);
+  if (!g.ok()) return no_device();
   hipStream_t stream = s->rt->stream;
   hipError_t e = hipSuccess;
   if (conv_history && s->hist_elems)
@@ -311,6 +323,10 @@ qm_status qm_dn_snapshots_create(qm_runtime* rt, const qm_dn_weights* w, uint32_
   s->hist_stride = s->hist_elems ? s->hist_elems : 1;  // the state's buffer size, so one-row sets can swap
   s->rec_elems = (size_t)w->cfg.value_heads * w->cfg.value_head_dim * w->cfg.key_head_dim;
   DeviceGuard g(rt->device);
+  if (!g.ok()) {
+    delete s;
+    return no_device();
+  }
   hipError_t e = hipMalloc(&s->hist, (size_t)rows * s->hist_stride * sizeof(float));
   if (e == hipSuccess) e = hipMalloc(&s->rec, (size_t)rows * s->rec_elems * sizeof(float));
   if (e == hipSuccess) e = hipMemsetAsync(s->hist, 0, (size_t)rows * s->hist_stride * sizeof(float), rt->stream);
@@ -359,6 +375,7 @@ qm_status qm_dn_snapshot_restore(qm_dn_snapshots* s, uint32_t row, qm_dn_state* 
     return QM_OK;
   }
   DeviceGuard g(s->rt->device);
+  if (!g.ok()) return no_device();
   hipStream_t stream = s->rt->stream;
   hipError_t e = hipSuccess;
   if (s->hist_elems)

@@ -34,6 +34,8 @@ namespace qm {
 
 qm_status fail(qm_status status, const char* fmt, ...);
 qm_status hip_check(hipError_t err, const char* what);
+// QM_ERR_NO_DEVICE for a call on a runtime created without a device.
+qm_status no_device();
 qm_status ensure_scratch(qm_runtime* rt, size_t bytes);
 qm_status ensure_partials(qm_runtime* rt, size_t bytes);
 qm_status ensure_counters(qm_runtime* rt, size_t count);
@@ -69,10 +71,13 @@ uint32_t kv_heads_of(const qm_kv* kv);
 uint32_t kv_head_dim_of(const qm_kv* kv);
 const qm_runtime* kv_runtime_of(const qm_kv* kv);
 
+// Makes `device` current for its scope.  ok() is false for a runtime
+// without a device (QM_DEVICE_NONE), whose calls stop at no_device().
 class DeviceGuard {
  public:
   explicit DeviceGuard(int device);
   ~DeviceGuard();
+  bool ok() const { return dev_ >= 0; }
 
  private:
   int prev_ = 0;

@@ -120,6 +120,7 @@ qm_status kv_grow(qm_kv* kv, uint64_t tokens) {
   if (new_pages > (uint64_t)kMaxSplits * kMaxPagesPerSplit || new_pages * kv_page_bytes(kv) > (1ull << 40))
     return fail(QM_ERR_DIMENSION_OVERFLOW, "Q8 KV token capacity %llu", (unsigned long long)cap_tokens);
   DeviceGuard g(kv->rt->device);
+  if (!g.ok()) return no_device();
   KvBuffers nb;
   qm_status st = alloc_buffers(kv, (uint32_t)new_pages, &nb);
   if (st != QM_OK) return st;
@@ -407,6 +408,10 @@ qm_status qm_kv_create(qm_runtime* rt, uint32_t kv_heads, uint32_t head_dim, uin
   kv->max_tokens = max_tokens;
   // allocate_q8_kv_state(kv_heads, head_dim, 16): one page to start with.
   DeviceGuard g(rt->device);
+  if (!g.ok()) {
+    delete kv;
+    return no_device();
+  }
   if ((st = kv_grow(kv, max_tokens ? std::min<uint32_t>(16, max_tokens) : 16)) == QM_OK) st = hip_check(hipStreamSynchronize(rt->stream), "KV cache allocation");
   if (st != QM_OK) {
     free_kv(kv);
@@ -451,6 +456,7 @@ qm_status qm_kv_reserve(qm_kv* kv, uint32_t additional) {
   if (count == 0) return QM_OK;
   commit_pages(kv, first, count);
   DeviceGuard g(kv->rt->device);
+  if (!g.ok()) return no_device();
   hipError_t e = hipMemcpyAsync(kv->d_pt + first, kv->pages.data() + first, count * sizeof(int32_t),
                                 hipMemcpyHostToDevice, kv->rt->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(kv->rt->stream);
@@ -481,6 +487,7 @@ qm_status qm_kv_clone(const qm_kv* src, qm_kv** out) {
   std::copy(src->pages.begin(), src->pages.end(), kv->pages.begin());
   kv->next_page_id = src->next_page_id;
   DeviceGuard g(src->rt->device);
+  if (!g.ok()) return no_device();
   const size_t n = (size_t)src->next_page_id;
   hipStream_t s = src->rt->stream;
   hipError_t e = hipMemcpyAsync(kv->d_pt, src->d_pt, src->cap_pages * sizeof(int32_t), hipMemcpyDeviceToDevice, s);
@@ -502,6 +509,7 @@ qm_status qm_kv_clone(const qm_kv* src, qm_kv** out) {
 qm_status qm_kv_read(const qm_kv* kv, int8_t* keys, int8_t* values, float* key_scales, float* value_scales) {
   if (!kv) return fail(QM_ERR_NULL_POINTER, "kv is NULL");
   DeviceGuard g(kv->rt->device);
+  if (!g.ok()) return no_device();
   const size_t n = (size_t)kv->next_page_id;
   const uint32_t KVH = kv->kv_heads, D = kv->head_dim, Dp = kv->dp, T = kv->length;
   std::vector<int8_t> hk(n * kv_page_bytes(kv)), hv(n * kv_page_bytes(kv));
@@ -537,6 +545,7 @@ qm_status qm_attn_decode(qm_runtime* rt, qm_kv* const* seqs, uint32_t B, const u
   qm_status st = check_decode_args(rt, seqs, B, q, gate, k, v, H, o);
   if (st != QM_OK) return st;
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   // Growth and workspace first: once a chunk is committed nothing but the
   // launch itself can fail.
   if ((st = attn_decode_prepare(rt, seqs, B, H)) != QM_OK) return st;
@@ -557,6 +566,7 @@ qm_status qm_attn_decode_noalloc(qm_runtime* rt, qm_kv* const* seqs, uint32_t B,
                   "sequence %u: no room for another token without allocating (reserve capacity first)", b);
   }
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   AttnScratch ws{};
   if ((st = hip_check(attn_noalloc_scratch(rt->device, &ws), "attention scratch")) != QM_OK) return st;
   std::vector<DecodeChunk> chunks;
@@ -581,6 +591,7 @@ qm_status qm_attn_prefill(qm_runtime* rt, qm_kv* seq, const uint16_t* q, const u
   const uint64_t end = (uint64_t)seq->length + M;
   if (end > 0xFFFFFFFFull) return fail(QM_ERR_DIMENSION_OVERFLOW, "Q8 KV token capacity");
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   if ((st = kv_grow(seq, end)) != QM_OK) return st;
   const uint32_t start = seq->length;
   AttnSeq sd = seq_desc(seq);
@@ -661,5 +672,7 @@ qm_status qm_attn_prepare(qm_runtime* rt, const qm_rope_config* rope, uint32_t M
   a.has_sections = rope->has_mrope_sections ? 1u : 0u;
   a.theta = rope->rope_theta;
   a.eps = epsilon;
+  DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   return hip_check(launch_attn_prepare(a, rt->stream), "attention prepare launch");
 }

@@ -49,11 +49,9 @@ Q4Job to_job(const qm_q4_job& j, uint16_t* out) {
 
 qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const uint16_t* x, uint32_t K,
                  uint32_t M, const char* what) {
+  // The decode kernel needs no workspace; the GEMM's split-K plans do.
   size_t pbytes = 0, counters = 0;
-  if (M <= kDecodeMaxRows)
-    q4_decode_workspace(jobs, n, swiglu, K, M, &pbytes, &counters);
-  else
-    q4_gemm_workspace(jobs, n, swiglu, K, M, &pbytes, &counters);
+  if (M > kDecodeMaxRows) q4_gemm_workspace(jobs, n, swiglu, K, M, &pbytes, &counters);
   qm_status st = ensure_partials(rt, pbytes);
   if (st == QM_OK) st = ensure_counters(rt, counters);
   if (st == QM_OK && M > kDecodeMaxRows) st = ensure_xh(rt, q4_gemm_xh_bytes(K, M));
@@ -83,6 +81,7 @@ qm_status qm::q4_project_modes(qm_runtime* rt, const qm_q4_job* jobs, void* cons
     q[i].mode = modes[i];
   }
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   return launch(rt, q, n_jobs, false, x, in_elems, M, "Q4 projection launch");
 }
 
@@ -104,6 +103,7 @@ qm_status qm_q4_project(qm_runtime* rt, const qm_q4_job* jobs, int n_jobs, const
     q[i] = to_job(jobs[i], outputs[i]);
   }
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   return launch(rt, q, n_jobs, false, x, in_elems, M, "Q4 projection launch");
 }
 
@@ -119,6 +119,7 @@ qm_status qm_q4_swiglu(qm_runtime* rt, const qm_q4_job* gate, const qm_q4_job* u
   if (!h) return fail(QM_ERR_NULL_POINTER, "h is NULL");
   Q4Job q[2] = {to_job(*gate, h), to_job(*up, nullptr)};
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   return launch(rt, q, 2, true, x, in_elems, M, "Q4 SwiGLU launch");
 }
 
@@ -134,6 +135,7 @@ qm_status qm_q4_mlp(qm_runtime* rt, const qm_q4_job* gate, const qm_q4_job* up, 
   if ((st = validate_job(down, gate->out_rows, "down")) != QM_OK) return st;
   if (!y) return fail(QM_ERR_NULL_POINTER, "y is NULL");
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   const size_t h_bytes = (size_t)M * gate->out_rows * 2;
   if ((st = ensure_scratch(rt, h_bytes)) != QM_OK) return st;
   uint16_t* h = (uint16_t*)rt->scratch;

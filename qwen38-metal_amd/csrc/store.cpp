@@ -368,6 +368,7 @@ qm_status parse_shard_header(const Shard& sh, size_t shard_index, std::map<std::
 qm_status upload_bytes(qm_runtime* rt, const uint8_t* src, uint64_t bytes, void** out) {
   *out = nullptr;
   DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
   void* dev = nullptr;
   hipError_t e = hipMalloc(&dev, bytes ? bytes : 1);
   if (e != hipSuccess) return hip_check(e, "weight upload allocation");
