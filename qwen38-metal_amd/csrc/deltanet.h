@@ -28,6 +28,11 @@ struct DnArgs {
   // workspace / output
   float* conv_out;  // [M][channels]: q^, k^, v after conv + prepare
   float* chunk_ws;  // chunked prefill: per (chunk, value head) dn_chunk_floats() floats
+  // Single-token step over 16-row groups of S: the rows' outputs o [VH][dv]
+  // before the gated norm, and per-head arrival counters [VH] (zero between
+  // launches; the last group of a head to arrive resets its counter).
+  float* step_o;
+  unsigned* step_ctr;
   float* out;       // [M][VH][dv]
   uint16_t* out_bf16;  // single-token step only: the output rounded to bf16 as well (or NULL)
   // optional state images after tokens 0 .. snap_rows - 1 (speculative
@@ -49,6 +54,10 @@ bool dn_use_chunked(const DnArgs& a);
 inline size_t dn_chunk_ws_bytes(uint32_t M, uint32_t value_heads) {
   return (size_t)((M + kDnChunk - 1) / kDnChunk) * value_heads * kDnChunkFloats * sizeof(float);
 }
+
+// Whether a single-token step runs split over 16-row groups of S (then
+// step_o and step_ctr must be set).
+bool dn_step_split(const DnArgs& a);
 
 hipError_t launch_deltanet(const DnArgs& a, hipStream_t st);
 

@@ -411,27 +411,48 @@ __global__ __launch_bounds__(kThreads) void dn_scan_kernel(DnArgs a) {
 // Gated RMS norm of one (token, value head) output row by one wave: reads
 // o_in[c], writes out[c] = o * rsqrt(mean o^2 + eps) * norm * silu(z).
 // Shared by the prefill path and the fused step.
-__device__ __forceinline__ void gate_norm_row(const DnArgs& a, const float* o_in, const float* z, float* out,
-                                              uint32_t lane, uint16_t* out_bf16 = nullptr) {
-  float v[4];  // dv <= 256
+// Core of the gated norm for one row held by a wave (lane: elements lane +
+// 64 i): v the outputs, nrm the norm weights, sz = silu(z).
+__device__ __forceinline__ void gate_norm_core(const DnArgs& a, const float (&v)[4], const float (&nrm)[4],
+                                               const float (&sz)[4], float* out, uint32_t lane, uint16_t* out_bf16) {
   float ss = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t c = lane + 64 * i;
-    v[i] = c < a.dv ? o_in[c] : 0.0f;
-    ss += v[i] * v[i];
-  }
+  for (int i = 0; i < 4; ++i) ss += v[i] * v[i];
   ss = wave_sum(ss);
   const float scale = 1.0f / sqrtf(ss / (float)a.dv + a.eps);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t c = lane + 64 * i;
     if (c < a.dv) {
-      const float r = v[i] * scale * a.norm[c] * silu_f(z[c]);
+      const float r = v[i] * scale * nrm[i] * sz[i];
       out[c] = r;
       if (out_bf16) out_bf16[c] = f32_to_bf16(r);
     }
   }
+}
+// Norm weights and silu(z) of one row (zero past dv).
+__device__ __forceinline__ void gate_norm_operands(const DnArgs& a, const float* z, uint32_t lane, float (&nrm)[4],
+                                                   float (&sz)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t c = lane + 64 * i;
+    nrm[i] = c < a.dv ? a.norm[c] : 0.0f;
+    sz[i] = c < a.dv ? silu_f(z[c]) : 0.0f;
+  }
+}
+// Gated RMS norm of one (token, value head) output row by one wave: reads
+// o_in[c], writes out[c] = o * rsqrt(mean o^2 + eps) * norm * silu(z).
+// Shared by the prefill path and the step kernels.
+__device__ __forceinline__ void gate_norm_row(const DnArgs& a, const float* o_in, const float* z, float* out,
+                                              uint32_t lane, uint16_t* out_bf16 = nullptr) {
+  float v[4], nrm[4], sz[4];  // dv <= 256
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t c = lane + 64 * i;
+    v[i] = c < a.dv ? o_in[c] : 0.0f;
+  }
+  gate_norm_operands(a, z, lane, nrm, sz);
+  gate_norm_core(a, v, nrm, sz, out, lane, out_bf16);
 }
 
 // One wave per (token, value head), blocks of 1 or 4 waves; in place on `out`.
@@ -543,6 +564,124 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_kernel(DnArgs a) {
     float* out = a.out + (size_t)vh * a.dv;
     gate_norm_row(a, o_s, a.z + (size_t)vh * a.dv, out, lane, a.out_bf16 ? a.out_bf16 + (size_t)vh * a.dv : nullptr);
   }
+}
+
+// The decode step split over 16-row groups of S: grid VH * ceil(dv / 16),
+// one workgroup per (value head, row group), so the 4 MiB of S stream from
+// every CU instead of one per head.  Per workgroup:
+//  wave 0: q^, k^ of key head kh (prep_key_head; only group 0 of the first
+//          value head of the key group writes that key head's history);
+//  wave 1: conv of the group's 16 v channels;
+//  thread 128: g and beta;
+// then the 16-lane row groups update the 16 rows (delta_row_token).  The
+// gated norm needs all dv outputs of the head: every group stores its o
+// values (written through to memory) and counts itself in; the last of the
+// head's groups to arrive reads the dv values back and applies
+// gate_norm_row.  Every output is formed by the same device functions as in
+// the fused step and the prefill path, so a step still equals a one-token
+// prefill bit for bit.
+template <int EPT>
+__global__ __launch_bounds__(kStepThreads) void dn_step_split_kernel(DnArgs a) {
+  __shared__ __attribute__((aligned(16))) float qk_s[2][16][EPT];  // [q | k][lane][e]
+  __shared__ float v_s[kStepRows];
+  __shared__ float gb_s[2];
+  __shared__ unsigned last_s;
+  const uint32_t groups = (a.dv + kStepRows - 1) / kStepRows;
+  const uint32_t vh = blockIdx.x / groups, rg = blockIdx.x % groups;
+  const uint32_t row0 = rg * kStepRows;
+  const uint32_t group = a.value_heads / a.key_heads;
+  const uint32_t kh = vh / group;
+  const uint32_t key_el = a.key_heads * a.dk;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const bool key_hist = rg == 0 && vh % group == 0 && a.kernel > 1;
+
+  const int r = threadIdx.x / 16, l = threadIdx.x % 16;
+  const uint32_t row = row0 + r;
+  const size_t srow = ((size_t)vh * a.dv + row) * a.dk;
+  float s[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const uint32_t j = l + 16 * e;
+    s[e] = row < a.dv && j < a.dk ? a.s_in[srow + j] : 0.0f;
+  }
+
+  // Wave 0 of every group loads the gated norm's operands early: the group
+  // that arrives last needs them right away.
+  float nrm[4], sz[4];
+  if (wave == 0) {
+    gate_norm_operands(a, a.z + (size_t)vh * a.dv, lane, nrm, sz);
+    float cq[4], ck[4];
+    prep_key_head(a, 0, kh, lane, cq, ck, key_hist ? a.hist_out : nullptr);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = lane + 64 * i;
+      if (c < 16 * EPT) {
+        qk_s[0][c % 16][c / 16] = c < a.dk ? cq[i] : 0.0f;
+        qk_s[1][c % 16][c / 16] = c < a.dk ? ck[i] : 0.0f;
+      }
+    }
+  } else if (wave == 1) {
+    if (lane < kStepRows) {
+      const uint32_t c = row0 + lane;
+      const uint32_t ch = 2 * key_el + vh * a.dv + min(c, a.dv - 1);
+      float vv = 0.0f;
+      if (a.kernel <= kTaps) {
+        ConvIn cv;
+        conv_load(a, ch, 0, cv);
+        vv = conv_finish(a, cv);
+        if (c < a.dv && a.kernel > 1) conv_store_history(a, ch, cv, a.hist_out);
+      } else {
+        vv = conv_silu(a, ch, 0, c < a.dv && a.kernel > 1 ? a.hist_out : nullptr);
+      }
+      v_s[lane] = c < a.dv ? vv : 0.0f;
+    }
+  } else if (threadIdx.x == 128) {
+    const float neg_a = -expf(a.a_log[vh]);
+    gb_s[0] = expf(neg_a * softplus_f(a.a[vh] + a.dt_bias[vh]));
+    gb_s[1] = sigmoid_f(a.b[vh]);
+  }
+  __syncthreads();
+
+  float kk[EPT], qq[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    kk[e] = qk_s[1][l][e];
+    qq[e] = qk_s[0][l][e];
+  }
+  const float o = delta_row_token<EPT>(s, kk, qq, gb_s[0], gb_s[1], v_s[r]);
+  if (row < a.dv) {
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const uint32_t j = l + 16 * e;
+      if (j < a.dk) a.s_out[srow + j] = s[e];
+    }
+  }
+  // Publish this group's outputs, written through to memory (the head's
+  // groups run on different XCDs, whose L2s are not coherent), and count in.
+  constexpr int kSys = 0x11;  // sc0 sc1
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      a.step_o + (size_t)vh * a.dv, (short)0, (int)(a.dv * 4), 0x00020000);
+  if (l == 0 && row < a.dv) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o), ro, row * 4, 0, kSys);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stores are complete
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(a.step_ctr + vh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = prev == groups - 1;
+    if (last) __hip_atomic_store(a.step_ctr + vh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_s = last ? 1u : 0u;
+  }
+  __syncthreads();
+  if (last_s == 0u || wave != 0) return;
+  // The head's dv outputs (lane c: c + 64 i), then the shared gated norm.
+  float ov[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t c = lane + 64 * i;
+    const float v = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ro, min(c, a.dv - 1) * 4, 0, kSys));
+    ov[i] = c < a.dv ? v : 0.0f;
+  }
+  gate_norm_core(a, ov, nrm, sz, a.out + (size_t)vh * a.dv, lane,
+                 a.out_bf16 ? a.out_bf16 + (size_t)vh * a.dv : nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -1026,6 +1165,12 @@ void launch_scan(const DnArgs& a, hipStream_t st) {
 
 }  // namespace
 
+bool dn_step_split(const DnArgs& a) {
+  if (a.M != 1 || a.dk > 128 || a.dv > 256) return false;
+  const char* env = getenv("QM38_DN_STEP_SPLIT");
+  return env ? atoi(env) != 0 : true;
+}
+
 bool dn_use_chunked(const DnArgs& a) {
   if (a.dk != kCD || a.dv != kCD || a.snap_rows > 0 || a.M <= 1 || a.value_heads % a.key_heads != 0) return false;
   const char* env = getenv("QM38_DN_CHUNKED");
@@ -1036,6 +1181,15 @@ bool dn_use_chunked(const DnArgs& a) {
 hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
   if (a.dk == 0 || a.dk > 256 || a.dv == 0 || a.dv > 256 || a.M == 0) return hipErrorInvalidValue;
   // One token with S rows that fit the fused kernel's registers: one launch.
+  if (dn_step_split(a)) {
+    if (!a.step_o || !a.step_ctr) return hipErrorInvalidValue;
+    const dim3 grid(a.value_heads * ((a.dv + kStepRows - 1) / kStepRows)), block(kStepThreads);
+    if (a.dk <= 64)
+      hipLaunchKernelGGL(dn_step_split_kernel<4>, grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL(dn_step_split_kernel<8>, grid, block, 0, st, a);
+    return hipGetLastError();
+  }
   if (a.M == 1 && a.dk <= 128 && a.dv <= 128) {
     const dim3 grid(a.value_heads), block(kStepThreads);
     const uint32_t ept = (a.dk + 15) / 16, passes = (a.dv + kStepRows - 1) / kStepRows;

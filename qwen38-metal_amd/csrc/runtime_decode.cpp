@@ -480,15 +480,18 @@ qm_status qm_decode_graph_create(qm_runtime* rt, qm_decode_state* st, const qm_d
   }
   g->cap.stream = g->cap_stream;
   // Size the captured calls' workspace beforehand (no allocation may happen
-  // while capturing): the DeltaNet step's conv buffer is its only one.
-  size_t conv_bytes = 4;
+  // while capturing): the DeltaNet step's conv buffer, output exchange and
+  // arrival counters are its only ones.
+  size_t step_bytes = 4;
+  uint32_t step_ctrs = 1;
   for (const qm_decode_layer& L : g->layers)
     if (L.linear) {
       const qm_dn_config& c = dn_weights_config(L.linear->dn_weights);
-      conv_bytes = std::max<size_t>(conv_bytes, (2ull * c.key_heads * c.key_head_dim +
-                                                  (size_t)c.value_heads * c.value_head_dim) * 4);
+      step_bytes = std::max(step_bytes, dn_step_scratch_bytes(c));
+      step_ctrs = std::max(step_ctrs, c.value_heads);
     }
-  s = ensure_scratch(&g->cap, conv_bytes);
+  s = ensure_scratch(&g->cap, step_bytes);
+  if (s == QM_OK) s = ensure_counters(&g->cap, step_ctrs);
   // Two variants, one per history parity; capturing flips the states'
   // parity exactly as running would, so the second capture starts from the
   // first one's end and ends where the first began.

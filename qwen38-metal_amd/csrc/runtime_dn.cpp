@@ -149,10 +149,14 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
   d.s_out = to->rec;
   if (snaps && M > 1) d.snap_rows = M - 1;  // decides the path below
   const size_t chunk_bytes = dn_use_chunked(d) ? dn_chunk_ws_bytes(M, c.value_heads) : 0;
-  qm_status st = ensure_scratch(rt, conv_bytes + chunk_bytes);
+  const size_t step_bytes = dn_step_split(d) ? ((size_t)c.value_heads * c.value_head_dim * 4 + 255) & ~size_t(255) : 0;
+  qm_status st = ensure_scratch(rt, conv_bytes + chunk_bytes + step_bytes);
+  if (st == QM_OK && step_bytes) st = ensure_counters(rt, c.value_heads);
   if (st != QM_OK) return st;
   d.conv_out = (float*)rt->scratch;
   d.chunk_ws = chunk_bytes ? (float*)((char*)rt->scratch + conv_bytes) : nullptr;
+  d.step_o = step_bytes ? (float*)((char*)rt->scratch + conv_bytes + chunk_bytes) : nullptr;
+  d.step_ctr = step_bytes ? rt->counters : nullptr;
   d.out = out;
   // The fused single-token kernel also writes the bf16 copy; other paths
   // convert afterwards.
@@ -178,6 +182,11 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
 }
 
 }  // namespace
+
+size_t qm::dn_step_scratch_bytes(const qm_dn_config& c) {
+  const size_t channels = 2ull * c.key_heads * c.key_head_dim + (size_t)c.value_heads * c.value_head_dim;
+  return ((channels * 4 + 255) & ~size_t(255)) + (((size_t)c.value_heads * c.value_head_dim * 4 + 255) & ~size_t(255));
+}
 
 qm_status qm::dn_step_bf16(qm_runtime* rt, const qm_dn_weights* w, qm_dn_state* st, const float* qkv, const float* z,
                            const float* b, const float* a, float eps, float* out, uint16_t* out_bf16) {

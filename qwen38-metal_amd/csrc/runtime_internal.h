@@ -48,6 +48,8 @@ qm_status q4_project_modes(qm_runtime* rt, const qm_q4_job* jobs, void* const* o
 // qm_dn_step that also writes the output rounded to bf16 into out_bf16.
 qm_status dn_step_bf16(qm_runtime* rt, const qm_dn_weights* w, qm_dn_state* st, const float* qkv, const float* z,
                        const float* b, const float* a, float eps, float* out, uint16_t* out_bf16);
+// Scratch bytes a single-token qm_dn_step needs (its counters: value_heads).
+size_t dn_step_scratch_bytes(const qm_dn_config& c);
 // Frees a runtime's grow-only buffers (not the runtime itself).
 void release_buffers(qm_runtime* rt);
 
