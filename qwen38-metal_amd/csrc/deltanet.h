@@ -47,9 +47,10 @@ struct DnArgs {
 // Chunked prefill (WY / UT form over chunks of kDnChunk tokens): used for
 // long prefills without state images at head dims 128 / 128 (or when
 // QM38_DN_CHUNKED forces it on or off).  Its workspace per (chunk, value
-// head): W [64][128], U~ [64][128], P [64][64], G [64].
+// head): W [64][128], U~ [64][128], P [64][64], G [64] and the decayed keys
+// transposed, K~^T [128][64] (K~^T[c][i] = e^{G_63 - G_i} k^[i][c]).
 constexpr uint32_t kDnChunk = 64;
-constexpr size_t kDnChunkFloats = 64 * 128 * 2 + 64 * 64 + 64;
+constexpr size_t kDnChunkFloats = 64 * 128 * 2 + 64 * 64 + 64 + 128 * 64;
 bool dn_use_chunked(const DnArgs& a);
 inline size_t dn_chunk_ws_bytes(uint32_t M, uint32_t value_heads) {
   return (size_t)((M + kDnChunk - 1) / kDnChunk) * value_heads * kDnChunkFloats * sizeof(float);

@@ -149,21 +149,27 @@ __device__ __forceinline__ float row_sum(float v) {
 // q^ and k^ of key head kh at token t, computed by one wave: lane holds
 // channels c = lane + 64 i (i < 4; dk <= 256).  Shared by the prefill path
 // and the fused step so both round identically.
+// NQ: channel slots per lane that can be live (ceil(dk / 64)); the others
+// stay zero, as they would with all four slots (their squares add nothing).
+template <int NQ = 4>
 __device__ __forceinline__ void prep_key_head(const DnArgs& a, uint32_t t, uint32_t kh, uint32_t lane, float (&qo)[4],
                                               float (&ko)[4], float* hist_dst) {
+  static_assert(NQ >= 1 && NQ <= 4, "slots");
   const uint32_t key_el = a.key_heads * a.dk;
   float qs = 0.0f, ks = 0.0f;
+#pragma unroll
+  for (int i = NQ; i < 4; ++i) qo[i] = ko[i] = 0.0f;
   if (a.kernel <= kTaps) {
     // All operands of the lane's (up to 8) outputs in flight at once.
     ConvIn cq[4], ck[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NQ; ++i) {
       const uint32_t c = min(lane + 64 * i, a.dk - 1);
       conv_load(a, kh * a.dk + c, (int)t, cq[i]);
       conv_load(a, key_el + kh * a.dk + c, (int)t, ck[i]);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NQ; ++i) {
       const uint32_t c = lane + 64 * i;
       const bool ok = c < a.dk;
       qo[i] = ok ? conv_finish(a, cq[i]) : 0.0f;
@@ -175,7 +181,7 @@ __device__ __forceinline__ void prep_key_head(const DnArgs& a, uint32_t t, uint3
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NQ; ++i) {
       const uint32_t c = lane + 64 * i;
       const bool ok = c < a.dk;
       qo[i] = ok ? conv_silu_loop(a, kh * a.dk + c, (int)t) : 0.0f;
@@ -187,7 +193,7 @@ __device__ __forceinline__ void prep_key_head(const DnArgs& a, uint32_t t, uint3
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NQ; ++i) {
     qs = fmaf(qo[i], qo[i], qs);
     ks = fmaf(ko[i], ko[i], ks);
   }
@@ -197,7 +203,7 @@ __device__ __forceinline__ void prep_key_head(const DnArgs& a, uint32_t t, uint3
   const float qscale = 1.0f / sqrtf(qs / (float)a.dk + a.eps);
   const float kscale = 1.0f / sqrtf(ks / (float)a.dk + a.eps);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NQ; ++i) {
     qo[i] = qo[i] * qscale * inv * inv;
     ko[i] = ko[i] * kscale * inv;
   }
@@ -456,11 +462,38 @@ __device__ __forceinline__ void gate_norm_row(const DnArgs& a, const float* o_in
 }
 
 // One wave per (token, value head), blocks of 1 or 4 waves; in place on `out`.
+// kNormRows (token, head) rows per wave, all of their loads issued before
+// the first row is normalised; the per-row arithmetic is gate_norm_core's.
+constexpr int kNormRows = 4;
 __global__ __launch_bounds__(kThreads) void dn_gate_norm_kernel(DnArgs a) {
-  const uint32_t item = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (item >= a.M * a.value_heads) return;
-  float* o = a.out + (size_t)item * a.dv;
-  gate_norm_row(a, o, a.z + (size_t)item * a.dv, o, threadIdx.x & 63);
+  const uint32_t items = a.M * a.value_heads;
+  const uint32_t first = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * kNormRows;
+  if (first >= items) return;
+  const uint32_t lane = threadIdx.x & 63;
+  float v[kNormRows][4], sz[kNormRows][4], nrm[4];
+#pragma unroll
+  for (int r = 0; r < kNormRows; ++r) {
+    const size_t base = (size_t)min(first + r, items - 1) * a.dv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = lane + 64 * i;
+      v[r][i] = c < a.dv ? a.out[base + c] : 0.0f;
+      sz[r][i] = c < a.dv ? a.z[base + c] : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t c = lane + 64 * i;
+    nrm[i] = c < a.dv ? a.norm[c] : 0.0f;
+  }
+#pragma unroll
+  for (int r = 0; r < kNormRows; ++r) {
+    if (first + r >= items) break;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sz[r][i] = silu_f(sz[r][i]);  // gate_norm_operands
+    float* o = a.out + (size_t)(first + r) * a.dv;
+    gate_norm_core(a, v[r], nrm, sz[r], o, lane, nullptr);
+  }
 }
 
 // The whole decode step (M = 1) in one launch: block = value head vh.
@@ -503,7 +536,7 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_kernel(DnArgs a) {
 
   if (wave == 0) {
     float cq[4], ck[4];
-    prep_key_head(a, 0, kh, lane, cq, ck, key_hist ? a.hist_out : nullptr);
+    prep_key_head<EPT / 4>(a, 0, kh, lane, cq, ck, key_hist ? a.hist_out : nullptr);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t c = lane + 64 * i;
@@ -611,7 +644,7 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_split_kernel(DnArgs a) {
   if (wave == 0) {
     gate_norm_operands(a, a.z + (size_t)vh * a.dv, lane, nrm, sz);
     float cq[4], ck[4];
-    prep_key_head(a, 0, kh, lane, cq, ck, key_hist ? a.hist_out : nullptr);
+    prep_key_head<EPT / 4>(a, 0, kh, lane, cq, ck, key_hist ? a.hist_out : nullptr);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t c = lane + 64 * i;
@@ -694,7 +727,7 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_split_kernel(DnArgs a) {
 // prep_key_head's, operation for operation, so the outputs equal the
 // per-token kernel's bit for bit.  NS = channel slots per lane and class
 // (ceil(head dim / 64)); kernels of up to kTaps taps.
-constexpr int kConvTile = 16;
+constexpr int kConvTile = 32;
 template <int NS>
 __global__ __launch_bounds__(kThreads) void dn_conv_tiled_kernel(DnArgs a) {
   constexpr int S2 = 2 * NS;  // q slots 0..NS-1, k slots NS..2NS-1 (value units use the first NS)
@@ -735,8 +768,9 @@ __global__ __launch_bounds__(kThreads) void dn_conv_tiled_kernel(DnArgs a) {
     }
   }
   const float inv = 1.0f / sqrtf((float)a.dk);
-  for (int tb = t0; tb < t1; tb += 4) {
-    float xs[4][S2];
+  // Inputs of four tokens per batch; the next batch's loads are issued
+  // before the current batch is computed.
+  auto load_batch = [&](int tb, float (&xs)[4][S2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < 4; ++k)
 #pragma unroll
@@ -744,6 +778,16 @@ __global__ __launch_bounds__(kThreads) void dn_conv_tiled_kernel(DnArgs a) {
         const int t = min(tb + k, t1 - 1);
         xs[k][s] = s < ns ? a.qkv[(size_t)t * a.channels + ch[s]] : 0.0f;
       }
+  };
+  float xn[4][S2];
+  load_batch(t0, xn);
+  for (int tb = t0; tb < t1; tb += 4) {
+    float xs[4][S2];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int s = 0; s < S2; ++s) xs[k][s] = xn[k][s];
+    load_batch(tb + 4, xn);  // clamped to the tile: past its end a harmless reload
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int t = tb + k;
@@ -831,31 +875,47 @@ constexpr int kCD = 128;        // head dims of the chunked path
 constexpr int kCStride = 132;   // LDS row stride (floats) of [64][128] tiles: conflict-free 16-byte reads
 constexpr int kAStride = 68;    // LDS row stride of the 64 x 64 triangular matrix
 
+// LDS of dn_chunk_prep_kernel (dynamic, so the compiler's register budget
+// follows the VGPR occupancy target rather than the LDS-bound one): k^ and
+// q^ rows of the chunk, then G and beta.  Once the products are formed the
+// q^ rows' space holds the 64 x 64 triangular matrix A.
+constexpr uint32_t kPrepLds = (2 * 64 * kCStride + 3 * 64) * 4;
 __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
-  __shared__ __attribute__((aligned(16))) float ks_s[64 * kCStride];
-  __shared__ __attribute__((aligned(16))) float a_s[64 * kAStride];
-  __shared__ float g_s[64], beta_s[64];
+  extern __shared__ __attribute__((aligned(16))) float prep_lds[];
+  float* ks_s = prep_lds;
+  float* qs_s = prep_lds + 64 * kCStride;
+  float* g_s = prep_lds + 2 * 64 * kCStride;
+  float* beta_s = g_s + 64;
+  float* dk_s = g_s + 128;  // e^{G_63 - G_i}
+  float* a_s = qs_s;  // [64][kAStride], once the q^ rows are consumed
   const uint32_t VH = a.value_heads;
   const uint32_t h = blockIdx.x % VH, c = blockIdx.x / VH;
   const uint32_t kh = h / (VH / a.key_heads);
   const uint32_t key_el = a.key_heads * kCD;
   const uint32_t t0 = c * kDnChunk;
   const uint32_t nt = min(kDnChunk, a.M - t0);
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   float* ws = a.chunk_ws + ((size_t)c * VH + h) * kDnChunkFloats;
   float* Wg = ws;
   float* Ug = ws + 64 * kCD;
   float* Pg = Ug + 64 * kCD;
   float* Gg = Pg + 64 * 64;
+  float* KTg = Gg + 64;
 
-  // k^ rows of the chunk (zero past the last token) into LDS.
+  // q^ and k^ rows of the chunk (zero past the last token) into LDS.
 #pragma unroll
   for (int p = 0; p < 8; ++p) {
     const uint32_t idx = tid + 256 * p;  // float4 index over [64][32]
     const uint32_t t = idx / 32, j4 = idx % 32;
-    f32x4 kv = {0.f, 0.f, 0.f, 0.f};
-    if (t < nt) kv = *(const f32x4*)(a.conv_out + (size_t)(t0 + t) * a.channels + key_el + kh * kCD + 4 * j4);
+    f32x4 kv = {0.f, 0.f, 0.f, 0.f}, qv = {0.f, 0.f, 0.f, 0.f};
+    if (t < nt) {
+      const float* row = a.conv_out + (size_t)(t0 + t) * a.channels + kh * kCD + 4 * j4;
+      qv = *(const f32x4*)row;
+      kv = *(const f32x4*)(row + key_el);
+    }
     *(f32x4*)(ks_s + t * kCStride + 4 * j4) = kv;
+    *(f32x4*)(qs_s + t * kCStride + 4 * j4) = qv;
   }
   // Log decays, their running sum and beta (wave 0; padding tokens: lg = 0,
   // beta = 0, so they change nothing).
@@ -874,47 +934,68 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
     }
     g_s[lane] = G;
     beta_s[lane] = beta;
+    dk_s[lane] = expf(__shfl(G, 63) - G);
     Gg[lane] = G;
   }
   __syncthreads();
 
-  // K K^T and Q K^T on the lower-triangular 16 x 16 tiles (tn <= tm): 20
-  // tiles, 5 per wave.  The MFMA reduction index is permuted (lane group g of
-  // step (m, e) carries k = 16 m + 4 g + e), so every operand is one 16-byte
-  // read per lane and step group (q^ rows straight from memory).
-  const uint32_t j = lane & 15, grp = lane >> 4;
-  for (int tix = wave; tix < 20; tix += 4) {
-    const bool is_q = tix >= 10;
-    int rem = is_q ? tix - 10 : tix, tm = 0;
-    while (rem > tm) rem -= ++tm;
-    const int tn = rem;  // tile (tm, tn), tn <= tm
-    const uint32_t ta = 16 * tm + j;
-    const float* qa = a.conv_out + (size_t)(t0 + (ta < nt ? ta : 0)) * a.channels + kh * kCD + 4 * grp;
-    const float* xa = ks_s + ta * kCStride + 4 * grp;
-    const float* xb = ks_s + (16 * tn + j) * kCStride + 4 * grp;
-    f32x4 av[8];
+  // K~^T[c][i] = e^{G_63 - G_i} k^[i][c]: the scan's operand for the state
+  // update, written once here (16-byte stores of four consecutive tokens).
 #pragma unroll
-    for (int m = 0; m < 8; ++m)
-      av[m] = is_q ? (ta < nt ? *(const f32x4*)(qa + 16 * m) : f32x4{0.f, 0.f, 0.f, 0.f}) : *(const f32x4*)(xa + 16 * m);
+  for (int p = 0; p < 8; ++p) {
+    const uint32_t idx = tid + 256 * p;  // over [128 columns][16 token quads]
+    const uint32_t col = idx / 16, i4 = idx % 16;
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = dk_s[4 * i4 + e] * ks_s[(4 * i4 + e) * kCStride + col];
+    *(f32x4*)(KTg + col * 64 + 4 * i4) = v;
+  }
+
+  // Q K^T, then K K^T, on the lower-triangular 16 x 16 tiles (tn <= tm):
+  // 10 tiles each, spread over the waves.  Q K^T goes straight to P; once
+  // every wave is past it the q^ rows' space takes A from K K^T.  The MFMA
+  // reduction index is permuted (lane group g of step (m, e) carries
+  // k = 16 m + 4 g + e), so every operand is one 16-byte LDS read.
+  const uint32_t j = lane & 15, grp = lane >> 4;
+  auto tile = [&](const float* xs, int tix, floatx4& acc, int& tm, int& tn) __attribute__((always_inline)) {
+    int rem = tix;
+    tm = 0;
+    while (rem > tm) rem -= ++tm;
+    tn = rem;
+    const float* xa = xs + (16 * tm + j) * kCStride + 4 * grp;
+    const float* xb = ks_s + (16 * tn + j) * kCStride + 4 * grp;
     floatx4 ac[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
+      const f32x4 av = *(const f32x4*)(xa + 16 * m);
       const f32x4 bv = *(const f32x4*)(xb + 16 * m);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ac[e] = mfma_f32_4(av[m][e], bv[e], ac[e]);
+      for (int e = 0; e < 4; ++e) ac[e] = mfma_f32_4(av[e], bv[e], ac[e]);
     }
-    const floatx4 acc = (ac[0] + ac[1]) + (ac[2] + ac[3]);
+    acc = (ac[0] + ac[1]) + (ac[2] + ac[3]);
+  };
+  for (int tix = (int)wave; tix < 10; tix += 4) {
+    floatx4 acc;
+    int tm, tn;
+    tile(qs_s, tix, acc, tm, tn);
     // acc[r]: row t = 16 tm + 4 grp + r, column i = 16 tn + j.
     const uint32_t i = 16 * tn + j;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t t = 16 * tm + 4 * grp + r;
-      const float dec = expf(g_s[t] - g_s[i]);
-      if (is_q) {
-        Pg[t * 64 + i] = i <= t ? dec * acc[r] : 0.0f;
-      } else {
-        a_s[t * kAStride + i] = i < t ? beta_s[t] * dec * acc[r] : 0.0f;
-      }
+      Pg[t * 64 + i] = i <= t ? expf(g_s[t] - g_s[i]) * acc[r] : 0.0f;
+    }
+  }
+  __syncthreads();  // the q^ rows are consumed; their space becomes A
+  for (int tix = 3 - (int)wave; tix < 10; tix += 4) {
+    floatx4 acc;
+    int tm, tn;
+    tile(ks_s, tix, acc, tm, tn);
+    const uint32_t i = 16 * tn + j;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t t = 16 * tm + 4 * grp + r;
+      a_s[t * kAStride + i] = i < t ? beta_s[t] * expf(g_s[t] - g_s[i]) * acc[r] : 0.0f;
     }
   }
   // P is zero above the diagonal blocks too, so its readers need no bounds.
@@ -959,52 +1040,42 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
 
 // grid: VH * 8 blocks (block = rg * VH + h: the 8 row groups of a head share
 // blockIdx mod 8, i.e. one XCD and its L2, where they read the same chunk
-// operands), 256 threads.  Every wave keeps the group's 16 rows of S in
-// registers (MFMA A layout).  Per chunk, wave w owns tokens 16 w .. 16 w + 15:
-//   U_w^T = U~_w^T - S W_w^T                      (its 16 tokens)
-//   O_w^T = S (Gamma Q_w)^T + sum_{i <= t} U^T P   (after the exchange)
-//   D_w   = U_w^T diag(e^{G_C - G_i}) K_w          (its share of the S update)
-// then one barrier: U^T and the four shares D_w meet in LDS (two buffers,
-// alternating by chunk, so the next chunk never overwrites what a slower wave
-// still reads), and every wave forms S <- Gamma_C S + sum_w D_w itself.  The
+// operands), 256 threads.  The group's 16 rows of S live in LDS.  Per chunk,
+// wave w owns tokens 16 w .. 16 w + 15 and columns 32 w .. 32 w + 31:
+//   U_w^T = U~_w^T - S W_w^T                 (its 16 tokens, from S in LDS)
+//   O_w^T = Gamma S Q_w^T + sum_{i <= t} U^T P  (after U^T is exchanged)
+//   S[:, cols_w] <- Gamma_C S[:, cols_w] + U^T K~[:, cols_w]   (all 64 tokens)
+// with one barrier after the U^T exchange and one after the S update.  The
 // next chunk's operands are loaded into registers while the current chunk
 // is computed (each register set is refilled right after its last use).
 __global__ __launch_bounds__(256) void dn_chunk_scan_kernel(DnArgs a) {
-  __shared__ __attribute__((aligned(16))) float u_s[2][16 * kAStride];      // U^T [row][token]
-  __shared__ __attribute__((aligned(16))) float d_s[2][4][16 * kCStride];   // D_w [row][col]
-  __shared__ __attribute__((aligned(16))) float k_s[4][16 * kCStride];      // each wave's 16 k^ rows
+  __shared__ __attribute__((aligned(16))) float u_s[16 * kAStride];  // U^T [row][token]
+  __shared__ __attribute__((aligned(16))) float s_s[16 * kCStride];  // S [row][col]
   const uint32_t VH = a.value_heads;
   const uint32_t h = blockIdx.x % VH, rg = blockIdx.x / VH;
   const uint32_t kh = h / (VH / a.key_heads);
-  const uint32_t key_el = a.key_heads * kCD;
   const uint32_t row0 = rg * 16;
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t j = lane & 15, grp = lane >> 4;
   const uint32_t nchunks = (a.M + kDnChunk - 1) / kDnChunk;
-  const uint32_t tok = 16 * wave + j;        // this lane's token column in U and O
-  const uint32_t ktok = 16 * wave + 4 * grp;  // first of the 4 tokens this lane carries in D_w
+  const uint32_t tok = 16 * wave + j;  // this lane's token column in U and O
+  const uint32_t col_w = 32 * wave;    // first of the wave's S columns
 
-  f32x4 Wv[8], qv[8], Uv, Pv[4];
+  f32x4 Wv[8], qv[8], Uv, Pv[4], Kv[2][4];
   bool q_ok;  // this lane's token exists in the loaded chunk
-  f32x4 kr[8];     // the wave's 16 k^ rows as loaded: row 16 w + 2 p + grp / 2, float4 (grp % 2) * 16 + j
-  uint32_t k_rows;  // tokens in the chunk kr was loaded for
-  float G_tok, G_last, Gk[4];
+  float G_tok, G_last;
   auto ws_of = [&](uint32_t c) { return a.chunk_ws + ((size_t)c * VH + h) * kDnChunkFloats; };
   // Rows past the last token read a valid row and are weighted by zero.
-  // Issue order follows first use in the next chunk: the decays, then W, q
-  // and U~ (first phase), then k^ and P (after the exchange), so the waits
-  // at the top of a chunk leave the later loads in flight.
+  // Masks are applied where the values are used, so the loads stay in
+  // flight.  The MFMA reduction index is permuted: lane group grp of step
+  // (m, e) carries k = 16 m + 4 grp + e, so each operand is one 16-byte read.
   auto load_wqu = [&](uint32_t c) __attribute__((always_inline)) {
     const float* ws = ws_of(c);
     const uint32_t t0 = c * kDnChunk, nt = min(kDnChunk, a.M - t0);
     const float* Gg = ws + 2 * 64 * kCD + 64 * 64;
     G_tok = Gg[tok];
     G_last = Gg[63];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) Gk[e] = Gg[ktok + e];
-    // (Masks are applied where the values are used, not here, so that the
-    // loads stay in flight.)
     const float* qrow = a.conv_out + (size_t)(t0 + (tok < nt ? tok : 0)) * a.channels + kh * kCD;
     q_ok = tok < nt;
 #pragma unroll
@@ -1014,106 +1085,78 @@ __global__ __launch_bounds__(256) void dn_chunk_scan_kernel(DnArgs a) {
     }
     Uv = *(const f32x4*)(ws + 64 * kCD + tok * kCD + row0 + 4 * grp);
   };
-  // The wave's 16 k^ rows, 16-byte loads (lane: row 16 w + 2 p + grp / 2,
-  // float4 column (grp % 2) * 16 + j); they reach the MFMA operand layout
-  // through the wave's own LDS rows.
-  auto load_k = [&](uint32_t c) __attribute__((always_inline)) {
-    const uint32_t t0 = c * kDnChunk, nt = min(kDnChunk, a.M - t0);
+  // P[tok][i] and K~^T[col][i] in the B layout (i = 16 m + 4 grp + e).
+  auto load_pk = [&](uint32_t c) __attribute__((always_inline)) {
+    const float* ws = ws_of(c);
+    const float* Pg = ws + 2 * 64 * kCD;
+    const float* KTg = Pg + 64 * 64 + 64;
 #pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      const uint32_t t = 16 * wave + 2 * p + grp / 2;
-      const float* krow = a.conv_out + (size_t)(t0 + (t < nt ? t : 0)) * a.channels + key_el + kh * kCD;
-      kr[p] = *(const f32x4*)(krow + 4 * ((grp % 2) * 16 + j));
+    for (int m = 0; m < 4; ++m) {
+      Pv[m] = *(const f32x4*)(Pg + tok * 64 + 16 * m + 4 * grp);
+#pragma unroll
+      for (int n = 0; n < 2; ++n) Kv[n][m] = *(const f32x4*)(KTg + (col_w + 16 * n + j) * 64 + 16 * m + 4 * grp);
     }
-    k_rows = nt;
-  };
-  auto load_p = [&](uint32_t c) __attribute__((always_inline)) {
-    const float* Pg = ws_of(c) + 2 * 64 * kCD;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) Pv[m] = *(const f32x4*)(Pg + tok * 64 + 16 * m + 4 * grp);
   };
 
-  // Initial rows of S in A layout: sa[m][e] = S[row0 + j][16 m + 4 grp + e].
-  f32x4 sa[8];
+  // Initial rows of S into LDS.
   {
-    const float* sin = a.s_in + ((size_t)h * kCD + row0 + j) * kCD + 4 * grp;
+    const float* sin = a.s_in + ((size_t)h * kCD + row0) * kCD;
 #pragma unroll
-    for (int m = 0; m < 8; ++m) sa[m] = *(const f32x4*)(sin + 16 * m);
+    for (int p = 0; p < 2; ++p) {
+      const uint32_t idx = tid + 256 * p;  // float4 index over [16][32]
+      const uint32_t r = idx / 32, c4 = idx % 32;
+      *(f32x4*)(s_s + r * kCStride + 4 * c4) = *(const f32x4*)(sin + r * kCD + 4 * c4);
+    }
   }
+  load_wqu(0);
+  load_pk(0);
+  __syncthreads();
 
-  // First half of chunk c: U^T (exchanged through u_s), O^T's S Q^T term,
-  // the wave's share D_w of the S update (to d_s).  The next chunk's W, q,
-  // U~, decays and k^ rows are loaded once this chunk's are consumed.
-  auto head = [&](uint32_t c, floatx4& acc_o) __attribute__((always_inline)) {
-    const uint32_t pb = c & 1;
+  floatx4 d[2];  // the wave's columns of S in the MFMA output layout (rows 4 grp + r, column col_w + 16 n + j)
+  for (uint32_t c = 0; c < nchunks; ++c) {
+    const uint32_t t0 = c * kDnChunk, nt = min(kDnChunk, a.M - t0);
     const uint32_t cn = min(c + 1, nchunks - 1);  // the last chunk reloads itself (unused)
-    const float gam = q_ok ? expf(G_tok) : 0.0f, gam_l = G_last;
-    float dk4[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) dk4[e] = expf(gam_l - Gk[e]);
     // (a) U^T[row][tok] = U~[tok][row] - sum_k S[row][k] W[tok][k]
-    // (b1) O^T[row][tok] = sum_k S[row][k] Gamma_tok q[tok][k]
-    // The MFMA reduction index is permuted: lane group grp of step (m, e)
-    // carries k = 16 m + 4 grp + e, so each operand is one 16-byte read.
+    // (b1) O^T[row][tok] = Gamma_tok sum_k S[row][k] q[tok][k]
     floatx4 au[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     floatx4 ao[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int m = 0; m < 8; ++m)
+    for (int m = 0; m < 8; ++m) {
+      const f32x4 sa = *(const f32x4*)(s_s + j * kCStride + 16 * m + 4 * grp);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        au[m & 1] = mfma_f32_4(sa[m][e], Wv[m][e], au[m & 1]);
-        ao[m & 1] = mfma_f32_4(sa[m][e], gam * qv[m][e], ao[m & 1]);
+        au[m & 1] = mfma_f32_4(sa[e], Wv[m][e], au[m & 1]);
+        ao[m & 1] = mfma_f32_4(sa[e], qv[m][e], ao[m & 1]);
       }
+    }
+    const float gam = q_ok ? expf(G_tok) : 0.0f, gam_c = expf(G_last);
     const floatx4 acc_u = au[0] + au[1];
-    acc_o = ao[0] + ao[1];
-    float* us = u_s[pb];
+    floatx4 acc_o = (ao[0] + ao[1]) * gam;
+    // The S columns this wave updates, in the output layout, before any
+    // wave writes the new values (after the barrier below).
 #pragma unroll
-    for (int r = 0; r < 4; ++r) us[(4 * grp + r) * kAStride + tok] = Uv[r] - acc_u[r];
-    // k^ rows of the wave's tokens: registers -> the wave's LDS rows -> the
-    // operand layout (k^[ktok + e][16 n + j]).  Same wave: no barrier.
-    float* ksw = k_s[wave];
+    for (int n = 0; n < 2; ++n)
 #pragma unroll
-    for (int p = 0; p < 8; ++p)
-      *(f32x4*)(ksw + (2 * p + grp / 2) * kCStride + 4 * ((grp % 2) * 16 + j)) =
-          kr[p] * (16 * wave + 2 * p + grp / 2 < k_rows ? 1.0f : 0.0f);
+      for (int r = 0; r < 4; ++r) d[n][r] = gam_c * s_s[(4 * grp + r) * kCStride + col_w + 16 * n + j];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) u_s[(4 * grp + r) * kAStride + tok] = Uv[r] - acc_u[r];
     load_wqu(cn);
-    load_k(cn);
-    // D_w[row][col] = sum_{i in w} U^T[row][i] e^{G_C - G_i} k[i][col]
-    const f32x4 uw = *(const f32x4*)(us + j * kAStride + ktok);
-    float kv[4][8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-#pragma unroll
-      for (int n = 0; n < 8; ++n) kv[e][n] = ksw[(4 * grp + e) * kCStride + 16 * n + j];
-    floatx4 d[8];
-#pragma unroll
-    for (int n = 0; n < 8; ++n) d[n] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-#pragma unroll
-      for (int n = 0; n < 8; ++n) d[n] = mfma_f32_4(uw[e], dk4[e] * kv[e][n], d[n]);
-    float* ds = d_s[pb][wave];
-#pragma unroll
-    for (int n = 0; n < 8; ++n)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) ds[(4 * grp + r) * kCStride + 16 * n + j] = d[n][r];
-  };
-  // Second half of chunk c (after the barrier): O^T's P U^T term and its
-  // store, then S <- Gamma_C S + sum_w D_w.
-  auto tail = [&](uint32_t c, floatx4 acc_o, float gam_c) __attribute__((always_inline)) {
-    const uint32_t pb = c & 1;
-    const uint32_t t0 = c * kDnChunk, nt = min(kDnChunk, a.M - t0);
-    const float* us = u_s[pb];
-    // (b2) O^T[row][tok] += sum_{i <= tok} U^T[row][i] P[tok][i]; all four
-    // token blocks (P is zero past the diagonal block), so no branch.
+    lds_barrier();  // U^T complete; every wave is done reading S
+    // (b2) O^T[row][tok] += sum_{i <= tok} U^T[row][i] P[tok][i] (all four
+    // token blocks: P is zero past the diagonal block, so no branch), and
+    // S[:, cols_w] += U^T K~[:, cols_w] over the chunk's 64 tokens.
     floatx4 ap[2] = {acc_o, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      const f32x4 ua = *(const f32x4*)(us + j * kAStride + 16 * m + 4 * grp);
+      const f32x4 ua = *(const f32x4*)(u_s + j * kAStride + 16 * m + 4 * grp);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ap[e & 1] = mfma_f32_4(ua[e], Pv[m][e], ap[e & 1]);
+      for (int e = 0; e < 4; ++e) {
+        ap[e & 1] = mfma_f32_4(ua[e], Pv[m][e], ap[e & 1]);
+#pragma unroll
+        for (int n = 0; n < 2; ++n) d[n] = mfma_f32_4(ua[e], Kv[n][m][e], d[n]);
+      }
     }
-    load_p(min(c + 1, nchunks - 1));
+    load_pk(cn);
     acc_o = ap[0] + ap[1];
     // A buffer store bounded to the chunk's nt rows: tokens past the end are
     // dropped by the hardware, so the store needs no branch.
@@ -1124,37 +1167,17 @@ __global__ __launch_bounds__(256) void dn_chunk_scan_kernel(DnArgs a) {
         u32x4{__float_as_uint(acc_o[0]), __float_as_uint(acc_o[1]), __float_as_uint(acc_o[2]),
               __float_as_uint(acc_o[3])},
         ro, tok * row_bytes + (h * kCD + row0 + 4 * grp) * 4, 0, 0);
-    // S <- Gamma_C S + sum_w D_w (A layout, fixed order of w).
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      f32x4 acc = sa[m] * gam_c;
+    for (int n = 0; n < 2; ++n)
 #pragma unroll
-      for (int w = 0; w < 4; ++w) acc += *(const f32x4*)(d_s[pb][w] + j * kCStride + 16 * m + 4 * grp);
-      sa[m] = acc;
-    }
-  };
-
-  load_wqu(0);
-  load_k(0);
-  load_p(0);
-  floatx4 acc_o;
-  float gam_c = expf(G_last);
-  head(0, acc_o);
-  lds_barrier();  // U^T and every D_w of chunk 0 complete
-  // Iteration c finishes chunk c - 1 and starts chunk c: its loop-carried
-  // loads were all issued a full phase before the loop boundary.
-  for (uint32_t c = 1; c < nchunks; ++c) {
-    tail(c - 1, acc_o, gam_c);
-    gam_c = expf(G_last);
-    head(c, acc_o);
-    lds_barrier();
+      for (int r = 0; r < 4; ++r) s_s[(4 * grp + r) * kCStride + col_w + 16 * n + j] = d[n][r];
+    lds_barrier();  // the new S is complete; U^T is consumed
   }
-  tail(nchunks - 1, acc_o, gam_c);
-  float* sout = a.s_out + ((size_t)h * kCD + row0 + j) * kCD + 4 * grp;
-  if (wave == 0) {
+  float* sout = a.s_out + ((size_t)h * kCD + row0) * kCD;
 #pragma unroll
-    for (int m = 0; m < 8; ++m) *(f32x4*)(sout + 16 * m) = sa[m];
-  }
+  for (int n = 0; n < 2; ++n)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sout[(4 * grp + r) * kCD + col_w + 16 * n + j] = d[n][r];
 }
 
 template <int EPT>
@@ -1221,7 +1244,7 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
   if (dn_use_chunked(a)) {
     if (!a.chunk_ws) return hipErrorInvalidValue;
     const uint32_t nchunks = (a.M + kDnChunk - 1) / kDnChunk;
-    hipLaunchKernelGGL(dn_chunk_prep_kernel, dim3(nchunks * a.value_heads), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(dn_chunk_prep_kernel, dim3(nchunks * a.value_heads), dim3(256), kPrepLds, st, a);
     hipLaunchKernelGGL(dn_chunk_scan_kernel, dim3(a.value_heads * (kCD / 16)), dim3(256), 0, st, a);
   } else {
     const uint32_t ept = (a.dk + kLanesPerRow - 1) / kLanesPerRow;
@@ -1236,9 +1259,9 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
     else
       launch_scan<16>(a, st);
   }
-  const uint32_t wpb = a.M * a.value_heads >= 1024 ? kThreads / 64 : 1;
-  const uint32_t norm_items = a.M * a.value_heads;
-  hipLaunchKernelGGL(dn_gate_norm_kernel, dim3((norm_items + wpb - 1) / wpb), dim3(64 * wpb), 0, st, a);
+  const uint32_t norm_waves = (a.M * a.value_heads + kNormRows - 1) / kNormRows;
+  const uint32_t wpb = norm_waves >= 1024 ? kThreads / 64 : 1;
+  hipLaunchKernelGGL(dn_gate_norm_kernel, dim3((norm_waves + wpb - 1) / wpb), dim3(64 * wpb), 0, st, a);
   return hipGetLastError();
 }
 

@@ -104,7 +104,12 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const uint16_t* __restric
   uint32_t h[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    const _Float16 f = (_Float16)bf16_to_f32(e[k]);
+    // Saturate to the fp16 range: a bf16 activation beyond +-65504 becomes
+    // +-65504 rather than an infinity that would poison the whole output row
+    // (NaN compares false both ways and passes through as NaN).
+    float v = bf16_to_f32(e[k]);
+    v = v > 65504.0f ? 65504.0f : (v < -65504.0f ? -65504.0f : v);
+    const _Float16 f = (_Float16)v;
     h[k] = __builtin_bit_cast(uint16_t, f);
   }
   u32x4 o;

@@ -303,6 +303,7 @@ def test_decode_layers_match_oracle(rt, torch_dev):
     got = _hidden(rt, st)
     ref = _oracle_tokens(model, h0, 3)
     err = np.max(np.abs(got - ref)) / np.max(np.abs(ref))
+    print(f"decode composition rel err {err:.3e}")
     assert err < 2e-2, f"hidden after 3 tokens: rel err {err:.3e}"
 
 

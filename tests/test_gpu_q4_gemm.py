@@ -97,6 +97,33 @@ def test_constant_nibble_closed_form(rt, torch_dev):
     assert_bf16_close(got, xs @ wg.T, what="constant nibble")
 
 
+def test_activation_beyond_fp16_range_saturates(rt, torch_dev):
+    # The GEMM stages activations in fp16; a bf16 value beyond +-65504 is
+    # clamped to +-65504 instead of becoming an infinity, so the result equals
+    # the exact projection of the clamped input and every output stays finite.
+    rng = np.random.default_rng(21)
+    N, K, M = 192, 512, 40
+    mat = synth.q4_matrix(rng, N, K)
+    xf = synth.bf16_to_f32(synth.bf16_normal(rng, (M, K)))
+    xf[3, 17] = 1.0e5
+    xf[9, 300] = -3.0e6
+    xf[20, :8] = 7.0e4
+    xb = synth.f32_to_bf16(xf)
+    (got,) = _project(rt, torch_dev, [mat], xb, M)
+    assert np.all(np.isfinite(got))
+    # 65504 is not a bf16 value; by linearity P(clamp(x)) = P(x') - P(d), where
+    # x' holds +-65536 at the clamped places and d holds +-32 there (both exact
+    # in bf16).
+    xv = synth.bf16_to_f32(xb)
+    big = np.abs(xv) > 65504.0
+    xp = np.where(big, np.sign(xv) * 65536.0, xv).astype(np.float32)
+    d = np.where(big, np.sign(xv) * 32.0, 0.0).astype(np.float32)
+    want = (oracle.q4_project(synth.f32_to_bf16(xp), *mat).astype(np.float64)
+            - oracle.q4_project(synth.f32_to_bf16(d), *mat))
+    for m in range(M):  # row by row: the saturated rows' scale would hide the rest
+        assert_bf16_close(got[m], want[m], what=f"saturated activations, row {m}")
+
+
 @pytest.mark.parametrize("M", [64, 256, 300])
 def test_swiglu_and_mlp(rt, torch_dev, M):
     # fused_q4_mlp_batch_matches_cpu_reference (metal_runtime.rs:10726) at M = 256.
