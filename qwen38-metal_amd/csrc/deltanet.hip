@@ -728,102 +728,84 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_split_kernel(DnArgs a) {
 // per-token kernel's bit for bit.  NS = channel slots per lane and class
 // (ceil(head dim / 64)); kernels of up to kTaps taps.
 constexpr int kConvTile = 32;
-template <int NS>
-__global__ __launch_bounds__(kThreads) void dn_conv_tiled_kernel(DnArgs a) {
-  constexpr int S2 = 2 * NS;  // q slots 0..NS-1, k slots NS..2NS-1 (value units use the first NS)
-  const uint32_t units = a.key_heads + a.value_heads;
-  const uint32_t tiles = (a.M + kConvTile - 1) / kConvTile;
-  const uint32_t item = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-  if (item >= tiles * units) return;
-  // Units of one tile are consecutive: a block's waves share token rows.
-  const uint32_t tile = item / units, u = item % units;
-  const uint32_t lane = threadIdx.x & 63;
+constexpr int kConvBatch = 4;  // tokens whose inputs are loaded together
+// One wave's tile: KEY units carry q and k (2 NS slots), value units v (NS);
+// HW = kernel - 1 history taps.
+template <int NS, int HW, bool KEY>
+__device__ __forceinline__ void conv_tile(const DnArgs& a, uint32_t tile, uint32_t u, uint32_t lane) {
+  constexpr int S = KEY ? 2 * NS : NS;  // q slots 0..NS-1, k slots NS..2NS-1
   const uint32_t key_el = a.key_heads * a.dk;
-  const int hw = (int)a.kernel - 1;
-  const bool key = u < a.key_heads;
-  const int ns = key ? S2 : NS;  // live slots (wave-uniform)
-  const uint32_t width = key ? a.dk : a.dv;
-  uint32_t ch[S2];
-  bool ok[S2];
+  const uint32_t width = KEY ? a.dk : a.dv;
+  uint32_t ch[S];
+  bool ok[S];
 #pragma unroll
   for (int i = 0; i < NS; ++i) {
     const uint32_t c = lane + 64 * i;
+    const uint32_t cc = c < width ? c : 0;
     ok[i] = c < width;
-    ok[NS + i] = key && c < width;
-    const uint32_t cc = ok[i] ? c : 0;
-    ch[i] = key ? u * a.dk + cc : 2 * key_el + (u - a.key_heads) * a.dv + cc;
-    ch[NS + i] = key ? key_el + u * a.dk + cc : ch[i];
+    ch[i] = KEY ? u * a.dk + cc : 2 * key_el + (u - a.key_heads) * a.dv + cc;
+    if (KEY) {
+      ok[NS + i] = ok[i];
+      ch[NS + i] = key_el + u * a.dk + cc;
+    }
   }
-  float w[S2][kTaps], win[S2][kTaps];  // win[s][j] = x(t - hw + j) for j < hw
+  float w[S][HW + 1], win[S][HW + 1];  // win[s][j] = x(t - HW + j) for j < HW
   const int t0 = (int)(tile * kConvTile);
   const int t1 = min((int)a.M, t0 + kConvTile);
 #pragma unroll
-  for (int s = 0; s < S2; ++s) {
-    if (s >= ns) break;
+  for (int s = 0; s < S; ++s)
 #pragma unroll
-    for (int j = 0; j < kTaps; ++j) {
-      const int jj = j <= hw ? j : hw;
-      w[s][j] = j <= hw ? a.conv_w[(size_t)ch[s] * a.kernel + jj] : 0.0f;
-      win[s][j] = j < hw ? conv_input(a, ch[s], t0 - hw + j) : 0.0f;
+    for (int j = 0; j <= HW; ++j) {
+      w[s][j] = a.conv_w[(size_t)ch[s] * a.kernel + j];
+      win[s][j] = j < HW ? conv_input(a, ch[s], t0 - HW + j) : 0.0f;
     }
-  }
   const float inv = 1.0f / sqrtf((float)a.dk);
-  // Inputs of four tokens per batch; the next batch's loads are issued
+  // Inputs of kConvBatch tokens per batch; the next batch's loads are issued
   // before the current batch is computed.
-  auto load_batch = [&](int tb, float (&xs)[4][S2]) __attribute__((always_inline)) {
+  auto load_batch = [&](int tb, float (&xs)[kConvBatch][S]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < kConvBatch; ++k)
 #pragma unroll
-      for (int s = 0; s < S2; ++s) {
-        const int t = min(tb + k, t1 - 1);
-        xs[k][s] = s < ns ? a.qkv[(size_t)t * a.channels + ch[s]] : 0.0f;
-      }
+      for (int s = 0; s < S; ++s) xs[k][s] = a.qkv[(size_t)min(tb + k, t1 - 1) * a.channels + ch[s]];
   };
-  float xn[4][S2];
+  float xn[kConvBatch][S];
   load_batch(t0, xn);
-  for (int tb = t0; tb < t1; tb += 4) {
-    float xs[4][S2];
+  for (int tb = t0; tb < t1; tb += kConvBatch) {
+    float xs[kConvBatch][S];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < kConvBatch; ++k)
 #pragma unroll
-      for (int s = 0; s < S2; ++s) xs[k][s] = xn[k][s];
-    load_batch(tb + 4, xn);  // clamped to the tile: past its end a harmless reload
+      for (int s = 0; s < S; ++s) xs[k][s] = xn[k][s];
+    load_batch(tb + kConvBatch, xn);  // clamped to the tile: past its end a harmless reload
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < kConvBatch; ++k) {
       const int t = tb + k;
       if (t >= t1) break;
       float* row = a.conv_out + (size_t)t * a.channels;
       float* hist_dst = history_target(a, (uint32_t)t);
-      float y[S2];
+      float y[S];
 #pragma unroll
-      for (int s = 0; s < S2; ++s) {
+      for (int s = 0; s < S; ++s) {
         const float x = xs[k][s];
-        // conv_finish: w[hw] * x(t), then taps 0 .. hw - 1 in order.
-        float wl = w[s][0];
+        // conv_finish's roundings: w[HW] * x(t), then taps 0 .. HW - 1 in order.
+        float sum = __fmul_rn(w[s][HW], x);
 #pragma unroll
-        for (int jx = 1; jx < kTaps; ++jx) wl = hw == jx ? w[s][jx] : wl;
-        float sum = __fmul_rn(wl, x);  // conv_finish's roundings
-#pragma unroll
-        for (int jx = 0; jx < kTaps - 1; ++jx)
-          if (jx < hw) sum = fmaf(w[s][jx], win[s][jx], sum);
+        for (int jx = 0; jx < HW; ++jx) sum = fmaf(w[s][jx], win[s][jx], sum);
         y[s] = silu_f(sum);
-        // Slide the window: x(t - hw + 1 .. t).
+        // Slide the window: x(t - HW + 1 .. t).
 #pragma unroll
-        for (int jx = 0; jx < kTaps - 1; ++jx) {
-          if (jx + 1 < hw) win[s][jx] = win[s][jx + 1];
-          else if (jx + 1 == hw) win[s][jx] = x;
-        }
-        if (hist_dst && s < ns && ok[s]) {
+        for (int jx = 0; jx + 1 < HW; ++jx) win[s][jx] = win[s][jx + 1];
+        if (HW > 0) win[s][HW - 1] = x;
+        if (HW > 0 && hist_dst && ok[s]) {
 #pragma unroll
-          for (int jx = 0; jx < kTaps - 1; ++jx)
-            if (jx < hw) hist_dst[(size_t)ch[s] * hw + jx] = win[s][jx];
+          for (int jx = 0; jx < HW; ++jx) hist_dst[(size_t)ch[s] * HW + jx] = win[s][jx];
         }
       }
-      if (key) {
+      if (KEY) {
         float qs = 0.0f, ks = 0.0f;
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
-          const float yq = ok[i] ? y[i] : 0.0f, yk = ok[NS + i] ? y[NS + i] : 0.0f;
+          const float yq = ok[i] ? y[i] : 0.0f, yk = ok[i] ? y[NS + i] : 0.0f;
           qs = fmaf(yq, yq, qs);
           ks = fmaf(yk, yk, ks);
         }
@@ -844,6 +826,20 @@ __global__ __launch_bounds__(kThreads) void dn_conv_tiled_kernel(DnArgs a) {
       }
     }
   }
+}
+template <int NS, int HW>
+__global__ __launch_bounds__(kThreads) void dn_conv_tiled_kernel(DnArgs a) {
+  const uint32_t units = a.key_heads + a.value_heads;
+  const uint32_t tiles = (a.M + kConvTile - 1) / kConvTile;
+  const uint32_t item = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (item >= tiles * units) return;
+  // Units of one tile are consecutive: a block's waves share token rows.
+  const uint32_t tile = item / units, u = item % units;
+  const uint32_t lane = threadIdx.x & 63;
+  if (u < a.key_heads)
+    conv_tile<NS, HW, true>(a, tile, u, lane);
+  else
+    conv_tile<NS, HW, false>(a, tile, u, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1201,6 +1197,24 @@ bool dn_use_chunked(const DnArgs& a) {
   return a.M >= 2 * kDnChunk;
 }
 
+template <int NS>
+void launch_conv_tiled_ns(const DnArgs& a, dim3 grid, dim3 block, hipStream_t st) {
+  switch (a.kernel) {
+    case 1: hipLaunchKernelGGL((dn_conv_tiled_kernel<NS, 0>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((dn_conv_tiled_kernel<NS, 1>), grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((dn_conv_tiled_kernel<NS, 2>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((dn_conv_tiled_kernel<NS, 3>), grid, block, 0, st, a); break;
+  }
+}
+void launch_conv_tiled(const DnArgs& a, uint32_t ns, dim3 grid, dim3 block, hipStream_t st) {
+  if (ns <= 1)
+    launch_conv_tiled_ns<1>(a, grid, block, st);
+  else if (ns <= 2)
+    launch_conv_tiled_ns<2>(a, grid, block, st);
+  else
+    launch_conv_tiled_ns<4>(a, grid, block, st);
+}
+
 hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
   if (a.dk == 0 || a.dk > 256 || a.dv == 0 || a.dv > 256 || a.M == 0) return hipErrorInvalidValue;
   // One token with S rows that fit the fused kernel's registers: one launch.
@@ -1231,12 +1245,7 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
     const uint32_t items = ((a.M + kConvTile - 1) / kConvTile) * units;
     const dim3 grid((items + 3) / 4), block(kThreads);
     const uint32_t ns = (std::max(a.dk, a.dv) + 63) / 64;
-    if (ns <= 1)
-      hipLaunchKernelGGL(dn_conv_tiled_kernel<1>, grid, block, 0, st, a);
-    else if (ns <= 2)
-      hipLaunchKernelGGL(dn_conv_tiled_kernel<2>, grid, block, 0, st, a);
-    else
-      hipLaunchKernelGGL(dn_conv_tiled_kernel<4>, grid, block, 0, st, a);
+    launch_conv_tiled(a, ns, grid, block, st);
   } else {
     const uint32_t prep_items = a.M * units;
     hipLaunchKernelGGL(dn_conv_prepare_kernel, dim3((prep_items + 3) / 4), dim3(kThreads), 0, st, a);

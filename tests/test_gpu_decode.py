@@ -7,7 +7,7 @@
 * qm_decode_layers (decode_layers, metal_runtime.rs:2022-2084) on a small
   model of DeltaNet and full-attention layers: bit-equal to the same token
   issued as separate entry-point calls (each parity-tested on its own), and
-  within 2e-2 of max|hidden| of an oracle composition (fp64/fp32 CPU
+  within 1e-2 of max|hidden| of an oracle composition (fp64/fp32 CPU
   functions with the GPU's bf16 rounding points) after three tokens.
 * qm_decode_graph: bit-equal to qm_decode_layers over five tokens (both
   history-parity variants), and QM_ERR_GRAPH_STALE once a captured buffer
@@ -304,7 +304,12 @@ def test_decode_layers_match_oracle(rt, torch_dev):
     ref = _oracle_tokens(model, h0, 3)
     err = np.max(np.abs(got - ref)) / np.max(np.abs(ref))
     print(f"decode composition rel err {err:.3e}")
-    assert err < 2e-2, f"hidden after 3 tokens: rel err {err:.3e}"
+    # The oracle rounds at the kernels' bf16 points, so what remains are
+    # rounding-boundary flips: one element landing on the other side of a
+    # bf16 rounding point moves by 2^-8 relative and is carried through the
+    # following layers and tokens (measured 6.9e-3 after three tokens of
+    # three layers).
+    assert err < 1e-2, f"hidden after 3 tokens: rel err {err:.3e}"
 
 
 @pytest.mark.parametrize("kinds", [("linear", "full", "linear"), ("full", "full"), ("linear", "linear")])
