@@ -875,7 +875,7 @@ constexpr int kAStride = 68;    // LDS row stride of the 64 x 64 triangular matr
 // follows the VGPR occupancy target rather than the LDS-bound one): k^ and
 // q^ rows of the chunk, then G and beta.  Once the products are formed the
 // q^ rows' space holds the 64 x 64 triangular matrix A.
-constexpr uint32_t kPrepLds = (2 * 64 * kCStride + 3 * 64) * 4;
+constexpr uint32_t kPrepLds = (2 * 64 * kCStride + 4 * 64) * 4;
 __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float prep_lds[];
   float* ks_s = prep_lds;
@@ -883,6 +883,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   float* g_s = prep_lds + 2 * 64 * kCStride;
   float* beta_s = g_s + 64;
   float* dk_s = g_s + 128;  // e^{G_63 - G_i}
+  float* bg_s = g_s + 192;  // beta_i e^{G_i}
   float* a_s = qs_s;  // [64][kAStride], once the q^ rows are consumed
   const uint32_t VH = a.value_heads;
   const uint32_t h = blockIdx.x % VH, c = blockIdx.x / VH;
@@ -913,6 +914,23 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
     *(f32x4*)(ks_s + t * kCStride + 4 * j4) = kv;
     *(f32x4*)(qs_s + t * kCStride + 4 * j4) = qv;
   }
+  // v of the wave's U~ columns (32 w + 16 nn + j) for the solve at the end,
+  // loaded now so the loads overlap everything before it (rows past the last
+  // token read row 0 and are masked at use).
+  const uint32_t j = lane & 15, grp = lane >> 4;
+  float vpre[4][2][4];
+  {
+    const float* vsrc = a.conv_out + (size_t)t0 * a.channels + 2 * key_el + h * kCD + 32 * wave + j;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int nn = 0; nn < 2; ++nn)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t t = 16 * b + 4 * grp + r;
+          vpre[b][nn][r] = vsrc[(size_t)(t < nt ? t : 0) * a.channels + 16 * nn];
+        }
+  }
   // Log decays, their running sum and beta (wave 0; padding tokens: lg = 0,
   // beta = 0, so they change nothing).
   if (wave == 0) {
@@ -931,6 +949,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
     g_s[lane] = G;
     beta_s[lane] = beta;
     dk_s[lane] = expf(__shfl(G, 63) - G);
+    bg_s[lane] = beta * expf(G);
     Gg[lane] = G;
   }
   __syncthreads();
@@ -952,7 +971,6 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   // every wave is past it the q^ rows' space takes A from K K^T.  The MFMA
   // reduction index is permuted (lane group g of step (m, e) carries
   // k = 16 m + 4 g + e), so every operand is one 16-byte LDS read.
-  const uint32_t j = lane & 15, grp = lane >> 4;
   auto tile = [&](const float* xs, int tix, floatx4& acc, int& tm, int& tn) __attribute__((always_inline)) {
     int rem = tix;
     tm = 0;
@@ -991,7 +1009,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t t = 16 * tm + 4 * grp + r;
-      a_s[t * kAStride + i] = i < t ? beta_s[t] * expf(g_s[t] - g_s[i]) * acc[r] : 0.0f;
+      a_s[t * kAStride + i] = i < t ? -(beta_s[t] * expf(g_s[t] - g_s[i]) * acc[r]) : 0.0f;  // -A
     }
   }
   // P is zero above the diagonal blocks too, so its readers need no bounds.
@@ -1003,35 +1021,68 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   }
   __syncthreads();
 
-  // Forward substitution (I + A) X = R, one column per thread: columns
-  // 0..127 are R = beta Gamma k (giving W), 128..255 R = beta v (giving U~).
-  // Four partial sums per row keep four independent FMA chains.
-  float x[64];
-  if (tid < kCD) {
+  // Solve (I + A) X = R in 16-row blocks b (A unit lower triangular):
+  //   X_b = T_b (R_b - sum_{c<b} A_bc X_c),  T_b = (I + A_bb)^{-1},
+  // on fp32 MFMA.  R's columns are beta Gamma k (giving W) and beta v (giving
+  // U~); wave w owns W columns 32 w .. 32 w + 31 (tiles n = 0, 1) and the
+  // same U~ columns (tiles n = 2, 3).
+  // With the reduction index of MFMA step r permuted to k = 4 grp + r, an
+  // output tile (rows 4 grp + r, column j in lane (j, grp)) is directly the
+  // B operand of the next product, so X stays in registers.
+  // T_b first: wave b, lane jj < 16 owns column jj (T_b[t][jj] = delta_t,jj
+  // + sum_{i<t} (-A)[t][i] T_b[i][jj]).
+  float* t_s = a_s + 64 * kAStride;  // T_b [4][16][17]
+  if (lane < 16) {
+    const uint32_t b = wave, jj = lane;
+    const float* ab = a_s + 16 * b * kAStride + 16 * b;
+    float tc[16];
 #pragma unroll
-    for (int t = 0; t < 64; ++t) x[t] = beta_s[t] * expf(g_s[t]) * ks_s[t * kCStride + tid];
-  } else {
-    const uint32_t col = tid - kCD;
-    const float* vsrc = a.conv_out + 2 * key_el + h * kCD + col;
+    for (int t = 0; t < 16; ++t) {
+      float v = (uint32_t)t == jj ? 1.0f : 0.0f;
 #pragma unroll
-    for (int t = 0; t < 64; ++t) x[t] = (uint32_t)t < nt ? beta_s[t] * vsrc[(size_t)(t0 + t) * a.channels] : 0.0f;
-  }
-#pragma unroll
-  for (int t = 1; t < 64; ++t) {
-    const float* arow = a_s + t * kAStride;
-    float p[4] = {x[t], 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int i4 = 0; i4 < t; i4 += 4) {
-      const f32x4 av = *(const f32x4*)(arow + i4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (i4 + e < t) p[e] -= av[e] * x[i4 + e];
+      for (int i = 0; i < t; ++i) v = fmaf(ab[t * kAStride + i], tc[i], v);
+      tc[t] = v;
+      t_s[(16 * b + t) * 17 + jj] = v;
     }
-    x[t] = (p[0] + p[1]) + (p[2] + p[3]);
   }
-  float* dst = tid < kCD ? Wg + tid : Ug + (tid - kCD);
+  __syncthreads();
+  const uint32_t cw = 32 * wave + j;  // the lane's column within W and within U~ (plus 16 nn)
+  floatx4 X[4][4];  // [block b][tile n]: X[16 b + 4 grp + r][tile column]
 #pragma unroll
-  for (int t = 0; t < 64; ++t) dst[t * kCD] = x[t];
+  for (int b = 0; b < 4; ++b) {
+    floatx4 acc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t t = 16 * b + 4 * grp + r;
+#pragma unroll
+      for (int nn = 0; nn < 2; ++nn) {
+        acc[nn][r] = bg_s[t] * ks_s[t * kCStride + cw + 16 * nn];
+        acc[2 + nn][r] = t < nt ? beta_s[t] * vpre[b][nn][r] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < b; ++c) {
+      const f32x4 av = *(const f32x4*)(a_s + (16 * b + j) * kAStride + 16 * c + 4 * grp);  // (-A)_bc
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int n = 0; n < 4; ++n) acc[n] = mfma_f32_4(av[r], X[c][n][r], acc[n]);
+    }
+    const f32x4 tv = *(const f32x4*)(t_s + (16 * b + j) * 17 + 4 * grp);
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      X[b][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) X[b][n] = mfma_f32_4(tv[r], acc[n][r], X[b][n]);
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        (n < 2 ? Wg : Ug)[(16 * b + 4 * grp + r) * kCD + cw + 16 * (n & 1)] = X[b][n][r];
 }
 
 // grid: VH * 8 blocks (block = rg * VH + h: the 8 row groups of a head share
