@@ -37,6 +37,7 @@ sys.path.insert(0, str(ROOT / "qwen38-metal_amd"))
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, GB/s
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 MFMA, TFLOP/s
+FP32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 (matrix), TFLOP/s
 
 H, I, QKV = 5120, 17408, 10240
 ATT_H, ATT_KVH, ATT_D = 64, 8, 128
@@ -359,6 +360,12 @@ def deltanet_legs(rt, dev, rng, steps, warmup):
         key = "deltanet_step" if M == 1 else "deltanet_prefill_2048"
         out[key] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                     "tokens_per_s": round(M / (ms * 1e-3), 1)}
+        if M > 1:
+            # The recurrence's arithmetic (decay, S k, update, S q: 7 dk dv per
+            # token and head), priced against the fp32 MFMA peak the chunked
+            # scan runs on.
+            tf = 7.0 * dk * dv * VH * M / (ms * 1e-3) / 1e12
+            out[key].update({"TFLOP/s": round(tf, 2), "fp32_mfma_frac": round(tf / FP32_PEAK_TFLOPS, 4)})
     st.close()
     w.close()
     return out
