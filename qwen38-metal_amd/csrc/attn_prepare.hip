@@ -20,9 +20,11 @@
 // table (one angle, sine and cosine per frequency, shared by all heads) in
 // LDS; then each of the 8 waves prepares every (8 * groups)-th head of the
 // row, issuing the loads of up to 8 heads at once.  Short calls (decode) use
-// many head groups, long prompts one per row.  Lane l holds elements 4 l .. 4 l + 3 (head_dim <= 256): the sum of
-// squares is a wave reduction and each rotation partner (element c +- rd/2) is
-// fetched from its lane by a cross-lane shuffle.
+// many head groups, long prompts one per row.  A wave holds two heads when
+// head_dim <= 128 (32 lanes each), else one; lane l of a head holds elements
+// 4 l .. 4 l + 3: the sum of squares is a reduction over the head's lanes and
+// each rotation partner (element c +- rd/2) is fetched from its lane by a
+// cross-lane shuffle.
 #include "common.h"
 #include "prepare.h"
 
@@ -42,15 +44,32 @@ __device__ __forceinline__ float pick4(const float (&x)[4], uint32_t k) {
 // for c < half, c - half above.  For a given j every lower receiver wants
 // element (j + half) % 4 of its source lane and every upper receiver element
 // (j - half) % 4, so each lane sends those two and each receiver keeps one.
-__device__ __forceinline__ float partner(const float (&x)[4], uint32_t lane, uint32_t j, uint32_t half) {
-  const uint32_t c = 4 * lane + j;
+// hl: the lane's index within its head's lanes, which start at lane `base`.
+__device__ __forceinline__ float partner(const float (&x)[4], uint32_t hl, uint32_t base, uint32_t j,
+                                         uint32_t half) {
+  const uint32_t c = 4 * hl + j;
   const bool lower = c < half;
-  const float up_val = __shfl(pick4(x, (j + half) & 3u), (int)((c + half) >> 2) & 63);
-  const float dn_val = __shfl(pick4(x, (j - half) & 3u), (int)((c - half) >> 2) & 63);
+  const float up_val = __shfl(pick4(x, (j + half) & 3u), (int)(base + (((c + half) >> 2) & 63)) & 63);
+  const float dn_val = __shfl(pick4(x, (j - half) & 3u), (int)(base + (((c - half) >> 2) & 63)) & 63);
   return lower ? up_val : dn_val;
 }
 
+// Sum over each 32-lane half of the wave (wave_allsum without its last step).
+__device__ __forceinline__ float half_allsum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));  // row_ror:4
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+// HPW heads per wave: 2 when head_dim <= 128 (32 lanes per head), else 1.
+// For head_dim <= 128 the one-head form's upper 32 lanes add only zeros, so
+// both forms give the same sums bit for bit.
+template <int HPW>
 __global__ __launch_bounds__(64 * kPrepWaves) void attn_prepare_kernel(PrepArgs a) {
+  constexpr uint32_t kLanesPerHead = 64 / HPW;
   __shared__ float cos_s[kPrepMaxHeadDim / 2], sin_s[kPrepMaxHeadDim / 2];
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const uint32_t row = a.row0 + blockIdx.x;
@@ -80,8 +99,10 @@ __global__ __launch_bounds__(64 * kPrepWaves) void attn_prepare_kernel(PrepArgs 
   __syncthreads();
 
   const uint32_t units = a.H + a.KVH;  // query heads, then key heads
+  const uint32_t slots = (units + HPW - 1) / HPW;  // wave work items of HPW heads
   const bool vec = hd % 4 == 0;
-  const uint32_t c0 = 4 * lane;
+  const uint32_t hl = lane % kLanesPerHead, hsel = lane / kLanesPerHead, base = hsel * kLanesPerHead;
+  const uint32_t c0 = 4 * hl;
   const bool mine = c0 < hd;
   // This lane's norm weights, read once (not inside each head's chain).
   float wq[4], wk[4];
@@ -90,12 +111,12 @@ __global__ __launch_bounds__(64 * kPrepWaves) void attn_prepare_kernel(PrepArgs 
     wq[j] = c0 + j < hd ? a.q_norm[c0 + j] : 0.0f;
     wk[j] = c0 + j < hd ? a.k_norm[c0 + j] : 0.0f;
   }
-  for (uint32_t first = blockIdx.y * kPrepWaves + wave; first < units; first += hstride * kPrepBatch) {
-    // Issue the loads of up to kPrepBatch heads (and the query heads' gates).
+  for (uint32_t first = blockIdx.y * kPrepWaves + wave; first < slots; first += hstride * kPrepBatch) {
+    // Issue the loads of up to kPrepBatch slots (and the query heads' gates).
     uint2 in[kPrepBatch], gt[kPrepBatch];
 #pragma unroll
     for (int b = 0; b < kPrepBatch; ++b) {
-      const uint32_t u = first + hstride * b;
+      const uint32_t u = (first + hstride * b) * HPW + hsel;
       in[b] = uint2{0u, 0u};
       gt[b] = uint2{0u, 0u};
       if (u < units && mine) {
@@ -123,8 +144,10 @@ __global__ __launch_bounds__(64 * kPrepWaves) void attn_prepare_kernel(PrepArgs 
     }
 #pragma unroll
     for (int b = 0; b < kPrepBatch; ++b) {
-      const uint32_t u = first + hstride * b;
-      if (u >= units) break;  // wave-uniform
+      const uint32_t slot = first + hstride * b;
+      if (slot >= slots) break;  // wave-uniform
+      const uint32_t u = slot * HPW + hsel;
+      const bool live = u < units;  // the second head of the last slot may not exist
       const bool is_q = u < a.H;
       const uint32_t bits[2] = {in[b].x, in[b].y};
       float x[4];
@@ -134,7 +157,7 @@ __global__ __launch_bounds__(64 * kPrepWaves) void attn_prepare_kernel(PrepArgs 
         x[j] = bf16_to_f32((bits[j / 2] >> (16 * (j % 2))) & 0xFFFFu);
         ss += x[j] * x[j];
       }
-      ss = wave_allsum(ss);
+      ss = HPW == 2 ? half_allsum(ss) : wave_allsum(ss);
       const float scale = 1.0f / sqrtf(ss / (float)hd + a.eps);
 #pragma unroll
       for (int j = 0; j < 4; ++j) x[j] = mine && c0 + j < hd ? x[j] * scale * (is_q ? wq[j] : wk[j]) : 0.0f;
@@ -142,14 +165,14 @@ __global__ __launch_bounds__(64 * kPrepWaves) void attn_prepare_kernel(PrepArgs 
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t c = c0 + j;
-        const float other = partner(x, lane, (uint32_t)j, half);  // every lane joins the shuffles
+        const float other = partner(x, hl, base, (uint32_t)j, half);  // every lane joins the shuffles
         y[j] = x[j];
         if (c < rd) {
           const uint32_t f = c < half ? c : c - half;
           y[j] = c < half ? x[j] * cos_s[f] - other * sin_s[f] : x[j] * cos_s[f] + other * sin_s[f];
         }
       }
-      if (!mine) continue;
+      if (!mine || !live) continue;
       if (is_q) {
         const size_t o = ((size_t)row * a.H + u) * hd + c0;
         if (vec) {
@@ -189,10 +212,15 @@ hipError_t launch_attn_prepare(const PrepArgs& a, hipStream_t st) {
     // Head groups per row: enough blocks to cover the CUs a few times over
     // (one head per wave at M = 1; one block per row for long prompts).
     const uint32_t rows = std::min(kMaxGridY, a.M - r0);
-    const uint32_t max_groups = (a.H + a.KVH + kPrepWaves - 1) / kPrepWaves;
+    const uint32_t hpw = a.head_dim <= 64 * 4 / 2 ? 2 : 1;
+    const uint32_t slots = (a.H + a.KVH + hpw - 1) / hpw;
+    const uint32_t max_groups = (slots + kPrepWaves - 1) / kPrepWaves;
     const uint32_t groups = std::max(1u, std::min(max_groups, (1024u + rows - 1) / rows));
     const dim3 grid(rows, groups);
-    hipLaunchKernelGGL(attn_prepare_kernel, grid, dim3(64 * kPrepWaves), 0, st, c);
+    if (hpw == 2)
+      hipLaunchKernelGGL(attn_prepare_kernel<2>, grid, dim3(64 * kPrepWaves), 0, st, c);
+    else
+      hipLaunchKernelGGL(attn_prepare_kernel<1>, grid, dim3(64 * kPrepWaves), 0, st, c);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
