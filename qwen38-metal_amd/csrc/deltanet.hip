@@ -151,7 +151,8 @@ __device__ __forceinline__ float row_sum(float v) {
 // and the fused step so both round identically.
 // NQ: channel slots per lane that can be live (ceil(dk / 64)); the others
 // stay zero, as they would with all four slots (their squares add nothing).
-template <int NQ = 4>
+// PART: 1 = q only, 2 = k only, 3 = both (each with the same operations).
+template <int NQ = 4, int PART = 3>
 __device__ __forceinline__ void prep_key_head(const DnArgs& a, uint32_t t, uint32_t kh, uint32_t lane, float (&qo)[4],
                                               float (&ko)[4], float* hist_dst) {
   static_assert(NQ >= 1 && NQ <= 4, "slots");
@@ -165,18 +166,18 @@ __device__ __forceinline__ void prep_key_head(const DnArgs& a, uint32_t t, uint3
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const uint32_t c = min(lane + 64 * i, a.dk - 1);
-      conv_load(a, kh * a.dk + c, (int)t, cq[i]);
-      conv_load(a, key_el + kh * a.dk + c, (int)t, ck[i]);
+      if (PART & 1) conv_load(a, kh * a.dk + c, (int)t, cq[i]);
+      if (PART & 2) conv_load(a, key_el + kh * a.dk + c, (int)t, ck[i]);
     }
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const uint32_t c = lane + 64 * i;
       const bool ok = c < a.dk;
-      qo[i] = ok ? conv_finish(a, cq[i]) : 0.0f;
-      ko[i] = ok ? conv_finish(a, ck[i]) : 0.0f;
+      qo[i] = ok && (PART & 1) ? conv_finish(a, cq[i]) : 0.0f;
+      ko[i] = ok && (PART & 2) ? conv_finish(a, ck[i]) : 0.0f;
       if (ok && hist_dst) {
-        conv_store_history(a, kh * a.dk + c, cq[i], hist_dst);
-        conv_store_history(a, key_el + kh * a.dk + c, ck[i], hist_dst);
+        if (PART & 1) conv_store_history(a, kh * a.dk + c, cq[i], hist_dst);
+        if (PART & 2) conv_store_history(a, key_el + kh * a.dk + c, ck[i], hist_dst);
       }
     }
   } else {
@@ -184,11 +185,11 @@ __device__ __forceinline__ void prep_key_head(const DnArgs& a, uint32_t t, uint3
     for (int i = 0; i < NQ; ++i) {
       const uint32_t c = lane + 64 * i;
       const bool ok = c < a.dk;
-      qo[i] = ok ? conv_silu_loop(a, kh * a.dk + c, (int)t) : 0.0f;
-      ko[i] = ok ? conv_silu_loop(a, key_el + kh * a.dk + c, (int)t) : 0.0f;
+      qo[i] = ok && (PART & 1) ? conv_silu_loop(a, kh * a.dk + c, (int)t) : 0.0f;
+      ko[i] = ok && (PART & 2) ? conv_silu_loop(a, key_el + kh * a.dk + c, (int)t) : 0.0f;
       if (ok && hist_dst) {
-        shift_history(a, kh * a.dk + c, (int)t, hist_dst);
-        shift_history(a, key_el + kh * a.dk + c, (int)t, hist_dst);
+        if (PART & 1) shift_history(a, kh * a.dk + c, (int)t, hist_dst);
+        if (PART & 2) shift_history(a, key_el + kh * a.dk + c, (int)t, hist_dst);
       }
     }
   }
@@ -197,8 +198,8 @@ __device__ __forceinline__ void prep_key_head(const DnArgs& a, uint32_t t, uint3
     qs = fmaf(qo[i], qo[i], qs);
     ks = fmaf(ko[i], ko[i], ks);
   }
-  qs = wave_sum(qs);
-  ks = wave_sum(ks);
+  if (PART & 1) qs = wave_sum(qs);
+  if (PART & 2) ks = wave_sum(ks);
   const float inv = 1.0f / sqrtf((float)a.dk);
   const float qscale = 1.0f / sqrtf(qs / (float)a.dk + a.eps);
   const float kscale = 1.0f / sqrtf(ks / (float)a.dk + a.eps);
@@ -602,10 +603,11 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_kernel(DnArgs a) {
 // The decode step split over 16-row groups of S: grid VH * ceil(dv / 16),
 // one workgroup per (value head, row group), so the 4 MiB of S stream from
 // every CU instead of one per head.  Per workgroup:
-//  wave 0: q^, k^ of key head kh (prep_key_head; only group 0 of the first
-//          value head of the key group writes that key head's history);
+//  waves 0 and 2: q^ and k^ of key head kh (prep_key_head, one half each;
+//          only group 0 of the first value head of the key group writes that
+//          key head's history);
 //  wave 1: conv of the group's 16 v channels;
-//  thread 128: g and beta;
+//  thread 192: g and beta;
 // then the 16-lane row groups update the 16 rows (delta_row_token).  The
 // gated norm needs all dv outputs of the head: every group stores its o
 // values (written through to memory) and counts itself in; the last of the
@@ -644,14 +646,19 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_split_kernel(DnArgs a) {
   if (wave == 0) {
     gate_norm_operands(a, a.z + (size_t)vh * a.dv, lane, nrm, sz);
     float cq[4], ck[4];
-    prep_key_head<EPT / 4>(a, 0, kh, lane, cq, ck, key_hist ? a.hist_out : nullptr);
+    prep_key_head<EPT / 4, 1>(a, 0, kh, lane, cq, ck, key_hist ? a.hist_out : nullptr);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t c = lane + 64 * i;
-      if (c < 16 * EPT) {
-        qk_s[0][c % 16][c / 16] = c < a.dk ? cq[i] : 0.0f;
-        qk_s[1][c % 16][c / 16] = c < a.dk ? ck[i] : 0.0f;
-      }
+      if (c < 16 * EPT) qk_s[0][c % 16][c / 16] = c < a.dk ? cq[i] : 0.0f;
+    }
+  } else if (wave == 2) {
+    float cq[4], ck[4];
+    prep_key_head<EPT / 4, 2>(a, 0, kh, lane, cq, ck, key_hist ? a.hist_out : nullptr);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = lane + 64 * i;
+      if (c < 16 * EPT) qk_s[1][c % 16][c / 16] = c < a.dk ? ck[i] : 0.0f;
     }
   } else if (wave == 1) {
     if (lane < kStepRows) {
@@ -668,7 +675,7 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_split_kernel(DnArgs a) {
       }
       v_s[lane] = c < a.dv ? vv : 0.0f;
     }
-  } else if (threadIdx.x == 128) {
+  } else if (threadIdx.x == 192) {
     const float neg_a = -expf(a.a_log[vh]);
     gb_s[0] = expf(neg_a * softplus_f(a.a[vh] + a.dt_bias[vh]));
     gb_s[1] = sigmoid_f(a.b[vh]);
