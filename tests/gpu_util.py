@@ -1,6 +1,8 @@
 """Helpers for GPU parity tests: numpy <-> device tensors and tolerances."""
 from __future__ import annotations
 
+import os
+
 import numpy as np
 
 
@@ -39,14 +41,18 @@ def bf16_half_ulp(v: np.ndarray) -> np.ndarray:
     return np.where(a > 0, 2.0 ** (e - 8), 0.0)
 
 
-def assert_bf16_close(got_f32: np.ndarray, ref_f32: np.ndarray, rel: float = 2e-3, what: str = ""):
+def assert_bf16_close(got_f32: np.ndarray, ref_f32: np.ndarray, rel: float = 1e-4, what: str = ""):
     """bf16 outputs vs an fp32/fp64 oracle.
 
     The kernel's result before its final bf16 store must lie within
     rel * max|ref| of the oracle: |got - ref| - halfulp_bf16(got) <= rel * max|ref|.
     (The store itself rounds to nearest-even, which alone can move a value by
-    up to 2^-8 relative, more than the 2e-3 budget, so it is accounted for
-    separately instead of being charged to the arithmetic.)
+    up to 2^-8 relative, so it is accounted for separately instead of being
+    charged to the arithmetic.)  The default 1e-4 is 20x below the 2e-3 bar
+    for bf16 outputs; the largest arithmetic error any GPU test measures
+    against its oracle is 3.2e-5 (causal prefill attention), except where a
+    test compares against a deliberately different chain and says so.
+    QM38_TOL_LOG=<file> appends each call's measured errors to <file>.
     Returns the arithmetic error (normwise).
     """
     got = np.asarray(got_f32, np.float64)
@@ -57,6 +63,11 @@ def assert_bf16_close(got_f32: np.ndarray, ref_f32: np.ndarray, rel: float = 2e-
     excess = np.maximum(np.abs(got - ref) - bf16_half_ulp(got) * (1 + 1e-6), 0.0)
     err = np.max(excess) / scale
     raw = np.max(np.abs(got - ref)) / scale
+    log = os.environ.get("QM38_TOL_LOG")  # measured errors, for choosing each test's bound
+    if log:
+        with open(log, "a") as f:
+            test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+            f.write(f"{test}\t{what}\t{err:.3e}\t{raw:.3e}\t{rel:.1e}\n")
     assert err <= rel, f"{what}: arithmetic rel err {err:.3e} > {rel:.1e} (raw incl. bf16 rounding {raw:.3e})"
     assert raw <= rel + 2.0 ** -8, f"{what}: raw rel err {raw:.3e}"
     return err

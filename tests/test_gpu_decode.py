@@ -3,7 +3,7 @@
 * qm_residual_rmsnorm / qm_residual_add against the oracle's
   qo_residual_rmsnorm (qwen38_add_in_place + qwen38_rms_norm(_rows),
   qwen38.metal:4250-4333): the fp32 residual add bit for bit, the bf16 norm
-  within 2e-3 of max|ref| beyond the final rounding.
+  within 1e-4 of max|ref| beyond the final rounding.
 * qm_decode_layers (decode_layers, metal_runtime.rs:2022-2084) on a small
   model of DeltaNet and full-attention layers: bit-equal to the same token
   issued as separate entry-point calls (each parity-tested on its own), and

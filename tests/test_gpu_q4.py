@@ -5,8 +5,8 @@ mapped_q4_batch_reuses_one_input_without_changing_results (:9685),
 mapped_q4_matmul_batch_matches_each_prompt_row (:9766),
 batch_simd_q4_matmul_short_batch_matches_cpu_reference (:9812) and
 fused_q4_mlp_batch_matches_cpu_reference (:10726), plus seeded
-BASELINE-shape cases.  Tolerance: bf16 outputs within 2e-3 of max |ref|
-(fp64-accumulated oracle).
+BASELINE-shape cases.  Tolerance: bf16 outputs within 1e-4 of max |ref|
+beyond the bf16 output rounding (fp64-accumulated oracle).
 """
 from __future__ import annotations
 
@@ -88,7 +88,7 @@ def test_matmul_rows_equal_per_row_matvec(rt, torch_dev):
     (batch,) = _project(rt, torch_dev, [mat], xb, M)
     for m in range(M):
         (row,) = _project(rt, torch_dev, [mat], xb[m:m + 1], 1)
-        assert_bf16_close(batch[m:m + 1], row.astype(np.float64), rel=4e-3)
+        assert_bf16_close(batch[m:m + 1], row.astype(np.float64))
 
 
 def test_identity_bias_cancels(rt, torch_dev):
@@ -134,7 +134,7 @@ def test_swiglu_pair_and_mlp(rt, torch_dev, M):
     # and against the all-fp32 chain (h not rounded): rounding h to bf16 is
     # the only extra error
     y_ref32 = oracle.q4_project(synth.f32_to_bf16(h_ref), *down)
-    assert_bf16_close(bf16_dev_to_f32(y), y_ref32, rel=6e-3, what="mlp y vs unrounded-h chain")
+    assert_bf16_close(bf16_dev_to_f32(y), y_ref32, rel=1e-3, what="mlp y vs unrounded-h chain")
 
 
 @pytest.mark.parametrize("M", [1, 4, 8])

@@ -6,8 +6,8 @@ wide_simdgroup_q4_matmul_batch_matches_cpu_reference (:10620) and
 fused_q4_mlp_batch_matches_cpu_reference at M = 256 (:10726), plus the
 BASELINE prefill shapes.  The kernel computes like the reference's prefill
 path: fp16(q*s + b) weights, fp16 activations, fp32 accumulation; the
-oracle is exact (fp64).  Bar: bf16 outputs within 2e-3 of max|ref| beyond
-bf16 rounding.
+oracle is exact (fp64).  Bar: bf16 outputs within 1e-4 of max|ref| beyond
+the bf16 output rounding (tests/gpu_util.py).
 """
 from __future__ import annotations
 
@@ -94,7 +94,9 @@ def test_constant_nibble_closed_form(rt, torch_dev):
     (got,) = _project(rt, torch_dev, [(packed, s, b)], xb, M)
     xs = synth.bf16_to_f32(xb).astype(np.float64).reshape(M, K // 64, 64).sum(-1)
     wg = synth.bf16_to_f32(s).astype(np.float64) * c + synth.bf16_to_f32(b).astype(np.float64)
-    assert_bf16_close(got, xs @ wg.T, what="constant nibble")
+    # The kernel's weights are fp16(q s + b) (the reference's prefill
+    # numerics); the closed form uses the exact s c + b: about 2e-4 apart.
+    assert_bf16_close(got, xs @ wg.T, rel=1e-3, what="constant nibble")
 
 
 def test_activation_beyond_fp16_range_saturates(rt, torch_dev):
