@@ -882,7 +882,7 @@ constexpr int kAStride = 68;    // LDS row stride of the 64 x 64 triangular matr
 // follows the VGPR occupancy target rather than the LDS-bound one): k^ and
 // q^ rows of the chunk, then G and beta.  Once the products are formed the
 // q^ rows' space holds the 64 x 64 triangular matrix A.
-constexpr uint32_t kPrepLds = (2 * 64 * kCStride + 4 * 64) * 4;
+constexpr uint32_t kPrepLds = (2 * 64 * kCStride + 5 * 64) * 4;
 __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float prep_lds[];
   float* ks_s = prep_lds;
@@ -891,6 +891,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   float* beta_s = g_s + 64;
   float* dk_s = g_s + 128;  // e^{G_63 - G_i}
   float* bg_s = g_s + 192;  // beta_i e^{G_i}
+  float* gm_s = g_s + 256;  // e^{G_i}
   float* a_s = qs_s;  // [64][kAStride], once the q^ rows are consumed
   const uint32_t VH = a.value_heads;
   const uint32_t h = blockIdx.x % VH, c = blockIdx.x / VH;
@@ -901,11 +902,12 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   float* ws = a.chunk_ws + ((size_t)c * VH + h) * kDnChunkFloats;
-  float* Wg = ws;
-  float* Ug = ws + 64 * kCD;
-  float* Pg = Ug + 64 * kCD;
-  float* Gg = Pg + 64 * 64;
-  float* KTg = Gg + 64;
+  float* Wg = ws + kDnWsW;
+  float* Ug = ws + kDnWsU;
+  float* Pg = ws + kDnWsP;
+  float* Gg = ws + kDnWsG;
+  float* KTg = ws + kDnWsKT;
+  float* Qg = ws + kDnWsQ;
 
   // q^ and k^ rows of the chunk (zero past the last token) into LDS.
 #pragma unroll
@@ -957,20 +959,30 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
     beta_s[lane] = beta;
     dk_s[lane] = expf(__shfl(G, 63) - G);
     bg_s[lane] = beta * expf(G);
+    gm_s[lane] = expf(G);
     Gg[lane] = G;
   }
   __syncthreads();
 
-  // K~^T[c][i] = e^{G_63 - G_i} k^[i][c]: the scan's operand for the state
-  // update, written once here (16-byte stores of four consecutive tokens).
+  // The scan's operands in its MFMA operand order (dn_ws_index): K~^T[c][i] =
+  // e^{G_63 - G_i} k^[i][c] for the state update and Gamma_t q^[t][k] for
+  // the output, one contiguous 16-byte store per lane and float4.
 #pragma unroll
   for (int p = 0; p < 8; ++p) {
-    const uint32_t idx = tid + 256 * p;  // over [128 columns][16 token quads]
-    const uint32_t col = idx / 16, i4 = idx % 16;
+    const uint32_t idx = tid + 256 * p;  // float4 index: [w 4][n 2][m 4][g 4][j 16]
+    const uint32_t jj = idx % 16, gg = (idx / 16) % 4, mm = (idx / 64) % 4, nn = (idx / 256) % 2, ww = idx / 512;
+    const uint32_t col = 32 * ww + 16 * nn + jj, i0 = 16 * mm + 4 * gg;
     f32x4 v;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = dk_s[4 * i4 + e] * ks_s[(4 * i4 + e) * kCStride + col];
-    *(f32x4*)(KTg + col * 64 + 4 * i4) = v;
+    for (int e = 0; e < 4; ++e) v[e] = dk_s[i0 + e] * ks_s[(i0 + e) * kCStride + col];
+    *(f32x4*)(KTg + 4 * idx) = v;
+  }
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const uint32_t idx = tid + 256 * p;  // float4 index: [w 4][m 8][g 4][j 16]
+    const uint32_t jj = idx % 16, gg = (idx / 16) % 4, mm = (idx / 64) % 8, ww = idx / 512;
+    const uint32_t t = 16 * ww + jj;
+    *(f32x4*)(Qg + 4 * idx) = *(const f32x4*)(qs_s + t * kCStride + 16 * mm + 4 * gg) * gm_s[t];
   }
 
   // Q K^T, then K K^T, on the lower-triangular 16 x 16 tiles (tn <= tm):
@@ -1004,7 +1016,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t t = 16 * tm + 4 * grp + r;
-      Pg[t * 64 + i] = i <= t ? expf(g_s[t] - g_s[i]) * acc[r] : 0.0f;
+      Pg[dn_ws_index(tm, tn, 4 * grp + r, j, 4)] = i <= t ? expf(g_s[t] - g_s[i]) * acc[r] : 0.0f;
     }
   }
   __syncthreads();  // the q^ rows are consumed; their space becomes A
@@ -1024,7 +1036,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
     const uint32_t tile = idx / 256, e = idx % 256;
     const uint32_t tm = tile < 3 ? 0 : tile < 5 ? 1 : 2;  // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
     const uint32_t tn = tile < 3 ? tile + 1 : tile < 5 ? tile - 1 : 3;
-    Pg[(16 * tm + e / 16) * 64 + 16 * tn + e % 16] = 0.0f;
+    Pg[256 * (4 * tm + tn) + e] = 0.0f;
   }
   __syncthreads();
 
@@ -1088,8 +1100,14 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        (n < 2 ? Wg : Ug)[(16 * b + 4 * grp + r) * kCD + cw + 16 * (n & 1)] = X[b][n][r];
+      for (int r = 0; r < 4; ++r) {
+        // X[b][n][r]: token 16 b + 4 grp + r, column 32 wave + 16 (n & 1) + j.
+        const uint32_t blk = 2 * wave + (n & 1);
+        if (n < 2)
+          Wg[dn_ws_index(b, blk, 4 * grp + r, j, 8)] = X[b][n][r];  // W[token][k], k block blk
+        else
+          Ug[dn_ws_index(blk, b, 4 * grp + r, j, 4)] = X[b][n][r];  // U~ columns of row group blk
+      }
 }
 
 // grid: VH * 8 blocks (block = rg * VH + h: the 8 row groups of a head share
@@ -1107,7 +1125,6 @@ __global__ __launch_bounds__(256) void dn_chunk_scan_kernel(DnArgs a) {
   __shared__ __attribute__((aligned(16))) float s_s[16 * kCStride];  // S [row][col]
   const uint32_t VH = a.value_heads;
   const uint32_t h = blockIdx.x % VH, rg = blockIdx.x / VH;
-  const uint32_t kh = h / (VH / a.key_heads);
   const uint32_t row0 = rg * 16;
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1117,38 +1134,33 @@ __global__ __launch_bounds__(256) void dn_chunk_scan_kernel(DnArgs a) {
   const uint32_t col_w = 32 * wave;    // first of the wave's S columns
 
   f32x4 Wv[8], qv[8], Uv, Pv[4], Kv[2][4];
-  bool q_ok;  // this lane's token exists in the loaded chunk
-  float G_tok, G_last;
+  float G_last;
   auto ws_of = [&](uint32_t c) { return a.chunk_ws + ((size_t)c * VH + h) * kDnChunkFloats; };
   // Rows past the last token read a valid row and are weighted by zero.
   // Masks are applied where the values are used, so the loads stay in
   // flight.  The MFMA reduction index is permuted: lane group grp of step
   // (m, e) carries k = 16 m + 4 grp + e, so each operand is one 16-byte read.
+  // Every operand is stored in this load order (dn_ws_index), so each load
+  // instruction reads 1 KB of consecutive memory.
+  const uint32_t lofs = 4 * (16 * grp + j);  // the lane's float4 within a 64-float4 block
   auto load_wqu = [&](uint32_t c) __attribute__((always_inline)) {
     const float* ws = ws_of(c);
-    const uint32_t t0 = c * kDnChunk, nt = min(kDnChunk, a.M - t0);
-    const float* Gg = ws + 2 * 64 * kCD + 64 * 64;
-    G_tok = Gg[tok];
-    G_last = Gg[63];
-    const float* qrow = a.conv_out + (size_t)(t0 + (tok < nt ? tok : 0)) * a.channels + kh * kCD;
-    q_ok = tok < nt;
+    G_last = ws[kDnWsG + 63];
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-      Wv[m] = *(const f32x4*)(ws + tok * kCD + 16 * m + 4 * grp);
-      qv[m] = *(const f32x4*)(qrow + 16 * m + 4 * grp);
+      Wv[m] = *(const f32x4*)(ws + kDnWsW + 256 * (8 * wave + m) + lofs);
+      qv[m] = *(const f32x4*)(ws + kDnWsQ + 256 * (8 * wave + m) + lofs);
     }
-    Uv = *(const f32x4*)(ws + 64 * kCD + tok * kCD + row0 + 4 * grp);
+    Uv = *(const f32x4*)(ws + kDnWsU + 1024 * rg + 256 * wave + lofs);
   };
   // P[tok][i] and K~^T[col][i] in the B layout (i = 16 m + 4 grp + e).
   auto load_pk = [&](uint32_t c) __attribute__((always_inline)) {
     const float* ws = ws_of(c);
-    const float* Pg = ws + 2 * 64 * kCD;
-    const float* KTg = Pg + 64 * 64 + 64;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      Pv[m] = *(const f32x4*)(Pg + tok * 64 + 16 * m + 4 * grp);
+      Pv[m] = *(const f32x4*)(ws + kDnWsP + 256 * (4 * wave + m) + lofs);
 #pragma unroll
-      for (int n = 0; n < 2; ++n) Kv[n][m] = *(const f32x4*)(KTg + (col_w + 16 * n + j) * 64 + 16 * m + 4 * grp);
+      for (int n = 0; n < 2; ++n) Kv[n][m] = *(const f32x4*)(ws + kDnWsKT + 256 * (8 * wave + 4 * n + m) + lofs);
     }
   };
 
@@ -1171,7 +1183,7 @@ __global__ __launch_bounds__(256) void dn_chunk_scan_kernel(DnArgs a) {
     const uint32_t t0 = c * kDnChunk, nt = min(kDnChunk, a.M - t0);
     const uint32_t cn = min(c + 1, nchunks - 1);  // the last chunk reloads itself (unused)
     // (a) U^T[row][tok] = U~[tok][row] - sum_k S[row][k] W[tok][k]
-    // (b1) O^T[row][tok] = Gamma_tok sum_k S[row][k] q[tok][k]
+    // (b1) O^T[row][tok] = sum_k S[row][k] Gamma_tok q[tok][k]
     floatx4 au[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     floatx4 ao[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -1183,9 +1195,9 @@ __global__ __launch_bounds__(256) void dn_chunk_scan_kernel(DnArgs a) {
         ao[m & 1] = mfma_f32_4(sa[e], qv[m][e], ao[m & 1]);
       }
     }
-    const float gam = q_ok ? expf(G_tok) : 0.0f, gam_c = expf(G_last);
+    const float gam_c = expf(G_last);
     const floatx4 acc_u = au[0] + au[1];
-    floatx4 acc_o = (ao[0] + ao[1]) * gam;
+    floatx4 acc_o = ao[0] + ao[1];
     // The S columns this wave updates, in the output layout, before any
     // wave writes the new values (after the barrier below).
 #pragma unroll
