@@ -1095,19 +1095,31 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
       for (int r = 0; r < 4; ++r) X[b][n] = mfma_f32_4(tv[r], acc[n][r], X[b][n]);
     }
   }
+  // X[b][n][r] is token 16 b + 4 grp + r, column 32 wave + 16 (n & 1) + j:
+  // four tokens of one column per lane, while the workspace order wants four
+  // columns of one token per float4.  Each wave transposes its tiles through
+  // its own LDS rows (W tiles, then U~ tiles) and stores 1 KB per instruction.
+  __syncthreads();  // every wave is past k^, A and T: their LDS is free
+  float* xt = prep_lds + wave * (8 * 16 * 20);  // 8 tiles of 16 x 16, row stride 20
 #pragma unroll
-  for (int b = 0; b < 4; ++b)
+  for (int half = 0; half < 2; ++half) {
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
+    for (int b = 0; b < 4; ++b)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        // X[b][n][r]: token 16 b + 4 grp + r, column 32 wave + 16 (n & 1) + j.
-        const uint32_t blk = 2 * wave + (n & 1);
-        if (n < 2)
-          Wg[dn_ws_index(b, blk, 4 * grp + r, j, 8)] = X[b][n][r];  // W[token][k], k block blk
-        else
-          Ug[dn_ws_index(blk, b, 4 * grp + r, j, 4)] = X[b][n][r];  // U~ columns of row group blk
-      }
+      for (int nn = 0; nn < 2; ++nn)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xt[(2 * b + nn) * 320 + (4 * grp + r) * 20 + j] = X[b][2 * half + nn][r];
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint32_t b = q / 2, nn = q % 2, blk = 2 * wave + nn;
+      const f32x4 v = *(const f32x4*)(xt + q * 320 + (lane % 16) * 20 + 4 * (lane / 16));
+      float* dst = half == 0 ? Wg + 256 * (8 * b + blk)   // W[token][k]: block (b, blk) of 8 column blocks
+                             : Ug + 256 * (4 * blk + b);  // U~: row group blk, token block b
+      *(f32x4*)(dst + 4 * lane) = v;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
 }
 
 // grid: VH * 8 blocks (block = rg * VH + h: the 8 row groups of a head share
