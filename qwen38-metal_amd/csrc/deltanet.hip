@@ -878,11 +878,17 @@ constexpr int kCD = 128;        // head dims of the chunked path
 constexpr int kCStride = 132;   // LDS row stride (floats) of [64][128] tiles: conflict-free 16-byte reads
 constexpr int kAStride = 68;    // LDS row stride of the 64 x 64 triangular matrix
 
+// SiLU from the hardware exp2 and reciprocal (about 2 ulp; the chunked path
+// is held to the fp64 oracle, not to the token-serial path's bits).
+__device__ __forceinline__ float silu_fast(float v) {
+  return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-v * 1.4426950408889634f));
+}
+
 // LDS of dn_chunk_prep_kernel (dynamic, so the compiler's register budget
 // follows the VGPR occupancy target rather than the LDS-bound one): k^ and
 // q^ rows of the chunk, then G and beta.  Once the products are formed the
 // q^ rows' space holds the 64 x 64 triangular matrix A.
-constexpr uint32_t kPrepLds = (2 * 64 * kCStride + 5 * 64) * 4;
+constexpr uint32_t kPrepLds = (2 * 64 * kCStride + 7 * 64) * 4;
 __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float prep_lds[];
   float* ks_s = prep_lds;
@@ -892,6 +898,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   float* dk_s = g_s + 128;  // e^{G_63 - G_i}
   float* bg_s = g_s + 192;  // beta_i e^{G_i}
   float* gm_s = g_s + 256;  // e^{G_i}
+  float* sc_s = g_s + 320;  // RMS scales of the chunk's q rows (0..63) and k rows (64..127)
   float* a_s = qs_s;  // [64][kAStride], once the q^ rows are consumed
   const uint32_t VH = a.value_heads;
   const uint32_t h = blockIdx.x % VH, c = blockIdx.x / VH;
@@ -909,36 +916,83 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   float* KTg = ws + kDnWsKT;
   float* Qg = ws + kDnWsQ;
 
-  // q^ and k^ rows of the chunk (zero past the last token) into LDS.
+  // The chunk's conv (kernel 4): thread tid owns key channel tid of key head
+  // kh (q 0..127, k 128..255) and walks the 64 tokens, 16 inputs per batch
+  // with the next batch in flight, writing silu(conv) into the q / k rows in
+  // LDS (zero past the last token).  The sums are conv_finish's, operation for
+  // operation; the SiLU is silu_fast.
+  const uint32_t kch = tid < kCD ? kh * kCD + tid : key_el + kh * kCD + (tid - kCD);
+  {
+    float w[4], win[3];
 #pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    const uint32_t idx = tid + 256 * p;  // float4 index over [64][32]
-    const uint32_t t = idx / 32, j4 = idx % 32;
-    f32x4 kv = {0.f, 0.f, 0.f, 0.f}, qv = {0.f, 0.f, 0.f, 0.f};
-    if (t < nt) {
-      const float* row = a.conv_out + (size_t)(t0 + t) * a.channels + kh * kCD + 4 * j4;
-      qv = *(const f32x4*)row;
-      kv = *(const f32x4*)(row + key_el);
+    for (int q = 0; q < 4; ++q) w[q] = a.conv_w[(size_t)kch * 4 + q];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) win[q] = conv_input(a, kch, (int)t0 - 3 + q);
+    float* dst = tid < kCD ? qs_s + tid : ks_s + (tid - kCD);
+    float xn[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) xn[k] = a.qkv[(size_t)min(t0 + k, a.M - 1) * a.channels + kch];
+    for (int tb = 0; tb < 64; tb += 16) {
+      float xb[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) xb[k] = xn[k];
+      const uint32_t tn = t0 + min(tb + 16, 48);  // the last batch reloads itself (unused)
+#pragma unroll
+      for (int k = 0; k < 16; ++k) xn[k] = a.qkv[(size_t)min(tn + k, a.M - 1) * a.channels + kch];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const float x = xb[k];
+        float sum = __fmul_rn(w[3], x);
+        sum = fmaf(w[0], win[0], sum);
+        sum = fmaf(w[1], win[1], sum);
+        sum = fmaf(w[2], win[2], sum);
+        win[0] = win[1];
+        win[1] = win[2];
+        win[2] = x;
+        dst[(tb + k) * kCStride] = (uint32_t)(tb + k) < nt ? silu_fast(sum) : 0.0f;
+      }
     }
-    *(f32x4*)(ks_s + t * kCStride + 4 * j4) = kv;
-    *(f32x4*)(qs_s + t * kCStride + 4 * j4) = qv;
   }
   // v of the wave's U~ columns (32 w + 16 nn + j) for the solve at the end,
-  // loaded now so the loads overlap everything before it (rows past the last
-  // token read row 0 and are masked at use).
+  // convolved here in registers: tokens 16 b + 4 grp + r need the inputs from
+  // three tokens earlier on (rows past the last token are masked at use).
   const uint32_t j = lane & 15, grp = lane >> 4;
   float vpre[4][2][4];
   {
-    const float* vsrc = a.conv_out + (size_t)t0 * a.channels + 2 * key_el + h * kCD + 32 * wave + j;
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int nn = 0; nn < 2; ++nn) {
+      const uint32_t vch = 2 * key_el + h * kCD + 32 * wave + 16 * nn + j;
+      float w[4];
 #pragma unroll
-      for (int nn = 0; nn < 2; ++nn)
+      for (int q = 0; q < 4; ++q) w[q] = a.conv_w[(size_t)vch * 4 + q];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        float x[7];
+#pragma unroll
+        for (int q = 0; q < 7; ++q) x[q] = conv_input(a, vch, min((int)(t0 + 16 * b + 4 * grp) - 3 + q, (int)a.M - 1));
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const uint32_t t = 16 * b + 4 * grp + r;
-          vpre[b][nn][r] = vsrc[(size_t)(t < nt ? t : 0) * a.channels + 16 * nn];
+          float sum = __fmul_rn(w[3], x[r + 3]);
+          sum = fmaf(w[0], x[r], sum);
+          sum = fmaf(w[1], x[r + 1], sum);
+          sum = fmaf(w[2], x[r + 2], sum);
+          vpre[b][nn][r] = silu_fast(sum);
         }
+      }
+    }
+  }
+  // The state's conv history after the last token: raw inputs of the final
+  // three tokens (from the old history when M < 3), written by the last
+  // chunk's workgroups (key channels by the first value head of each key head).
+  if (c + 1 == (a.M + kDnChunk - 1) / kDnChunk) {
+    if (h % (VH / a.key_heads) == 0)
+#pragma unroll
+      for (int q = 0; q < 3; ++q) a.hist_out[(size_t)kch * 3 + q] = conv_input(a, kch, (int)a.M - 3 + q);
+    if (tid < kCD) {
+      const uint32_t vch = 2 * key_el + h * kCD + tid;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) a.hist_out[(size_t)vch * 3 + q] = conv_input(a, vch, (int)a.M - 3 + q);
+    }
   }
   // Log decays, their running sum and beta (wave 0; padding tokens: lg = 0,
   // beta = 0, so they change nothing).
@@ -961,6 +1015,34 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
     bg_s[lane] = beta * expf(G);
     gm_s[lane] = expf(G);
     Gg[lane] = G;
+  }
+  __syncthreads();
+  // prep_key_head's RMS scales: row ri (q rows 0..63, k rows 64..127), lane l
+  // sums the squares of columns l and l + 64, then a wave sum.
+#pragma unroll 4
+  for (int q = 0; q < 32; ++q) {
+    const uint32_t ri = 32 * wave + q;
+    const float* row = (ri < 64 ? qs_s + ri * kCStride : ks_s + (ri - 64) * kCStride) + lane;
+    float ss = 0.0f;
+    ss = fmaf(row[0], row[0], ss);
+    ss = fmaf(row[64], row[64], ss);
+    ss = wave_sum(ss);
+    if (lane == 0) sc_s[ri] = 1.0f / sqrtf(ss / (float)kCD + a.eps);
+  }
+  __syncthreads();
+  {
+    const float inv = 1.0f / sqrtf((float)kCD);
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      const uint32_t idx = tid + 256 * p;  // float4 index over [128 rows][32]
+      const uint32_t ri = idx / 32, c4 = idx % 32;
+      float* px = (ri < 64 ? qs_s + ri * kCStride : ks_s + (ri - 64) * kCStride) + 4 * c4;
+      const float sc = sc_s[ri];
+      f32x4 v = *(const f32x4*)px;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = ri < 64 ? v[e] * sc * inv * inv : v[e] * sc * inv;
+      *(f32x4*)px = v;
+    }
   }
   __syncthreads();
 
@@ -1273,7 +1355,9 @@ bool dn_step_split(const DnArgs& a) {
 }
 
 bool dn_use_chunked(const DnArgs& a) {
-  if (a.dk != kCD || a.dv != kCD || a.snap_rows > 0 || a.M <= 1 || a.value_heads % a.key_heads != 0) return false;
+  if (a.dk != kCD || a.dv != kCD || a.kernel != 4 || a.snap_rows > 0 || a.M <= 1 ||
+      a.value_heads % a.key_heads != 0)
+    return false;
   const char* env = getenv("QM38_DN_CHUNKED");
   if (env) return atoi(env) != 0;
   return a.M >= 2 * kDnChunk;
@@ -1323,7 +1407,10 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
     return hipGetLastError();
   }
   const uint32_t units = a.key_heads + a.value_heads;
-  if (a.kernel <= kTaps) {
+  const bool chunked = dn_use_chunked(a);
+  if (chunked) {
+    // The chunk prep kernel convolves its own inputs.
+  } else if (a.kernel <= kTaps) {
     const uint32_t items = ((a.M + kConvTile - 1) / kConvTile) * units;
     const dim3 grid((items + 3) / 4), block(kThreads);
     const uint32_t ns = (std::max(a.dk, a.dv) + 63) / 64;
@@ -1332,7 +1419,7 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
     const uint32_t prep_items = a.M * units;
     hipLaunchKernelGGL(dn_conv_prepare_kernel, dim3((prep_items + 3) / 4), dim3(kThreads), 0, st, a);
   }
-  if (dn_use_chunked(a)) {
+  if (chunked) {
     if (!a.chunk_ws) return hipErrorInvalidValue;
     const uint32_t nchunks = (a.M + kDnChunk - 1) / kDnChunk;
     hipLaunchKernelGGL(dn_chunk_prep_kernel, dim3(nchunks * a.value_heads), dim3(256), kPrepLds, st, a);
