@@ -888,7 +888,7 @@ __device__ __forceinline__ float silu_fast(float v) {
 // follows the VGPR occupancy target rather than the LDS-bound one): k^ and
 // q^ rows of the chunk, then G and beta.  Once the products are formed the
 // q^ rows' space holds the 64 x 64 triangular matrix A.
-constexpr uint32_t kPrepLds = (2 * 64 * kCStride + 7 * 64) * 4;
+constexpr uint32_t kPrepLds = (2 * 64 * kCStride + 9 * 64) * 4;
 __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float prep_lds[];
   float* ks_s = prep_lds;
@@ -899,6 +899,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   float* bg_s = g_s + 192;  // beta_i e^{G_i}
   float* gm_s = g_s + 256;  // e^{G_i}
   float* sc_s = g_s + 320;  // RMS scales of the chunk's q rows (0..63) and k rows (64..127)
+  double* gd_s = (double*)(g_s + 448);  // G in fp64: pairwise differences without cancellation
   float* a_s = qs_s;  // [64][kAStride], once the q^ rows are consumed
   const uint32_t VH = a.value_heads;
   const uint32_t h = blockIdx.x % VH, c = blockIdx.x / VH;
@@ -1003,15 +1004,19 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
       lg = -expf(a.a_log[h]) * softplus_f(a.a[ti] + a.dt_bias[h]);
       beta = sigmoid_f(a.b[ti]);
     }
-    float G = lg;
+    // The running sum in fp64: a decay e^{G_t - G_i} taken from two long fp32
+    // sums would lose the low bits of G_t - G_i to cancellation.
+    double Gd = lg;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-      const float o = __shfl_up(G, off);
-      if (lane >= (uint32_t)off) G += o;
+      const double o = __shfl_up(Gd, off);
+      if (lane >= (uint32_t)off) Gd += o;
     }
+    const float G = (float)Gd;
+    gd_s[lane] = Gd;
     g_s[lane] = G;
     beta_s[lane] = beta;
-    dk_s[lane] = expf(__shfl(G, 63) - G);
+    dk_s[lane] = expf((float)(__shfl(Gd, 63) - Gd));
     bg_s[lane] = beta * expf(G);
     gm_s[lane] = expf(G);
     Gg[lane] = G;
@@ -1098,7 +1103,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t t = 16 * tm + 4 * grp + r;
-      Pg[dn_ws_index(tm, tn, 4 * grp + r, j, 4)] = i <= t ? expf(g_s[t] - g_s[i]) * acc[r] : 0.0f;
+      Pg[dn_ws_index(tm, tn, 4 * grp + r, j, 4)] = i <= t ? expf((float)(gd_s[t] - gd_s[i])) * acc[r] : 0.0f;
     }
   }
   __syncthreads();  // the q^ rows are consumed; their space becomes A
@@ -1110,7 +1115,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t t = 16 * tm + 4 * grp + r;
-      a_s[t * kAStride + i] = i < t ? -(beta_s[t] * expf(g_s[t] - g_s[i]) * acc[r]) : 0.0f;  // -A
+      a_s[t * kAStride + i] = i < t ? -(beta_s[t] * expf((float)(gd_s[t] - gd_s[i])) * acc[r]) : 0.0f;  // -A
     }
   }
   // P is zero above the diagonal blocks too, so its readers need no bounds.

@@ -67,6 +67,10 @@ def _close(got, ref, tol=TOL, what=""):
     assert np.all(np.isfinite(got)), what
     scale = max(np.max(np.abs(ref)), 1e-30)
     err = np.max(np.abs(got - ref)) / scale
+    log = os.environ.get("QM38_TOL_LOG")  # measured errors, for choosing the bound
+    if log:
+        with open(log, "a") as f:
+            f.write(f"{os.environ.get('PYTEST_CURRENT_TEST', '?').split(' ')[0]}\t{what}\t{err:.3e}\t-\t{tol:.1e}\n")
     assert err <= tol, f"{what}: rel err {err:.3e} > {tol:.1e}"
     return err
 
