@@ -884,6 +884,29 @@ __device__ __forceinline__ float silu_fast(float v) {
   return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-v * 1.4426950408889634f));
 }
 
+// fp32 x = hi + lo + O(2^-18 |x|) in bf16 (both rounded to nearest even):
+// products of split operands as hi*hi + hi*lo + lo*hi on the bf16 MFMA keep
+// about 2^-17 relative error per product, against 2^-9 for plain bf16.
+// Eight floats become the bf16x8 operands hi and lo (element e = float e).
+__device__ __forceinline__ void split_bf16x8(const f32x4& a, const f32x4& b, u32x4& hi, u32x4& lo) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const bf2 h = {(__bf16)v[2 * p], (__bf16)v[2 * p + 1]};
+    const uint32_t hb = __builtin_bit_cast(uint32_t, h);
+    const bf2 l = {(__bf16)(v[2 * p] - __uint_as_float(hb << 16)),
+                   (__bf16)(v[2 * p + 1] - __uint_as_float(hb & 0xFFFF0000u))};
+    hi[p] = hb;
+    lo[p] = __builtin_bit_cast(uint32_t, l);
+  }
+}
+// Split-bf16 operand blocks in the workspace: block (nb, s) of an operand
+// with S steps of 32 along its reduction dimension holds, for lane
+// (j, g) = (lane % 16, lane / 16), the 8 elements [16 nb + j][32 s + 8 g + e]:
+// hi at 8 lane + e, lo 512 further (in bf16 units; 2 KB per block).
+__device__ __forceinline__ uint32_t dn_b3_block(uint32_t nb, uint32_t s, uint32_t S) { return (nb * S + s) * 1024; }
+
 // LDS of dn_chunk_prep_kernel (dynamic, so the compiler's register budget
 // follows the VGPR occupancy target rather than the LDS-bound one): k^ and
 // q^ rows of the chunk, then G and beta.  Once the products are formed the
@@ -1051,25 +1074,39 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   }
   __syncthreads();
 
-  // The scan's operands in its MFMA operand order (dn_ws_index): K~^T[c][i] =
-  // e^{G_63 - G_i} k^[i][c] for the state update and Gamma_t q^[t][k] for
-  // the output, one contiguous 16-byte store per lane and float4.
+  // The scan's B operands as split bf16 blocks (dn_b3_block): K~^T[c][i] =
+  // e^{G_63 - G_i} k^[i][c] (8 column blocks, 2 steps over i) for the state
+  // update and Gamma_t q^[t][k] (4 token blocks, 4 steps over k) for the
+  // output; 2 x 16 bytes per lane and block.
+  {
+    uint16_t* kt3 = (uint16_t*)KTg;
+    uint16_t* q3 = (uint16_t*)Qg;
 #pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    const uint32_t idx = tid + 256 * p;  // float4 index: [w 4][n 2][m 4][g 4][j 16]
-    const uint32_t jj = idx % 16, gg = (idx / 16) % 4, mm = (idx / 64) % 4, nn = (idx / 256) % 2, ww = idx / 512;
-    const uint32_t col = 32 * ww + 16 * nn + jj, i0 = 16 * mm + 4 * gg;
-    f32x4 v;
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t item = tid + 256 * p, ln = item % 64, blk = item / 64;  // blk = nb * 2 + s
+      const uint32_t col = 16 * (blk / 2) + ln % 16, i0 = 32 * (blk % 2) + 8 * (ln / 16);
+      f32x4 v0, v1;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = dk_s[i0 + e] * ks_s[(i0 + e) * kCStride + col];
-    *(f32x4*)(KTg + 4 * idx) = v;
-  }
+      for (int e = 0; e < 4; ++e) {
+        v0[e] = dk_s[i0 + e] * ks_s[(i0 + e) * kCStride + col];
+        v1[e] = dk_s[i0 + 4 + e] * ks_s[(i0 + 4 + e) * kCStride + col];
+      }
+      u32x4 hi, lo;
+      split_bf16x8(v0, v1, hi, lo);
+      *(u32x4*)(kt3 + blk * 1024 + 8 * ln) = hi;
+      *(u32x4*)(kt3 + blk * 1024 + 512 + 8 * ln) = lo;
+    }
 #pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    const uint32_t idx = tid + 256 * p;  // float4 index: [w 4][m 8][g 4][j 16]
-    const uint32_t jj = idx % 16, gg = (idx / 16) % 4, mm = (idx / 64) % 8, ww = idx / 512;
-    const uint32_t t = 16 * ww + jj;
-    *(f32x4*)(Qg + 4 * idx) = *(const f32x4*)(qs_s + t * kCStride + 16 * mm + 4 * gg) * gm_s[t];
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t item = tid + 256 * p, ln = item % 64, blk = item / 64;  // blk = nb * 4 + s
+      const uint32_t t = 16 * (blk / 4) + ln % 16, k0 = 32 * (blk % 4) + 8 * (ln / 16);
+      const float* src = qs_s + t * kCStride + k0;
+      const float gm = gm_s[t];
+      u32x4 hi, lo;
+      split_bf16x8(*(const f32x4*)src * gm, *(const f32x4*)(src + 4) * gm, hi, lo);
+      *(u32x4*)(q3 + blk * 1024 + 8 * ln) = hi;
+      *(u32x4*)(q3 + blk * 1024 + 512 + 8 * ln) = lo;
+    }
   }
 
   // Q K^T, then K K^T, on the lower-triangular 16 x 16 tiles (tn <= tm):
@@ -1197,13 +1234,26 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) xt[(2 * b + nn) * 320 + (4 * grp + r) * 20 + j] = X[b][2 * half + nn][r];
     __builtin_amdgcn_wave_barrier();
+    if (half == 0) {
+      // W[token][k] as split bf16: token block b, step s = wave (k 32 w ..
+      // 32 w + 31): lane (j, g) takes row j, columns 8 g .. 8 g + 7 of the
+      // wave's 32 columns, i.e. tile nn = g / 2 at column 8 (g % 2).
+      uint16_t* w3 = (uint16_t*)Wg;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint32_t b = q / 2, nn = q % 2, blk = 2 * wave + nn;
-      const f32x4 v = *(const f32x4*)(xt + q * 320 + (lane % 16) * 20 + 4 * (lane / 16));
-      float* dst = half == 0 ? Wg + 256 * (8 * b + blk)   // W[token][k]: block (b, blk) of 8 column blocks
-                             : Ug + 256 * (4 * blk + b);  // U~: row group blk, token block b
-      *(f32x4*)(dst + 4 * lane) = v;
+      for (int b = 0; b < 4; ++b) {
+        const float* src = xt + (2 * b + grp / 2) * 320 + j * 20 + 8 * (grp % 2);
+        u32x4 hi, lo;
+        split_bf16x8(*(const f32x4*)src, *(const f32x4*)(src + 4), hi, lo);
+        *(u32x4*)(w3 + dn_b3_block(b, wave, 4) + 8 * lane) = hi;
+        *(u32x4*)(w3 + dn_b3_block(b, wave, 4) + 512 + 8 * lane) = lo;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const uint32_t b = q / 2, nn = q % 2, blk = 2 * wave + nn;
+        const f32x4 v = *(const f32x4*)(xt + q * 320 + (lane % 16) * 20 + 4 * (lane / 16));
+        *(f32x4*)(Ug + 256 * (4 * blk + b) + 4 * lane) = v;  // U~: row group blk, token block b
+      }
     }
     __builtin_amdgcn_wave_barrier();
   }
@@ -1232,7 +1282,8 @@ __global__ __launch_bounds__(256) void dn_chunk_scan_kernel(DnArgs a) {
   const uint32_t tok = 16 * wave + j;  // this lane's token column in U and O
   const uint32_t col_w = 32 * wave;    // first of the wave's S columns
 
-  f32x4 Wv[8], qv[8], Uv, Pv[4], Kv[2][4];
+  u32x4 Wh[4], Wl[4], Qh[4], Ql[4], Kh[2][2], Kl[2][2];  // split bf16 B operands
+  f32x4 Uv, Pv[4];
   float G_last;
   auto ws_of = [&](uint32_t c) { return a.chunk_ws + ((size_t)c * VH + h) * kDnChunkFloats; };
   // Rows past the last token read a valid row and are weighted by zero.
@@ -1245,22 +1296,32 @@ __global__ __launch_bounds__(256) void dn_chunk_scan_kernel(DnArgs a) {
   auto load_wqu = [&](uint32_t c) __attribute__((always_inline)) {
     const float* ws = ws_of(c);
     G_last = ws[kDnWsG + 63];
+    const uint16_t* w3 = (const uint16_t*)(ws + kDnWsW);
+    const uint16_t* q3 = (const uint16_t*)(ws + kDnWsQ);
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      Wv[m] = *(const f32x4*)(ws + kDnWsW + 256 * (8 * wave + m) + lofs);
-      qv[m] = *(const f32x4*)(ws + kDnWsQ + 256 * (8 * wave + m) + lofs);
+    for (int s = 0; s < 4; ++s) {
+      const uint32_t o = dn_b3_block(wave, s, 4) + 8 * lane;
+      Wh[s] = *(const u32x4*)(w3 + o);
+      Wl[s] = *(const u32x4*)(w3 + o + 512);
+      Qh[s] = *(const u32x4*)(q3 + o);
+      Ql[s] = *(const u32x4*)(q3 + o + 512);
     }
     Uv = *(const f32x4*)(ws + kDnWsU + 1024 * rg + 256 * wave + lofs);
   };
-  // P[tok][i] and K~^T[col][i] in the B layout (i = 16 m + 4 grp + e).
+  // P[tok][i] (fp32, i = 16 m + 4 grp + e) and K~^T[col][i] (split bf16).
   auto load_pk = [&](uint32_t c) __attribute__((always_inline)) {
     const float* ws = ws_of(c);
+    const uint16_t* kt3 = (const uint16_t*)(ws + kDnWsKT);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      Pv[m] = *(const f32x4*)(ws + kDnWsP + 256 * (4 * wave + m) + lofs);
+    for (int m = 0; m < 4; ++m) Pv[m] = *(const f32x4*)(ws + kDnWsP + 256 * (4 * wave + m) + lofs);
 #pragma unroll
-      for (int n = 0; n < 2; ++n) Kv[n][m] = *(const f32x4*)(ws + kDnWsKT + 256 * (8 * wave + 4 * n + m) + lofs);
-    }
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint32_t o = dn_b3_block(2 * wave + n, s, 2) + 8 * lane;
+        Kh[n][s] = *(const u32x4*)(kt3 + o);
+        Kl[n][s] = *(const u32x4*)(kt3 + o + 512);
+      }
   };
 
   // Initial rows of S into LDS.
@@ -1283,20 +1344,25 @@ __global__ __launch_bounds__(256) void dn_chunk_scan_kernel(DnArgs a) {
     const uint32_t cn = min(c + 1, nchunks - 1);  // the last chunk reloads itself (unused)
     // (a) U^T[row][tok] = U~[tok][row] - sum_k S[row][k] W[tok][k]
     // (b1) O^T[row][tok] = sum_k S[row][k] Gamma_tok q[tok][k]
-    floatx4 au[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    floatx4 ao[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    // Split-bf16 products on v_mfma_f32_16x16x32_bf16: S (A operand, row j,
+    // k = 32 s + 8 grp + e) is split here, W and Gamma q come split.
+    floatx4 au[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    floatx4 ao[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const f32x4 sa = *(const f32x4*)(s_s + j * kCStride + 16 * m + 4 * grp);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        au[m & 1] = mfma_f32_4(sa[e], Wv[m][e], au[m & 1]);
-        ao[m & 1] = mfma_f32_4(sa[e], qv[m][e], ao[m & 1]);
-      }
+    for (int s = 0; s < 4; ++s) {
+      const float* sp = s_s + j * kCStride + 32 * s + 8 * grp;
+      u32x4 sh, sl;
+      split_bf16x8(*(const f32x4*)sp, *(const f32x4*)(sp + 4), sh, sl);
+      au[0] = mfma16x16x32(sh, Wh[s], au[0]);
+      ao[0] = mfma16x16x32(sh, Qh[s], ao[0]);
+      au[1] = mfma16x16x32(sh, Wl[s], au[1]);
+      ao[1] = mfma16x16x32(sh, Ql[s], ao[1]);
+      au[2] = mfma16x16x32(sl, Wh[s], au[2]);
+      ao[2] = mfma16x16x32(sl, Qh[s], ao[2]);
     }
     const float gam_c = expf(G_last);
-    const floatx4 acc_u = au[0] + au[1];
-    floatx4 acc_o = ao[0] + ao[1];
+    const floatx4 acc_u = au[0] + (au[1] + au[2]);
+    floatx4 acc_o = ao[0] + (ao[1] + ao[2]);
     // The S columns this wave updates, in the output layout, before any
     // wave writes the new values (after the barrier below).
 #pragma unroll
@@ -1315,12 +1381,23 @@ __global__ __launch_bounds__(256) void dn_chunk_scan_kernel(DnArgs a) {
     for (int m = 0; m < 4; ++m) {
       const f32x4 ua = *(const f32x4*)(u_s + j * kAStride + 16 * m + 4 * grp);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        ap[e & 1] = mfma_f32_4(ua[e], Pv[m][e], ap[e & 1]);
-#pragma unroll
-        for (int n = 0; n < 2; ++n) d[n] = mfma_f32_4(ua[e], Kv[n][m][e], d[n]);
-      }
+      for (int e = 0; e < 4; ++e) ap[e & 1] = mfma_f32_4(ua[e], Pv[m][e], ap[e & 1]);
     }
+    floatx4 dx[2][2] = {{{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}, {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const float* up = u_s + j * kAStride + 32 * s + 8 * grp;
+      u32x4 uh, ul;
+      split_bf16x8(*(const f32x4*)up, *(const f32x4*)(up + 4), uh, ul);
+#pragma unroll
+      for (int n = 0; n < 2; ++n) d[n] = mfma16x16x32(uh, Kh[n][s], d[n]);
+#pragma unroll
+      for (int n = 0; n < 2; ++n) dx[n][0] = mfma16x16x32(uh, Kl[n][s], dx[n][0]);
+#pragma unroll
+      for (int n = 0; n < 2; ++n) dx[n][1] = mfma16x16x32(ul, Kh[n][s], dx[n][1]);
+    }
+#pragma unroll
+    for (int n = 0; n < 2; ++n) d[n] += dx[n][0] + dx[n][1];
     load_pk(cn);
     acc_o = ap[0] + ap[1];
     // A buffer store bounded to the chunk's nt rows: tokens past the end are
