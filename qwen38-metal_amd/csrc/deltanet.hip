@@ -30,6 +30,7 @@ namespace qm {
 namespace {
 
 constexpr int kThreads = 256;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kLanesPerRow = 16;                   // lanes sharing one S row in the scan
 constexpr int kRowsPerWg = kThreads / kLanesPerRow;  // S rows per scan workgroup
 constexpr int kTokChunk = 32;                      // tokens staged in LDS per scan iteration
@@ -415,21 +416,39 @@ __global__ __launch_bounds__(kThreads) void dn_scan_kernel(DnArgs a) {
   }
 }
 
-// Gated RMS norm of one (token, value head) output row by one wave: reads
-// o_in[c], writes out[c] = o * rsqrt(mean o^2 + eps) * norm * silu(z).
-// Shared by the prefill path and the fused step.
-// Core of the gated norm for one row held by a wave (lane: elements lane +
-// 64 i): v the outputs, nrm the norm weights, sz = silu(z).
+// Gated RMS norm of (token, value head) output rows: out[c] = o *
+// rsqrt(mean o^2 + eps) * norm * silu(z).  A row is held by LPR lanes (64, or
+// 32 when dv <= 128 so two rows share a wave); lane rl of the row holds
+// elements 4 rl .. 4 rl + 3 (dv <= 256).  The sum of squares is reduced over
+// the row's lanes; with dv <= 128 a 64-lane row's upper lanes add only zeros,
+// so both widths give the same bits.
+__device__ __forceinline__ float half_sum(float v) {  // wave_sum within each 32-lane half
+  v = row16_sum(v);
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+template <int LPR = 64, bool VEC = false>
 __device__ __forceinline__ void gate_norm_core(const DnArgs& a, const float (&v)[4], const float (&nrm)[4],
-                                               const float (&sz)[4], float* out, uint32_t lane, uint16_t* out_bf16) {
+                                               const float (&sz)[4], float* out, uint32_t rl, uint16_t* out_bf16,
+                                               bool live = true) {
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) ss += v[i] * v[i];
-  ss = wave_sum(ss);
+  ss = LPR == 64 ? wave_sum(ss) : half_sum(ss);
   const float scale = 1.0f / sqrtf(ss / (float)a.dv + a.eps);
+  if (!live) return;
+  if (VEC) {  // dv % 4 == 0: the lane's four elements are all in the row or all past it
+    if (4 * rl < a.dv) {
+      f32x4 r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = v[i] * scale * nrm[i] * sz[i];
+      *(f32x4*)(out + 4 * rl) = r;
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t c = lane + 64 * i;
+    const uint32_t c = 4 * rl + i;
     if (c < a.dv) {
       const float r = v[i] * scale * nrm[i] * sz[i];
       out[c] = r;
@@ -438,62 +457,69 @@ __device__ __forceinline__ void gate_norm_core(const DnArgs& a, const float (&v)
   }
 }
 // Norm weights and silu(z) of one row (zero past dv).
-__device__ __forceinline__ void gate_norm_operands(const DnArgs& a, const float* z, uint32_t lane, float (&nrm)[4],
+__device__ __forceinline__ void gate_norm_operands(const DnArgs& a, const float* z, uint32_t rl, float (&nrm)[4],
                                                    float (&sz)[4]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t c = lane + 64 * i;
+    const uint32_t c = 4 * rl + i;
     nrm[i] = c < a.dv ? a.norm[c] : 0.0f;
     sz[i] = c < a.dv ? silu_f(z[c]) : 0.0f;
   }
 }
-// Gated RMS norm of one (token, value head) output row by one wave: reads
-// o_in[c], writes out[c] = o * rsqrt(mean o^2 + eps) * norm * silu(z).
-// Shared by the prefill path and the step kernels.
+// One row by one wave: reads o_in[c], writes out[c].
 __device__ __forceinline__ void gate_norm_row(const DnArgs& a, const float* o_in, const float* z, float* out,
                                               uint32_t lane, uint16_t* out_bf16 = nullptr) {
   float v[4], nrm[4], sz[4];  // dv <= 256
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t c = lane + 64 * i;
+    const uint32_t c = 4 * lane + i;
     v[i] = c < a.dv ? o_in[c] : 0.0f;
   }
   gate_norm_operands(a, z, lane, nrm, sz);
   gate_norm_core(a, v, nrm, sz, out, lane, out_bf16);
 }
 
-// One wave per (token, value head), blocks of 1 or 4 waves; in place on `out`.
-// kNormRows (token, head) rows per wave, all of their loads issued before
-// the first row is normalised; the per-row arithmetic is gate_norm_core's.
-constexpr int kNormRows = 4;
+// In place on `out`, kNormSlots x (64 / LPR) rows per wave, all of their
+// loads (16 bytes a lane when VEC, dv % 4 == 0) issued before the first row
+// is normalised; the per-row arithmetic is gate_norm_core's.
+constexpr int kNormSlots = 4;
+template <int LPR, bool VEC>
 __global__ __launch_bounds__(kThreads) void dn_gate_norm_kernel(DnArgs a) {
+  constexpr int kRows = 64 / LPR;  // rows per slot
   const uint32_t items = a.M * a.value_heads;
-  const uint32_t first = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * kNormRows;
+  const uint32_t first = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * kNormSlots * kRows;
   if (first >= items) return;
-  const uint32_t lane = threadIdx.x & 63;
-  float v[kNormRows][4], sz[kNormRows][4], nrm[4];
+  const uint32_t lane = threadIdx.x & 63, rl = lane % LPR, hs = lane / LPR;
+  const bool lane_live = 4 * rl < a.dv;
+  float v[kNormSlots][4], sz[kNormSlots][4], nrm[4];
 #pragma unroll
-  for (int r = 0; r < kNormRows; ++r) {
-    const size_t base = (size_t)min(first + r, items - 1) * a.dv;
+  for (int q = 0; q < kNormSlots; ++q) {
+    const size_t base = (size_t)min(first + q * kRows + hs, items - 1) * a.dv + 4 * min(rl, (a.dv - 1) / 4);
+    if (VEC) {
+      const f32x4 ov = *(const f32x4*)(a.out + base), zv = *(const f32x4*)(a.z + base);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t c = lane + 64 * i;
-      v[r][i] = c < a.dv ? a.out[base + c] : 0.0f;
-      sz[r][i] = c < a.dv ? a.z[base + c] : 0.0f;
+      for (int i = 0; i < 4; ++i) {
+        v[q][i] = lane_live ? ov[i] : 0.0f;
+        sz[q][i] = lane_live ? zv[i] : 0.0f;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool ok = 4 * rl + i < a.dv;
+        v[q][i] = ok ? a.out[base + i] : 0.0f;
+        sz[q][i] = ok ? a.z[base + i] : 0.0f;
+      }
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t c = lane + 64 * i;
-    nrm[i] = c < a.dv ? a.norm[c] : 0.0f;
-  }
+  for (int i = 0; i < 4; ++i) nrm[i] = 4 * rl + i < a.dv ? a.norm[4 * rl + i] : 0.0f;
 #pragma unroll
-  for (int r = 0; r < kNormRows; ++r) {
-    if (first + r >= items) break;
+  for (int q = 0; q < kNormSlots; ++q) {
+    if (first + q * kRows >= items) break;  // wave-uniform
+    const uint32_t row = first + q * kRows + hs;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sz[r][i] = silu_f(sz[r][i]);  // gate_norm_operands
-    float* o = a.out + (size_t)(first + r) * a.dv;
-    gate_norm_core(a, v[r], nrm, sz[r], o, lane, nullptr);
+    for (int i = 0; i < 4; ++i) sz[q][i] = silu_f(sz[q][i]);  // gate_norm_operands
+    gate_norm_core<LPR, VEC>(a, v[q], nrm, sz[q], a.out + (size_t)row * a.dv, rl, nullptr, row < items);
   }
 }
 
@@ -712,11 +738,11 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_split_kernel(DnArgs a) {
   }
   __syncthreads();
   if (last_s == 0u || wave != 0) return;
-  // The head's dv outputs (lane c: c + 64 i), then the shared gated norm.
+  // The head's dv outputs (lane l: 4 l .. 4 l + 3), then the shared gated norm.
   float ov[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t c = lane + 64 * i;
+    const uint32_t c = 4 * lane + i;
     const float v = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ro, min(c, a.dv - 1) * 4, 0, kSys));
     ov[i] = c < a.dv ? v : 0.0f;
   }
@@ -869,7 +895,6 @@ __global__ __launch_bounds__(kThreads) void dn_conv_tiled_kernel(DnArgs a) {
 // solve); dn_chunk_scan_kernel then walks the chunks in order.  Rows of S
 // stay independent (row j of S only meets column j of U), so each workgroup
 // owns 16 rows of one head in the same way as the token scan.
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ floatx4 mfma_f32_4(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -1519,9 +1544,19 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
     else
       launch_scan<16>(a, st);
   }
-  const uint32_t norm_waves = (a.M * a.value_heads + kNormRows - 1) / kNormRows;
+  const uint32_t lpr = a.dv <= 128 ? 32 : 64, per_wave = kNormSlots * (64 / lpr);
+  const uint32_t norm_waves = (a.M * a.value_heads + per_wave - 1) / per_wave;
   const uint32_t wpb = norm_waves >= 1024 ? kThreads / 64 : 1;
-  hipLaunchKernelGGL(dn_gate_norm_kernel, dim3((norm_waves + wpb - 1) / wpb), dim3(64 * wpb), 0, st, a);
+  const dim3 ngrid((norm_waves + wpb - 1) / wpb), nblock(64 * wpb);
+  const bool vec = a.dv % 4 == 0;
+  if (lpr == 32 && vec)
+    hipLaunchKernelGGL((dn_gate_norm_kernel<32, true>), ngrid, nblock, 0, st, a);
+  else if (lpr == 32)
+    hipLaunchKernelGGL((dn_gate_norm_kernel<32, false>), ngrid, nblock, 0, st, a);
+  else if (vec)
+    hipLaunchKernelGGL((dn_gate_norm_kernel<64, true>), ngrid, nblock, 0, st, a);
+  else
+    hipLaunchKernelGGL((dn_gate_norm_kernel<64, false>), ngrid, nblock, 0, st, a);
   return hipGetLastError();
 }
 
