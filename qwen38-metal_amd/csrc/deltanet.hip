@@ -937,7 +937,8 @@ __device__ __forceinline__ uint32_t dn_b3_block(uint32_t nb, uint32_t s, uint32_
 // q^ rows of the chunk, then G and beta.  Once the products are formed the
 // q^ rows' space holds the 64 x 64 triangular matrix A.
 constexpr uint32_t kPrepLds = (2 * 64 * kCStride + 9 * 64) * 4;
-__global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
+constexpr int kPrepThreads = 512;  // 8 waves
+__global__ __launch_bounds__(kPrepThreads, 2) void dn_chunk_prep_kernel(DnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float prep_lds[];
   float* ks_s = prep_lds;
   float* qs_s = prep_lds + 64 * kCStride;
@@ -957,6 +958,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   const uint32_t nt = min(kDnChunk, a.M - t0);
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t j = lane & 15, grp = lane >> 4;
   float* ws = a.chunk_ws + ((size_t)c * VH + h) * kDnChunkFloats;
   float* Wg = ws + kDnWsW;
   float* Ug = ws + kDnWsU;
@@ -965,29 +967,33 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   float* KTg = ws + kDnWsKT;
   float* Qg = ws + kDnWsQ;
 
-  // The chunk's conv (kernel 4): thread tid owns key channel tid of key head
-  // kh (q 0..127, k 128..255) and walks the 64 tokens, 16 inputs per batch
-  // with the next batch in flight, writing silu(conv) into the q / k rows in
-  // LDS (zero past the last token).  The sums are conv_finish's, operation for
-  // operation; the SiLU is silu_fast.
-  const uint32_t kch = tid < kCD ? kh * kCD + tid : key_el + kh * kCD + (tid - kCD);
+  // The chunk's conv (kernel 4): threads tid and tid + 256 own key channel
+  // tid % 256 of key head kh (q 0..127, k 128..255), the first half of the
+  // 64 tokens and the second, and write silu(conv) into the q / k rows in LDS
+  // (zero past the last token).  16 inputs per batch with the next batch in
+  // flight.  The sums are conv_finish's, operation for operation; the SiLU is
+  // silu_fast.
+  const uint32_t kc = tid % 256, th0 = 32 * (tid / 256);
+  const uint32_t kch = kc < kCD ? kh * kCD + kc : key_el + kh * kCD + (kc - kCD);
   {
     float w[4], win[3];
 #pragma unroll
     for (int q = 0; q < 4; ++q) w[q] = a.conv_w[(size_t)kch * 4 + q];
 #pragma unroll
-    for (int q = 0; q < 3; ++q) win[q] = conv_input(a, kch, (int)t0 - 3 + q);
-    float* dst = tid < kCD ? qs_s + tid : ks_s + (tid - kCD);
+    for (int q = 0; q < 3; ++q) win[q] = conv_input(a, kch, min((int)(t0 + th0) - 3 + q, (int)a.M - 1));
+    float* dst = kc < kCD ? qs_s + kc : ks_s + (kc - kCD);
     float xn[16];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) xn[k] = a.qkv[(size_t)min(t0 + k, a.M - 1) * a.channels + kch];
-    for (int tb = 0; tb < 64; tb += 16) {
+    for (int k = 0; k < 16; ++k) xn[k] = a.qkv[(size_t)min(t0 + th0 + k, a.M - 1) * a.channels + kch];
+#pragma unroll
+    for (int tb = 0; tb < 32; tb += 16) {
       float xb[16];
 #pragma unroll
       for (int k = 0; k < 16; ++k) xb[k] = xn[k];
-      const uint32_t tn = t0 + min(tb + 16, 48);  // the last batch reloads itself (unused)
+      if (tb == 0) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) xn[k] = a.qkv[(size_t)min(tn + k, a.M - 1) * a.channels + kch];
+        for (int k = 0; k < 16; ++k) xn[k] = a.qkv[(size_t)min(t0 + th0 + 16 + k, a.M - 1) * a.channels + kch];
+      }
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         const float x = xb[k];
@@ -998,35 +1004,32 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
         win[0] = win[1];
         win[1] = win[2];
         win[2] = x;
-        dst[(tb + k) * kCStride] = (uint32_t)(tb + k) < nt ? silu_fast(sum) : 0.0f;
+        const uint32_t t = th0 + tb + k;
+        dst[t * kCStride] = t < nt ? silu_fast(sum) : 0.0f;
       }
     }
   }
-  // v of the wave's U~ columns (32 w + 16 nn + j) for the solve at the end,
-  // convolved here in registers: tokens 16 b + 4 grp + r need the inputs from
-  // three tokens earlier on (rows past the last token are masked at use).
-  const uint32_t j = lane & 15, grp = lane >> 4;
-  float vpre[4][2][4];
+  // v of the wave's U~ columns (16 w + j) for the solve at the end, convolved
+  // here in registers: tokens 16 b + 4 grp + r need the inputs from three
+  // tokens earlier on (rows past the last token are masked at use).
+  float vpre[4][4];
   {
+    const uint32_t vch = 2 * key_el + h * kCD + 16 * wave + j;
+    float w[4];
 #pragma unroll
-    for (int nn = 0; nn < 2; ++nn) {
-      const uint32_t vch = 2 * key_el + h * kCD + 32 * wave + 16 * nn + j;
-      float w[4];
+    for (int q = 0; q < 4; ++q) w[q] = a.conv_w[(size_t)vch * 4 + q];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) w[q] = a.conv_w[(size_t)vch * 4 + q];
+    for (int b = 0; b < 4; ++b) {
+      float x[7];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        float x[7];
+      for (int q = 0; q < 7; ++q) x[q] = conv_input(a, vch, min((int)(t0 + 16 * b + 4 * grp) - 3 + q, (int)a.M - 1));
 #pragma unroll
-        for (int q = 0; q < 7; ++q) x[q] = conv_input(a, vch, min((int)(t0 + 16 * b + 4 * grp) - 3 + q, (int)a.M - 1));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float sum = __fmul_rn(w[3], x[r + 3]);
-          sum = fmaf(w[0], x[r], sum);
-          sum = fmaf(w[1], x[r + 1], sum);
-          sum = fmaf(w[2], x[r + 2], sum);
-          vpre[b][nn][r] = silu_fast(sum);
-        }
+      for (int r = 0; r < 4; ++r) {
+        float sum = __fmul_rn(w[3], x[r + 3]);
+        sum = fmaf(w[0], x[r], sum);
+        sum = fmaf(w[1], x[r + 1], sum);
+        sum = fmaf(w[2], x[r + 2], sum);
+        vpre[b][r] = silu_fast(sum);
       }
     }
   }
@@ -1034,11 +1037,11 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   // three tokens (from the old history when M < 3), written by the last
   // chunk's workgroups (key channels by the first value head of each key head).
   if (c + 1 == (a.M + kDnChunk - 1) / kDnChunk) {
-    if (h % (VH / a.key_heads) == 0)
+    if (tid < 256 && h % (VH / a.key_heads) == 0)
 #pragma unroll
       for (int q = 0; q < 3; ++q) a.hist_out[(size_t)kch * 3 + q] = conv_input(a, kch, (int)a.M - 3 + q);
-    if (tid < kCD) {
-      const uint32_t vch = 2 * key_el + h * kCD + tid;
+    if (tid >= 256 && tid < 256 + kCD) {
+      const uint32_t vch = 2 * key_el + h * kCD + (tid - 256);
 #pragma unroll
       for (int q = 0; q < 3; ++q) a.hist_out[(size_t)vch * 3 + q] = conv_input(a, vch, (int)a.M - 3 + q);
     }
@@ -1073,8 +1076,8 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   // prep_key_head's RMS scales: row ri (q rows 0..63, k rows 64..127), lane l
   // sums the squares of columns l and l + 64, then a wave sum.
 #pragma unroll 4
-  for (int q = 0; q < 32; ++q) {
-    const uint32_t ri = 32 * wave + q;
+  for (int q = 0; q < 16; ++q) {
+    const uint32_t ri = 16 * wave + q;
     const float* row = (ri < 64 ? qs_s + ri * kCStride : ks_s + (ri - 64) * kCStride) + lane;
     float ss = 0.0f;
     ss = fmaf(row[0], row[0], ss);
@@ -1086,8 +1089,8 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   {
     const float inv = 1.0f / sqrtf((float)kCD);
 #pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      const uint32_t idx = tid + 256 * p;  // float4 index over [128 rows][32]
+    for (int p = 0; p < 8; ++p) {
+      const uint32_t idx = tid + kPrepThreads * p;  // float4 index over [128 rows][32]
       const uint32_t ri = idx / 32, c4 = idx % 32;
       float* px = (ri < 64 ? qs_s + ri * kCStride : ks_s + (ri - 64) * kCStride) + 4 * c4;
       const float sc = sc_s[ri];
@@ -1107,8 +1110,8 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
     uint16_t* kt3 = (uint16_t*)KTg;
     uint16_t* q3 = (uint16_t*)Qg;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint32_t item = tid + 256 * p, ln = item % 64, blk = item / 64;  // blk = nb * 2 + s
+    for (int p = 0; p < 2; ++p) {
+      const uint32_t item = tid + kPrepThreads * p, ln = item % 64, blk = item / 64;  // blk = nb * 2 + s
       const uint32_t col = 16 * (blk / 2) + ln % 16, i0 = 32 * (blk % 2) + 8 * (ln / 16);
       f32x4 v0, v1;
 #pragma unroll
@@ -1122,8 +1125,8 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
       *(u32x4*)(kt3 + blk * 1024 + 512 + 8 * ln) = lo;
     }
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint32_t item = tid + 256 * p, ln = item % 64, blk = item / 64;  // blk = nb * 4 + s
+    for (int p = 0; p < 2; ++p) {
+      const uint32_t item = tid + kPrepThreads * p, ln = item % 64, blk = item / 64;  // blk = nb * 4 + s
       const uint32_t t = 16 * (blk / 4) + ln % 16, k0 = 32 * (blk % 4) + 8 * (ln / 16);
       const float* src = qs_s + t * kCStride + k0;
       const float gm = gm_s[t];
@@ -1135,8 +1138,8 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   }
 
   // Q K^T, then K K^T, on the lower-triangular 16 x 16 tiles (tn <= tm):
-  // 10 tiles each, spread over the waves.  Q K^T goes straight to P; once
-  // every wave is past it the q^ rows' space takes A from K K^T.  The MFMA
+  // 10 tiles each over the 8 waves.  Q K^T goes straight to P; once every
+  // wave is past it the q^ rows' space takes A from K K^T.  The MFMA
   // reduction index is permuted (lane group g of step (m, e) carries
   // k = 16 m + 4 g + e), so every operand is one 16-byte LDS read.
   auto tile = [&](const float* xs, int tix, floatx4& acc, int& tm, int& tn) __attribute__((always_inline)) {
@@ -1156,7 +1159,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
     }
     acc = (ac[0] + ac[1]) + (ac[2] + ac[3]);
   };
-  for (int tix = (int)wave; tix < 10; tix += 4) {
+  for (int tix = (int)wave; tix < 10; tix += 8) {
     floatx4 acc;
     int tm, tn;
     tile(qs_s, tix, acc, tm, tn);
@@ -1169,7 +1172,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
     }
   }
   __syncthreads();  // the q^ rows are consumed; their space becomes A
-  for (int tix = 3 - (int)wave; tix < 10; tix += 4) {
+  for (int tix = 9 - (int)wave; tix >= 0; tix -= 8) {
     floatx4 acc;
     int tm, tn;
     tile(ks_s, tix, acc, tm, tn);
@@ -1181,7 +1184,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
     }
   }
   // P is zero above the diagonal blocks too, so its readers need no bounds.
-  for (uint32_t idx = tid; idx < 6 * 256; idx += 256) {
+  for (uint32_t idx = tid; idx < 6 * 256; idx += kPrepThreads) {
     const uint32_t tile = idx / 256, e = idx % 256;
     const uint32_t tm = tile < 3 ? 0 : tile < 5 ? 1 : 2;  // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
     const uint32_t tn = tile < 3 ? tile + 1 : tile < 5 ? tile - 1 : 3;
@@ -1192,15 +1195,15 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
   // Solve (I + A) X = R in 16-row blocks b (A unit lower triangular):
   //   X_b = T_b (R_b - sum_{c<b} A_bc X_c),  T_b = (I + A_bb)^{-1},
   // on fp32 MFMA.  R's columns are beta Gamma k (giving W) and beta v (giving
-  // U~); wave w owns W columns 32 w .. 32 w + 31 (tiles n = 0, 1) and the
-  // same U~ columns (tiles n = 2, 3).
+  // U~); wave w owns W columns 16 w .. 16 w + 15 (tile n = 0) and the same
+  // U~ columns (tile n = 1).
   // With the reduction index of MFMA step r permuted to k = 4 grp + r, an
   // output tile (rows 4 grp + r, column j in lane (j, grp)) is directly the
   // B operand of the next product, so X stays in registers.
-  // T_b first: wave b, lane jj < 16 owns column jj (T_b[t][jj] = delta_t,jj
-  // + sum_{i<t} (-A)[t][i] T_b[i][jj]).
+  // T_b first: wave b < 4, lane jj < 16 owns column jj (T_b[t][jj] =
+  // delta_t,jj + sum_{i<t} (-A)[t][i] T_b[i][jj]).
   float* t_s = a_s + 64 * kAStride;  // T_b [4][16][17]
-  if (lane < 16) {
+  if (wave < 4 && lane < 16) {
     const uint32_t b = wave, jj = lane;
     const float* ab = a_s + 16 * b * kAStride + 16 * b;
     float tc[16];
@@ -1214,70 +1217,67 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(DnArgs a) {
     }
   }
   __syncthreads();
-  const uint32_t cw = 32 * wave + j;  // the lane's column within W and within U~ (plus 16 nn)
-  floatx4 X[4][4];  // [block b][tile n]: X[16 b + 4 grp + r][tile column]
+  const uint32_t cw = 16 * wave + j;  // the lane's column within W and within U~
+  floatx4 X[4][2];  // [block b][tile n]: X[16 b + 4 grp + r][tile column]
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    floatx4 acc[4];
+    floatx4 acc[2];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t t = 16 * b + 4 * grp + r;
-#pragma unroll
-      for (int nn = 0; nn < 2; ++nn) {
-        acc[nn][r] = bg_s[t] * ks_s[t * kCStride + cw + 16 * nn];
-        acc[2 + nn][r] = t < nt ? beta_s[t] * vpre[b][nn][r] : 0.0f;
-      }
+      acc[0][r] = bg_s[t] * ks_s[t * kCStride + cw];
+      acc[1][r] = t < nt ? beta_s[t] * vpre[b][r] : 0.0f;
     }
 #pragma unroll
-    for (int c = 0; c < b; ++c) {
-      const f32x4 av = *(const f32x4*)(a_s + (16 * b + j) * kAStride + 16 * c + 4 * grp);  // (-A)_bc
+    for (int cb = 0; cb < b; ++cb) {
+      const f32x4 av = *(const f32x4*)(a_s + (16 * b + j) * kAStride + 16 * cb + 4 * grp);  // (-A)_bc
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int n = 0; n < 4; ++n) acc[n] = mfma_f32_4(av[r], X[c][n][r], acc[n]);
+        for (int n = 0; n < 2; ++n) acc[n] = mfma_f32_4(av[r], X[cb][n][r], acc[n]);
     }
     const f32x4 tv = *(const f32x4*)(t_s + (16 * b + j) * 17 + 4 * grp);
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
+    for (int n = 0; n < 2; ++n) {
       X[b][n] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int r = 0; r < 4; ++r) X[b][n] = mfma_f32_4(tv[r], acc[n][r], X[b][n]);
     }
   }
-  // X[b][n][r] is token 16 b + 4 grp + r, column 32 wave + 16 (n & 1) + j:
-  // four tokens of one column per lane, while the workspace order wants four
-  // columns of one token per float4.  Each wave transposes its tiles through
-  // its own LDS rows (W tiles, then U~ tiles) and stores 1 KB per instruction.
+  // X[b][n][r] is token 16 b + 4 grp + r, column 16 wave + j: four tokens of
+  // one column per lane, while the workspace order wants consecutive columns
+  // of one token.  Each wave transposes its tiles through its own LDS rows
+  // (W tiles, then U~ tiles).
   __syncthreads();  // every wave is past k^, A and T: their LDS is free
-  float* xt = prep_lds + wave * (8 * 16 * 20);  // 8 tiles of 16 x 16, row stride 20
+  float* xt = prep_lds + wave * (4 * 16 * 20);  // 4 tiles of 16 x 16, row stride 20
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
+  for (int n = 0; n < 2; ++n) {
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
-      for (int nn = 0; nn < 2; ++nn)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) xt[(2 * b + nn) * 320 + (4 * grp + r) * 20 + j] = X[b][2 * half + nn][r];
+      for (int r = 0; r < 4; ++r) xt[b * 320 + (4 * grp + r) * 20 + j] = X[b][n][r];
     __builtin_amdgcn_wave_barrier();
-    if (half == 0) {
-      // W[token][k] as split bf16: token block b, step s = wave (k 32 w ..
-      // 32 w + 31): lane (j, g) takes row j, columns 8 g .. 8 g + 7 of the
-      // wave's 32 columns, i.e. tile nn = g / 2 at column 8 (g % 2).
+    if (n == 0) {
+      // W[token][k] as split bf16, block (token block b, step s = wave / 2):
+      // the step's lanes with grp in {2 (wave % 2), 2 (wave % 2) + 1} hold
+      // columns 16 (wave % 2) + 8 (grp % 2) + e, i.e. this wave's tile.
       uint16_t* w3 = (uint16_t*)Wg;
+      if (grp / 2 == wave % 2) {
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const float* src = xt + (2 * b + grp / 2) * 320 + j * 20 + 8 * (grp % 2);
-        u32x4 hi, lo;
-        split_bf16x8(*(const f32x4*)src, *(const f32x4*)(src + 4), hi, lo);
-        *(u32x4*)(w3 + dn_b3_block(b, wave, 4) + 8 * lane) = hi;
-        *(u32x4*)(w3 + dn_b3_block(b, wave, 4) + 512 + 8 * lane) = lo;
+        for (int b = 0; b < 4; ++b) {
+          const float* src = xt + b * 320 + j * 20 + 8 * (grp % 2);
+          u32x4 hi, lo;
+          split_bf16x8(*(const f32x4*)src, *(const f32x4*)(src + 4), hi, lo);
+          *(u32x4*)(w3 + dn_b3_block(b, wave / 2, 4) + 8 * lane) = hi;
+          *(u32x4*)(w3 + dn_b3_block(b, wave / 2, 4) + 512 + 8 * lane) = lo;
+        }
       }
     } else {
+      // U~: row group wave, token block b (fp32, dn_ws_index order).
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const uint32_t b = q / 2, nn = q % 2, blk = 2 * wave + nn;
-        const f32x4 v = *(const f32x4*)(xt + q * 320 + (lane % 16) * 20 + 4 * (lane / 16));
-        *(f32x4*)(Ug + 256 * (4 * blk + b) + 4 * lane) = v;  // U~: row group blk, token block b
+      for (int b = 0; b < 4; ++b) {
+        const f32x4 v = *(const f32x4*)(xt + b * 320 + (lane % 16) * 20 + 4 * (lane / 16));
+        *(f32x4*)(Ug + 256 * (4 * wave + b) + 4 * lane) = v;
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -1529,7 +1529,7 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
   if (chunked) {
     if (!a.chunk_ws) return hipErrorInvalidValue;
     const uint32_t nchunks = (a.M + kDnChunk - 1) / kDnChunk;
-    hipLaunchKernelGGL(dn_chunk_prep_kernel, dim3(nchunks * a.value_heads), dim3(256), kPrepLds, st, a);
+    hipLaunchKernelGGL(dn_chunk_prep_kernel, dim3(nchunks * a.value_heads), dim3(kPrepThreads), kPrepLds, st, a);
     hipLaunchKernelGGL(dn_chunk_scan_kernel, dim3(a.value_heads * (kCD / 16)), dim3(256), 0, st, a);
   } else {
     const uint32_t ept = (a.dk + kLanesPerRow - 1) / kLanesPerRow;
