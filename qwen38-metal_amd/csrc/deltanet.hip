@@ -1286,96 +1286,93 @@ __global__ __launch_bounds__(kPrepThreads, 2) void dn_chunk_prep_kernel(DnArgs a
 
 // grid: VH * 8 blocks (block = rg * VH + h: the 8 row groups of a head share
 // blockIdx mod 8, i.e. one XCD and its L2, where they read the same chunk
-// operands), 256 threads.  The group's 16 rows of S live in LDS.  Per chunk,
-// wave w owns tokens 16 w .. 16 w + 15 and columns 32 w .. 32 w + 31:
-//   U_w^T = U~_w^T - S W_w^T                 (its 16 tokens, from S in LDS)
-//   O_w^T = Gamma S Q_w^T + sum_{i <= t} U^T P  (after U^T is exchanged)
-//   S[:, cols_w] <- Gamma_C S[:, cols_w] + U^T K~[:, cols_w]   (all 64 tokens)
-// with one barrier after the U^T exchange and one after the S update.  The
-// next chunk's operands are loaded into registers while the current chunk
-// is computed (each register set is refilled right after its last use).
-__global__ __launch_bounds__(256) void dn_chunk_scan_kernel(DnArgs a) {
+// operands), 512 threads.  The group's 16 rows of S live in LDS.  Waves w and
+// w + 4 share tokens 16 w .. 16 w + 15 and split the reduction over k of
+//   U_w^T = U~_w^T - S W_w^T,   O_w^T = S (Gamma Q_w)^T        (k halves)
+// (partials meet in LDS); then, after U^T is exchanged, wave v of 8 updates
+// columns 16 v .. 16 v + 15 of S as Gamma_C S + U^T K~ over the chunk's 64
+// tokens, and waves 0..3 add the intra-chunk term sum_{i <= t} U^T P and
+// store O.  Waves w and w + 4 run on one SIMD, so one's memory and LDS waits
+// overlap the other's MFMAs.  The products with S and with U^T are split-bf16
+// triples on the bf16 MFMA; P U^T is fp32.  The next chunk's operands are
+// loaded while the current chunk is computed.
+constexpr int kScanThreads = 512;
+__global__ __launch_bounds__(kScanThreads) void dn_chunk_scan_kernel(DnArgs a) {
   __shared__ __attribute__((aligned(16))) float u_s[16 * kAStride];  // U^T [row][token]
   __shared__ __attribute__((aligned(16))) float s_s[16 * kCStride];  // S [row][col]
+  __shared__ __attribute__((aligned(16))) float xp_s[4][64][8];      // the upper k half's partials
   const uint32_t VH = a.value_heads;
   const uint32_t h = blockIdx.x % VH, rg = blockIdx.x / VH;
   const uint32_t row0 = rg * 16;
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t tw = wave % 4, khalf = wave / 4;  // token block, k half
   const uint32_t j = lane & 15, grp = lane >> 4;
   const uint32_t nchunks = (a.M + kDnChunk - 1) / kDnChunk;
-  const uint32_t tok = 16 * wave + j;  // this lane's token column in U and O
-  const uint32_t col_w = 32 * wave;    // first of the wave's S columns
+  const uint32_t tok = 16 * tw + j;   // this lane's token column in U and O
+  const uint32_t col_w = 16 * wave;   // first of the wave's S columns
 
-  u32x4 Wh[4], Wl[4], Qh[4], Ql[4], Kh[2][2], Kl[2][2];  // split bf16 B operands
+  u32x4 Wh[2], Wl[2], Qh[2], Ql[2], Kh[2], Kl[2];  // split bf16 B operands (the wave's k half / columns)
   f32x4 Uv, Pv[4];
   float G_last;
   auto ws_of = [&](uint32_t c) { return a.chunk_ws + ((size_t)c * VH + h) * kDnChunkFloats; };
-  // Rows past the last token read a valid row and are weighted by zero.
-  // Masks are applied where the values are used, so the loads stay in
-  // flight.  The MFMA reduction index is permuted: lane group grp of step
-  // (m, e) carries k = 16 m + 4 grp + e, so each operand is one 16-byte read.
-  // Every operand is stored in this load order (dn_ws_index), so each load
-  // instruction reads 1 KB of consecutive memory.
   const uint32_t lofs = 4 * (16 * grp + j);  // the lane's float4 within a 64-float4 block
+  // Rows past the last token read valid data and are weighted by zero.
   auto load_wqu = [&](uint32_t c) __attribute__((always_inline)) {
     const float* ws = ws_of(c);
     G_last = ws[kDnWsG + 63];
     const uint16_t* w3 = (const uint16_t*)(ws + kDnWsW);
     const uint16_t* q3 = (const uint16_t*)(ws + kDnWsQ);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const uint32_t o = dn_b3_block(wave, s, 4) + 8 * lane;
+    for (int s = 0; s < 2; ++s) {
+      const uint32_t o = dn_b3_block(tw, 2 * khalf + s, 4) + 8 * lane;
       Wh[s] = *(const u32x4*)(w3 + o);
       Wl[s] = *(const u32x4*)(w3 + o + 512);
       Qh[s] = *(const u32x4*)(q3 + o);
       Ql[s] = *(const u32x4*)(q3 + o + 512);
     }
-    Uv = *(const f32x4*)(ws + kDnWsU + 1024 * rg + 256 * wave + lofs);
+    if (khalf == 0) Uv = *(const f32x4*)(ws + kDnWsU + 1024 * rg + 256 * tw + lofs);
   };
-  // P[tok][i] (fp32, i = 16 m + 4 grp + e) and K~^T[col][i] (split bf16).
+  // P[tok][i] (fp32, i = 16 m + 4 grp + e; waves 0..3) and K~^T[col][i]
+  // (split bf16, the wave's 16 columns).
   auto load_pk = [&](uint32_t c) __attribute__((always_inline)) {
     const float* ws = ws_of(c);
     const uint16_t* kt3 = (const uint16_t*)(ws + kDnWsKT);
+    if (khalf == 0) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m) Pv[m] = *(const f32x4*)(ws + kDnWsP + 256 * (4 * wave + m) + lofs);
+      for (int m = 0; m < 4; ++m) Pv[m] = *(const f32x4*)(ws + kDnWsP + 256 * (4 * tw + m) + lofs);
+    }
 #pragma unroll
-    for (int n = 0; n < 2; ++n)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const uint32_t o = dn_b3_block(2 * wave + n, s, 2) + 8 * lane;
-        Kh[n][s] = *(const u32x4*)(kt3 + o);
-        Kl[n][s] = *(const u32x4*)(kt3 + o + 512);
-      }
+    for (int s = 0; s < 2; ++s) {
+      const uint32_t o = dn_b3_block(wave, s, 2) + 8 * lane;
+      Kh[s] = *(const u32x4*)(kt3 + o);
+      Kl[s] = *(const u32x4*)(kt3 + o + 512);
+    }
   };
 
   // Initial rows of S into LDS.
   {
     const float* sin = a.s_in + ((size_t)h * kCD + row0) * kCD;
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const uint32_t idx = tid + 256 * p;  // float4 index over [16][32]
-      const uint32_t r = idx / 32, c4 = idx % 32;
-      *(f32x4*)(s_s + r * kCStride + 4 * c4) = *(const f32x4*)(sin + r * kCD + 4 * c4);
-    }
+    const uint32_t r = tid / 32, c4 = tid % 32;  // float4 index over [16][32]
+    *(f32x4*)(s_s + r * kCStride + 4 * c4) = *(const f32x4*)(sin + r * kCD + 4 * c4);
   }
   load_wqu(0);
   load_pk(0);
   __syncthreads();
 
-  floatx4 d[2];  // the wave's columns of S in the MFMA output layout (rows 4 grp + r, column col_w + 16 n + j)
+  floatx4 d;  // the wave's 16 columns of S in the MFMA output layout (rows 4 grp + r, column col_w + j)
   for (uint32_t c = 0; c < nchunks; ++c) {
     const uint32_t t0 = c * kDnChunk, nt = min(kDnChunk, a.M - t0);
     const uint32_t cn = min(c + 1, nchunks - 1);  // the last chunk reloads itself (unused)
     // (a) U^T[row][tok] = U~[tok][row] - sum_k S[row][k] W[tok][k]
     // (b1) O^T[row][tok] = sum_k S[row][k] Gamma_tok q[tok][k]
-    // Split-bf16 products on v_mfma_f32_16x16x32_bf16: S (A operand, row j,
-    // k = 32 s + 8 grp + e) is split here, W and Gamma q come split.
+    // over this wave's k half: S (A operand, row j, k = 32 s + 8 grp + e) is
+    // split here, W and Gamma q come split.
     floatx4 au[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     floatx4 ao[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const float* sp = s_s + j * kCStride + 32 * s + 8 * grp;
+    for (int s = 0; s < 2; ++s) {
+      const float* sp = s_s + j * kCStride + 32 * (2 * khalf + s) + 8 * grp;
       u32x4 sh, sl;
       split_bf16x8(*(const f32x4*)sp, *(const f32x4*)(sp + 4), sh, sl);
       au[0] = mfma16x16x32(sh, Wh[s], au[0]);
@@ -1386,65 +1383,66 @@ __global__ __launch_bounds__(256) void dn_chunk_scan_kernel(DnArgs a) {
       ao[2] = mfma16x16x32(sl, Qh[s], ao[2]);
     }
     const float gam_c = expf(G_last);
-    const floatx4 acc_u = au[0] + (au[1] + au[2]);
+    floatx4 acc_u = au[0] + (au[1] + au[2]);
     floatx4 acc_o = ao[0] + (ao[1] + ao[2]);
     // The S columns this wave updates, in the output layout, before any
-    // wave writes the new values (after the barrier below).
+    // wave writes the new values (after the second barrier below).
 #pragma unroll
-    for (int n = 0; n < 2; ++n)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) d[n][r] = gam_c * s_s[(4 * grp + r) * kCStride + col_w + 16 * n + j];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) u_s[(4 * grp + r) * kAStride + tok] = Uv[r] - acc_u[r];
-    load_wqu(cn);
-    lds_barrier();  // U^T complete; every wave is done reading S
-    // (b2) O^T[row][tok] += sum_{i <= tok} U^T[row][i] P[tok][i] (all four
-    // token blocks: P is zero past the diagonal block, so no branch), and
-    // S[:, cols_w] += U^T K~[:, cols_w] over the chunk's 64 tokens.
-    floatx4 ap[2] = {acc_o, {0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const f32x4 ua = *(const f32x4*)(u_s + j * kAStride + 16 * m + 4 * grp);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ap[e & 1] = mfma_f32_4(ua[e], Pv[m][e], ap[e & 1]);
+    for (int r = 0; r < 4; ++r) d[r] = gam_c * s_s[(4 * grp + r) * kCStride + col_w + j];
+    if (khalf == 1) {
+      *(f32x4*)&xp_s[tw][lane][0] = acc_u;
+      *(f32x4*)&xp_s[tw][lane][4] = acc_o;
     }
-    floatx4 dx[2][2] = {{{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}, {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}};
+    lds_barrier();  // the upper halves' partials are in LDS
+    if (khalf == 0) {
+      acc_u += *(const f32x4*)&xp_s[tw][lane][0];
+      acc_o += *(const f32x4*)&xp_s[tw][lane][4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) u_s[(4 * grp + r) * kAStride + tok] = Uv[r] - acc_u[r];
+    }
+    load_wqu(cn);  // W, q and U~ of this chunk are consumed
+    lds_barrier();  // U^T complete; every wave is done reading S and the partials
+    // S[:, cols_w] += U^T K~[:, cols_w] over the chunk's 64 tokens.
+    floatx4 dx[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const float* up = u_s + j * kAStride + 32 * s + 8 * grp;
       u32x4 uh, ul;
       split_bf16x8(*(const f32x4*)up, *(const f32x4*)(up + 4), uh, ul);
-#pragma unroll
-      for (int n = 0; n < 2; ++n) d[n] = mfma16x16x32(uh, Kh[n][s], d[n]);
-#pragma unroll
-      for (int n = 0; n < 2; ++n) dx[n][0] = mfma16x16x32(uh, Kl[n][s], dx[n][0]);
-#pragma unroll
-      for (int n = 0; n < 2; ++n) dx[n][1] = mfma16x16x32(ul, Kh[n][s], dx[n][1]);
+      d = mfma16x16x32(uh, Kh[s], d);
+      dx[0] = mfma16x16x32(uh, Kl[s], dx[0]);
+      dx[1] = mfma16x16x32(ul, Kh[s], dx[1]);
     }
+    d += dx[0] + dx[1];
+    if (khalf == 0) {
+      // (b2) O^T[row][tok] += sum_{i <= tok} U^T[row][i] P[tok][i] (all four
+      // token blocks: P is zero past the diagonal block, so no branch).
+      floatx4 ap[2] = {acc_o, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int n = 0; n < 2; ++n) d[n] += dx[n][0] + dx[n][1];
+      for (int m = 0; m < 4; ++m) {
+        const f32x4 ua = *(const f32x4*)(u_s + j * kAStride + 16 * m + 4 * grp);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ap[e & 1] = mfma_f32_4(ua[e], Pv[m][e], ap[e & 1]);
+      }
+      acc_o = ap[0] + ap[1];
+      // A buffer store bounded to the chunk's nt rows: tokens past the end
+      // are dropped by the hardware, so the store needs no branch.
+      const uint32_t row_bytes = VH * kCD * 4;
+      const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+          a.out + (size_t)t0 * VH * kCD, (short)0, (int)(nt * row_bytes), 0x00020000);
+      __builtin_amdgcn_raw_buffer_store_b128(
+          u32x4{__float_as_uint(acc_o[0]), __float_as_uint(acc_o[1]), __float_as_uint(acc_o[2]),
+                __float_as_uint(acc_o[3])},
+          ro, tok * row_bytes + (h * kCD + row0 + 4 * grp) * 4, 0, 0);
+    }
     load_pk(cn);
-    acc_o = ap[0] + ap[1];
-    // A buffer store bounded to the chunk's nt rows: tokens past the end are
-    // dropped by the hardware, so the store needs no branch.
-    const uint32_t row_bytes = VH * kCD * 4;
-    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
-        a.out + (size_t)t0 * VH * kCD, (short)0, (int)(nt * row_bytes), 0x00020000);
-    __builtin_amdgcn_raw_buffer_store_b128(
-        u32x4{__float_as_uint(acc_o[0]), __float_as_uint(acc_o[1]), __float_as_uint(acc_o[2]),
-              __float_as_uint(acc_o[3])},
-        ro, tok * row_bytes + (h * kCD + row0 + 4 * grp) * 4, 0, 0);
 #pragma unroll
-    for (int n = 0; n < 2; ++n)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s_s[(4 * grp + r) * kCStride + col_w + 16 * n + j] = d[n][r];
+    for (int r = 0; r < 4; ++r) s_s[(4 * grp + r) * kCStride + col_w + j] = d[r];
     lds_barrier();  // the new S is complete; U^T is consumed
   }
   float* sout = a.s_out + ((size_t)h * kCD + row0) * kCD;
 #pragma unroll
-  for (int n = 0; n < 2; ++n)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sout[(4 * grp + r) * kCD + col_w + 16 * n + j] = d[n][r];
+  for (int r = 0; r < 4; ++r) sout[(4 * grp + r) * kCD + col_w + j] = d[r];
 }
 
 template <int EPT>
@@ -1530,7 +1528,7 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
     if (!a.chunk_ws) return hipErrorInvalidValue;
     const uint32_t nchunks = (a.M + kDnChunk - 1) / kDnChunk;
     hipLaunchKernelGGL(dn_chunk_prep_kernel, dim3(nchunks * a.value_heads), dim3(kPrepThreads), kPrepLds, st, a);
-    hipLaunchKernelGGL(dn_chunk_scan_kernel, dim3(a.value_heads * (kCD / 16)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(dn_chunk_scan_kernel, dim3(a.value_heads * (kCD / 16)), dim3(kScanThreads), 0, st, a);
   } else {
     const uint32_t ept = (a.dk + kLanesPerRow - 1) / kLanesPerRow;
     if (ept <= 1)
