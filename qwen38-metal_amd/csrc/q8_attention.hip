@@ -22,8 +22,12 @@
 //      bf16 hi + lo (error ~2^-16), again with a +128 correction.
 //    The S^T/O^T orientation keeps every head in one lane column, so the
 //    softmax statistics never move between lanes except for the 4-way max.
-//    Decode splits the pages of a sequence over workgroups (4 waves each,
-//    combined in LDS); split partials are merged by q8_combine_kernel.
+//    Decode splits the pages of a sequence over workgroups (combined in
+//    LDS): one 8-wave workgroup per CU when all splits fit one such round,
+//    else two 4-wave ones per CU.  With one workgroup the CU's waves share
+//    one split, and the waves whose first loads queued behind the others'
+//    no longer hold up a second workgroup's.  Split partials are merged by
+//    q8_combine_kernel.
 //  Head dimensions 1..256 run on pages of the next storage width Dp (64,
 //  128 or 256) whose extra dimensions hold zero; queries, gates, outputs and
 //  the appended K/V rows keep the caller's real head dimension.
@@ -209,21 +213,22 @@ __device__ __forceinline__ float max4_across_kq(float v) {
   return p > q ? p : q;
 }
 
-template <int D>
+template <int D, int W>
 struct DecodeLds {
+  static constexpr int kWaves = W;
   static constexpr int kRing = D == 256 ? 2 : 4;  // pages in flight per wave
   static constexpr int kK = 16 * D, kV = 16 * D, kS = 512;  // K, V, scales (K 256 B + V 256 B)
   static constexpr int kPage = kK + kV + kS;
   static constexpr int kWaveRing = kRing * kPage;
   static constexpr int kPad = 17;  // floats per (wave, d) row of the O reduction (16 columns + 1)
-  static constexpr int kRed = 4 * D * kPad * 4 + (3 * 4 + 2) * 16 * 4;  // O, m, l, weights, max, sums
-  static constexpr int kBytes = 4 * kWaveRing > kRed ? 4 * kWaveRing : kRed;
+  static constexpr int kRed = W * D * kPad * 4 + (3 * W + 2) * 16 * 4;  // O, m, l, weights, max, sums
+  static constexpr int kBytes = W * kWaveRing > kRed ? W * kWaveRing : kRed;
 };
 
-template <int D>
-__global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
-  using L = DecodeLds<D>;
-  constexpr int kWaves = 4, kDB = D / 16, kKS = D / 32, kRing = L::kRing;
+template <int D, int W>
+__global__ __launch_bounds__(64 * W) void q8_decode_kernel(AttnArgs args) {
+  using L = DecodeLds<D, W>;
+  constexpr int kWaves = W, kDB = D / 16, kKS = D / 32, kRing = L::kRing;
   constexpr int kKChunks = D / 16;          // 16-byte chunks per K token row
   constexpr int kKDma = D / 64;             // DMA instructions per K (and V) page
   constexpr int kDmaPerPage = 2 * kKDma + 2;
@@ -479,8 +484,8 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   __syncthreads();  // the rings are reused for the reduction
   constexpr int kPad = L::kPad;
   float* red_o = reinterpret_cast<float*>(lds);  // [wave][d][kPad]
-  float(*red_m)[16] = reinterpret_cast<float(*)[16]>(lds + 4 * D * kPad * 4);
-  float(*red_l)[16] = red_m + 4;
+  float(*red_m)[16] = reinterpret_cast<float(*)[16]>(lds + kWaves * D * kPad * 4);
+  float(*red_l)[16] = red_m + kWaves;
 #pragma unroll
   for (int db = 0; db < kDB; ++db)
 #pragma unroll
@@ -492,8 +497,8 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   __syncthreads();
   // Per (wave, column) weights exp2(m_w - max) and the column sums, once;
   // the element loop below is then multiply-adds only.
-  float(*red_f)[16] = red_l + 4;  // [wave][col]
-  float* red_mx = red_l[4 + kWaves];
+  float(*red_f)[16] = red_l + kWaves;  // [wave][col]
+  float* red_mx = red_l[2 * kWaves];
   float* red_L = red_mx + 16;
   if (threadIdx.x < 16) {
     const uint32_t c = threadIdx.x;
@@ -518,7 +523,7 @@ __global__ __launch_bounds__(256) void q8_decode_kernel(AttnArgs args) {
   float* po = args.partials;
   float* pm = args.partials + o_rows * D;
   constexpr uint32_t kD4 = D / 4;
-  for (uint32_t e = threadIdx.x; e < gh * kD4; e += 256) {
+  for (uint32_t e = threadIdx.x; e < gh * kD4; e += 64 * kWaves) {
     const uint32_t c = e / kD4, d0 = 4 * (e % kD4);
     floatx4 O = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -883,7 +888,10 @@ hipError_t launch_attn_d(const AttnArgs& a, uint32_t units, bool need_combine, h
     return launch_prefill<D, 1>(a, st);
   }
   if (need_combine && !a.partials) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(q8_decode_kernel<D>, dim3(units), dim3(256), 0, st, a);
+  if (a.wg_waves == 8)
+    hipLaunchKernelGGL((q8_decode_kernel<D, 8>), dim3(units), dim3(512), 0, st, a);
+  else
+    hipLaunchKernelGGL((q8_decode_kernel<D, 4>), dim3(units), dim3(256), 0, st, a);
   if (need_combine)
     hipLaunchKernelGGL(q8_combine_kernel<D>, dim3(a.n_seqs * a.heads * (D / 32)), dim3(256), 0, st, a);
   return hipGetLastError();

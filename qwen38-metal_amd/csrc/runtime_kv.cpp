@@ -229,12 +229,12 @@ struct DecodeChunk {
   bool combine = false;
 };
 
-// Split plan of one chunk: about `target` workgroups (one residency round,
-// two 256-thread workgroups per CU), each split a multiple of 4 pages (one
-// per wave), and every split within the kernel's page limits.
+// Split plan of one chunk.  Each split is a multiple of 4 pages within the
+// kernel's page limits, and all splits should run in one residency round:
+// one 8-wave workgroup per CU if the splits fit that (measured faster at 32K:
+// the CU's waves share one split), else two 4-wave workgroups per CU.
 qm_status plan_decode_chunk(qm_runtime* rt, qm_kv* const* seqs, uint32_t nb, DecodeChunk* c) {
   const uint32_t KVH = seqs[0]->kv_heads;
-  const uint32_t target = (uint32_t)env_int("QM38_ATTN_TARGET_WGS", 2 * rt->cu_count);
   AttnArgs& at = c->at;
   uint64_t total_pages = 0;
   uint32_t max_pages = 0;
@@ -250,22 +250,33 @@ qm_status plan_decode_chunk(qm_runtime* rt, qm_kv* const* seqs, uint32_t nb, Dec
   }
   if ((uint64_t)max_pages > (uint64_t)kMaxSplits * kMaxPagesPerSplit)
     return fail(QM_ERR_CAPACITY_EXCEEDED, "sequence of %u pages exceeds the decode kernel's limit", max_pages);
-  uint64_t pps = (total_pages * KVH + target - 1) / target;
-  pps = std::max<uint64_t>(4, (pps + 3) / 4 * 4);
-  const int forced = env_int("QM38_ATTN_PPS", 0);
-  if (forced > 0) pps = (uint64_t)forced;
-  pps = std::max<uint64_t>(pps, (max_pages + kMaxSplits - 1) / kMaxSplits);
-  // Ceil-division per sequence can push the unit count past one residency
-  // round, which would leave a nearly empty second round as long as the
-  // first: grow the split until every unit fits.
   auto units_for = [&](uint64_t q) {
     uint64_t u = 0;
     for (uint32_t i = 0; i < nb; ++i) u += ((at.seqs[i].len + 15) / 16 + q - 1) / q * KVH;
     return u;
   };
-  if (forced <= 0)
-    while (pps < kMaxPagesPerSplit && units_for(pps) > target) pps += 4;
-  pps = std::min<uint64_t>(pps, kMaxPagesPerSplit);
+  const int forced = env_int("QM38_ATTN_PPS", 0);
+  // Pages per split for about `target` workgroups.  Ceil-division per
+  // sequence can push the unit count past one residency round, which would
+  // leave a nearly empty second round as long as the first: grow the split
+  // until every unit fits.
+  auto pps_for = [&](uint32_t target) {
+    uint64_t pps = (total_pages * KVH + target - 1) / target;
+    pps = std::max<uint64_t>(4, (pps + 3) / 4 * 4);
+    if (forced > 0) pps = (uint64_t)forced;
+    pps = std::max<uint64_t>(pps, (max_pages + kMaxSplits - 1) / kMaxSplits);
+    if (forced <= 0)
+      while (pps < kMaxPagesPerSplit && units_for(pps) > target) pps += 4;
+    return std::min<uint64_t>(pps, kMaxPagesPerSplit);
+  };
+  const int waves_env = env_int("QM38_ATTN_WAVES", 0);
+  const int target_env = env_int("QM38_ATTN_TARGET_WGS", 0);
+  uint32_t waves = 8;
+  uint64_t pps = pps_for(target_env > 0 ? (uint32_t)target_env : rt->cu_count);
+  if (waves_env == 4 || (waves_env != 8 && units_for(pps) > rt->cu_count)) {
+    waves = 4;
+    pps = pps_for(target_env > 0 ? (uint32_t)target_env : 2 * rt->cu_count);
+  }
   uint32_t units = 0, parts = 0;
   for (uint32_t i = 0; i < nb; ++i) {
     const uint32_t pages = (at.seqs[i].len + 15) / 16;
@@ -280,6 +291,7 @@ qm_status plan_decode_chunk(qm_runtime* rt, qm_kv* const* seqs, uint32_t nb, Dec
     }
   }
   at.pages_per_split = (uint32_t)pps;
+  at.wg_waves = waves;
   c->units = units;
   c->parts = parts;
   return QM_OK;

@@ -247,7 +247,10 @@ def _fill(rt, dev, cache, mirror, rng, n, H, KVH, D):
 @pytest.mark.parametrize("D,H,KVH", [(256, 24, 4), (128, 64, 8), (128, 16, 2), (64, 8, 8), (256, 16, 1),
                                       (128, 32, 4)])
 @pytest.mark.parametrize("pps", [0, 1])
-def test_decode_ragged_batch(rt, torch_dev, D, H, KVH, pps):
+@pytest.mark.parametrize("waves", [4, 8])
+def test_decode_ragged_batch(rt, torch_dev, D, H, KVH, pps, waves):
+    # Both workgroup shapes of the decode kernel (two 4-wave workgroups per
+    # CU, or one 8-wave workgroup), whichever the planner would pick.
     rng = np.random.default_rng(D * 7 + H * 3 + KVH + pps)
     lens = [0, 15, 16, 17, 100, 333]
     caches = [rt.create_q8_kv_state(KVH, D, 512) for _ in lens]
@@ -256,6 +259,7 @@ def test_decode_ragged_batch(rt, torch_dev, D, H, KVH, pps):
         _fill(rt, torch_dev, c, m, rng, n, H, KVH, D)
     if pps:
         os.environ["QM38_ATTN_PPS"] = str(pps)
+    os.environ["QM38_ATTN_WAVES"] = str(waves)
     try:
         for it in range(2):
             q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, len(lens), H, KVH, D, gate=(it == 0))
@@ -267,21 +271,26 @@ def test_decode_ragged_batch(rt, torch_dev, D, H, KVH, pps):
                 assert_bf16_close(got[b:b + 1], ref, what=f"seq {b} len {m.k.shape[0]} it {it}")
     finally:
         os.environ.pop("QM38_ATTN_PPS", None)
+        os.environ.pop("QM38_ATTN_WAVES", None)
     for c, m in zip(caches, mirrors):
         _check_cache(c, m)
 
 
 @pytest.mark.parametrize("D,H,KVH", [(128, 64, 8), (64, 8, 8)])
-def test_decode_long_split_page_ids(rt, torch_dev, D, H, KVH):
-    """Splits of 320 pages give each wave 80 pages: the first 64 ids come from
-    the per-wave id vector, the rest (including the page this step
-    materialises, page 620 = wave 0's 76th page of split 1) from scalar loads."""
+@pytest.mark.parametrize("waves,pps", [(4, 320), (8, 576)])
+def test_decode_long_split_page_ids(rt, torch_dev, D, H, KVH, waves, pps):
+    """Waves past 64 pages of their split: the first 64 ids come from the
+    per-wave id vector, the rest from scalar loads.  4 waves, splits of 320
+    pages: 80 pages a wave, and the page this step materialises, page 620, is
+    wave 0's 76th page of split 1.  8 waves, splits of 576 pages: 72 pages a
+    wave in split 0."""
     rng = np.random.default_rng(D + H)
     n = 620 * 16
     cache = rt.create_q8_kv_state(KVH, D, n + 64)
     mirror = Mirror(KVH, D)
     _fill(rt, torch_dev, cache, mirror, rng, n, H, KVH, D)
-    os.environ["QM38_ATTN_PPS"] = "320"
+    os.environ["QM38_ATTN_PPS"] = str(pps)
+    os.environ["QM38_ATTN_WAVES"] = str(waves)
     try:
         for it in range(2):
             q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, 1, H, KVH, D, gate=(it == 1))
@@ -291,6 +300,7 @@ def test_decode_long_split_page_ids(rt, torch_dev, D, H, KVH):
             assert_bf16_close(got, ref, what=f"len {mirror.k.shape[0]} it {it}")
     finally:
         os.environ.pop("QM38_ATTN_PPS", None)
+        os.environ.pop("QM38_ATTN_WAVES", None)
     _check_cache(cache, mirror)
 
 
