@@ -970,69 +970,60 @@ __global__ __launch_bounds__(kPrepThreads, 2) void dn_chunk_prep_kernel(DnArgs a
   // The chunk's conv (kernel 4): threads tid and tid + 256 own key channel
   // tid % 256 of key head kh (q 0..127, k 128..255), the first half of the
   // 64 tokens and the second, and write silu(conv) into the q / k rows in LDS
-  // (zero past the last token).  16 inputs per batch with the next batch in
-  // flight.  The sums are conv_finish's, operation for operation; the SiLU is
-  // silu_fast.
+  // (zero past the last token).  The sums are conv_finish's, operation for
+  // operation; the SiLU is silu_fast.
   const uint32_t kc = tid % 256, th0 = 32 * (tid / 256);
   const uint32_t kch = kc < kCD ? kh * kCD + kc : key_el + kh * kCD + (kc - kCD);
+  // Every conv input of the thread is loaded before any is used, so the
+  // workgroup pays one memory round trip for its inputs: the v values of the
+  // wave's U~ columns (16 w + j) for the solve at the end (tokens
+  // 16 b + 4 grp + r need the inputs from three tokens earlier on; rows past
+  // the last token are masked at use), then the key channel's 32 tokens.
+  float vw[4], vx[4][7];
   {
-    float w[4], win[3];
+    const uint32_t vch = 2 * key_el + h * kCD + 16 * wave + j;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) vw[q] = a.conv_w[(size_t)vch * 4 + q];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int q = 0; q < 7; ++q)
+        vx[b][q] = conv_input(a, vch, min((int)(t0 + 16 * b + 4 * grp) - 3 + q, (int)a.M - 1));
+  }
+  {
+    float w[4], win[3], xk[32];
 #pragma unroll
     for (int q = 0; q < 4; ++q) w[q] = a.conv_w[(size_t)kch * 4 + q];
 #pragma unroll
     for (int q = 0; q < 3; ++q) win[q] = conv_input(a, kch, min((int)(t0 + th0) - 3 + q, (int)a.M - 1));
+#pragma unroll
+    for (int k = 0; k < 32; ++k) xk[k] = a.qkv[(size_t)min(t0 + th0 + k, a.M - 1) * a.channels + kch];
     float* dst = kc < kCD ? qs_s + kc : ks_s + (kc - kCD);
-    float xn[16];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) xn[k] = a.qkv[(size_t)min(t0 + th0 + k, a.M - 1) * a.channels + kch];
-#pragma unroll
-    for (int tb = 0; tb < 32; tb += 16) {
-      float xb[16];
-#pragma unroll
-      for (int k = 0; k < 16; ++k) xb[k] = xn[k];
-      if (tb == 0) {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) xn[k] = a.qkv[(size_t)min(t0 + th0 + 16 + k, a.M - 1) * a.channels + kch];
-      }
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const float x = xb[k];
-        float sum = __fmul_rn(w[3], x);
-        sum = fmaf(w[0], win[0], sum);
-        sum = fmaf(w[1], win[1], sum);
-        sum = fmaf(w[2], win[2], sum);
-        win[0] = win[1];
-        win[1] = win[2];
-        win[2] = x;
-        const uint32_t t = th0 + tb + k;
-        dst[t * kCStride] = t < nt ? silu_fast(sum) : 0.0f;
-      }
+    for (int k = 0; k < 32; ++k) {
+      const float x = xk[k];
+      float sum = __fmul_rn(w[3], x);
+      sum = fmaf(w[0], win[0], sum);
+      sum = fmaf(w[1], win[1], sum);
+      sum = fmaf(w[2], win[2], sum);
+      win[0] = win[1];
+      win[1] = win[2];
+      win[2] = x;
+      const uint32_t t = th0 + k;
+      dst[t * kCStride] = t < nt ? silu_fast(sum) : 0.0f;
     }
   }
-  // v of the wave's U~ columns (16 w + j) for the solve at the end, convolved
-  // here in registers: tokens 16 b + 4 grp + r need the inputs from three
-  // tokens earlier on (rows past the last token are masked at use).
   float vpre[4][4];
-  {
-    const uint32_t vch = 2 * key_el + h * kCD + 16 * wave + j;
-    float w[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) w[q] = a.conv_w[(size_t)vch * 4 + q];
+  for (int b = 0; b < 4; ++b)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      float x[7];
-#pragma unroll
-      for (int q = 0; q < 7; ++q) x[q] = conv_input(a, vch, min((int)(t0 + 16 * b + 4 * grp) - 3 + q, (int)a.M - 1));
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float sum = __fmul_rn(w[3], x[r + 3]);
-        sum = fmaf(w[0], x[r], sum);
-        sum = fmaf(w[1], x[r + 1], sum);
-        sum = fmaf(w[2], x[r + 2], sum);
-        vpre[b][r] = silu_fast(sum);
-      }
+    for (int r = 0; r < 4; ++r) {
+      float sum = __fmul_rn(vw[3], vx[b][r + 3]);
+      sum = fmaf(vw[0], vx[b][r], sum);
+      sum = fmaf(vw[1], vx[b][r + 1], sum);
+      sum = fmaf(vw[2], vx[b][r + 2], sum);
+      vpre[b][r] = silu_fast(sum);
     }
-  }
   // The state's conv history after the last token: raw inputs of the final
   // three tokens (from the old history when M < 3), written by the last
   // chunk's workgroups (key channels by the first value head of each key head).
@@ -1074,16 +1065,22 @@ __global__ __launch_bounds__(kPrepThreads, 2) void dn_chunk_prep_kernel(DnArgs a
   }
   __syncthreads();
   // prep_key_head's RMS scales: row ri (q rows 0..63, k rows 64..127), lane l
-  // sums the squares of columns l and l + 64, then a wave sum.
-#pragma unroll 4
-  for (int q = 0; q < 16; ++q) {
-    const uint32_t ri = 16 * wave + q;
-    const float* row = (ri < 64 ? qs_s + ri * kCStride : ks_s + (ri - 64) * kCStride) + lane;
-    float ss = 0.0f;
-    ss = fmaf(row[0], row[0], ss);
-    ss = fmaf(row[64], row[64], ss);
-    ss = wave_sum(ss);
-    if (lane == 0) sc_s[ri] = 1.0f / sqrtf(ss / (float)kCD + a.eps);
+  // sums the squares of columns l and l + 64, then a wave sum.  The wave's 16
+  // rows are reduced side by side, and lane q forms row q's scale.
+  {
+    float ss[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const uint32_t ri = 16 * wave + q;
+      const float* row = (ri < 64 ? qs_s + ri * kCStride : ks_s + (ri - 64) * kCStride) + lane;
+      ss[q] = fmaf(row[64], row[64], fmaf(row[0], row[0], 0.0f));
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) ss[q] = wave_sum(ss[q]);
+    float mine = ss[0];
+#pragma unroll
+    for (int q = 1; q < 16; ++q) mine = lane == (uint32_t)q ? ss[q] : mine;
+    if (lane < 16) sc_s[16 * wave + lane] = 1.0f / sqrtf(mine / (float)kCD + a.eps);
   }
   __syncthreads();
   {
