@@ -149,7 +149,7 @@ __device__ __forceinline__ float row_sum(float v) {
 
 // q^ and k^ of key head kh at token t, computed by one wave: lane holds
 // channels c = lane + 64 i (i < 4; dk <= 256).  Shared by the prefill path
-// and the fused step so both round identically.
+// and the step kernels so both round identically.
 // NQ: channel slots per lane that can be live (ceil(dk / 64)); the others
 // stay zero, as they would with all four slots (their squares add nothing).
 // PART: 1 = q only, 2 = k only, 3 = both (each with the same operations).
@@ -245,7 +245,7 @@ __global__ __launch_bounds__(kThreads) void dn_conv_prepare_kernel(DnArgs a) {
 
 // One token of the delta rule on the EPT-element segment of one S row that a
 // lane holds (lane l: columns l + 16 e): returns o = S q^ for the row (all
-// 16 lanes of the row get it).  Shared by the scan and the fused step.
+// 16 lanes of the row get it).  Shared by the scan and the step kernels.
 template <int EPT>
 __device__ __forceinline__ float delta_row_token(float (&s)[EPT], const float (&kk)[EPT], const float (&qq)[EPT],
                                                  float g, float beta, float v) {
@@ -523,36 +523,37 @@ __global__ __launch_bounds__(kThreads) void dn_gate_norm_kernel(DnArgs a) {
   }
 }
 
-// The whole decode step (M = 1) in one launch: block = value head vh.
-//  wave 0: q^, k^ of key head kh (prep_key_head); wave 1: conv of vh's v
-//  channels; thread 128: g and beta.  Then the 16-lane row groups update the
-//  dv rows of S in dv / 16 passes (delta_row_token), and wave 0 applies the
-//  gated norm (gate_norm_row).  The arithmetic is the three-launch path's,
-//  call for call, so a step equals a one-token prefill bit for bit.  (A
-//  1024-thread block with 64 rows per pass compiled to code whose results
-//  differ from the prefill path's in the last bit for some heads, so the
-//  block stays at 256 threads.)
+// Rows of S per pass of the split step kernel's 256 threads (16 lanes a row).
 constexpr int kStepThreads = 256;
-constexpr int kStepRows = kStepThreads / 16;  // S rows per pass
-template <int EPT, int PASSES>
-__global__ __launch_bounds__(kStepThreads) void dn_step_kernel(DnArgs a) {
+constexpr int kStepRows = kStepThreads / 16;
+
+// The decode step with one 1024-thread workgroup per value head (dv <= 128):
+// 64 rows of S per pass, so a head takes at most two passes, and the gated
+// norm has all dv outputs in its own LDS: no exchange between workgroups.
+// Waves 0 and 2 prepare q^ and k^ (one half each), wave 1 convolves the
+// head's v channels, thread 192 forms g and beta.  Every output is formed by
+// the device functions of the other step kernels and the prefill path, so
+// a step still equals a one-token prefill bit for bit.
+constexpr int kHeadThreads = 1024;
+constexpr int kHeadRows = kHeadThreads / 16;  // S rows per pass
+template <int EPT>
+__global__ __launch_bounds__(kHeadThreads) void dn_step_head_kernel(DnArgs a) {
+  constexpr int PASSES = 2;
   __shared__ __attribute__((aligned(16))) float qk_s[2][16][EPT];  // [q | k][lane][e]
-  __shared__ float v_s[kStepRows * PASSES], o_s[kStepRows * PASSES];
+  __shared__ float v_s[kHeadRows * PASSES], o_s[kHeadRows * PASSES];
   __shared__ float gb_s[2];
   const uint32_t vh = blockIdx.x;
   const uint32_t group = a.value_heads / a.key_heads;
   const uint32_t kh = vh / group;
   const uint32_t key_el = a.key_heads * a.dk;
-  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  // The first value head of a key group also writes that key head's history.
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const bool key_hist = vh % group == 0 && a.kernel > 1;
 
-  // S rows of this block: pass p, row kStepRows p + r, columns l + 16 e.
   const int r = threadIdx.x / 16, l = threadIdx.x % 16;
   float s[PASSES][EPT];
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
-    const uint32_t row = kStepRows * p + r;
+    const uint32_t row = kHeadRows * p + r;
     const size_t srow = ((size_t)vh * a.dv + row) * a.dk;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
@@ -561,20 +562,24 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_kernel(DnArgs a) {
     }
   }
 
-  if (wave == 0) {
+  // Wave 0 loads the gated norm's operands early (it applies the norm at the
+  // end), then prepares q^; wave 2 prepares k^ meanwhile.
+  float nrm[4], sz[4];
+  if (wave == 0 || wave == 2) {
+    if (wave == 0) gate_norm_operands(a, a.z + (size_t)vh * a.dv, lane, nrm, sz);
     float cq[4], ck[4];
-    prep_key_head<EPT / 4>(a, 0, kh, lane, cq, ck, key_hist ? a.hist_out : nullptr);
+    if (wave == 0)
+      prep_key_head<EPT / 4, 1>(a, 0, kh, lane, cq, ck, key_hist ? a.hist_out : nullptr);
+    else
+      prep_key_head<EPT / 4, 2>(a, 0, kh, lane, cq, ck, key_hist ? a.hist_out : nullptr);
+    const int qk = wave == 0 ? 0 : 1;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t c = lane + 64 * i;
-      if (c < 16 * EPT) {
-        qk_s[0][c % 16][c / 16] = c < a.dk ? cq[i] : 0.0f;
-        qk_s[1][c % 16][c / 16] = c < a.dk ? ck[i] : 0.0f;
-      }
+      if (c < 16 * EPT) qk_s[qk][c % 16][c / 16] = c < a.dk ? (qk == 0 ? cq[i] : ck[i]) : 0.0f;
     }
   } else if (wave == 1) {
-    // Both of the lane's value channels loaded before either is finished.
-    constexpr int kV = (kStepRows * PASSES + 63) / 64;
+    constexpr int kV = (kHeadRows * PASSES + 63) / 64;
     if (a.kernel <= kTaps) {
       ConvIn cv[kV];
 #pragma unroll
@@ -582,16 +587,16 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_kernel(DnArgs a) {
 #pragma unroll
       for (int i = 0; i < kV; ++i) {
         const uint32_t c = lane + 64 * i;
-        if (c < kStepRows * PASSES) v_s[c] = c < a.dv ? conv_finish(a, cv[i]) : 0.0f;
+        if (c < kHeadRows * PASSES) v_s[c] = c < a.dv ? conv_finish(a, cv[i]) : 0.0f;
         if (c < a.dv && a.kernel > 1) conv_store_history(a, 2 * key_el + vh * a.dv + c, cv[i], a.hist_out);
       }
     } else {
-      for (uint32_t c = lane; c < kStepRows * PASSES; c += 64) {
+      for (uint32_t c = lane; c < kHeadRows * PASSES; c += 64) {
         const uint32_t ch = 2 * key_el + vh * a.dv + c;
         v_s[c] = c < a.dv ? conv_silu(a, ch, 0, a.kernel > 1 && c < a.dv ? a.hist_out : nullptr) : 0.0f;
       }
     }
-  } else if (threadIdx.x == 128) {
+  } else if (threadIdx.x == 192) {
     const float neg_a = -expf(a.a_log[vh]);
     gb_s[0] = expf(neg_a * softplus_f(a.a[vh] + a.dt_bias[vh]));
     gb_s[1] = sigmoid_f(a.b[vh]);
@@ -607,7 +612,7 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_kernel(DnArgs a) {
   const float g = gb_s[0], beta = gb_s[1];
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
-    const uint32_t row = kStepRows * p + r;
+    const uint32_t row = kHeadRows * p + r;
     const float o = delta_row_token<EPT>(s[p], kk, qq, g, beta, v_s[row]);
     if (l == 0) o_s[row] = o;
     if (row < a.dv) {
@@ -621,8 +626,14 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_kernel(DnArgs a) {
   }
   __syncthreads();
   if (wave == 0) {
-    float* out = a.out + (size_t)vh * a.dv;
-    gate_norm_row(a, o_s, a.z + (size_t)vh * a.dv, out, lane, a.out_bf16 ? a.out_bf16 + (size_t)vh * a.dv : nullptr);
+    float ov[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = 4 * lane + i;
+      ov[i] = c < a.dv ? o_s[c] : 0.0f;
+    }
+    gate_norm_core(a, ov, nrm, sz, a.out + (size_t)vh * a.dv, lane,
+                   a.out_bf16 ? a.out_bf16 + (size_t)vh * a.dv : nullptr);
   }
 }
 
@@ -639,7 +650,7 @@ __global__ __launch_bounds__(kStepThreads) void dn_step_kernel(DnArgs a) {
 // values (written through to memory) and counts itself in; the last of the
 // head's groups to arrive reads the dv values back and applies
 // gate_norm_row.  Every output is formed by the same device functions as in
-// the fused step and the prefill path, so a step still equals a one-token
+// the per-head step and the prefill path, so a step still equals a one-token
 // prefill bit for bit.
 template <int EPT>
 __global__ __launch_bounds__(kStepThreads) void dn_step_split_kernel(DnArgs a) {
@@ -1450,11 +1461,15 @@ void launch_scan(const DnArgs& a, hipStream_t st) {
 
 }  // namespace
 
-bool dn_step_split(const DnArgs& a) {
-  if (a.M != 1 || a.dk > 128 || a.dv > 256) return false;
-  const char* env = getenv("QM38_DN_STEP_SPLIT");
+// One token with head dims <= 128: one 1024-thread workgroup per value head
+// (QM38_DN_STEP_HEAD=0 forces the split kernel instead).
+bool dn_step_head(const DnArgs& a) {
+  if (a.M != 1 || a.dk > 128 || a.dv > 128) return false;
+  const char* env = getenv("QM38_DN_STEP_HEAD");
   return env ? atoi(env) != 0 : true;
 }
+
+bool dn_step_split(const DnArgs& a) { return a.M == 1 && a.dk <= 128 && a.dv <= 256 && !dn_step_head(a); }
 
 bool dn_use_chunked(const DnArgs& a) {
   if (a.dk != kCD || a.dv != kCD || a.kernel != 4 || a.snap_rows > 0 || a.M <= 1 ||
@@ -1486,6 +1501,13 @@ void launch_conv_tiled(const DnArgs& a, uint32_t ns, dim3 grid, dim3 block, hipS
 hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
   if (a.dk == 0 || a.dk > 256 || a.dv == 0 || a.dv > 256 || a.M == 0) return hipErrorInvalidValue;
   // One token with S rows that fit the fused kernel's registers: one launch.
+  if (dn_step_head(a)) {
+    if (a.dk <= 64)
+      hipLaunchKernelGGL(dn_step_head_kernel<4>, dim3(a.value_heads), dim3(kHeadThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL(dn_step_head_kernel<8>, dim3(a.value_heads), dim3(kHeadThreads), 0, st, a);
+    return hipGetLastError();
+  }
   if (dn_step_split(a)) {
     if (!a.step_o || !a.step_ctr) return hipErrorInvalidValue;
     const dim3 grid(a.value_heads * ((a.dv + kStepRows - 1) / kStepRows)), block(kStepThreads);
@@ -1493,19 +1515,6 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
       hipLaunchKernelGGL(dn_step_split_kernel<4>, grid, block, 0, st, a);
     else
       hipLaunchKernelGGL(dn_step_split_kernel<8>, grid, block, 0, st, a);
-    return hipGetLastError();
-  }
-  if (a.M == 1 && a.dk <= 128 && a.dv <= 128) {
-    const dim3 grid(a.value_heads), block(kStepThreads);
-    const uint32_t ept = (a.dk + 15) / 16, passes = (a.dv + kStepRows - 1) / kStepRows;
-    if (ept <= 4 && passes <= 4)
-      hipLaunchKernelGGL((dn_step_kernel<4, 4>), grid, block, 0, st, a);
-    else if (ept <= 4)
-      hipLaunchKernelGGL((dn_step_kernel<4, 8>), grid, block, 0, st, a);
-    else if (passes <= 4)
-      hipLaunchKernelGGL((dn_step_kernel<8, 4>), grid, block, 0, st, a);
-    else
-      hipLaunchKernelGGL((dn_step_kernel<8, 8>), grid, block, 0, st, a);
     return hipGetLastError();
   }
   const uint32_t units = a.key_heads + a.value_heads;

@@ -158,7 +158,7 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
   d.step_o = step_bytes ? (float*)((char*)rt->scratch + conv_bytes + chunk_bytes) : nullptr;
   d.step_ctr = step_bytes ? rt->counters : nullptr;
   d.out = out;
-  // The fused single-token kernel also writes the bf16 copy; other paths
+  // The single-token kernels also write the bf16 copy; other paths
   // convert afterwards.
   const bool fused_bf16 = out_bf16 && M == 1 && c.key_head_dim <= 128 && c.value_head_dim <= 128;
   if (fused_bf16) d.out_bf16 = out_bf16;

@@ -252,6 +252,34 @@ def test_prefill_2048_tokens(rt, torch_dev):
     _close(st.read()[1], S_ref, what="2048 state vs fp64 oracle")
 
 
+@pytest.mark.parametrize("shape", [sh for sh in SHAPES if sh[2] <= 128 and sh[3] <= 128])
+def test_step_kernels_agree(rt, torch_dev, shape):
+    # The single-token kernels (one 1024-thread workgroup per value head, the
+    # default at head dims <= 128; 16-row groups exchanging their outputs,
+    # forced here) run the same per-row arithmetic: outputs, history and state
+    # bit-equal over several tokens, and within the oracle bar.
+    cfg, c = _cfg(*shape)
+    M = 4
+    rng = np.random.default_rng(sum(shape) + 5)
+    wts, acts = _synth(rng, c, M)
+    w = rt.create_deltanet_weights(cfg, *wts)
+    runs = []
+    for head in ("1", "0"):
+        os.environ["QM38_DN_STEP_HEAD"] = head
+        try:
+            st = w.create_state()
+            outs = np.stack([_step(rt, torch_dev, w, st, *(x[t] for x in acts), 1e-6) for t in range(M)])
+            runs.append((outs, *st.read()))
+        finally:
+            os.environ.pop("QM38_DN_STEP_HEAD", None)
+    for x, y, what in zip(runs[0], runs[1], ("out", "history", "state")):
+        assert np.array_equal(x, y), what
+    hist, S = _zero_state(c)
+    ref, _, S_ref = oracle.deltanet_prefill(c, *wts, *acts, 1e-6, hist, S, f64=True)
+    _close(runs[0][0], ref, what=f"steps {shape}")
+    _close(runs[0][2], S_ref, what=f"state {shape}")
+
+
 def test_beta_zero_only_decays(rt, torch_dev):
     cfg, c = _cfg(2, 4, 128, 128, 1)
     rng = np.random.default_rng(3)
