@@ -466,6 +466,27 @@ __device__ __forceinline__ void gate_norm_operands(const DnArgs& a, const float*
     sz[i] = c < a.dv ? silu_f(z[c]) : 0.0f;
   }
 }
+// The same operands in two halves, so the loads can go out early and the
+// SiLU wait for them only where it is needed: raw loads (clamped
+// addresses), then the zeroing past dv and silu(z).
+__device__ __forceinline__ void gate_norm_load(const DnArgs& a, const float* z, uint32_t rl, float (&nrm)[4],
+                                               float (&zr)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t c = min(4 * rl + i, a.dv - 1);
+    nrm[i] = a.norm[c];
+    zr[i] = z[c];
+  }
+}
+__device__ __forceinline__ void gate_norm_finish(const DnArgs& a, uint32_t rl, float (&nrm)[4], const float (&zr)[4],
+                                                 float (&sz)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bool ok = 4 * rl + i < a.dv;
+    nrm[i] = ok ? nrm[i] : 0.0f;
+    sz[i] = ok ? silu_f(zr[i]) : 0.0f;
+  }
+}
 // One row by one wave: reads o_in[c], writes out[c].
 __device__ __forceinline__ void gate_norm_row(const DnArgs& a, const float* o_in, const float* z, float* out,
                                               uint32_t lane, uint16_t* out_bf16 = nullptr) {
@@ -562,11 +583,12 @@ __global__ __launch_bounds__(kHeadThreads) void dn_step_head_kernel(DnArgs a) {
     }
   }
 
-  // Wave 0 loads the gated norm's operands early (it applies the norm at the
-  // end), then prepares q^; wave 2 prepares k^ meanwhile.
-  float nrm[4], sz[4];
+  // Wave 0 loads the gated norm's operands first (it applies the norm at the
+  // end, and forms silu(z) only then), then prepares q^; wave 2 prepares k^
+  // meanwhile.
+  float nrm[4], zr[4], sz[4];
   if (wave == 0 || wave == 2) {
-    if (wave == 0) gate_norm_operands(a, a.z + (size_t)vh * a.dv, lane, nrm, sz);
+    if (wave == 0) gate_norm_load(a, a.z + (size_t)vh * a.dv, lane, nrm, zr);
     float cq[4], ck[4];
     if (wave == 0)
       prep_key_head<EPT / 4, 1>(a, 0, kh, lane, cq, ck, key_hist ? a.hist_out : nullptr);
@@ -626,6 +648,7 @@ __global__ __launch_bounds__(kHeadThreads) void dn_step_head_kernel(DnArgs a) {
   }
   __syncthreads();
   if (wave == 0) {
+    gate_norm_finish(a, lane, nrm, zr, sz);
     float ov[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
