@@ -213,6 +213,11 @@ __device__ __forceinline__ float max4_across_kq(float v) {
   return p > q ? p : q;
 }
 
+template <bool B>
+struct BoolTag {
+  static constexpr bool value = B;
+};
+
 template <int D, int W>
 struct DecodeLds {
   static constexpr int kWaves = W;
@@ -716,14 +721,13 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
   const float sm_scale = kLog2e / sqrtf((float)dr);
 
   floatx4 o[CB][kDB];
-  float m_run[CB], l_lane[CB], ps_lane[CB];
+  float m_run[CB], l_lane[CB];
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
 #pragma unroll
     for (int i = 0; i < kDB; ++i) o[cb][i] = floatx4{0.f, 0.f, 0.f, 0.f};
     m_run[cb] = -INFINITY;
     l_lane[cb] = 0.0f;
-    ps_lane[cb] = 0.0f;
   }
 
   const size_t kv_page_stride = (size_t)KVH * 16 * D;
@@ -749,7 +753,10 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
     r.ks = *(const floatx4*)(sq.ks + sbase);
     r.vs = *(const floatx4*)(sq.vs + sbase);
   };
-  auto process_page = [&](uint32_t p, const PageRegs& r) __attribute__((always_inline)) {
+  // MASKED is false for pages every column of the wave sees whole (all but
+  // the last few): those skip the causal compare and select per score.
+  auto process_page = [&](uint32_t p, const PageRegs& r, auto masked) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked)::value;
     // K as fp16 of 1024 + (k + 128) (one AND-OR per pair), unpacked once for
     // every block.
     u32x4 ka[kKS];
@@ -761,95 +768,111 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
       ka[2 * j] = u32x4{l0.x, l0.y, h0.x, h0.y};
       ka[2 * j + 1] = u32x4{l1.x, l1.y, h1.x, h1.y};
     }
+    // V unbiased (signed bytes -> bf16, exact): O accumulates only
+    // sum_t v_t p'_t.
     u32x2 va[kDB];
 #pragma unroll
-    for (int db = 0; db < kDB; ++db) va[db] = q8x4_to_bf16_biased(r.v[db]);
+    for (int db = 0; db < kDB; ++db) va[db] = q8x4_to_bf16_signed(r.v[db]);
+    float kss[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) kss[rr] = r.ks[rr] * sm_scale;
+    // S^T[token][col] over D in kKS steps of 32; the blocks' chains are
+    // independent and interleave.
+    floatx4 s4[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) s4[cb] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < kKS; ++j)
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) s4[cb] = mfma16x16x32_f16(ka[j], qb[cb][j], s4[cb]);
+    u32x4 pb[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
-      // S^T[token][col] over D in kKS steps of 32.
-      floatx4 s4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < kKS; ++j) s4 = mfma16x16x32_f16(ka[j], qb[cb][j], s4);
+      // Columns without a query row hold q = 0: their scores are finite and
+      // their results are never stored.
       float sc[4];
-      float bmax = -INFINITY;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const uint32_t t = p * 16 + 4 * kq + rr;
-        const bool ok = col_ok[cb] && t < visible[cb];
-        sc[rr] = ok ? (s4[rr] - qcorr[cb]) * r.ks[rr] * sm_scale : -INFINITY;
-        bmax = fmaxf(bmax, sc[rr]);
+        sc[rr] = (s4[cb][rr] - qcorr[cb]) * kss[rr];
+        if constexpr (MASKED) {
+          if (p * 16 + 4 * kq + rr >= visible[cb]) sc[rr] = -INFINITY;
+        }
       }
-      bmax = max4_across_kq(bmax);
+      const float bmax = max4_across_kq(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
       // Lazy rescaling: the reference maximum moves only when a score exceeds
       // it by more than 2^8, so exp2(s - m) <= 256 stays exact in fp32 and the
       // pass over every accumulator is rare; the final division by l removes
-      // the choice of reference.
+      // the choice of reference.  Page 0 holds a visible token for every
+      // column, so m_run is finite from the first page on.
       const float m_new = bmax > m_run[cb] + 8.0f ? bmax : m_run[cb];
       const bool moved = m_new != m_run[cb];
-      const float corr = moved ? exp2f(m_run[cb] - m_new) : 1.0f;
+      const float corr = moved ? __builtin_amdgcn_exp2f(m_run[cb] - m_new) : 1.0f;
       m_run[cb] = m_new;
       float pw[4];
-      float psum = 0.0f, pvsum = 0.0f;
+      float psum = 0.0f;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const float e = sc[rr] == -INFINITY ? 0.0f : exp2f(sc[rr] - m_new);
+        // v_exp_f32 directly: arguments are <= 8, exp2(-inf) = 0 for masked
+        // tokens, and a flushed tiny probability is below the fp32
+        // resolution of the running sum.
+        const float e = __builtin_amdgcn_exp2f(sc[rr] - m_new);
         psum += e;
-        pw[rr] = sc[rr] == -INFINITY ? 0.0f : e * r.vs[rr];  // fold the V scale (never NaN for masked rows)
-        pvsum += pw[rr];
+        pw[rr] = e * r.vs[rr];  // fold the V scale
       }
       l_lane[cb] = l_lane[cb] * corr + psum;
-      ps_lane[cb] = ps_lane[cb] * corr + pvsum;
-      // P'^T as bf16 hi + lo (B operand: k = tokens 4kq..4kq+3, column col).
-      uint32_t hi[4], lo[4];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        hi[rr] = __float_as_uint(pw[rr]) & 0xFFFF0000u;
-        lo[rr] = f32_to_bf16(pw[rr] - __uint_as_float(hi[rr]));
-      }
-      const u32x2 phi = {(hi[0] >> 16) | hi[1], (hi[2] >> 16) | hi[3]};
-      const u32x2 plo = {lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
       if (__builtin_amdgcn_ballot_w64(moved)) {
 #pragma unroll
         for (int db = 0; db < kDB; ++db) o[cb][db] *= corr;
       }
+      // P'^T as bf16 hi + lo (error ~2^-16), both in the K dimension of one
+      // 16x16x32 MFMA: lane (d, kq) supplies A = V^T[d][4 kq .. 4 kq + 3]
+      // twice and B = (hi, lo) of the same four tokens.
+      const uint32_t h01 = pack_bf16x2(pw[0], pw[1]), h23 = pack_bf16x2(pw[2], pw[3]);
+      pb[cb] = u32x4{h01, h23, pack_bf16x2(pw[0] - bf16_lo_f32(h01), pw[1] - bf16_hi_f32(h01)),
+                     pack_bf16x2(pw[2] - bf16_lo_f32(h23), pw[3] - bf16_hi_f32(h23))};
+    }
 #pragma unroll
-      for (int db = 0; db < kDB; ++db) {
-        const floatx4 od = mfma16x16x16(va[db], phi, o[cb][db]);
-        o[cb][db] = mfma16x16x16(va[db], plo, od);
-      }
+    for (int db = 0; db < kDB; ++db) {
+      const u32x4 vv = {va[db].x, va[db].y, va[db].x, va[db].y};
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) o[cb][db] = mfma16x16x32(vv, pb[cb], o[cb][db]);
     }
   };
-
-  // Two register sets deep: the next page's loads are in flight while the
-  // current one is reduced; its page-table entry is read a step earlier.
-  uint32_t p = 0;
-  PageRegs ra, rb;
-  int32_t phys_next = 0;
-  if (p < p_end) load_page(sq.pt[p], ra);
-  if (p + 1 < p_end) phys_next = sq.pt[p + 1];
-  while (p < p_end) {
-    if (p + 1 < p_end) {
-      load_page(phys_next, rb);
-      if (p + 2 < p_end) phys_next = sq.pt[p + 2];
+  // Pages [p0, p1) in one mode, two register sets deep: the next page's
+  // loads are in flight while the current one is reduced; its page-table
+  // entry is read a step earlier.
+  auto run = [&](uint32_t p0, uint32_t p1, auto masked) __attribute__((always_inline)) {
+    uint32_t p = p0;
+    PageRegs ra, rb;
+    int32_t phys_next = 0;
+    if (p < p1) load_page(sq.pt[p], ra);
+    if (p + 1 < p1) phys_next = sq.pt[p + 1];
+    while (p < p1) {
+      if (p + 1 < p1) {
+        load_page(phys_next, rb);
+        if (p + 2 < p1) phys_next = sq.pt[p + 2];
+      }
+      process_page(p, ra, masked);
+      ++p;
+      if (p >= p1) break;
+      if (p + 1 < p1) {
+        load_page(phys_next, ra);
+        if (p + 2 < p1) phys_next = sq.pt[p + 2];
+      }
+      process_page(p, rb, masked);
+      ++p;
     }
-    process_page(p, ra);
-    ++p;
-    if (p >= p_end) break;
-    if (p + 1 < p_end) {
-      load_page(phys_next, ra);
-      if (p + 2 < p_end) phys_next = sq.pt[p + 2];
-    }
-    process_page(p, rb);
-    ++p;
-  }
+  };
+  // Pages below full_end are visible to every row of the wave.
+  const uint32_t full_end = min(min(args.start + row_base + 1, sq.len) / 16, p_end);
+  run(0, full_end, BoolTag<false>{});
+  run(full_end, p_end, BoolTag<true>{});
 
   // O^T lane layout: column col, rows d = 16 db + 4 kq + r.
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
     float l_tot = l_lane[cb] + __shfl_xor(l_lane[cb], 16);
     l_tot += __shfl_xor(l_tot, 32);
-    float ps_tot = ps_lane[cb] + __shfl_xor(ps_lane[cb], 16);
-    ps_tot += __shfl_xor(ps_tot, 32);
     if (!col_ok[cb]) continue;
     const float inv = 1.0f / fmaxf(l_tot, FLT_MIN);
     const size_t obase = ((size_t)qrow[cb] * H + head) * dr;
@@ -859,7 +882,7 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
       for (int r = 0; r < 4; ++r) {
         const uint32_t d = 16 * db + 4 * kq + r;
         if (d >= dr) continue;
-        float v = (o[cb][db][r] - 128.0f * ps_tot) * inv;  // V was accumulated as v + 128
+        float v = o[cb][db][r] * inv;
         if (args.gate) v *= sigmoid_f(bf16_to_f32(args.gate[obase + d]));
         args.o[obase + d] = f32_to_bf16(v);
       }
