@@ -667,9 +667,6 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
   const uint32_t kvh = blockIdx.x % KVH;
   const uint32_t row_base = ((blockIdx.x / KVH) * kWaves + wave) * rows_per_wave;
   const AttnSeq& sq = args.seqs[0];
-  const uint32_t last_row = min(args.rows, row_base + rows_per_wave) - 1;
-  const uint32_t vis_max = min(args.start + last_row + 1, sq.len);
-  const uint32_t p_end = row_base < args.rows ? (vis_max + 15) / 16 : 0;
 
   const uint32_t ch = col % gh, cr = col / gh;
   const uint32_t head = kvh * gh + ch;
@@ -733,58 +730,93 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
   const size_t kv_page_stride = (size_t)KVH * 16 * D;
   const int tok = lane & 15;  // A-operand row: token of QK^T, d row of PV^T
 
-  // One page's operands in registers: lane (tok, kq) holds K[tok][D/4*kq ..
-  // + D/4) (16 B per two QK k-steps), V^T[16 db + tok][4 kq .. 4 kq + 3] for
-  // every d block, and the scales of tokens 4 kq .. 4 kq + 3.
-  struct PageRegs {
-    u32x4 k[kKS / 2];
-    uint32_t v[kDB];
-    floatx4 ks, vs;
+  // The four waves walk the same pages.  Each page is unpacked once per
+  // workgroup into an LDS stage (each wave a quarter of it) and every wave
+  // reads its MFMA operands from there:
+  //   K: u32x4 unit (j, kq, tok) = fp16 of 1024 + (k + 128) for
+  //      K[tok][D/4 kq + 8 j .. + 7] in the order d0,d2,d1,d3,d4,d6,d5,d7,
+  //      at row j * 4 + kq, slot tok ^ (row & 15);
+  //   V: u32x2 unit (db, kq, d) = bf16 of V^T[16 db + d][4 kq .. 4 kq + 3]
+  //      at row db * 4 + kq, slot d ^ 4 kq;
+  //   scales: K scale * softmax scale, then V scale, per token.
+  // The slot swizzles keep both the unpacking writes and the operand reads
+  // (16 lanes, one row, all slots) free of bank conflicts.
+  constexpr int kKUnits = 16 * D / 8;  // 8-byte units of one page's K (or V)
+  constexpr int kPerLane = (kKUnits / 4 + 63) / 64;
+  constexpr int kStage = 16 * D * 2 + 16 * D * 2 + 128;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kStage];
+  const int wave_unit0 = wave * (kKUnits / 4);
+
+  // Last row of the workgroup bounds every wave's page walk, so all waves
+  // pass the same barriers; pages past a wave's own rows are fully masked.
+  const uint32_t wg_row0 = (blockIdx.x / KVH) * kWaves * rows_per_wave;
+  const uint32_t wg_last = min(args.rows, wg_row0 + kWaves * rows_per_wave) - 1;
+  const uint32_t n_pages = (min(args.start + wg_last + 1, sq.len) + 15) / 16;
+
+  struct Raw {
+    u32x2 k[kPerLane], v[kPerLane];
+    float sc;
   };
-  auto load_page = [&](int32_t phys, PageRegs& r) __attribute__((always_inline)) {
-    const size_t pbase = (size_t)phys * kv_page_stride;
-    const int8_t* kr = sq.k + pbase + (size_t)kvh * 16 * D + tok * D + D / 4 * kq;
+  auto fetch = [&](int32_t phys, Raw& r) __attribute__((always_inline)) {
+    const size_t base = (size_t)phys * kv_page_stride + (size_t)kvh * 16 * D;
 #pragma unroll
-    for (int j = 0; j < kKS / 2; ++j) r.k[j] = *(const u32x4*)(kr + 16 * j);
-    const int8_t* vr = sq.v + pbase + (size_t)kvh * D * 16 + tok * 16 + 4 * kq;
-#pragma unroll
-    for (int db = 0; db < kDB; ++db) r.v[db] = *(const uint32_t*)(vr + 256 * db);
-    const size_t sbase = ((size_t)phys * KVH + kvh) * 16 + 4 * kq;
-    r.ks = *(const floatx4*)(sq.ks + sbase);
-    r.vs = *(const floatx4*)(sq.vs + sbase);
-  };
-  // MASKED is false for pages every column of the wave sees whole (all but
-  // the last few): those skip the causal compare and select per score.
-  auto process_page = [&](uint32_t p, const PageRegs& r, auto masked) __attribute__((always_inline)) {
-    constexpr bool MASKED = decltype(masked)::value;
-    // K as fp16 of 1024 + (k + 128) (one AND-OR per pair), unpacked once for
-    // every block.
-    u32x4 ka[kKS];
-#pragma unroll
-    for (int j = 0; j < kKS / 2; ++j) {
-      const u32x4 kb = r.k[j];
-      const u32x2 l0 = q8x4_to_f16_biased(kb.x), h0 = q8x4_to_f16_biased(kb.y);
-      const u32x2 l1 = q8x4_to_f16_biased(kb.z), h1 = q8x4_to_f16_biased(kb.w);
-      ka[2 * j] = u32x4{l0.x, l0.y, h0.x, h0.y};
-      ka[2 * j + 1] = u32x4{l1.x, l1.y, h1.x, h1.y};
+    for (int i = 0; i < kPerLane; ++i) {
+      const int u = lane + 64 * i;
+      if (u < kKUnits / 4) {
+        const size_t off = base + 8 * (size_t)(wave_unit0 + u);
+        r.k[i] = *(const u32x2*)(sq.k + off);
+        r.v[i] = *(const u32x2*)(sq.v + off);
+      }
     }
-    // V unbiased (signed bytes -> bf16, exact): O accumulates only
-    // sum_t v_t p'_t.
-    u32x2 va[kDB];
+    if (wave == 0 && lane < 32) {
+      const size_t si = ((size_t)phys * KVH + kvh) * 16 + (lane & 15);
+      r.sc = lane < 16 ? sq.ks[si] * sm_scale : sq.vs[si];
+    }
+  };
+  auto stage_in = [&](const Raw& r, int st) __attribute__((always_inline)) {
+    uint8_t* base = lds + st * kStage;
 #pragma unroll
-    for (int db = 0; db < kDB; ++db) va[db] = q8x4_to_bf16_signed(r.v[db]);
-    float kss[4];
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) kss[rr] = r.ks[rr] * sm_scale;
+    for (int i = 0; i < kPerLane; ++i) {
+      const int u = lane + 64 * i;
+      if (u < kKUnits / 4) {
+        const int g = wave_unit0 + u;
+        // K unit: token g / (D / 8), 8-byte chunk c = kq * kKS + j.
+        const int kt = g / (D / 8), c = g % (D / 8);
+        const u32x2 l = q8x4_to_f16_biased(r.k[i].x), h = q8x4_to_f16_biased(r.k[i].y);
+        const int krow = (c % kKS) * 4 + c / kKS;
+        *(u32x4*)(base + 16 * (krow * 16 + (kt ^ (krow & 15)))) = u32x4{l.x, l.y, h.x, h.y};
+        // V unit: d row g / 2, tokens 8 (g & 1) .. + 7 = kq 2 (g & 1), + 1.
+        const int d = g >> 1, kq0 = 2 * (g & 1);
+        const u32x2 v0 = q8x4_to_bf16_signed(r.v[i].x), v1 = q8x4_to_bf16_signed(r.v[i].y);
+        uint8_t* vb = base + 16 * D * 2;
+        *(u32x2*)(vb + 8 * (((d >> 4) * 4 + kq0) * 16 + ((d & 15) ^ (4 * kq0)))) = v0;
+        *(u32x2*)(vb + 8 * (((d >> 4) * 4 + kq0 + 1) * 16 + ((d & 15) ^ (4 * kq0 + 4)))) = v1;
+      }
+    }
+    if (wave == 0 && lane < 32) *(float*)(base + 16 * D * 4 + 4 * lane) = r.sc;
+  };
+
+  // Softmax and P'V of page p from LDS stage st.  MASKED is false for pages
+  // every column of the wave sees whole (all but the last few): those skip
+  // the causal compare and select per score.
+  auto compute = [&](uint32_t p, int st, auto masked) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked)::value;
+    const uint8_t* base = lds + st * kStage;
+    const u32x4* kl = (const u32x4*)base;
+    const u32x2* vl = (const u32x2*)(base + 16 * D * 2);
+    const floatx4 kss = *(const floatx4*)(base + 16 * D * 4 + 16 * kq);
+    const floatx4 vs = *(const floatx4*)(base + 16 * D * 4 + 64 + 16 * kq);
     // S^T[token][col] over D in kKS steps of 32; the blocks' chains are
     // independent and interleave.
     floatx4 s4[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) s4[cb] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < kKS; ++j)
+    for (int j = 0; j < kKS; ++j) {
+      const u32x4 ka = kl[(j * 4 + kq) * 16 + (tok ^ ((j * 4 + kq) & 15))];
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) s4[cb] = mfma16x16x32_f16(ka[j], qb[cb][j], s4[cb]);
+      for (int cb = 0; cb < CB; ++cb) s4[cb] = mfma16x16x32_f16(ka, qb[cb][j], s4[cb]);
+    }
     u32x4 pb[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
@@ -817,56 +849,61 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
         // resolution of the running sum.
         const float e = __builtin_amdgcn_exp2f(sc[rr] - m_new);
         psum += e;
-        pw[rr] = e * r.vs[rr];  // fold the V scale
+        pw[rr] = e * vs[rr];  // fold the V scale
+        if constexpr (MASKED) {
+          if (sc[rr] == -INFINITY) pw[rr] = 0.0f;  // whatever an unwritten slot's scale holds
+        }
       }
       l_lane[cb] = l_lane[cb] * corr + psum;
       if (__builtin_amdgcn_ballot_w64(moved)) {
 #pragma unroll
         for (int db = 0; db < kDB; ++db) o[cb][db] *= corr;
       }
-      // P'^T as bf16 hi + lo (error ~2^-16), both in the K dimension of one
-      // 16x16x32 MFMA: lane (d, kq) supplies A = V^T[d][4 kq .. 4 kq + 3]
-      // twice and B = (hi, lo) of the same four tokens.
+      // P'^T as bf16 hi + lo (error ~2^-16): B operands of two 16x16x16
+      // MFMAs (k = tokens 4 kq .. 4 kq + 3, column col).
       const uint32_t h01 = pack_bf16x2(pw[0], pw[1]), h23 = pack_bf16x2(pw[2], pw[3]);
       pb[cb] = u32x4{h01, h23, pack_bf16x2(pw[0] - bf16_lo_f32(h01), pw[1] - bf16_hi_f32(h01)),
                      pack_bf16x2(pw[2] - bf16_lo_f32(h23), pw[3] - bf16_hi_f32(h23))};
     }
+    // V unbiased (signed bytes -> bf16, exact): O accumulates only
+    // sum_t v_t p'_t.
 #pragma unroll
     for (int db = 0; db < kDB; ++db) {
-      const u32x4 vv = {va[db].x, va[db].y, va[db].x, va[db].y};
+      const u32x2 va = vl[(db * 4 + kq) * 16 + (tok ^ (4 * kq))];
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) o[cb][db] = mfma16x16x32(vv, pb[cb], o[cb][db]);
+      for (int cb = 0; cb < CB; ++cb) {
+        o[cb][db] = mfma16x16x16(va, u32x2{pb[cb].x, pb[cb].y}, o[cb][db]);
+        o[cb][db] = mfma16x16x16(va, u32x2{pb[cb].z, pb[cb].w}, o[cb][db]);
+      }
     }
   };
-  // Pages [p0, p1) in one mode, two register sets deep: the next page's
-  // loads are in flight while the current one is reduced; its page-table
-  // entry is read a step earlier.
-  auto run = [&](uint32_t p0, uint32_t p1, auto masked) __attribute__((always_inline)) {
-    uint32_t p = p0;
-    PageRegs ra, rb;
-    int32_t phys_next = 0;
-    if (p < p1) load_page(sq.pt[p], ra);
-    if (p + 1 < p1) phys_next = sq.pt[p + 1];
-    while (p < p1) {
-      if (p + 1 < p1) {
-        load_page(phys_next, rb);
-        if (p + 2 < p1) phys_next = sq.pt[p + 2];
-      }
-      process_page(p, ra, masked);
-      ++p;
-      if (p >= p1) break;
-      if (p + 1 < p1) {
-        load_page(phys_next, ra);
-        if (p + 2 < p1) phys_next = sq.pt[p + 2];
-      }
-      process_page(p, rb, masked);
-      ++p;
+
+  // Pipeline, one barrier per page: page p + 1's quarter (fetched a page
+  // earlier) is unpacked into the other stage, page p + 2's quarter is
+  // fetched, then page p is reduced from its stage.  The barrier waits on LDS
+  // only, so the fetch stays in flight across it.
+  Raw raw;
+  if (n_pages > 0) {
+    fetch(sq.pt[0], raw);
+    stage_in(raw, 0);
+    if (n_pages > 1) fetch(sq.pt[1], raw);
+  }
+  lds_barrier();
+  int32_t ph_next = n_pages > 2 ? sq.pt[2] : 0;
+  auto step = [&](uint32_t p, auto masked) __attribute__((always_inline)) {
+    const int st = p & 1;
+    if (p + 1 < n_pages) stage_in(raw, st ^ 1);
+    if (p + 2 < n_pages) {
+      fetch(ph_next, raw);
+      if (p + 3 < n_pages) ph_next = sq.pt[p + 3];
     }
+    compute(p, st, masked);
+    lds_barrier();
   };
   // Pages below full_end are visible to every row of the wave.
-  const uint32_t full_end = min(min(args.start + row_base + 1, sq.len) / 16, p_end);
-  run(0, full_end, BoolTag<false>{});
-  run(full_end, p_end, BoolTag<true>{});
+  const uint32_t full_end = min(min(args.start + row_base + 1, sq.len) / 16, n_pages);
+  for (uint32_t p = 0; p < full_end; ++p) step(p, BoolTag<false>{});
+  for (uint32_t p = full_end; p < n_pages; ++p) step(p, BoolTag<true>{});
 
   // O^T lane layout: column col, rows d = 16 db + 4 kq + r.
 #pragma unroll
