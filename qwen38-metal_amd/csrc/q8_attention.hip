@@ -859,8 +859,10 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
 #pragma unroll
         for (int db = 0; db < kDB; ++db) o[cb][db] *= corr;
       }
-      // P'^T as bf16 hi + lo (error ~2^-16): B operands of two 16x16x16
-      // MFMAs (k = tokens 4 kq .. 4 kq + 3, column col).
+      // P'^T as bf16 hi + lo (error ~2^-16), both in the K dimension of one
+      // 16x16x32 MFMA: lane (d, kq) supplies A = V^T[d][4 kq .. 4 kq + 3]
+      // twice and B = (hi, lo) of the same four tokens (the legacy 16x16x16
+      // form costs as many cycles as the 16x16x32 one).
       const uint32_t h01 = pack_bf16x2(pw[0], pw[1]), h23 = pack_bf16x2(pw[2], pw[3]);
       pb[cb] = u32x4{h01, h23, pack_bf16x2(pw[0] - bf16_lo_f32(h01), pw[1] - bf16_hi_f32(h01)),
                      pack_bf16x2(pw[2] - bf16_lo_f32(h23), pw[3] - bf16_hi_f32(h23))};
@@ -870,11 +872,9 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
 #pragma unroll
     for (int db = 0; db < kDB; ++db) {
       const u32x2 va = vl[(db * 4 + kq) * 16 + (tok ^ (4 * kq))];
+      const u32x4 vv = {va.x, va.y, va.x, va.y};
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        o[cb][db] = mfma16x16x16(va, u32x2{pb[cb].x, pb[cb].y}, o[cb][db]);
-        o[cb][db] = mfma16x16x16(va, u32x2{pb[cb].z, pb[cb].w}, o[cb][db]);
-      }
+      for (int cb = 0; cb < CB; ++cb) o[cb][db] = mfma16x16x32(vv, pb[cb], o[cb][db]);
     }
   };
 
