@@ -15,11 +15,12 @@
 //    flash attention over Q8 pages.  A wave owns one KV head and the GQA group
 //    of <= 16 query heads sharing it (decode), or CB blocks of 16 (row, head)
 //    columns (prefill).  Per 16-token page:
-//      S^T = K Q^T on MFMA 16x16x32 (K bytes -> bf16 of k+128 exactly, the
-//      +128 is removed with a per-head correction),
-//      online softmax in fp32 (exp2 domain),
-//      O^T += V^T P^T on MFMA 16x16x16 with P' = p * v_scale split into
-//      bf16 hi + lo (error ~2^-16), again with a +128 correction.
+//      S^T = K Q^T on fp16 MFMA 16x16x32 (K bytes -> fp16 of 1024 + (k + 128)
+//      exactly, one AND-OR per pair; 1152 * sum(q) is removed per column),
+//      online softmax in fp32 (exp2 domain, lazy rescaling),
+//      O^T += V^T P^T on bf16 MFMA 16x16x32 with V as exact signed bf16 and
+//      P' = p * v_scale split into bf16 hi + lo (error ~2^-16), both halves
+//      in the MFMA's K dimension.
 //    The S^T/O^T orientation keeps every head in one lane column, so the
 //    softmax statistics never move between lanes except for the 4-way max.
 //    Decode splits the pages of a sequence over workgroups (combined in
@@ -644,9 +645,9 @@ __global__ __launch_bounds__(256) void q8_combine_kernel(AttnArgs args) {
 
 // Causal prefill: blockIdx.x = rb * KVH + kvh.  A wave owns CB column
 // blocks of 16 (row, head) columns, i.e. CB * 16 / gh query rows of one KV
-// head, and streams the pages its last row can see through two register
-// sets.  Each page's K and V are unpacked once into MFMA A operands and serve
-// all CB blocks: K/V traffic per column falls by CB.
+// head; the workgroup's four waves own consecutive rows and walk the same
+// pages, which are unpacked once per workgroup into LDS (each wave a
+// quarter) and serve every wave's CB blocks.
 template <int D, int CB>
 __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
   constexpr int kWaves = 4;
