@@ -207,11 +207,11 @@ __device__ __forceinline__ floatx4 mfma16x16x32_f16(u32x4 a, u32x4 b, floatx4 c)
 // column) with the gfx950 row-swap permutes instead of LDS shuffles.
 __device__ __forceinline__ float max4_across_kq(float v) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  const float x = __uint_as_float(a[0]), y = __uint_as_float(a[1]);
-  const float m = x > y ? x : y;
+  // fmaxf is v_max_f32 (one operation; the operands are never NaN), where a
+  // compare and select would be two plus a VCC hazard wait.
+  const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-  const float p = __uint_as_float(b[0]), q = __uint_as_float(b[1]);
-  return p > q ? p : q;
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 template <bool B>
