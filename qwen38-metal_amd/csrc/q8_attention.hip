@@ -666,7 +666,11 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
   // so every row block of one KV head runs on the same XCD(s) and its pages
   // (1.5 MiB per head at 6K tokens, d = 128) stay in that XCD's L2.
   const uint32_t kvh = blockIdx.x % KVH;
-  const uint32_t row_base = ((blockIdx.x / KVH) * kWaves + wave) * rows_per_wave;
+  // Row blocks are dealt last first: the later rows see the most pages, and
+  // starting the longest workgroups first lets the short ones fill the
+  // slots they free (the grid runs in about two residency rounds).
+  const uint32_t rb = row_blocks - 1 - blockIdx.x / KVH;
+  const uint32_t row_base = (rb * kWaves + wave) * rows_per_wave;
   const AttnSeq& sq = args.seqs[0];
 
   const uint32_t ch = col % gh, cr = col / gh;
@@ -750,7 +754,7 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
 
   // Last row of the workgroup bounds every wave's page walk, so all waves
   // pass the same barriers; pages past a wave's own rows are fully masked.
-  const uint32_t wg_row0 = (blockIdx.x / KVH) * kWaves * rows_per_wave;
+  const uint32_t wg_row0 = rb * kWaves * rows_per_wave;
   const uint32_t wg_last = min(args.rows, wg_row0 + kWaves * rows_per_wave) - 1;
   const uint32_t n_pages = (min(args.start + wg_last + 1, sq.len) + 15) / 16;
 
