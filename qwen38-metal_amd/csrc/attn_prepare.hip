@@ -29,6 +29,7 @@
 #include "prepare.h"
 
 #include <algorithm>
+#include <cmath>
 
 namespace qm {
 namespace {
@@ -87,7 +88,7 @@ __global__ __launch_bounds__(64 * kPrepWaves) void attn_prepare_kernel(PrepArgs 
     const uint32_t p = a.positions ? a.positions[(size_t)axis * a.M + row] : a.base + row;
     // fp64 angle, reduced to [-pi, pi] with a two-part 2 pi (error ~1e-11 rad
     // at 1e5 rad), then single-precision sine and cosine of the small argument.
-    const double angle = (double)p * pow((double)a.theta, -(double)(2 * i) / (double)rd);
+    const double angle = (double)p * a.inv_freq[i];
     const double turns = rint(angle * 0.15915494309189535);
     double r = fma(-turns, 6.283185307179586, angle);
     r = fma(-turns, 2.4492935982947064e-16, r);
@@ -206,8 +207,11 @@ __global__ __launch_bounds__(64 * kPrepWaves) void attn_prepare_kernel(PrepArgs 
 
 hipError_t launch_attn_prepare(const PrepArgs& a, hipStream_t st) {
   constexpr uint32_t kMaxGridY = 65535;  // rows per launch (kept below the y limit for symmetry)
+  PrepArgs f = a;
+  for (uint32_t i = 0; i < a.rotary_dim / 2 && i < kPrepMaxHeadDim / 2; ++i)
+    f.inv_freq[i] = pow((double)a.theta, -(double)(2 * i) / (double)a.rotary_dim);
   for (uint32_t r0 = 0; r0 < a.M; r0 += kMaxGridY) {
-    PrepArgs c = a;
+    PrepArgs c = f;
     c.row0 = r0;
     // Head groups per row: enough blocks to cover the CUs a few times over
     // (one head per wave at M = 1; one block per row for long prompts).

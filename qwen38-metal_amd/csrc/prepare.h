@@ -21,6 +21,9 @@ struct PrepArgs {
   uint32_t row0;  // first row of this launch (the launcher splits M into grid-sized chunks)
   uint32_t base, section1, section2, has_sections;
   float theta, eps;
+  // theta^(-2 i / rotary_dim) in fp64 for i < rotary_dim / 2, filled by
+  // launch_attn_prepare (the launch arguments carry them to every block).
+  double inv_freq[kPrepMaxHeadDim / 2];
 };
 
 hipError_t launch_attn_prepare(const PrepArgs& a, hipStream_t st);
