@@ -122,18 +122,6 @@ __global__ __launch_bounds__(64) void q8_append_kernel(AppendArgs args) {
 // ---------------------------------------------------------------------------
 // Attention
 // ---------------------------------------------------------------------------
-// 4 int8 -> 4 bf16 of (int8 + 128), exact (values 1..255 fit bf16).
-__device__ __forceinline__ u32x2 q8x4_to_bf16_biased(uint32_t w) {
-  const uint32_t u = w ^ 0x80808080u;
-  const float f0 = (float)((u >> 0) & 0xFFu);
-  const float f1 = (float)((u >> 8) & 0xFFu);
-  const float f2 = (float)((u >> 16) & 0xFFu);
-  const float f3 = (float)((u >> 24) & 0xFFu);
-  u32x2 r;
-  r.x = perm_b32(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
-  r.y = perm_b32(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
-  return r;
-}
 
 // ---------------------------------------------------------------------------
 // Decode: pages stream through a per-wave LDS ring by buffer->LDS DMA
