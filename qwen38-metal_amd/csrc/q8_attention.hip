@@ -120,10 +120,6 @@ __global__ __launch_bounds__(64) void q8_append_kernel(AppendArgs args) {
 }
 
 // ---------------------------------------------------------------------------
-// Attention
-// ---------------------------------------------------------------------------
-
-// ---------------------------------------------------------------------------
 // Decode: pages stream through a per-wave LDS ring by buffer->LDS DMA
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
