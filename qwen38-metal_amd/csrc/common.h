@@ -95,6 +95,19 @@ __device__ __forceinline__ float wave_allsum(float v) {
   return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
+// Maximum over the 64 lanes with the same DPP / permlane steps (exact in any
+// order, so it equals a shuffle tree's result).
+__device__ __forceinline__ float wave_allmax(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+
 // Workgroup barrier that orders LDS only: waits for the wave's own LDS
 // operations (lgkmcnt) but leaves its global loads and stores in flight,
 // unlike __syncthreads(), whose workgroup fence also drains vmcnt.  Use it

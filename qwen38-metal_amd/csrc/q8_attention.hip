@@ -45,34 +45,57 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// A row's values 4 lane .. 4 lane + 3 (zero past dr): one 16-byte load when
+// dr is a multiple of 4.
+__device__ __forceinline__ void q8_load_row(const float* src, uint32_t dr, int lane, float (&vals)[4]) {
+  if (dr % 4 == 0) {
+    const floatx4 v = (uint32_t)lane * 4 < dr ? *(const floatx4*)(src + lane * 4) : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vals[i] = v[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vals[i] = (uint32_t)lane * 4 + i < dr ? src[lane * 4 + i] : 0.0f;
+  }
+}
+
+// Quantises one row held 4 values per lane as qwen38_q8_kv_append does:
+// s = max(absmax / 127, FLT_MIN), q = round-half-away(clamp(x / s, -127,
+// 127)), IEEE division.  Returns s.
+__device__ __forceinline__ float q8_quant_vals(const float (&vals)[4], int8_t (&qv)[4]) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) amax = fmaxf(amax, fabsf(vals[i]));
+  amax = wave_allmax(amax);
+  const float s = fmaxf(amax / 127.0f, FLT_MIN);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) qv[i] = (int8_t)roundf(fminf(fmaxf(vals[i] / s, -127.0f), 127.0f));
+  return s;
+}
+
+__device__ __forceinline__ float q8_quant_row(const float* src, uint32_t dr, int lane, int8_t (&qv)[4]) {
+  float vals[4];
+  q8_load_row(src, dr, lane, vals);
+  return q8_quant_vals(vals, qv);
+}
+
+__device__ __forceinline__ uint32_t pack_q8x4(const int8_t (&qv)[4]) {
+  return (uint32_t)(uint8_t)qv[0] | ((uint32_t)(uint8_t)qv[1] << 8) | ((uint32_t)(uint8_t)qv[2] << 16) |
+         ((uint32_t)(uint8_t)qv[3] << 24);
+}
+
 // Quantises one (token, kv_head) row of K (kind 0) or V (kind 1) with one
-// 64-lane wave and stores it into page `page` slot `slot`.  Matches
-// qwen38_q8_kv_append: s = max(absmax / 127, FLT_MIN), q = round-half-away
-// (clamp(x / s, -127, 127)), IEEE division.  `src` holds the dr real
-// dimensions; the page row has Dp, and dimensions dr..Dp-1 store zero.
+// 64-lane wave and stores it into page `page` slot `slot`.  `src` holds the
+// dr real dimensions; the page row has Dp, and dimensions dr..Dp-1 store
+// zero.
 __device__ __forceinline__ void q8_store_row(const AttnSeq& sq, const float* src, uint32_t kind, int32_t page,
                                              uint32_t slot, uint32_t kvh, uint32_t kvh_count, uint32_t dr,
                                              uint32_t Dp, int lane) {
-  float vals[4];
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t d = lane * 4 + i;
-    vals[i] = d < dr ? src[d] : 0.0f;
-    amax = fmaxf(amax, fabsf(vals[i]));
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-  const float s = fmaxf(amax / 127.0f, FLT_MIN);
   int8_t qv[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) qv[i] = (int8_t)roundf(fminf(fmaxf(vals[i] / s, -127.0f), 127.0f));
+  const float s = q8_quant_row(src, dr, lane, qv);
   const size_t pkv = (size_t)page * kvh_count + kvh;
   if ((uint32_t)lane * 4 < Dp) {
     if (kind == 0) {
-      const uint32_t packed = (uint32_t)(uint8_t)qv[0] | ((uint32_t)(uint8_t)qv[1] << 8) |
-                              ((uint32_t)(uint8_t)qv[2] << 16) | ((uint32_t)(uint8_t)qv[3] << 24);
-      *(uint32_t*)(sq.k + (pkv * 16 + slot) * Dp + lane * 4) = packed;
+      *(uint32_t*)(sq.k + (pkv * 16 + slot) * Dp + lane * 4) = pack_q8x4(qv);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) sq.v[(pkv * Dp + lane * 4 + i) * 16 + slot] = qv[i];
@@ -117,6 +140,61 @@ __global__ __launch_bounds__(64) void q8_append_kernel(AppendArgs args) {
   }
   const float* src = (kind == 0 ? args.k : args.v) + ((size_t)item * kvh_count + kvh) * D;
   q8_store_row(sq, src, kind, page_id(sq, token / 16), token % 16, kvh, kvh_count, D, Dp, lane);
+}
+
+// Prefill append, one workgroup per (page, kv_head) of the rows' pages: each
+// wave quantises tokens of the page (K rows go straight to the page, V values
+// into an LDS copy of the page's d-major V block), then each thread stores one
+// 16-token V row of the block with one 16-byte write.  A page the call only
+// partly fills first takes its existing V rows into LDS, so the slots of
+// earlier tokens keep their bytes.  The same quantiser as q8_store_row: the
+// bytes and scales do not depend on the kernel that wrote them.
+constexpr int kAppendWaves = 4;
+__global__ __launch_bounds__(64 * kAppendWaves) void q8_append_pages_kernel(AppendArgs args) {
+  __shared__ __attribute__((aligned(16))) uint8_t vb[256 * 16];  // [d][slot], Dp <= 256
+  const uint32_t KVH = args.kv_heads, D = args.head_dim, Dp = args.head_dim_pad;
+  const AttnSeq& sq = args.seqs[0];
+  const uint32_t p = args.start / 16 + blockIdx.x / KVH, kvh = blockIdx.x % KVH;
+  const uint32_t tid = threadIdx.x, wave = tid >> 6;
+  const int lane = tid & 63;
+  const uint32_t lo = max(args.start, 16 * p) - 16 * p, hi = min(sq.len, 16 * p + 16) - 16 * p;
+  // Page-table entry of a page this call materialises (one writer per page).
+  if (kvh == 0 && tid == 0 && sq.new_page_count > 0 && (int32_t)p >= sq.new_page_first &&
+      (int32_t)p < sq.new_page_first + sq.new_page_count)
+    sq.pt[p] = sq.new_page_id + ((int32_t)p - sq.new_page_first);
+  const size_t pkv = (size_t)page_id(sq, p) * KVH + kvh;
+  int8_t* vpage = sq.v + pkv * Dp * 16;
+  if ((lo > 0 || hi < 16) && tid < Dp) *(u32x4*)(vb + 16 * tid) = *(const u32x4*)(vpage + 16 * tid);
+  __syncthreads();
+  // A wave's (up to) four tokens: every K and V load in flight first.
+  constexpr int kPer = 16 / kAppendWaves;
+  float kx[kPer][4], vx[kPer][4];
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const uint32_t slot = lo + wave + kAppendWaves * t;
+    const size_t row = ((size_t)(16 * p + min(slot, hi - 1) - args.start) * KVH + kvh) * D;
+    q8_load_row(args.k + row, D, lane, kx[t]);
+    q8_load_row(args.v + row, D, lane, vx[t]);
+  }
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const uint32_t slot = lo + wave + kAppendWaves * t;
+    if (slot >= hi) break;  // wave-uniform
+    int8_t qk[4], qv[4];
+    const float sk = q8_quant_vals(kx[t], qk);
+    const float sv = q8_quant_vals(vx[t], qv);
+    if ((uint32_t)lane * 4 < Dp) {
+      *(uint32_t*)(sq.k + (pkv * 16 + slot) * Dp + lane * 4) = pack_q8x4(qk);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vb[(lane * 4 + i) * 16 + slot] = (uint8_t)qv[i];
+    }
+    if (lane == 0) {
+      sq.ks[pkv * 16 + slot] = sk;
+      sq.vs[pkv * 16 + slot] = sv;
+    }
+  }
+  __syncthreads();
+  if (tid < Dp) *(u32x4*)(vpage + 16 * tid) = *(const u32x4*)(vb + 16 * tid);
 }
 
 // ---------------------------------------------------------------------------
@@ -949,7 +1027,14 @@ hipError_t launch_attn_d(const AttnArgs& a, uint32_t units, bool need_combine, h
 }  // namespace
 
 hipError_t launch_q8_append(const AppendArgs& a, uint32_t items, hipStream_t st) {
-  hipLaunchKernelGGL(q8_append_kernel, dim3(items * a.kv_heads * 2), dim3(64), 0, st, a);
+  if (items == 0) return hipSuccess;
+  if (a.decode) {
+    hipLaunchKernelGGL(q8_append_kernel, dim3(items * a.kv_heads * 2), dim3(64), 0, st, a);
+  } else {
+    // Rows start .. start + items - 1 of seqs[0] (whose len is start + items).
+    const uint32_t pages = (a.start + items - 1) / 16 - a.start / 16 + 1;
+    hipLaunchKernelGGL(q8_append_pages_kernel, dim3(pages * a.kv_heads), dim3(64 * kAppendWaves), 0, st, a);
+  }
   return hipGetLastError();
 }
 
