@@ -809,10 +809,10 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
   // The slot swizzles keep both the unpacking writes and the operand reads
   // (16 lanes, one row, all slots) free of bank conflicts.
   constexpr int kKUnits = 16 * D / 8;  // 8-byte units of one page's K (or V)
-  constexpr int kPerLane = (kKUnits / 4 + 63) / 64;
+  constexpr int kPerLane = (kKUnits / kWaves + 63) / 64;
   constexpr int kStage = 16 * D * 2 + 16 * D * 2 + 128;
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kStage];
-  const int wave_unit0 = wave * (kKUnits / 4);
+  const int wave_unit0 = wave * (kKUnits / kWaves);
 
   // Last row of the workgroup bounds every wave's page walk, so all waves
   // pass the same barriers; pages past a wave's own rows are fully masked.
@@ -829,7 +829,7 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
 #pragma unroll
     for (int i = 0; i < kPerLane; ++i) {
       const int u = lane + 64 * i;
-      if (u < kKUnits / 4) {
+      if (u < kKUnits / kWaves) {
         const size_t off = base + 8 * (size_t)(wave_unit0 + u);
         r.k[i] = *(const u32x2*)(sq.k + off);
         r.v[i] = *(const u32x2*)(sq.v + off);
@@ -845,7 +845,7 @@ __global__ __launch_bounds__(256) void q8_prefill_kernel(AttnArgs args) {
 #pragma unroll
     for (int i = 0; i < kPerLane; ++i) {
       const int u = lane + 64 * i;
-      if (u < kKUnits / 4) {
+      if (u < kKUnits / kWaves) {
         const int g = wave_unit0 + u;
         // K unit: token g / (D / 8), 8-byte chunk c = kq * kKS + j.
         const int kt = g / (D / 8), c = g % (D / 8);
