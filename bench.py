@@ -687,7 +687,9 @@ def stats_summary(prof_dir: str) -> int:
         "# causal prefill, including the 32K/128K cache fills of the attention legs; q4_gemm_kernel serves",
         "# M = 512 and 2048; q8_decode_kernel<128> serves the 32K single-sequence and ragged batch-8 legs).",
         "# The gate+up decode kernel (q4_decode_kernel<2, 1, true, true, true>, M = 1) is the bench's",
-        "# roofline kernel: its average here agrees with bench.py's avg_launch_us for that launch.",
+        "# roofline kernel.  bench.py's avg_launch_us for it comes from events around back-to-back",
+        "# launches, so it also holds the gap between launches (about 1-2 us) and reads that much above",
+        "# the kernel-only average here.",
         "",
         f"{'kernel':<100} {'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'pct':>7}",
     ]
