@@ -121,6 +121,46 @@ typedef struct qm_q4_job {
   uint32_t out_rows;
 } qm_q4_job;
 
+/* Every Q4 entry point below checks, on a device runtime and before anything
+ * is launched, that each tensor a job names lies inside one device
+ * allocation (hipMemGetAddressRange): weights out_rows*in/8 u32, scales and
+ * biases out_rows*in/64 bf16, and likewise the activation and output
+ * buffers.  A pointer inside no allocation fails with
+ * QM_ERR_INVALID_BUFFER_OFFSET, a tensor running past the end of its
+ * allocation with QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE, as
+ * validate_mapped_q4_affine_shape does for Metal buffers
+ * (metal_runtime.rs:8854-8898). */
+
+/* A device allocation and its length: the C counterpart of the
+ * `&metal::Buffer` a MappedQ4AffineJob borrows. */
+typedef struct qm_buffer {
+  const void* base;
+  uint64_t length; /* bytes */
+} qm_buffer;
+
+/* MappedQ4AffineJob (metal_runtime.rs:155-192): three tensors given as
+ * (buffer, byte offset), for weights mapped from one large checkpoint
+ * allocation.  The reference's `aligned` flag selects its unaligned kernel
+ * twins; here the resolved pointers must be 8-byte aligned instead. */
+typedef struct qm_q4_mapped_job {
+  qm_buffer weights;
+  uint64_t weight_offset;
+  qm_buffer scales;
+  uint64_t scale_offset;
+  qm_buffer biases;
+  uint64_t bias_offset;
+  uint32_t out_rows;
+} qm_q4_mapped_job;
+
+/* Resolves a mapped job for input width in_elems into a qm_q4_job, with the
+ * checks of validate_mapped_q4_affine_shape (metal_runtime.rs:8854-8898), in
+ * its order: EMPTY_DIMENSION (in_elems or out_rows zero), INPUT_NOT_GROUPED
+ * (in_elems % 64), INVALID_BUFFER_OFFSET (an offset beyond its buffer's
+ * length), DIMENSION_OVERFLOW, MAPPED_TENSOR_OUT_OF_RANGE (a tensor longer
+ * than what its buffer holds past the offset); then NULL_POINTER and
+ * MISALIGNED.  Host only: reads no device memory. */
+qm_status qm_q4_job_from_mapped(const qm_q4_mapped_job* mapped, uint32_t in_elems, qm_q4_job* out);
+
 /* y_j[m][n] = sum_g ( s_j[n][g] * sum_{i in g} q_j[n][i] x[m][i]
  *                    + b_j[n][g] * sum_{i in g} x[m][i] )
  * for every job j, all jobs reading the same activation x (bf16 [M][in]).
@@ -149,6 +189,15 @@ qm_status qm_q4_swiglu(qm_runtime* rt, const qm_q4_job* gate, const qm_q4_job* u
 qm_status qm_q4_mlp(qm_runtime* rt, const qm_q4_job* gate, const qm_q4_job* up,
                     const qm_q4_job* down, const uint16_t* x, uint32_t in_elems,
                     uint32_t M, uint16_t* y);
+
+/* Greedy token of every row: ids[m] = argmax_n y[m][n] over the fp32 (not
+ * bf16-rounded) projection y = job(x), the lowest index winning ties and NaN
+ * logits never winning (an all-NaN row gives 0).  Only the M ids reach
+ * memory; the logits never do.  ids is a device pointer, uint32 [M].
+ * Replaces q4_affine_argmax_mapped_batch (metal_runtime.rs:3797-3890) with
+ * qwen38_argmax_rows (qwen38.metal:4202-4244). */
+qm_status qm_q4_argmax(qm_runtime* rt, const qm_q4_job* job, const uint16_t* x,
+                       uint32_t in_elems, uint32_t M, uint32_t* ids);
 
 /* ------------------------------------------------------------------ */
 /* Paged Q8 KV cache                                                   */
@@ -216,8 +265,11 @@ qm_status qm_attn_decode(qm_runtime* rt, qm_kv* const* seqs, uint32_t B,
                          uint16_t* o);
 
 /* qm_attn_decode that allocates nothing: no counterpart in the reference.
- * For callers that cannot allocate device memory (code under HIP graph
- * capture, tight serving loops, harnesses that forbid hipMalloc).  The split
+ * For callers that cannot allocate device memory (tight serving loops,
+ * harnesses that forbid hipMalloc).  It is not meant for HIP graph capture:
+ * each call advances the caches' host-side length and page table when it is
+ * made, so a captured call would describe exactly one position (valid for one
+ * replay, and only while no later call grows the caches).  The split
  * partials live in a fixed 16 MiB device array of the library, one per GPU,
  * held until the process ends.  The caches are not grown: every sequence
  * must have room for its token (qm_kv_reserve beforehand), else

@@ -54,6 +54,7 @@ struct AttnArgs {
   uint32_t n_seqs;
   uint32_t pages_per_split;  // decode
   uint32_t wg_waves;         // decode: waves per workgroup (4: two workgroups per CU; 8: one)
+  int32_t prefill_cb;        // prefill: column blocks per wave (0: the default for D)
   uint32_t prefill;
   uint32_t rows;   // prefill: query rows
   uint32_t start;  // prefill: cache position of row 0

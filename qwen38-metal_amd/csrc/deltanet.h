@@ -42,6 +42,9 @@ struct DnArgs {
   float* snap_s;
   uint32_t snap_rows;
   uint64_t snap_hist_stride, snap_s_stride;
+  // kernel choice overrides (-1: default): the per-head step kernel, the
+  // chunked prefill
+  int32_t tune_step_head, tune_chunked;
 };
 
 // Chunked prefill (WY / UT form over chunks of kDnChunk tokens): used for

@@ -1488,8 +1488,7 @@ void launch_scan(const DnArgs& a, hipStream_t st) {
 // (QM38_DN_STEP_HEAD=0 forces the split kernel instead).
 bool dn_step_head(const DnArgs& a) {
   if (a.M != 1 || a.dk > 128 || a.dv > 128) return false;
-  const char* env = getenv("QM38_DN_STEP_HEAD");
-  return env ? atoi(env) != 0 : true;
+  return a.tune_step_head != 0;
 }
 
 bool dn_step_split(const DnArgs& a) { return a.M == 1 && a.dk <= 128 && a.dv <= 256 && !dn_step_head(a); }
@@ -1498,8 +1497,7 @@ bool dn_use_chunked(const DnArgs& a) {
   if (a.dk != kCD || a.dv != kCD || a.kernel != 4 || a.snap_rows > 0 || a.M <= 1 ||
       a.value_heads % a.key_heads != 0)
     return false;
-  const char* env = getenv("QM38_DN_CHUNKED");
-  if (env) return atoi(env) != 0;
+  if (a.tune_chunked >= 0) return a.tune_chunked != 0;
   return a.M >= 2 * kDnChunk;
 }
 

@@ -17,10 +17,39 @@ struct Q4Job {
   uint32_t tile_begin;  // filled by the launcher
   // Output of a decode (M <= 16) projection: 0 bf16; 1 fp32 holding the bf16-
   // rounded value (as if converted afterwards); 2 fp32 += the bf16-rounded
-  // value (a residual add).  `out` then points at fp32.  The GEMM takes 0 only.
+  // value (a residual add).  `out` then points at fp32.  3: argmax keys, one
+  // uint64 per activation row (`out` points at them; they must be zero and are
+  // maxed with atomics; launch_q4_argmax_finish turns them into row ids and
+  // clears them).  The GEMM takes 0 only.
   uint32_t mode;
 };
-constexpr uint32_t kQ4OutBf16 = 0, kQ4OutF32 = 1, kQ4OutAddF32 = 2;
+constexpr uint32_t kQ4OutBf16 = 0, kQ4OutF32 = 1, kQ4OutAddF32 = 2, kQ4OutArgmax = 3;
+
+// Planner inputs: the device's compute units and the QM38_* tuning overrides
+// (forced plans for measurements), read from the environment once, when a
+// runtime is created.  A value <= 0 (or -1 for the switches) keeps the
+// planner's own choice.
+struct Tuning {
+  int cus = 256;            // compute units (hipDeviceProp_t::multiProcessorCount)
+  int q4_nt = 0;            // QM38_Q4_NT: 16-row tiles per decode workgroup (1, 2)
+  int q4_xstage = 1;        // QM38_Q4_XSTAGE: 0 disables staged activations
+  int q4_xstage_max = 0;    // QM38_Q4_XSTAGE_MAX: LDS bytes of staged activations
+  int q4_target_waves = 0;  // QM38_Q4_TARGET_WAVES: resident waves the K split aims at
+  int q4_rpw = 0;           // QM38_Q4_RPW: rows per decode workgroup
+  int q4_split = 0;         // QM38_Q4_SPLIT: waves per decode workgroup
+  int q4_plan_log = 0;      // QM38_Q4_PLAN_LOG: print each new decode plan
+  int q4_fuse = 1;          // QM38_Q4_FUSE: 0 runs the MLP's down projection as its own launch
+  int gemm_splits = 0;      // QM38_GEMM_SPLITS: K splits of the prefill GEMM
+  int gemm_q = 0;           // QM38_GEMM_Q: stream-K steps per worker
+  int gemm_plan_log = 0;    // QM38_GEMM_PLAN_LOG
+  int attn_pps = 0;         // QM38_ATTN_PPS: pages per decode split
+  int attn_waves = 0;       // QM38_ATTN_WAVES: 4 or 8 waves per decode workgroup
+  int attn_target_wgs = 0;  // QM38_ATTN_TARGET_WGS
+  int prefill_cb = 0;       // QM38_PREFILL_CB: column blocks per prefill wave (1, 2, 4)
+  int dn_step_head = -1;    // QM38_DN_STEP_HEAD: 0 forces the split step kernel (-1: default)
+  int dn_chunked = -1;      // QM38_DN_CHUNKED: 1 / 0 forces the chunked / token-serial prefill (-1: default)
+};
+Tuning read_tuning(int cu_count);
 
 // Device workspace for kernels whose workgroups combine partial results:
 // `counters` are zero between launches (each kernel leaves them at zero).
@@ -31,6 +60,7 @@ struct Workspace {
   size_t counter_count;
   uint16_t* xh;  // prefill GEMM: fp16 copy of the activations
   size_t xh_bytes;
+  const Tuning* tune;
 };
 
 // Decode (weight-streaming) Q4 projection: M <= 16 activation rows.
@@ -38,12 +68,15 @@ struct Workspace {
 hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x,
                             uint32_t K, uint32_t M, const Workspace& ws, hipStream_t stream);
 
+// ids[m] from the argmax keys of a kQ4OutArgmax decode launch; zeroes the keys.
+hipError_t launch_q4_argmax_finish(unsigned long long* keys, uint32_t* ids, uint32_t M, hipStream_t stream);
+
 // Prefill Q4 GEMM (M > 16): Y[M][N] = X[M][K] * dequant(W)^T, bf16 out.
 // swiglu as above.
 size_t q4_gemm_xh_bytes(uint32_t K, uint32_t M);
 // Split-K partial bytes / counters a GEMM launch needs (0 when it does not split).
-void q4_gemm_workspace(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M, size_t* partial_bytes,
-                       size_t* counters);
+void q4_gemm_workspace(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M, const Tuning& tune,
+                       size_t* partial_bytes, size_t* counters);
 hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x,
                           uint32_t K, uint32_t M, const Workspace& ws, hipStream_t stream);
 

@@ -437,6 +437,39 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
       }
   }
 
+  if (!SWIGLU && args.jobs[j].mode == kQ4OutArgmax) {
+    // Greedy token per activation row (qwen38_argmax_rows, qwen38.metal:
+    // 4202-4244): the largest fp32 value, the lowest row index on ties, NaN
+    // never winning.  Key = (order-preserving bits of the value) << 32 |
+    // ~row, so one unsigned 64-bit maximum picks both; -0 counts as +0 (the
+    // reference compares values, and -0 == +0).  The tile's 16 lanes of a row
+    // group reduce, then one atomic per row and workgroup.
+    unsigned long long* keys = (unsigned long long*)args.jobs[j].out;
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+      unsigned long long best = 0;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const float v = acc[t][rr];
+        if (row_of[t] < n_valid && !__builtin_isnan(v)) {
+          const uint32_t b = v == 0.0f ? 0u : __float_as_uint(v);
+          const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+          const unsigned long long key =
+              ((unsigned long long)ord << 32) | (0xFFFFFFFFu - (row_base + row_of[t]));
+          best = key > best ? key : best;
+        }
+      }
+#pragma unroll
+      for (int off = 8; off >= 1; off >>= 1) {
+        const unsigned long long o = __shfl_xor(best, off);
+        best = o > best ? o : best;
+      }
+      const uint32_t m = 4 * kq + rr;
+      if (nl == 0 && m < args.M && best != 0) atomicMax(keys + m, best);
+    }
+    return;
+  }
+
 #pragma unroll
   for (int rr = 0; rr < R; ++rr) {
     const uint32_t m = 4 * kq + rr;
@@ -466,10 +499,6 @@ __global__ __launch_bounds__(512) void q4_decode_kernel(DecodeArgs args) {
   }
 }
 
-int env_int(const char* name, int fallback) {
-  const char* v = getenv(name);
-  return v ? atoi(v) : fallback;
-}
 
 // Kernel instance for the template parameters a plan selects.
 template <int NT, int R, bool SW>
@@ -507,29 +536,29 @@ struct Plan {
 //    of a tile cost arithmetic on zeros but no memory traffic.  Each candidate
 //    is scored by the rows on the busiest CU, with rounds past the first
 //    weighted by a quarter.
-Plan make_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M) {
+Plan make_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M, const Tuning& tn) {
   Plan best{};
   const uint32_t G = K / 64;
   uint64_t rows = 0;
   for (int i = 0; i < n_jobs; ++i) rows += jobs[i].rows;
-  const uint32_t cus = (uint32_t)env_int("QM38_CUS", 256);
+  const uint32_t cus = tn.cus > 0 ? (uint32_t)tn.cus : 256;
   int nt = swiglu ? 2 : ((rows / 32 >= (uint64_t)cus * 2) ? 2 : 1);
-  if (!swiglu && env_int("QM38_Q4_NT", 0) > 0) nt = env_int("QM38_Q4_NT", 1) >= 2 ? 2 : 1;
+  if (!swiglu && tn.q4_nt > 0) nt = tn.q4_nt >= 2 ? 2 : 1;
   // Staged activations when all M rows fit (each wave holds its K slice).
-  const uint32_t x_max = (uint32_t)env_int("QM38_Q4_XSTAGE_MAX", (int)kXStageMax);
-  const bool xw = M * (K * 2 + 16) <= x_max && env_int("QM38_Q4_XSTAGE", 1) != 0;
+  const uint32_t x_max = tn.q4_xstage_max > 0 ? (uint32_t)tn.q4_xstage_max : kXStageMax;
+  const bool xw = M * (K * 2 + 16) <= x_max && tn.q4_xstage != 0;
   const bool g8 = (G % 8) == 0;
   const void* fn = swiglu ? instance_m<2, true>(M, g8, xw)
                           : (nt == 2 ? instance_m<2, false>(M, g8, xw) : instance_m<1, false>(M, g8, xw));
   const uint32_t step = 4 * ring_depth(nt, xw);  // whole ring rounds per slice (also a multiple of 8)
   const uint32_t lds_cu = 160 * 1024;
-  const uint32_t target = (uint32_t)env_int("QM38_Q4_TARGET_WAVES", (int)(cus * 16));
+  const uint32_t target = tn.q4_target_waves > 0 ? (uint32_t)tn.q4_target_waves : cus * 16;
   const uint32_t r_max = 16u * (swiglu ? 1u : (uint32_t)nt);
   // Masked rows still cost arithmetic and activation staging: measured on the
   // BASELINE shapes, workgroups below 13/16 of their tiles lose more than the
   // balance gains.
   uint32_t r_hi = r_max, r_lo = (13 * r_max + 15) / 16;
-  if (env_int("QM38_Q4_RPW", 0) > 0) r_hi = r_lo = std::min<uint32_t>(r_max, (uint32_t)env_int("QM38_Q4_RPW", 16));
+  if (tn.q4_rpw > 0) r_hi = r_lo = std::min<uint32_t>(r_max, (uint32_t)tn.q4_rpw);
   double best_cost = 0.0;
   for (uint32_t r = r_hi; r >= r_lo && r > 0; --r) {
     Plan p{};
@@ -543,7 +572,7 @@ Plan make_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t 
     // each wave's longer slice overlaps its own loads with that work over
     // several ring rounds (measured: M = 4 / 8 sets +7 % / +9 %; slower at M = 1).
     if (M > 1) waves = std::min<uint32_t>(waves, 4);
-    if (env_int("QM38_Q4_SPLIT", 0) > 0) waves = (uint32_t)env_int("QM38_Q4_SPLIT", 1);
+    if (tn.q4_split > 0) waves = (uint32_t)tn.q4_split;
     waves = std::max<uint32_t>(1, std::min<uint32_t>(waves, kMaxWaves));
     int occ = 0;
     for (;;) {
@@ -581,13 +610,13 @@ struct PlanKey {
   int n_jobs;
   bool swiglu;
   uint32_t K, M;
-  int env[7];
+  Tuning tune;
   bool operator==(const PlanKey& o) const {
     return n_jobs == o.n_jobs && swiglu == o.swiglu && K == o.K && M == o.M &&
-           std::memcmp(rows, o.rows, sizeof(rows)) == 0 && std::memcmp(env, o.env, sizeof(env)) == 0;
+           std::memcmp(rows, o.rows, sizeof(rows)) == 0 && std::memcmp(&tune, &o.tune, sizeof(tune)) == 0;
   }
 };
-Plan cached_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M) {
+Plan cached_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M, const Tuning& tn) {
   static std::mutex mu;
   static PlanKey keys[8];
   static Plan plans[8];
@@ -598,14 +627,12 @@ Plan cached_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_
   k.swiglu = swiglu;
   k.K = K;
   k.M = M;
-  const char* names[7] = {"QM38_CUS", "QM38_Q4_NT", "QM38_Q4_XSTAGE", "QM38_Q4_TARGET_WAVES", "QM38_Q4_RPW",
-                          "QM38_Q4_SPLIT", "QM38_Q4_XSTAGE_MAX"};
-  for (int i = 0; i < 7; ++i) k.env[i] = env_int(names[i], -1);
+  k.tune = tn;
   std::lock_guard<std::mutex> lock(mu);
   for (int i = 0; i < used; ++i)
     if (keys[i] == k) return plans[i];
-  const Plan p = make_plan(jobs, n_jobs, swiglu, K, M);
-  if (env_int("QM38_Q4_PLAN_LOG", 0) > 0)
+  const Plan p = make_plan(jobs, n_jobs, swiglu, K, M, tn);
+  if (tn.q4_plan_log > 0)
     fprintf(stderr, "q4 decode plan: K=%u M=%u swiglu=%d rows0=%u -> nt=%d rpw=%u tiles=%u waves=%u gps=%u lds=%u\n", K,
             M, (int)swiglu, jobs[0].rows, p.nt, p.rpw, p.tiles, p.waves, p.gps, p.lds);
   if (p.fn) {
@@ -617,11 +644,27 @@ Plan cached_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_
   return p;
 }
 
+// ids[m] = the row index an argmax key holds (0 for a row whose logits were
+// all NaN: no key was stored); the keys return to zero for the next call.
+__global__ void q4_argmax_finish_kernel(unsigned long long* keys, uint32_t* ids, uint32_t M) {
+  const uint32_t m = blockIdx.x * blockDim.x + threadIdx.x;
+  if (m >= M) return;
+  const unsigned long long k = keys[m];
+  ids[m] = k ? 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull) : 0u;
+  keys[m] = 0;
+}
+
 }  // namespace
 
+hipError_t launch_q4_argmax_finish(unsigned long long* keys, uint32_t* ids, uint32_t M, hipStream_t stream) {
+  hipLaunchKernelGGL(q4_argmax_finish_kernel, dim3((M + 63) / 64), dim3(64), 0, stream, keys, ids, M);
+  return hipGetLastError();
+}
+
 hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x,
-                            uint32_t K, uint32_t M, const Workspace&, hipStream_t stream) {
-  const Plan p = cached_plan(jobs, n_jobs, swiglu, K, M);
+                            uint32_t K, uint32_t M, const Workspace& ws, hipStream_t stream) {
+  if (!ws.tune) return hipErrorInvalidValue;
+  const Plan p = cached_plan(jobs, n_jobs, swiglu, K, M, *ws.tune);
   if (!p.fn || p.lds > 160 * 1024) return hipErrorInvalidValue;
   DecodeArgs a{};
   a.x = x;

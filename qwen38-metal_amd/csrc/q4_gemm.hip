@@ -370,10 +370,6 @@ struct GemmPlan {
   size_t partial_bytes;  // 0 when every worker's range is whole tiles
 };
 
-int env_int_gemm(const char* name, int fallback) {
-  const char* v = getenv(name);
-  return v ? atoi(v) : fallback;
-}
 
 // Plan cost in units of one K step of one 256 x 256 tile (about 1.9 us on
 // MI355X), fitted to the measured BASELINE prefill shapes (M = 512, 2048).
@@ -394,7 +390,7 @@ double stream_cost(uint32_t tiles, uint32_t G, uint32_t Q, uint32_t cus) {
   return rounds * (Q + 20.0 * ((double)Q / G + 1.0) + 12.0 + 5.0 * pieces);
 }
 
-GemmPlan gemm_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M) {
+GemmPlan gemm_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M, const Tuning& tune) {
   GemmPlan p{};
   p.m_tiles = (M + kBM - 1) / kBM;
   uint32_t n_tiles = 0;
@@ -404,7 +400,7 @@ GemmPlan gemm_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint3
     for (int i = 0; i < n_jobs; ++i) n_tiles += (jobs[i].rows + kBN - 1) / kBN;
   }
   p.tiles = n_tiles * p.m_tiles;
-  const uint32_t G = K / 64, cus = 256;
+  const uint32_t G = K / 64, cus = tune.cus > 0 ? (uint32_t)tune.cus : 256;
   const uint64_t total = (uint64_t)p.tiles * G;
   // Candidates: K split into S equal slices per tile (S = 1: whole tiles;
   // S <= 8, slices of at least 8 steps), and stream-K with the steps dealt
@@ -430,7 +426,7 @@ GemmPlan gemm_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint3
       p.q = (uint32_t)q;
     }
   }
-  const int fs = env_int_gemm("QM38_GEMM_SPLITS", 0), fq = env_int_gemm("QM38_GEMM_Q", 0);
+  const int fs = tune.gemm_splits, fq = tune.gemm_q;
   if (fs > 0) {
     p.splits = std::min<uint32_t>((uint32_t)fs, G);
     p.q = (G + p.splits - 1) / p.splits;
@@ -446,9 +442,9 @@ GemmPlan gemm_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint3
 }
 }  // namespace
 
-void q4_gemm_workspace(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M, size_t* partial_bytes,
-                       size_t* counters) {
-  const GemmPlan p = gemm_plan(jobs, n_jobs, swiglu, K, M);
+void q4_gemm_workspace(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M, const Tuning& tune,
+                       size_t* partial_bytes, size_t* counters) {
+  const GemmPlan p = gemm_plan(jobs, n_jobs, swiglu, K, M, tune);
   *partial_bytes = p.partial_bytes;
   *counters = p.partial_bytes ? p.tiles : 0;
 }
@@ -459,8 +455,9 @@ hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint
   for (int i = 0; i < n_jobs; ++i)
     if (jobs[i].mode != kQ4OutBf16) return hipErrorInvalidValue;
   if (!ws.xh || ws.xh_bytes < q4_gemm_xh_bytes(K, M)) return hipErrorInvalidValue;
-  const GemmPlan plan = gemm_plan(jobs, n_jobs, swiglu, K, M);
-  static const bool log_plan = env_int_gemm("QM38_GEMM_PLAN_LOG", 0) != 0;
+  if (!ws.tune) return hipErrorInvalidValue;
+  const GemmPlan plan = gemm_plan(jobs, n_jobs, swiglu, K, M, *ws.tune);
+  const bool log_plan = ws.tune->gemm_plan_log != 0;
   static uint64_t logged = 0;  // debug aid: print each new shape's plan once
   const uint64_t key = ((uint64_t)M << 40) ^ ((uint64_t)K << 16) ^ plan.tiles ^ ((uint64_t)plan.q << 56);
   if (log_plan && key != logged && (logged = key))

@@ -1007,8 +1007,7 @@ hipError_t launch_attn_d(const AttnArgs& a, uint32_t units, bool need_combine, h
   if (a.prefill) {
     // Column blocks per wave: two up to D = 128 (registers for both blocks'
     // accumulators), one above; QM38_PREFILL_CB overrides (1, 2, 4).
-    const char* env = getenv("QM38_PREFILL_CB");
-    int cb = env ? atoi(env) : (D <= 128 ? 2 : 1);
+    int cb = a.prefill_cb > 0 ? a.prefill_cb : (D <= 128 ? 2 : 1);
     if (D > 128 && cb > 2) cb = 2;
     if (cb >= 4 && D <= 128) return launch_prefill<D, (D <= 128 ? 4 : 2)>(a, st);
     if (cb >= 2) return launch_prefill<D, 2>(a, st);

@@ -6,6 +6,7 @@
 
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -55,8 +56,7 @@ qm_status qm::no_device() {
 // Growing a buffer allocates and synchronises, which a stream under graph
 // capture cannot do: such a call fails instead of corrupting the capture.
 static qm_status capture_guard(qm_runtime* rt, const char* what) {
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(rt->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+  if (qm::stream_capturing(rt->stream))
     return qm::fail(QM_ERR_INVALID_ARGUMENT, "%s: workspace must grow while the stream is being captured", what);
   return QM_OK;
 }
@@ -140,6 +140,30 @@ qm_status qm::ensure_counters(qm_runtime* rt, size_t count) {
   return QM_OK;
 }
 
+bool qm::stream_capturing(hipStream_t s) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+    // The legacy stream cannot be queried while another blocking stream is
+    // capturing; the query's error must not reach a later launch's check.
+    (void)hipGetLastError();
+    return true;
+  }
+  return cs != hipStreamCaptureStatusNone;
+}
+
+qm_status qm::stream_after(qm_runtime* waiter, qm_runtime* signaler) {
+  if (!waiter || !signaler || waiter == signaler || waiter->stream == signaler->stream) return QM_OK;
+  if (waiter->device < 0 || signaler->device < 0) return QM_OK;
+  if (stream_capturing(waiter->stream) || stream_capturing(signaler->stream)) return QM_OK;
+  if (!signaler->order_event) {
+    hipError_t e = hipEventCreateWithFlags(&signaler->order_event, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_check(e, "stream order event");
+  }
+  hipError_t e = hipEventRecord(signaler->order_event, signaler->stream);
+  if (e == hipSuccess) e = hipStreamWaitEvent(waiter->stream, signaler->order_event, 0);
+  return hip_check(e, "stream order");
+}
+
 void qm::release_buffers(qm_runtime* rt) {
   if (rt->scratch) hipFree(rt->scratch);
   if (rt->counters) hipFree(rt->counters);
@@ -152,7 +176,34 @@ void qm::release_buffers(qm_runtime* rt) {
 
 qm::Workspace qm::workspace(qm_runtime* rt) {
   return Workspace{(float*)rt->partials, rt->partial_bytes, rt->counters, rt->counter_count, (uint16_t*)rt->xh,
-                   rt->xh_bytes};
+                   rt->xh_bytes, &rt->tune};
+}
+
+qm::Tuning qm::read_tuning(int cu_count) {
+  auto get = [](const char* name, int fallback) {
+    const char* v = getenv(name);
+    return v ? atoi(v) : fallback;
+  };
+  Tuning t{};
+  t.cus = cu_count;
+  t.q4_nt = get("QM38_Q4_NT", 0);
+  t.q4_xstage = get("QM38_Q4_XSTAGE", 1);
+  t.q4_xstage_max = get("QM38_Q4_XSTAGE_MAX", 0);
+  t.q4_target_waves = get("QM38_Q4_TARGET_WAVES", 0);
+  t.q4_rpw = get("QM38_Q4_RPW", 0);
+  t.q4_split = get("QM38_Q4_SPLIT", 0);
+  t.q4_plan_log = get("QM38_Q4_PLAN_LOG", 0);
+  t.q4_fuse = get("QM38_Q4_FUSE", 1);
+  t.gemm_splits = get("QM38_GEMM_SPLITS", 0);
+  t.gemm_q = get("QM38_GEMM_Q", 0);
+  t.gemm_plan_log = get("QM38_GEMM_PLAN_LOG", 0);
+  t.attn_pps = get("QM38_ATTN_PPS", 0);
+  t.attn_waves = get("QM38_ATTN_WAVES", 0);
+  t.attn_target_wgs = get("QM38_ATTN_TARGET_WGS", 0);
+  t.prefill_cb = get("QM38_PREFILL_CB", 0);
+  t.dn_step_head = get("QM38_DN_STEP_HEAD", -1);
+  t.dn_chunked = get("QM38_DN_CHUNKED", -1);
+  return t;
 }
 
 extern "C" {
@@ -195,6 +246,7 @@ qm_status qm_runtime_create(int device, qm_runtime** out) {
   if (device == QM_DEVICE_NONE) {
     qm_runtime* rt = new qm_runtime();
     rt->device = QM_DEVICE_NONE;
+    rt->tune = read_tuning(rt->cu_count);
     *out = rt;
     return QM_OK;
   }
@@ -209,6 +261,7 @@ qm_status qm_runtime_create(int device, qm_runtime** out) {
   if (!g.ok()) return no_device();
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) == hipSuccess) rt->cu_count = prop.multiProcessorCount;
+  rt->tune = read_tuning(rt->cu_count);
   *out = rt;
   return QM_OK;
 }
@@ -222,6 +275,7 @@ void qm_runtime_destroy(qm_runtime* rt) {
   DeviceGuard g(rt->device);
   hipStreamSynchronize(rt->stream);
   qm::release_buffers(rt);
+  if (rt->order_event) hipEventDestroy(rt->order_event);
   delete rt;
 }
 

@@ -60,11 +60,13 @@ namespace {
 
 bool job_ok(const qm_q4_job& j) { return j.weights && j.scales && j.biases && j.out_rows > 0; }
 
-qm_status check_job(const qm_q4_job& j, uint32_t rows, const char* what) {
+// A layer's job: pointers set, the expected height (rows = 0: any), and its
+// tensors inside their allocations for input width in_elems.
+qm_status check_job(const qm_runtime* rt, const qm_q4_job& j, uint32_t rows, uint32_t in_elems, const char* what) {
   if (!job_ok(j)) return fail(QM_ERR_NULL_POINTER, "%s: job pointers must be set and out_rows > 0", what);
   if (rows && j.out_rows != rows)
     return fail(QM_ERR_WRONG_LENGTH, "%s has %u output rows, expected %u", what, j.out_rows, rows);
-  return QM_OK;
+  return q4_job_ranges(rt, j, in_elems, what);
 }
 
 // Validates the layers (validate_decode_q4_job and the shape checks of the
@@ -91,11 +93,11 @@ qm_status check_layers(const qm_runtime* rt, uint32_t hidden, const qm_decode_la
         return fail(QM_ERR_WRONG_LENGTH, "layer %u: DeltaNet state was created for another configuration", i);
       const uint32_t channels = 2 * c.key_heads * c.key_head_dim + c.value_heads * c.value_head_dim;
       const uint32_t value = c.value_heads * c.value_head_dim;
-      if ((st = check_job(l.qkv, channels, "DeltaNet qkv")) != QM_OK) return st;
-      if ((st = check_job(l.z, value, "DeltaNet z")) != QM_OK) return st;
-      if ((st = check_job(l.b, c.value_heads, "DeltaNet b")) != QM_OK) return st;
-      if ((st = check_job(l.a, c.value_heads, "DeltaNet a")) != QM_OK) return st;
-      if ((st = check_job(l.out_proj, hidden, "DeltaNet out projection")) != QM_OK) return st;
+      if ((st = check_job(rt, l.qkv, channels, hidden, "DeltaNet qkv")) != QM_OK) return st;
+      if ((st = check_job(rt, l.z, value, hidden, "DeltaNet z")) != QM_OK) return st;
+      if ((st = check_job(rt, l.b, c.value_heads, hidden, "DeltaNet b")) != QM_OK) return st;
+      if ((st = check_job(rt, l.a, c.value_heads, hidden, "DeltaNet a")) != QM_OK) return st;
+      if ((st = check_job(rt, l.out_proj, hidden, value, "DeltaNet out projection")) != QM_OK) return st;
       if (value % 64 != 0) return fail(QM_ERR_INPUT_NOT_GROUPED, "layer %u: DeltaNet value elements %u", i, value);
       s.p[0] = std::max(s.p[0], channels);
       s.p[1] = std::max(s.p[1], value);
@@ -112,10 +114,10 @@ qm_status check_layers(const qm_runtime* rt, uint32_t hidden, const qm_decode_la
       if (l.rope.head_dim != D || H == 0 || H % KVH != 0)
         return fail(QM_ERR_INVALID_ATTENTION_SHAPE, "layer %u: heads %u / kv heads %u / head_dim %u vs cache %u", i,
                     H, KVH, l.rope.head_dim, D);
-      if ((st = check_job(l.q_proj, 2 * H * D, "query projection")) != QM_OK) return st;
-      if ((st = check_job(l.k_proj, KVH * D, "key projection")) != QM_OK) return st;
-      if ((st = check_job(l.v_proj, KVH * D, "value projection")) != QM_OK) return st;
-      if ((st = check_job(l.o_proj, hidden, "output projection")) != QM_OK) return st;
+      if ((st = check_job(rt, l.q_proj, 2 * H * D, hidden, "query projection")) != QM_OK) return st;
+      if ((st = check_job(rt, l.k_proj, KVH * D, hidden, "key projection")) != QM_OK) return st;
+      if ((st = check_job(rt, l.v_proj, KVH * D, hidden, "value projection")) != QM_OK) return st;
+      if ((st = check_job(rt, l.o_proj, hidden, H * D, "output projection")) != QM_OK) return st;
       if ((H * D) % 64 != 0) return fail(QM_ERR_INPUT_NOT_GROUPED, "layer %u: query elements %u", i, H * D);
       s.p[0] = std::max(s.p[0], 2 * H * D);
       s.p[1] = std::max(s.p[1], KVH * D);
@@ -126,9 +128,9 @@ qm_status check_layers(const qm_runtime* rt, uint32_t hidden, const qm_decode_la
       in_norm = l.input_norm, post_norm = l.post_attention_norm;
     }
     if (!in_norm || !post_norm) return fail(QM_ERR_NULL_POINTER, "layer %u: norm weights", i);
-    if ((st = check_job(*gate, 0, "MLP gate")) != QM_OK) return st;
-    if ((st = check_job(*up, gate->out_rows, "MLP up")) != QM_OK) return st;
-    if ((st = check_job(*down, hidden, "MLP down")) != QM_OK) return st;
+    if ((st = check_job(rt, *gate, 0, hidden, "MLP gate")) != QM_OK) return st;
+    if ((st = check_job(rt, *up, gate->out_rows, hidden, "MLP up")) != QM_OK) return st;
+    if ((st = check_job(rt, *down, hidden, gate->out_rows, "MLP down")) != QM_OK) return st;
     if (gate->out_rows % 64 != 0)
       return fail(QM_ERR_INPUT_NOT_GROUPED, "layer %u: MLP intermediate %u", i, gate->out_rows);
     s.inter = std::max(s.inter, gate->out_rows);
@@ -453,6 +455,7 @@ qm_status qm_decode_graph_create(qm_runtime* rt, qm_decode_state* st, const qm_d
   g->st_generation = st->generation;
   g->cap.device = rt->device;
   g->cap.cu_count = rt->cu_count;
+  g->cap.tune = rt->tune;
   // Copy the descriptors (the graph keeps using them for the eager calls).
   g->lin.reserve(n_layers);
   g->full.reserve(n_layers);

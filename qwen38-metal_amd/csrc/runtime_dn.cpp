@@ -133,6 +133,8 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
   d.channels = w->channels;
   d.M = M;
   d.eps = eps;
+  d.tune_step_head = rt->tune.dn_step_head;
+  d.tune_chunked = rt->tune.dn_chunked;
   d.conv_w = w->conv_w;
   d.a_log = w->a_log;
   d.dt_bias = w->dt_bias;
@@ -171,6 +173,9 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
   }
   DeviceGuard g(rt->device);
   if (!g.ok()) return no_device();
+  // States owned by another runtime: their pending work on that runtime's
+  // stream comes first, and later work there sees this call's result.
+  if ((st = stream_after(rt, from->rt)) != QM_OK || (st = stream_after(rt, to->rt)) != QM_OK) return st;
   hipError_t e = launch_deltanet(d, rt->stream);
   if (e != hipSuccess) return hip_check(e, "DeltaNet launch");
   if (out_bf16 && !fused_bf16) {
@@ -178,7 +183,7 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
     if ((e = launch_convert(&seg, 1, rt->stream)) != hipSuccess) return hip_check(e, "DeltaNet bf16 output");
   }
   if (c.conv_kernel_size > 1) to->cur = next;
-  return QM_OK;
+  return stream_after(to->rt, rt);
 }
 
 }  // namespace

@@ -10,6 +10,7 @@
 struct qm_runtime {
   int device = 0;
   int cu_count = 256;
+  qm::Tuning tune{};  // planner overrides, read once at creation
   hipStream_t stream = nullptr;
   // Grow-only scratch used by calls that need an intermediate buffer (the
   // MLP's h, attention split partials).  Calls on one runtime are serialised
@@ -28,6 +29,8 @@ struct qm_runtime {
   // hold the MLP's h while h itself is converted).
   void* xh = nullptr;
   size_t xh_bytes = 0;
+  // Orders this runtime's stream before another runtime's (stream_after).
+  hipEvent_t order_event = nullptr;
 };
 
 namespace qm {
@@ -42,6 +45,10 @@ qm_status ensure_counters(qm_runtime* rt, size_t count);
 qm_status ensure_xh(qm_runtime* rt, size_t bytes);
 // Workspace handed to kernels that split work across workgroups.
 Workspace workspace(qm_runtime* rt);
+// The device-allocation range checks of every Q4 entry point for one job of
+// input width in_elems (INVALID_BUFFER_OFFSET / MAPPED_TENSOR_OUT_OF_RANGE);
+// nothing is checked on a runtime without a device or a capturing stream.
+qm_status q4_job_ranges(const qm_runtime* rt, const qm_q4_job& j, uint32_t in_elems, const char* name);
 // qm_q4_project with a per-job output mode (kQ4Out*; fp32 modes need M <= 16).
 qm_status q4_project_modes(qm_runtime* rt, const qm_q4_job* jobs, void* const* outs, const uint32_t* modes,
                            int n_jobs, const uint16_t* x, uint32_t in_elems, uint32_t M);
@@ -50,6 +57,15 @@ qm_status dn_step_bf16(qm_runtime* rt, const qm_dn_weights* w, qm_dn_state* st, 
                        const float* b, const float* a, float eps, float* out, uint16_t* out_bf16);
 // Scratch bytes a single-token qm_dn_step needs (its counters: value_heads).
 size_t dn_step_scratch_bytes(const qm_dn_config& c);
+// Makes work enqueued from now on `waiter`'s stream wait for the work enqueued
+// so far on `signaler`'s stream (an event record + stream wait), so a cache or
+// state owned by one runtime can be used from another without racing its
+// pending work.  Nothing to do when both use one stream, or while either
+// stream is being captured (a capture cannot wait on an outside event).
+qm_status stream_after(qm_runtime* waiter, qm_runtime* signaler);
+// True while `s` is being captured, and also when the query itself fails (the
+// legacy stream while another stream captures); clears that query's error.
+bool stream_capturing(hipStream_t s);
 // Frees a runtime's grow-only buffers (not the runtime itself).
 void release_buffers(qm_runtime* rt);
 

@@ -38,10 +38,6 @@ struct qm_kv {
 
 namespace {
 
-int env_int(const char* name, int fallback) {
-  const char* v = getenv(name);
-  return v ? atoi(v) : fallback;
-}
 
 size_t kv_page_bytes(const qm_kv* kv) { return (size_t)kv->kv_heads * kv->page_tokens * kv->dp; }
 size_t scale_page_count(const qm_kv* kv) { return (size_t)kv->kv_heads * kv->page_tokens; }
@@ -255,7 +251,7 @@ qm_status plan_decode_chunk(qm_runtime* rt, qm_kv* const* seqs, uint32_t nb, Dec
     for (uint32_t i = 0; i < nb; ++i) u += ((at.seqs[i].len + 15) / 16 + q - 1) / q * KVH;
     return u;
   };
-  const int forced = env_int("QM38_ATTN_PPS", 0);
+  const int forced = rt->tune.attn_pps;
   // Pages per split for about `target` workgroups.  Ceil-division per
   // sequence can push the unit count past one residency round, which would
   // leave a nearly empty second round as long as the first: grow the split
@@ -269,8 +265,8 @@ qm_status plan_decode_chunk(qm_runtime* rt, qm_kv* const* seqs, uint32_t nb, Dec
       while (pps < kMaxPagesPerSplit && units_for(pps) > target) pps += 4;
     return std::min<uint64_t>(pps, kMaxPagesPerSplit);
   };
-  const int waves_env = env_int("QM38_ATTN_WAVES", 0);
-  const int target_env = env_int("QM38_ATTN_TARGET_WGS", 0);
+  const int waves_env = rt->tune.attn_waves;
+  const int target_env = rt->tune.attn_target_wgs;
   uint32_t waves = 8;
   uint64_t pps = pps_for(target_env > 0 ? (uint32_t)target_env : rt->cu_count);
   if (waves_env == 4 || (waves_env != 8 && units_for(pps) > rt->cu_count)) {
@@ -342,6 +338,12 @@ qm_status launch_decode(qm_runtime* rt, qm_kv* const* seqs, uint32_t B, const ui
                         const float* k, const float* v, uint32_t H, uint16_t* o, std::vector<DecodeChunk>& chunks,
                         float* partials, size_t partial_bytes) {
   const uint32_t KVH = seqs[0]->kv_heads, D = seqs[0]->head_dim, Dp = seqs[0]->dp;
+  // Caches owned by another runtime: their pending growth copies, reserves or
+  // prefills on that runtime's stream come first.
+  for (uint32_t b = 0; b < B; ++b) {
+    qm_status st = stream_after(rt, seqs[b]->rt);
+    if (st != QM_OK) return st;
+  }
   for (size_t ci = 0; ci < chunks.size(); ++ci) {
     DecodeChunk& c = chunks[ci];
     const uint32_t b0 = (uint32_t)ci * kMaxAttnSeqs, nb = c.at.n_seqs;
@@ -375,6 +377,11 @@ qm_status launch_decode(qm_runtime* rt, qm_kv* const* seqs, uint32_t B, const ui
       }
       return hip_check(e, "attention decode launch");
     }
+  }
+  // ... and later work on their own runtime's stream sees this token.
+  for (uint32_t b = 0; b < B; ++b) {
+    qm_status st = stream_after(seqs[b]->rt, rt);
+    if (st != QM_OK) return st;
   }
   return QM_OK;
 }
@@ -490,8 +497,9 @@ qm_status qm_kv_clone(const qm_kv* src, qm_kv** out) {
   qm_kv* kv = nullptr;
   qm_status st = qm_kv_create(src->rt, src->kv_heads, src->head_dim, src->page_tokens, src->max_tokens, &kv);
   if (st != QM_OK) return st;
-  // Same allocated capacity as the source (clone_q8_kv_state, :7338-7379).
-  if ((st = kv_grow(kv, (uint64_t)src->cap_pages * src->page_tokens)) != QM_OK) {
+  // Same capacity as the source (clone_q8_kv_state, :7338-7379): its pages
+  // may hold more tokens than max_tokens allows, so grow to what it may hold.
+  if ((st = kv_grow(kv, qm_kv_capacity(src))) != QM_OK) {
     qm_kv_destroy(kv);
     return st;
   }
@@ -631,6 +639,9 @@ qm_status qm_attn_prefill(qm_runtime* rt, qm_kv* seq, const uint16_t* q, const u
   at.rows = M;
   at.start = start;
   at.seqs[0] = sd;
+  at.prefill_cb = rt->tune.prefill_cb;
+  // A cache owned by another runtime: its pending work comes first.
+  if ((st = stream_after(rt, seq->rt)) != QM_OK) return st;
   commit_pages(seq, sd.new_page_first, sd.new_page_count);
   seq->length = start + M;
   hipError_t e = launch_q8_append(ap, M, rt->stream);
@@ -640,8 +651,9 @@ qm_status qm_attn_prefill(qm_runtime* rt, qm_kv* seq, const uint16_t* q, const u
   if (e != hipSuccess) {
     seq->length = start;
     rollback_pages(seq, sd.new_page_first, sd.new_page_count);
+    return hip_check(e, "attention prefill launch");
   }
-  return hip_check(e, "attention prefill launch");
+  return stream_after(seq->rt, rt);
 }
 
 }  // extern "C"

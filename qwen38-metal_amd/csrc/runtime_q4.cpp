@@ -1,5 +1,6 @@
 // C-ABI entry points of the MLX affine-Q4 projections (see include/qm38.h).
 #include <stdint.h>
+#include <stdio.h>
 
 #include "runtime_internal.h"
 
@@ -30,6 +31,53 @@ qm_status validate_job(const qm_q4_job* job, uint32_t in_elems, const char* name
   return QM_OK;
 }
 
+// The allocation holding [p, p + bytes) must exist and be long enough: the
+// device-pointer form of validate_mapped_q4_affine_shape's buffer checks
+// (metal_runtime.rs:8868-8895).  A runtime without a device has no
+// allocations to resolve and skips it.
+qm_status check_range(const qm_runtime* rt, const void* p, uint64_t bytes, const char* what) {
+  if (rt->device < 0) return QM_OK;
+  // The lookup is not allowed while the stream is being captured (HIP treats
+  // it as touching the legacy stream); captured calls were checked when the
+  // capture's caller validated its jobs (qm_decode_graph_create does).
+  if (stream_capturing(rt->stream)) return QM_OK;
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) != hipSuccess || !base) {
+    (void)hipGetLastError();
+    return fail(QM_ERR_INVALID_BUFFER_OFFSET, "%s (%p) lies inside no device allocation", what, p);
+  }
+  const uint64_t off = (uint64_t)((uintptr_t)p - (uintptr_t)base);
+  if ((uintptr_t)p < (uintptr_t)base || off > size)
+    return fail(QM_ERR_INVALID_BUFFER_OFFSET, "%s (%p) lies outside its allocation", what, p);
+  if (bytes > size - off)
+    return fail(QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE,
+                "%s needs %llu bytes but its allocation holds %llu past offset %llu", what,
+                (unsigned long long)bytes, (unsigned long long)(size - off), (unsigned long long)off);
+  return QM_OK;
+}
+
+}  // namespace
+
+qm_status qm::q4_job_ranges(const qm_runtime* rt, const qm_q4_job& j, uint32_t in_elems, const char* name) {
+  char what[96];
+  const uint64_t wbytes = (uint64_t)j.out_rows * (in_elems / 8) * 4;
+  const uint64_t abytes = (uint64_t)j.out_rows * (in_elems / kGroup) * 2;
+  qm_status st;
+  snprintf(what, sizeof(what), "%s weights", name);
+  if ((st = check_range(rt, j.weights, wbytes, what)) != QM_OK) return st;
+  snprintf(what, sizeof(what), "%s scales", name);
+  if ((st = check_range(rt, j.scales, abytes, what)) != QM_OK) return st;
+  snprintf(what, sizeof(what), "%s biases", name);
+  return check_range(rt, j.biases, abytes, what);
+}
+
+namespace {
+
+qm_status check_job_ranges(const qm_runtime* rt, const qm_q4_job& j, uint32_t in_elems, const char* name) {
+  return q4_job_ranges(rt, j, in_elems, name);
+}
+
 qm_status validate_x(const void* x, uint32_t M) {
   if (!x) return fail(QM_ERR_NULL_POINTER, "activation pointer is NULL");
   if (M == 0) return fail(QM_ERR_EMPTY_DIMENSION, "batch size must be greater than zero");
@@ -51,7 +99,7 @@ qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const ui
                  uint32_t M, const char* what) {
   // The decode kernel needs no workspace; the GEMM's split-K plans do.
   size_t pbytes = 0, counters = 0;
-  if (M > kDecodeMaxRows) q4_gemm_workspace(jobs, n, swiglu, K, M, &pbytes, &counters);
+  if (M > kDecodeMaxRows) q4_gemm_workspace(jobs, n, swiglu, K, M, rt->tune, &pbytes, &counters);
   qm_status st = ensure_partials(rt, pbytes);
   if (st == QM_OK) st = ensure_counters(rt, counters);
   if (st == QM_OK && M > kDecodeMaxRows) st = ensure_xh(rt, q4_gemm_xh_bytes(K, M));
@@ -82,6 +130,12 @@ qm_status qm::q4_project_modes(qm_runtime* rt, const qm_q4_job* jobs, void* cons
   }
   DeviceGuard g(rt->device);
   if (!g.ok()) return no_device();
+  if ((st = check_range(rt, x, (uint64_t)M * in_elems * 2, "activation")) != QM_OK) return st;
+  for (int i = 0; i < n_jobs; ++i) {
+    if ((st = check_job_ranges(rt, jobs[i], in_elems, "Q4 projection")) != QM_OK) return st;
+    const uint64_t ob = (uint64_t)M * jobs[i].out_rows * (modes[i] == kQ4OutBf16 ? 2 : 4);
+    if ((st = check_range(rt, outs[i], ob, "output")) != QM_OK) return st;
+  }
   return launch(rt, q, n_jobs, false, x, in_elems, M, "Q4 projection launch");
 }
 
@@ -104,6 +158,11 @@ qm_status qm_q4_project(qm_runtime* rt, const qm_q4_job* jobs, int n_jobs, const
   }
   DeviceGuard g(rt->device);
   if (!g.ok()) return no_device();
+  if ((st = check_range(rt, x, (uint64_t)M * in_elems * 2, "activation")) != QM_OK) return st;
+  for (int i = 0; i < n_jobs; ++i) {
+    if ((st = check_job_ranges(rt, jobs[i], in_elems, "Q4 projection")) != QM_OK) return st;
+    if ((st = check_range(rt, outputs[i], (uint64_t)M * jobs[i].out_rows * 2, "output")) != QM_OK) return st;
+  }
   return launch(rt, q, n_jobs, false, x, in_elems, M, "Q4 projection launch");
 }
 
@@ -120,6 +179,10 @@ qm_status qm_q4_swiglu(qm_runtime* rt, const qm_q4_job* gate, const qm_q4_job* u
   Q4Job q[2] = {to_job(*gate, h), to_job(*up, nullptr)};
   DeviceGuard g(rt->device);
   if (!g.ok()) return no_device();
+  if ((st = check_range(rt, x, (uint64_t)M * in_elems * 2, "activation")) != QM_OK) return st;
+  if ((st = check_job_ranges(rt, *gate, in_elems, "gate")) != QM_OK) return st;
+  if ((st = check_job_ranges(rt, *up, in_elems, "up")) != QM_OK) return st;
+  if ((st = check_range(rt, h, (uint64_t)M * gate->out_rows * 2, "h")) != QM_OK) return st;
   return launch(rt, q, 2, true, x, in_elems, M, "Q4 SwiGLU launch");
 }
 
@@ -136,6 +199,11 @@ qm_status qm_q4_mlp(qm_runtime* rt, const qm_q4_job* gate, const qm_q4_job* up, 
   if (!y) return fail(QM_ERR_NULL_POINTER, "y is NULL");
   DeviceGuard g(rt->device);
   if (!g.ok()) return no_device();
+  if ((st = check_range(rt, x, (uint64_t)M * in_elems * 2, "activation")) != QM_OK) return st;
+  if ((st = check_job_ranges(rt, *gate, in_elems, "gate")) != QM_OK) return st;
+  if ((st = check_job_ranges(rt, *up, in_elems, "up")) != QM_OK) return st;
+  if ((st = check_job_ranges(rt, *down, gate->out_rows, "down")) != QM_OK) return st;
+  if ((st = check_range(rt, y, (uint64_t)M * down->out_rows * 2, "y")) != QM_OK) return st;
   const size_t h_bytes = (size_t)M * gate->out_rows * 2;
   if ((st = ensure_scratch(rt, h_bytes)) != QM_OK) return st;
   uint16_t* h = (uint16_t*)rt->scratch;
@@ -143,6 +211,67 @@ qm_status qm_q4_mlp(qm_runtime* rt, const qm_q4_job* gate, const qm_q4_job* up, 
   if ((st = launch(rt, q, 2, true, x, in_elems, M, "MLP gate/up launch")) != QM_OK) return st;
   Q4Job d = to_job(*down, y);
   return launch(rt, &d, 1, false, h, gate->out_rows, M, "MLP down launch");
+}
+
+qm_status qm_q4_argmax(qm_runtime* rt, const qm_q4_job* job, const uint16_t* x, uint32_t in_elems, uint32_t M,
+                       uint32_t* ids) {
+  if (!rt) return fail(QM_ERR_NULL_POINTER, "runtime is NULL");
+  qm_status st = validate_x(x, M);
+  if (st != QM_OK) return st;
+  if ((st = validate_job(job, in_elems, "argmax")) != QM_OK) return st;
+  if (!ids) return fail(QM_ERR_NULL_POINTER, "ids is NULL");
+  DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
+  if ((st = check_range(rt, x, (uint64_t)M * in_elems * 2, "activation")) != QM_OK) return st;
+  if ((st = check_job_ranges(rt, *job, in_elems, "argmax")) != QM_OK) return st;
+  if ((st = check_range(rt, ids, (uint64_t)M * 4, "ids")) != QM_OK) return st;
+  // One 64-bit key per row of a chunk of at most 16 rows lives in the
+  // runtime's counters (zero between launches; the finishing kernel clears
+  // them).  Larger M runs the decode kernel chunk by chunk: each row's
+  // argmax is independent of the others.
+  if ((st = ensure_counters(rt, 2 * kDecodeMaxRows)) != QM_OK) return st;
+  unsigned long long* keys = (unsigned long long*)rt->counters;
+  const Workspace ws = workspace(rt);
+  for (uint32_t m0 = 0; m0 < M; m0 += kDecodeMaxRows) {
+    const uint32_t mc = M - m0 < kDecodeMaxRows ? M - m0 : kDecodeMaxRows;
+    Q4Job q = to_job(*job, (uint16_t*)keys);
+    q.mode = kQ4OutArgmax;
+    hipError_t e = launch_q4_decode(&q, 1, false, x + (size_t)m0 * in_elems, in_elems, mc, ws, rt->stream);
+    if (e == hipSuccess) e = launch_q4_argmax_finish(keys, ids + m0, mc, rt->stream);
+    if ((st = hip_check(e, "Q4 argmax launch")) != QM_OK) return st;
+  }
+  return QM_OK;
+}
+
+qm_status qm_q4_job_from_mapped(const qm_q4_mapped_job* m, uint32_t in_elems, qm_q4_job* out) {
+  if (!m || !out) return fail(QM_ERR_NULL_POINTER, "NULL argument");
+  if (in_elems == 0 || m->out_rows == 0)
+    return fail(QM_ERR_EMPTY_DIMENSION, "matrix dimensions must be greater than zero");
+  if (in_elems % kGroup != 0)
+    return fail(QM_ERR_INPUT_NOT_GROUPED, "input dimension %u is not divisible by affine group size %u", in_elems,
+                kGroup);
+  if (m->weight_offset > m->weights.length || m->scale_offset > m->scales.length ||
+      m->bias_offset > m->biases.length)
+    return fail(QM_ERR_INVALID_BUFFER_OFFSET, "a tensor offset lies beyond its buffer");
+  // Both products fit in 64 bits (u32 x u32); the byte lengths are checked
+  // against the buffers' remaining lengths below.
+  const uint64_t wbytes = (uint64_t)m->out_rows * (in_elems / 8) * 4;
+  const uint64_t abytes = (uint64_t)m->out_rows * (in_elems / kGroup) * 2;
+  if (wbytes > m->weights.length - m->weight_offset || abytes > m->scales.length - m->scale_offset ||
+      abytes > m->biases.length - m->bias_offset)
+    return fail(QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE, "a tensor of %u x %u runs past the end of its buffer",
+                m->out_rows, in_elems);
+  if (!m->weights.base || !m->scales.base || !m->biases.base)
+    return fail(QM_ERR_NULL_POINTER, "a buffer base is NULL");
+  qm_q4_job j{};
+  j.weights = (const uint32_t*)((const uint8_t*)m->weights.base + m->weight_offset);
+  j.scales = (const uint16_t*)((const uint8_t*)m->scales.base + m->scale_offset);
+  j.biases = (const uint16_t*)((const uint8_t*)m->biases.base + m->bias_offset);
+  j.out_rows = m->out_rows;
+  if (!aligned(j.weights, 8) || !aligned(j.scales, 8) || !aligned(j.biases, 8))
+    return fail(QM_ERR_MISALIGNED, "weights/scales/biases must resolve to 8-byte aligned addresses");
+  *out = j;
+  return QM_OK;
 }
 
 }  // extern "C"

@@ -36,7 +36,7 @@ EXPORTS = [
     "qm_status_string", "qm_last_error_message",
     "qm_runtime_create", "qm_runtime_destroy", "qm_runtime_set_stream", "qm_runtime_synchronize",
     "qm_device_alloc", "qm_device_free", "qm_upload", "qm_copy_to_device", "qm_copy_to_host",
-    "qm_q4_project", "qm_q4_swiglu", "qm_q4_mlp",
+    "qm_q4_project", "qm_q4_swiglu", "qm_q4_mlp", "qm_q4_argmax", "qm_q4_job_from_mapped",
     "qm_kv_create", "qm_kv_destroy", "qm_kv_length", "qm_kv_capacity", "qm_kv_allocated_pages", "qm_kv_page_for_token",
     "qm_kv_reserve", "qm_kv_truncate", "qm_kv_clone", "qm_kv_read",
     "qm_attn_decode", "qm_attn_decode_noalloc", "qm_attn_prefill", "qm_attn_prepare",
@@ -60,6 +60,18 @@ class QmError(RuntimeError):
 
 class Q4Job(C.Structure):
     _fields_ = [("weights", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p),
+                ("out_rows", C.c_uint32)]
+
+
+class Buffer(C.Structure):
+    """qm_buffer: a device allocation and its length in bytes."""
+    _fields_ = [("base", C.c_void_p), ("length", C.c_uint64)]
+
+
+class Q4MappedJob(C.Structure):
+    """qm_q4_mapped_job (MappedQ4AffineJob, metal_runtime.rs:155-192)."""
+    _fields_ = [("weights", Buffer), ("weight_offset", C.c_uint64), ("scales", Buffer),
+                ("scale_offset", C.c_uint64), ("biases", Buffer), ("bias_offset", C.c_uint64),
                 ("out_rows", C.c_uint32)]
 
 
@@ -137,6 +149,8 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "qm_q4_project": ([vp, C.POINTER(Q4Job), i32, vp, u32, u32, C.POINTER(vp)], i32),
         "qm_q4_swiglu": ([vp, C.POINTER(Q4Job), C.POINTER(Q4Job), vp, u32, u32, vp], i32),
         "qm_q4_mlp": ([vp, C.POINTER(Q4Job), C.POINTER(Q4Job), C.POINTER(Q4Job), vp, u32, u32, vp], i32),
+        "qm_q4_argmax": ([vp, C.POINTER(Q4Job), vp, u32, u32, vp], i32),
+        "qm_q4_job_from_mapped": ([C.POINTER(Q4MappedJob), u32, C.POINTER(Q4Job)], i32),
         "qm_kv_create": ([vp, u32, u32, u32, u32, C.POINTER(vp)], i32),
         "qm_kv_destroy": ([vp], None),
         "qm_kv_length": ([vp], u32),
@@ -239,6 +253,18 @@ class Runtime:
     def synchronize(self) -> None:
         _check(self.lib.qm_runtime_synchronize(self.handle))
 
+    def device_buffer(self, data=None, nbytes: int | None = None) -> "DeviceBuffer":
+        """A library allocation (qm_device_alloc) of nbytes, or holding a copy of
+        the numpy array `data` (qm_upload)."""
+        p = C.c_void_p()
+        if data is not None:
+            import numpy as np
+            a = np.ascontiguousarray(data)
+            _check(self.lib.qm_upload(self.handle, a.ctypes.data, a.nbytes, C.byref(p)))
+            return DeviceBuffer(self, p.value, a.nbytes)
+        _check(self.lib.qm_device_alloc(self.handle, nbytes, C.byref(p)))
+        return DeviceBuffer(self, p.value, nbytes)
+
     # ---- Q4 projections --------------------------------------------------
     @staticmethod
     def job(weights, scales, biases, out_rows: int) -> Q4Job:
@@ -257,6 +283,21 @@ class Runtime:
     def q4_mlp(self, gate: Q4Job, up: Q4Job, down: Q4Job, x, in_elems: int, M: int, y) -> None:
         _check(self.lib.qm_q4_mlp(self.handle, C.byref(gate), C.byref(up), C.byref(down), _ptr(x),
                                   in_elems, M, _ptr(y)))
+
+    def q4_affine_argmax(self, job: Q4Job, x, in_elems: int, M: int, ids) -> None:
+        """ids (uint32/int32 [M], device) = per-row argmax of job(x) (q4_affine_argmax_mapped_batch)."""
+        _check(self.lib.qm_q4_argmax(self.handle, C.byref(job), _ptr(x), in_elems, M, _ptr(ids)))
+
+    @staticmethod
+    def mapped_job(weights, weight_offset: int, scales, scale_offset: int, biases, bias_offset: int,
+                   out_rows: int, in_elems: int) -> Q4Job:
+        """A Q4Job from (buffer, offset) tensors, each buffer a (base, length) pair
+        (MappedQ4AffineJob::new + validate_mapped_q4_affine_shape)."""
+        m = Q4MappedJob(Buffer(*weights), weight_offset, Buffer(*scales), scale_offset, Buffer(*biases),
+                        bias_offset, out_rows)
+        j = Q4Job()
+        _check(load().qm_q4_job_from_mapped(C.byref(m), in_elems, C.byref(j)))
+        return j
 
     # ---- Q8 KV + attention -------------------------------------------------
     def create_q8_kv_state(self, kv_heads: int, head_dim: int, max_tokens: int = 0,

@@ -2,6 +2,7 @@
 from __future__ import annotations
 
 import os
+from contextlib import contextmanager
 
 import numpy as np
 
@@ -71,3 +72,32 @@ def assert_bf16_close(got_f32: np.ndarray, ref_f32: np.ndarray, rel: float = 1e-
     assert err <= rel, f"{what}: arithmetic rel err {err:.3e} > {rel:.1e} (raw incl. bf16 rounding {raw:.3e})"
     assert raw <= rel + 2.0 ** -8, f"{what}: raw rel err {raw:.3e}"
     return err
+
+
+@contextmanager
+def tuned(**env):
+    """A fresh runtime on cuda:0 (torch's current stream) whose planner uses
+    the given QM38_* overrides: the library reads them once, when a runtime
+    is created.  A value of None leaves that variable unset."""
+    import torch
+    import qm38
+    saved = {k: os.environ.get(k) for k in env}
+    try:
+        for k, v in env.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = str(v)
+        r = qm38.Runtime(0)
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    r.set_stream(torch.cuda.current_stream())
+    try:
+        yield r
+    finally:
+        torch.cuda.synchronize()
+        r.close()

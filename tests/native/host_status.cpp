@@ -77,6 +77,51 @@ static void runtime_cases(qm_runtime* rt) {
   huge.out_rows = 0xFFFFFFFFu;
   expect(qm_q4_project(rt, &huge, 1, x, 0xFFFFFFC0u, 1, outs), QM_ERR_DIMENSION_OVERFLOW, "weight count overflow");
 
+  // Mapped jobs (validate_mapped_q4_affine_shape, metal_runtime.rs:8854-8898):
+  // K = 128, 64 rows -> 4096 B of weights, 256 B of scales and of biases.
+  {
+    const qm_buffer wb{fake<const void>(0x100000), 8192}, sb{fake<const void>(0x200000), 512};
+    const qm_q4_mapped_job ok{wb, 4096, sb, 256, sb, 0, 64};
+    qm_q4_job out{};
+    expect(qm_q4_job_from_mapped(&ok, 128, &out), QM_OK, "mapped job in range");
+    if (out.weights != fake<const uint32_t>(0x101000) || out.scales != fake<const uint16_t>(0x200100) ||
+        out.biases != fake<const uint16_t>(0x200000) || out.out_rows != 64) {
+      fprintf(stderr, "FAIL mapped job resolves to the wrong pointers\n");
+      ++g_failures;
+    }
+    qm_q4_mapped_job m = ok;
+    m.weight_offset = 8193;
+    expect(qm_q4_job_from_mapped(&m, 128, &out), QM_ERR_INVALID_BUFFER_OFFSET, "weight offset past the buffer");
+    m = ok;
+    m.bias_offset = 513;
+    expect(qm_q4_job_from_mapped(&m, 128, &out), QM_ERR_INVALID_BUFFER_OFFSET, "bias offset past the buffer");
+    m = ok;
+    m.weight_offset = 4104;  // 4088 B left for 4096
+    expect(qm_q4_job_from_mapped(&m, 128, &out), QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE, "weights run past the buffer");
+    m = ok;
+    m.scale_offset = 264;  // 248 B left for 256
+    expect(qm_q4_job_from_mapped(&m, 128, &out), QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE, "scales run past the buffer");
+    m = ok;
+    m.out_rows = 65;
+    expect(qm_q4_job_from_mapped(&m, 128, &out), QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE, "one row too many");
+    m = ok;
+    m.weight_offset = 8192;  // offset == length is allowed, the tensor then does not fit
+    expect(qm_q4_job_from_mapped(&m, 128, &out), QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE, "offset at the buffer end");
+    expect(qm_q4_job_from_mapped(&ok, 100, &out), QM_ERR_INPUT_NOT_GROUPED, "mapped K not grouped");
+    m = ok;
+    m.out_rows = 0;
+    expect(qm_q4_job_from_mapped(&m, 128, &out), QM_ERR_EMPTY_DIMENSION, "mapped zero rows");
+    m = ok;
+    m.weight_offset = 4;
+    m.weights.length = 8200;
+    expect(qm_q4_job_from_mapped(&m, 128, &out), QM_ERR_MISALIGNED, "mapped weights misaligned");
+    expect(qm_q4_job_from_mapped(nullptr, 128, &out), QM_ERR_NULL_POINTER, "mapped job NULL");
+    uint32_t* ids = fake<uint32_t>(0x60000);
+    expect(qm_q4_argmax(rt, &job, x, 128, 3, ids), QM_ERR_NO_DEVICE, "valid argmax, no device");
+    expect(qm_q4_argmax(rt, &job, x, 128, 3, nullptr), QM_ERR_NULL_POINTER, "argmax ids NULL");
+    expect(qm_q4_argmax(rt, &job, x, 96, 3, ids), QM_ERR_INPUT_NOT_GROUPED, "argmax K not grouped");
+  }
+
   // KV cache and attention.
   qm_kv* kv = nullptr;
   expect(qm_kv_create(rt, 8, 300, 16, 0, &kv), QM_ERR_INVALID_ATTENTION_SHAPE, "head_dim 300");

@@ -24,7 +24,7 @@ import pytest
 
 import oracle
 import torch
-from gpu_util import assert_bf16_close, bf16_dev_to_f32, bf16_half_ulp, empty_bf16, to_dev
+from gpu_util import assert_bf16_close, bf16_dev_to_f32, bf16_half_ulp, empty_bf16, to_dev, tuned
 from qm38 import QmError, synth
 
 pytestmark = pytest.mark.gpu
@@ -257,21 +257,15 @@ def test_decode_ragged_batch(rt, torch_dev, D, H, KVH, pps, waves):
     mirrors = [Mirror(KVH, D) for _ in lens]
     for c, m, n in zip(caches, mirrors, lens):
         _fill(rt, torch_dev, c, m, rng, n, H, KVH, D)
-    if pps:
-        os.environ["QM38_ATTN_PPS"] = str(pps)
-    os.environ["QM38_ATTN_WAVES"] = str(waves)
-    try:
+    with tuned(QM38_ATTN_PPS=pps or None, QM38_ATTN_WAVES=waves) as trt:
         for it in range(2):
             q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, len(lens), H, KVH, D, gate=(it == 0))
-            got = _decode(rt, torch_dev, caches, q_bits, g_bits, k, v, H)
+            got = _decode(trt, torch_dev, caches, q_bits, g_bits, k, v, H)
             for b, (c, m) in enumerate(zip(caches, mirrors)):
                 m.append(k[b], v[b])
                 assert c.sequence_length == m.k.shape[0]
                 ref = m.reference(q_f[b:b + 1], None if g_f is None else g_f[b:b + 1], m.k.shape[0] - 1)
                 assert_bf16_close(got[b:b + 1], ref, what=f"seq {b} len {m.k.shape[0]} it {it}")
-    finally:
-        os.environ.pop("QM38_ATTN_PPS", None)
-        os.environ.pop("QM38_ATTN_WAVES", None)
     for c, m in zip(caches, mirrors):
         _check_cache(c, m)
 
@@ -289,18 +283,13 @@ def test_decode_long_split_page_ids(rt, torch_dev, D, H, KVH, waves, pps):
     cache = rt.create_q8_kv_state(KVH, D, n + 64)
     mirror = Mirror(KVH, D)
     _fill(rt, torch_dev, cache, mirror, rng, n, H, KVH, D)
-    os.environ["QM38_ATTN_PPS"] = str(pps)
-    os.environ["QM38_ATTN_WAVES"] = str(waves)
-    try:
+    with tuned(QM38_ATTN_PPS=pps, QM38_ATTN_WAVES=waves) as trt:
         for it in range(2):
             q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, 1, H, KVH, D, gate=(it == 1))
-            got = _decode(rt, torch_dev, [cache], q_bits, g_bits, k, v, H)
+            got = _decode(trt, torch_dev, [cache], q_bits, g_bits, k, v, H)
             mirror.append(k[0], v[0])
             ref = mirror.reference(q_f, g_f, mirror.k.shape[0] - 1)
             assert_bf16_close(got, ref, what=f"len {mirror.k.shape[0]} it {it}")
-    finally:
-        os.environ.pop("QM38_ATTN_PPS", None)
-        os.environ.pop("QM38_ATTN_WAVES", None)
     _check_cache(cache, mirror)
 
 
@@ -396,6 +385,35 @@ def test_clone_and_truncate(rt, torch_dev):
         _check_cache(c, m)
 
 
+@pytest.mark.parametrize("max_tokens", [20, 5])
+def test_clone_at_a_limit_below_the_page_size(rt, torch_dev, max_tokens):
+    # A limit that is not a multiple of 16: the pages hold more tokens than
+    # the limit allows, and the clone must take the capacity the source may
+    # use (clone_q8_kv_state, metal_runtime.rs:7338-7379), also for an empty
+    # cache and one filled to the limit.
+    D, H, KVH = 64, 4, 2
+    rng = np.random.default_rng(max_tokens)
+    a = rt.create_q8_kv_state(KVH, D, max_tokens)
+    e = a.clone()
+    assert e.sequence_length == 0
+    ma = Mirror(KVH, D)
+    _fill(rt, torch_dev, a, ma, rng, max_tokens, H, KVH, D)
+    assert a.sequence_length == max_tokens and a.capacity_tokens == max_tokens
+    b = a.clone()
+    assert b.sequence_length == max_tokens and b.capacity_tokens == max_tokens
+    _check_cache(b, ma)
+    with pytest.raises(QmError, match="CAPACITY_EXCEEDED"):
+        b.reserve(1)
+    b.truncate(max_tokens - 2)
+    mb = Mirror(KVH, D)
+    mb.append(ma.k[:max_tokens - 2], ma.v[:max_tokens - 2])
+    q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, 2, H, KVH, D)
+    got = _prefill(rt, torch_dev, b, q_bits, g_bits, k, v, H)
+    mb.append(k, v)
+    assert_bf16_close(got, mb.reference(q_f, g_f, max_tokens - 2), what="clone at the limit")
+    _check_cache(b, mb)
+
+
 @pytest.mark.parametrize("T", [4096, 32768])
 def test_long_context_decode(rt, torch_dev, T):
     D, H, KVH = 256, 24, 4
@@ -441,12 +459,9 @@ def test_odd_head_dims(rt, torch_dev, D, H, KVH):
             got = _prefill(rt, torch_dev, c, q_bits, g_bits, k, v, H)
             m.append(k, v)
             assert_bf16_close(got, m.reference(q_f, g_f, 0), what=f"prefill d={D} n={n}")
-    os.environ["QM38_ATTN_PPS"] = "4"  # split the 300-token cache: the merge runs
-    try:
+    with tuned(QM38_ATTN_PPS=4) as trt:  # split the 300-token cache: the merge runs
         q_bits, q_f, g_bits, g_f, k, v = _rand_qkv(rng, len(lens), H, KVH, D)
-        got = _decode(rt, torch_dev, caches, q_bits, g_bits, k, v, H)
-    finally:
-        os.environ.pop("QM38_ATTN_PPS", None)
+        got = _decode(trt, torch_dev, caches, q_bits, g_bits, k, v, H)
     for b, (c, m) in enumerate(zip(caches, mirrors)):
         m.append(k[b], v[b])
         ref = m.reference(q_f[b:b + 1], g_f[b:b + 1], m.k.shape[0] - 1)

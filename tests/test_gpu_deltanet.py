@@ -26,7 +26,7 @@ import numpy as np
 import pytest
 
 import oracle
-from gpu_util import from_dev, to_dev
+from gpu_util import from_dev, to_dev, tuned
 from qm38 import DnConfig, QmError
 
 pytestmark = pytest.mark.gpu
@@ -77,12 +77,10 @@ def _close(got, ref, tol=TOL, what=""):
 
 @contextmanager
 def _chunked(on: bool):
-    """Forces the chunked scan on or off for long and short prefills alike."""
-    os.environ["QM38_DN_CHUNKED"] = "1" if on else "0"
-    try:
-        yield
-    finally:
-        os.environ.pop("QM38_DN_CHUNKED", None)
+    """A runtime that forces the chunked scan on or off for long and short
+    prefills alike."""
+    with tuned(QM38_DN_CHUNKED=1 if on else 0) as r:
+        yield r
 
 
 def _zero_state(c):
@@ -218,8 +216,8 @@ def test_long_prefill_equals_steps(rt, torch_dev):
     wts, acts = _synth(rng, c, M)
     w = rt.create_deltanet_weights(cfg, *wts)
     pre, step = w.create_state(), w.create_state()
-    with _chunked(False):
-        got = _run(rt, torch_dev, w, pre, *acts, 1e-6)
+    with _chunked(False) as trt:
+        got = _run(trt, torch_dev, w, pre, *acts, 1e-6)
     steps = np.stack([_step(rt, torch_dev, w, step, *(x[t] for x in acts), 1e-6) for t in range(M)])
     assert np.array_equal(got, steps)
     for x, y in zip(pre.read(), step.read()):
@@ -265,13 +263,10 @@ def test_step_kernels_agree(rt, torch_dev, shape):
     w = rt.create_deltanet_weights(cfg, *wts)
     runs = []
     for head in ("1", "0"):
-        os.environ["QM38_DN_STEP_HEAD"] = head
-        try:
+        with tuned(QM38_DN_STEP_HEAD=head) as trt:
             st = w.create_state()
-            outs = np.stack([_step(rt, torch_dev, w, st, *(x[t] for x in acts), 1e-6) for t in range(M)])
+            outs = np.stack([_step(trt, torch_dev, w, st, *(x[t] for x in acts), 1e-6) for t in range(M)])
             runs.append((outs, *st.read()))
-        finally:
-            os.environ.pop("QM38_DN_STEP_HEAD", None)
     for x, y, what in zip(runs[0], runs[1], ("out", "history", "state")):
         assert np.array_equal(x, y), what
     hist, S = _zero_state(c)
@@ -454,10 +449,10 @@ def test_chunked_matches_oracle(rt, torch_dev, shape, M, decay):
     st = w.create_state()
     warm = [x[:9] for x in acts]
     rest = [x[9:] for x in acts]
-    with _chunked(False):
-        _run(rt, torch_dev, w, st, *warm, 1e-6)
-    with _chunked(True):
-        got = _run(rt, torch_dev, w, st, *rest, 1e-6)
+    with _chunked(False) as trt:
+        _run(trt, torch_dev, w, st, *warm, 1e-6)
+    with _chunked(True) as trt:
+        got = _run(trt, torch_dev, w, st, *rest, 1e-6)
     hist, S = _zero_state(c)
     _, hist, S = oracle.deltanet_prefill(c, *wts, *warm, 1e-6, hist, S, f64=True)
     ref, h_ref, S_ref = oracle.deltanet_prefill(c, *wts, *rest, 1e-6, hist, S, f64=True)
@@ -478,8 +473,8 @@ def test_chunked_shadow_prefill_leaves_source(rt, torch_dev):
     _run(rt, torch_dev, w, src, *[x[:9] for x in acts], 1e-6)
     before = [x.copy() for x in src.read()]
     shadow = w.create_state()
-    with _chunked(True):
-        got = _run(rt, torch_dev, w, shadow, *[x[9:] for x in acts], 1e-6, source=src)
+    with _chunked(True) as trt:
+        got = _run(trt, torch_dev, w, shadow, *[x[9:] for x in acts], 1e-6, source=src)
     after = src.read()
     assert np.array_equal(before[0], after[0]) and np.array_equal(before[1], after[1])
     hist, S = _zero_state(c)

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle
-from gpu_util import assert_bf16_close, bf16_dev_to_f32, empty_bf16, to_dev
+from gpu_util import assert_bf16_close, bf16_dev_to_f32, empty_bf16, to_dev, tuned
 from qm38 import QmError, synth
 
 pytestmark = pytest.mark.gpu
@@ -163,27 +163,26 @@ def test_decode_set_27b_shapes(rt, torch_dev, M):
 
 @pytest.mark.parametrize("nt,rpw", [(1, 16), (1, 13), (1, 10), (1, 8), (2, 32), (2, 20), (2, 17)])
 @pytest.mark.parametrize("M", [1, 3, 8])
-def test_rows_per_workgroup(rt, torch_dev, monkeypatch, nt, rpw, M):
+def test_rows_per_workgroup(torch_dev, nt, rpw, M):
     """Workgroups owning fewer rows than their 16-row tiles (the planner's
     balancing choice) mask the rest; forced here for several row counts that
     do not divide the projection heights, with several jobs in one launch and
     a SwiGLU pair."""
     import qm38
-    monkeypatch.setenv("QM38_Q4_NT", str(nt))
-    monkeypatch.setenv("QM38_Q4_RPW", str(rpw))
-    rng = np.random.default_rng(300 + nt * 50 + rpw + M)
-    K = 1024
-    mats = [synth.q4_matrix(rng, n, K) for n in (200, 37, 512)]
-    xb = synth.bf16_normal(rng, (M, K))
-    for mat, got in zip(mats, _project(rt, torch_dev, mats, xb, M)):
-        assert_bf16_close(got, oracle.q4_project(xb, *mat), what=f"rows {mat[0].shape[0]}")
-    I = 333
-    gate, up = synth.q4_matrix(rng, I, K), synth.q4_matrix(rng, I, K)
-    dg, du = _upload(torch_dev, *gate), _upload(torch_dev, *up)
-    h = empty_bf16((M, I), torch_dev)
-    rt.q4_swiglu(qm38.Runtime.job(*dg, I), qm38.Runtime.job(*du, I), to_dev(xb, torch_dev), K, M, h)
-    h_ref = oracle.swiglu(oracle.q4_project(xb, *gate), oracle.q4_project(xb, *up))
-    assert_bf16_close(bf16_dev_to_f32(h), h_ref, what="swiglu")
+    with tuned(QM38_Q4_NT=nt, QM38_Q4_RPW=rpw) as rt:
+        rng = np.random.default_rng(300 + nt * 50 + rpw + M)
+        K = 1024
+        mats = [synth.q4_matrix(rng, n, K) for n in (200, 37, 512)]
+        xb = synth.bf16_normal(rng, (M, K))
+        for mat, got in zip(mats, _project(rt, torch_dev, mats, xb, M)):
+            assert_bf16_close(got, oracle.q4_project(xb, *mat), what=f"rows {mat[0].shape[0]}")
+        I = 333
+        gate, up = synth.q4_matrix(rng, I, K), synth.q4_matrix(rng, I, K)
+        dg, du = _upload(torch_dev, *gate), _upload(torch_dev, *up)
+        h = empty_bf16((M, I), torch_dev)
+        rt.q4_swiglu(qm38.Runtime.job(*dg, I), qm38.Runtime.job(*du, I), to_dev(xb, torch_dev), K, M, h)
+        h_ref = oracle.swiglu(oracle.q4_project(xb, *gate), oracle.q4_project(xb, *up))
+        assert_bf16_close(bf16_dev_to_f32(h), h_ref, what="swiglu")
 
 
 def test_config1_4096(rt, torch_dev):
@@ -208,3 +207,136 @@ def test_rejects_incomplete_group(rt, torch_dev):
     with pytest.raises(QmError) as e:
         rt.q4_project([qm38.Runtime.job(w, s, b, 0)], x, 64, 1, [out])
     assert e.value.status == "QM_ERR_EMPTY_DIMENSION"
+
+
+def _argmax_ref(y: np.ndarray) -> np.ndarray:
+    """qwen38_argmax_rows (qwen38.metal:4202-4244): largest value, lowest index
+    on ties, NaN never winning (an all-NaN row gives 0)."""
+    out = np.zeros(y.shape[0], np.uint32)
+    for m in range(y.shape[0]):
+        row = np.where(np.isnan(y[m]), -np.inf, y[m])
+        if np.all(np.isnan(y[m])):
+            continue
+        out[m] = int(np.flatnonzero(row == row.max())[0])
+    return out
+
+
+def _argmax(rt, dev, mat, xb):
+    import torch
+    import qm38
+    w, s, b = _upload(dev, *mat)
+    M = xb.shape[0]
+    ids = torch.full((M,), -1, dtype=torch.int32, device=dev)
+    rt.q4_affine_argmax(qm38.Runtime.job(w, s, b, mat[0].shape[0]), to_dev(xb, dev), xb.shape[1], M, ids)
+    return from_dev_u32(ids)
+
+
+def from_dev_u32(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("M", [1, 3, 16, 37])
+def test_argmax_matches_oracle(rt, torch_dev, M):
+    # q4_affine_argmax_mapped_batch (metal_runtime.rs:3797): the greedy token
+    # of every row.  The kernel's fp32 sums and the fp64 oracle may order a
+    # near-tie differently, so a row must pick the oracle's winner unless the
+    # runner-up lies within the fp32 error bound; then its pick must be one of
+    # those near-maximal rows.  M = 37 runs in chunks of 16 rows.
+    rng = np.random.default_rng(4100 + M)
+    N, K = 1000, 512
+    mat = synth.q4_matrix(rng, N, K)
+    xb = synth.bf16_normal(rng, (M, K))
+    got = _argmax(rt, torch_dev, mat, xb)
+    ref = oracle.q4_project(xb, *mat)
+    tol = 1e-5 * np.max(np.abs(ref), axis=1)
+    for m in range(M):
+        near = np.flatnonzero(ref[m] >= ref[m].max() - tol[m])
+        assert got[m] in near, f"row {m}: picked {got[m]}, oracle winners {near}"
+        if len(near) == 1:
+            assert got[m] == near[0]
+
+
+def test_argmax_ties_nan_and_empty_rows(rt, torch_dev):
+    # Identical rows give bit-identical logits: the lowest index wins
+    # (qwen38.metal:4218-4221).  A NaN scale makes its row NaN, which never
+    # wins; an all-NaN activation row makes every logit NaN and gives 0.
+    rng = np.random.default_rng(77)
+    N, K = 517, 256
+    w, s, b = synth.q4_matrix(rng, N, K)
+    xb = synth.bf16_normal(rng, (3, K))
+    xb[1] = 0x7FC0  # bf16 NaN
+    r = int(np.argmax(oracle.q4_project(xb[:1], w, s, b)[0]))
+    for j in (3, N - 1, (r + 200) % N):
+        w[j], s[j], b[j] = w[r], s[r], b[r]
+    s[0] = 0x7FC0
+    got = _argmax(rt, torch_dev, (w, s, b), xb)
+    y = oracle.q4_project(xb, w, s, b)
+    assert np.isnan(y[0, 0]) and np.all(np.isnan(y[1]))
+    want = _argmax_ref(y)
+    assert want[0] == 3 and want[1] == 0
+    assert got[0] == 3 and got[1] == 0
+    assert got[2] == want[2] or y[2, got[2]] >= y[2].max() - 1e-5 * np.max(np.abs(y[2]))
+    # the same rows through the plain projection: the tie is exact in the kernel too
+    (proj,) = _project(rt, torch_dev, [(w, s, b)], xb[:1], 1)
+    assert proj[0, 3] == proj[0, r] == proj[0, N - 1]
+
+
+def test_projection_ranges_are_checked(rt, torch_dev):
+    # validate_mapped_q4_affine_shape (metal_runtime.rs:8854-8898): a tensor
+    # running past its allocation is refused before anything is launched, and
+    # a pointer inside no allocation is an invalid offset.  Sizes are whole
+    # 4 KiB pages so the allocation's length is exactly what was asked for.
+    import qm38
+    rng = np.random.default_rng(8)
+    N, K = 64, 1024
+    w, s, b = synth.q4_matrix(rng, N, K)
+    dw, ds, db = rt.device_buffer(w), rt.device_buffer(s), rt.device_buffer(b)
+    short_w = rt.device_buffer(w[:56])  # 28672 B of the 32768 needed
+    x = to_dev(synth.bf16_normal(rng, (1, K)), torch_dev)
+    out = empty_bf16((1, N), torch_dev)
+    rt.q4_project([qm38.Runtime.job(dw, ds, db, N)], x, K, 1, [out])  # in range
+    with pytest.raises(QmError) as e:
+        rt.q4_project([qm38.Runtime.job(short_w, ds, db, N)], x, K, 1, [out])
+    assert e.value.status == "QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE"
+    with pytest.raises(QmError) as e:  # one row too many for every tensor
+        rt.q4_project([qm38.Runtime.job(dw, ds, db, N + 1)], x, K, 1, [empty_bf16((1, N + 1), torch_dev)])
+    assert e.value.status == "QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE"
+    host = np.zeros(1 << 16, np.uint8)  # ordinary host memory: no device allocation
+    with pytest.raises(QmError) as e:
+        rt.q4_project([qm38.Runtime.job(host.ctypes.data, ds, db, N)], x, K, 1, [out])
+    assert e.value.status == "QM_ERR_INVALID_BUFFER_OFFSET"
+    small_out = rt.device_buffer(nbytes=64)
+    with pytest.raises(QmError) as e:  # the output needs 128 B
+        rt.q4_project([qm38.Runtime.job(dw, ds, db, N)], x, K, 1, [small_out])
+    assert e.value.status == "QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE"
+    with pytest.raises(QmError) as e:
+        rt.q4_affine_argmax(qm38.Runtime.job(short_w, ds, db, N), x, K, 1, out)
+    assert e.value.status == "QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE"
+
+
+def test_mapped_job_from_one_buffer(rt, torch_dev):
+    # MappedQ4AffineJob: weights, scales and biases at byte offsets of one
+    # checkpoint-like allocation give the same projection as separate tensors.
+    import qm38
+    rng = np.random.default_rng(9)
+    N, K = 96, 512
+    w, s, b = synth.q4_matrix(rng, N, K)
+    blob = np.concatenate([np.zeros(256, np.uint8), w.view(np.uint8).ravel(), s.view(np.uint8).ravel(),
+                           np.zeros(8, np.uint8), b.view(np.uint8).ravel()])
+    buf = rt.device_buffer(blob)
+    whole = (buf.ptr, blob.nbytes)
+    off_w, off_s = 256, 256 + w.nbytes
+    off_b = off_s + s.nbytes + 8
+    job = qm38.Runtime.mapped_job(whole, off_w, whole, off_s, whole, off_b, N, K)
+    xb = synth.bf16_normal(rng, (2, K))
+    out = empty_bf16((2, N), torch_dev)
+    rt.q4_project([job], to_dev(xb, torch_dev), K, 2, [out])
+    assert_bf16_close(bf16_dev_to_f32(out), oracle.q4_project(xb, w, s, b), what="mapped")
+    with pytest.raises(QmError) as e:
+        qm38.Runtime.mapped_job(whole, off_w, whole, off_s, whole, off_b + 8, N, K)
+    assert e.value.status == "QM_ERR_MAPPED_TENSOR_OUT_OF_RANGE"
+    with pytest.raises(QmError) as e:
+        qm38.Runtime.mapped_job(whole, blob.nbytes + 1, whole, off_s, whole, off_b, N, K)
+    assert e.value.status == "QM_ERR_INVALID_BUFFER_OFFSET"

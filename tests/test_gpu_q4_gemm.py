@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 import oracle
-from gpu_util import assert_bf16_close, bf16_dev_to_f32, empty_bf16, to_dev
+from gpu_util import assert_bf16_close, bf16_dev_to_f32, empty_bf16, to_dev, tuned
 from qm38 import synth
 
 pytestmark = pytest.mark.gpu
@@ -204,7 +204,7 @@ def test_split_k_swiglu_and_determinism(rt, torch_dev, M):
 
 @pytest.mark.parametrize("knob,q", [("Q", 1), ("Q", 3), ("Q", 8), ("Q", 13), ("Q", 32), ("Q", 45), ("Q", 97),
                                     ("Q", 200), ("SPLITS", 2), ("SPLITS", 3), ("SPLITS", 5), ("SPLITS", 32)])
-def test_worker_step_ranges(rt, torch_dev, monkeypatch, knob, q):
+def test_worker_step_ranges(torch_dev, knob, q):
     # Workers take Q consecutive K steps of the flattened (tile, group) range
     # (QM38_GEMM_Q forces Q; G = 32 here): Q = 32 is whole tiles, Q < 32 cuts
     # every tile into 2 or more pieces, Q > 32 gives ranges that end inside a
@@ -212,20 +212,20 @@ def test_worker_step_ranges(rt, torch_dev, monkeypatch, knob, q):
     # QM38_GEMM_SPLITS forces S slices per tile instead.  Every choice matches
     # the oracle and repeats bit for bit.
     import qm38
-    monkeypatch.setenv("QM38_GEMM_" + knob, str(q))
-    rng = np.random.default_rng(700 + q)
-    K, M = 2048, 300
-    mats = [synth.q4_matrix(rng, 300, K), synth.q4_matrix(rng, 100, K)]
-    xb = synth.bf16_normal(rng, (M, K))
-    got1 = _project(rt, torch_dev, mats, xb, M)
-    got2 = _project(rt, torch_dev, mats, xb, M)
-    for (w, s, b), g1, g2 in zip(mats, got1, got2):
-        assert_bf16_close(g1, oracle.q4_project(xb, w, s, b), what=f"{knob}={q}")
-        assert np.array_equal(g1, g2), f"{knob}={q}: result differs between calls"
-    I = 200
-    gate, up = synth.q4_matrix(rng, I, K), synth.q4_matrix(rng, I, K)
-    dg, du = _upload(torch_dev, *gate), _upload(torch_dev, *up)
-    h = empty_bf16((M, I), torch_dev)
-    rt.q4_swiglu(qm38.Runtime.job(*dg, I), qm38.Runtime.job(*du, I), to_dev(xb, torch_dev), K, M, h)
-    assert_bf16_close(bf16_dev_to_f32(h), oracle.swiglu(oracle.q4_project(xb, *gate), oracle.q4_project(xb, *up)),
-                      what=f"swiglu {knob}={q}")
+    with tuned(**{"QM38_GEMM_" + knob: q}) as rt:
+        rng = np.random.default_rng(700 + q)
+        K, M = 2048, 300
+        mats = [synth.q4_matrix(rng, 300, K), synth.q4_matrix(rng, 100, K)]
+        xb = synth.bf16_normal(rng, (M, K))
+        got1 = _project(rt, torch_dev, mats, xb, M)
+        got2 = _project(rt, torch_dev, mats, xb, M)
+        for (w, s, b), g1, g2 in zip(mats, got1, got2):
+            assert_bf16_close(g1, oracle.q4_project(xb, w, s, b), what=f"{knob}={q}")
+            assert np.array_equal(g1, g2), f"{knob}={q}: result differs between calls"
+        I = 200
+        gate, up = synth.q4_matrix(rng, I, K), synth.q4_matrix(rng, I, K)
+        dg, du = _upload(torch_dev, *gate), _upload(torch_dev, *up)
+        h = empty_bf16((M, I), torch_dev)
+        rt.q4_swiglu(qm38.Runtime.job(*dg, I), qm38.Runtime.job(*du, I), to_dev(xb, torch_dev), K, M, h)
+        assert_bf16_close(bf16_dev_to_f32(h), oracle.swiglu(oracle.q4_project(xb, *gate), oracle.q4_project(xb, *up)),
+                          what=f"swiglu {knob}={q}")

@@ -17,7 +17,7 @@ import os
 import numpy as np
 import pytest
 
-from gpu_util import bf16_dev_to_f32, empty_bf16, to_dev
+from gpu_util import bf16_dev_to_f32, empty_bf16, to_dev, tuned
 from qm38 import QmError, synth
 
 pytestmark = pytest.mark.gpu
@@ -88,13 +88,47 @@ def test_noalloc_refuses_growth_and_oversized_plans(rt, torch_dev):
     big.reserve(40001)
     big.truncate(0)
     _fill(rt, torch_dev, big, rng, 40000)
-    os.environ["QM38_ATTN_PPS"] = "4"
-    try:
+    with tuned(QM38_ATTN_PPS=4) as trt:
         with pytest.raises(QmError, match="CAPACITY_EXCEEDED"):
-            _decode(rt.gqa_attention_q8_noalloc, torch_dev, [big], q, g, k, v)
-    finally:
-        os.environ.pop("QM38_ATTN_PPS", None)
+            _decode(trt.gqa_attention_q8_noalloc, torch_dev, [big], q, g, k, v)
     assert big.sequence_length == 40000
     # The default plan of the same call fits.
     got = _decode(rt.gqa_attention_q8_noalloc, torch_dev, [big], q, g, k, v)
     assert big.sequence_length == 40001 and np.all(np.isfinite(got))
+
+
+def test_noalloc_allocates_no_device_memory(rt, torch_dev):
+    # The entry point's contract: no device allocation, measured as the
+    # device's free bytes around a call on a runtime that has never allocated
+    # a workspace.  The control (qm_attn_decode on another such runtime,
+    # planned with splits of 4 pages so that its partials take 20.8 MB) shows
+    # that the measurement sees an allocation of that size.
+    import torch
+    rng = np.random.default_rng(709)
+    a, b = _pair(rt, torch_dev, rng, [40000])
+    c, d = _pair(rt, torch_dev, rng, [40000])
+    q, g, k, v = _inputs(rng, 1)
+    qd, gd, kd, vd = (to_dev(t, torch_dev) for t in (q, g, k, v))
+    o = empty_bf16((1, H, D), torch_dev)
+    # The library's code object (with its fixed array) is loaded by earlier
+    # calls in this process; warm the symbol lookup once more on its own.
+    rt.gqa_attention_q8_noalloc(d, qd, gd, kd, vd, H, o)
+    torch.cuda.synchronize()
+
+    def free_bytes():
+        torch.cuda.synchronize()
+        return torch.cuda.mem_get_info()[0]
+
+    with tuned() as fresh:
+        before = free_bytes()
+        fresh.gqa_attention_q8_noalloc(b, qd, gd, kd, vd, H, o)
+        after = free_bytes()
+    with tuned(QM38_ATTN_PPS=4) as control:  # 625 splits: 20.8 MB of partials
+        c_before = free_bytes()
+        control.gqa_attention_q8(c, qd, gd, kd, vd, H, o)
+        c_after = free_bytes()
+    if c_before - c_after < (16 << 20):
+        pytest.skip(f"free-memory reading did not see the control's allocation ({c_before - c_after} B)")
+    assert before == after, f"qm_attn_decode_noalloc changed free device memory by {before - after} B"
+    for x in a + b + c + d:
+        x.close()
