@@ -158,7 +158,8 @@ def q4_sets(rng, dev):
 
 
 def q4_leg(rt, dev, sets, M: int, rng, steps, warmup):
-    """QKV, gate+up (SwiGLU), down over M rows; returns timings and byte / flop counts."""
+    """QKV with gate+up (SwiGLU) as one same-input set, then down, over M rows;
+    returns timings and byte / flop counts."""
     import torch
     from qm38 import synth
     x = dev_array(synth.bf16_normal(rng, (M, H)), dev)
@@ -166,10 +167,12 @@ def q4_leg(rt, dev, sets, M: int, rng, steps, warmup):
     h = torch.empty((M, I), dtype=torch.int16, device=dev)
     y = torch.empty((M, H), dtype=torch.int16, device=dev)
 
+    def qkv_gateup(j):
+        rt.q4_project_set([j["qkv"][0], j["gate"][0]], [None, j["up"][0]], x, H, M, [qkv_out, h])
+
     def step(i, marks):
         j = sets[i % NCOPY]
-        rt.q4_project([j["qkv"][0]], x, H, M, [qkv_out])
-        rt.q4_swiglu(j["gate"][0], j["up"][0], x, H, M, h)
+        qkv_gateup(j)
         rt.q4_project([j["down"][0]], h, I, M, [y])
 
     stream = torch.cuda.current_stream()
@@ -177,15 +180,14 @@ def q4_leg(rt, dev, sets, M: int, rng, steps, warmup):
     # Per-kernel durations: each projection alone, back to back (events only
     # around the whole run, so no event sits between the timed kernels).
     calls = {
-        "qkv": lambda i, m: rt.q4_project([sets[i % NCOPY]["qkv"][0]], x, H, M, [qkv_out]),
-        "gateup": lambda i, m: rt.q4_swiglu(sets[i % NCOPY]["gate"][0], sets[i % NCOPY]["up"][0], x, H, M, h),
+        "qkv_gateup": lambda i, m: qkv_gateup(sets[i % NCOPY]),
         "down": lambda i, m: rt.q4_project([sets[i % NCOPY]["down"][0]], h, I, M, [y]),
     }
     per = [timed(fn, stream, steps, 2)[0] for fn in calls.values()]
-    wbytes = {"qkv": q4_bytes(QKV, H), "gateup": 2 * q4_bytes(I, H), "down": q4_bytes(H, I)}
-    abytes = {"qkv": 2 * M * (H + QKV), "gateup": 2 * M * (H + I), "down": 2 * M * (I + H)}
-    flops = {"qkv": 2 * M * QKV * H, "gateup": 4 * M * I * H, "down": 2 * M * H * I}
-    kern = dict(zip(("qkv", "gateup", "down"), per))
+    wbytes = {"qkv_gateup": q4_bytes(QKV, H) + 2 * q4_bytes(I, H), "down": q4_bytes(H, I)}
+    abytes = {"qkv_gateup": 2 * M * (H + QKV + I), "down": 2 * M * (I + H)}
+    flops = {"qkv_gateup": 2 * M * QKV * H + 4 * M * I * H, "down": 2 * M * H * I}
+    kern = dict(zip(calls, per))
     q4_leg.last_step = step
     return ms, kern, wbytes, abytes, flops
 
@@ -549,13 +551,17 @@ def cpu_baseline_legs(seconds: float = 4.0):
 
 
 def traffic_from_profiles():
-    """HBM bytes per launch of the gate+up kernel, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE measurement (profiles/), or None."""
-    p = ROOT / "profiles" / "q4_decode_gateup_traffic.json"
+    """HBM bytes per launch of the roofline kernel (the QKV + gate/up set), from
+    the committed rocprofv3 FETCH_SIZE / WRITE_SIZE measurement (profiles/), or None."""
+    p = ROOT / "profiles" / TRAFFIC_FILE
     try:
         return json.loads(p.read_text()).get("bytes_per_launch")
     except (OSError, ValueError):
         return None
+
+
+TRAFFIC_FILE = "q4_stream_qkv_gateup_traffic.json"
+ROOF_KERNEL = "q4_stream_kernel"
 
 
 def _counter_rows(d: str, counter: str):
@@ -575,25 +581,25 @@ def _counter_rows(d: str, counter: str):
 
 
 def traffic_summary(fetch_dir: str, write_dir: str) -> int:
-    """HBM bytes per gate+up M=1 launch from FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each scaled by
-    what the same counter reads for a 256 MiB device copy of known size."""
+    """HBM bytes per QKV + gate/up (M=1) set launch from FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each
+    scaled by what the same counter reads for a 256 MiB device copy of known size."""
     copy_bytes = 256 << 20
     out = {"kernel": None, "calibration": {"copy_bytes": copy_bytes}, "raw_KiB_per_dispatch": {}}
     per = {}
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         rows = _counter_rows(d, counter)
         # The copy dispatches are the large non-q4 ones; the first (a small runtime copy) is excluded.
-        copies = [v for k, v in rows if "q4_decode" not in k and v * 1024 > copy_bytes / 4]
-        q4 = [(k, v) for k, v in rows if "q4_decode" in k]
+        copies = [v for k, v in rows if ROOF_KERNEL not in k and v * 1024 > copy_bytes / 4]
+        q4 = [(k, v) for k, v in rows if ROOF_KERNEL in k]
         if not copies or not q4:
-            raise RuntimeError(f"{counter}: expected copy and q4_decode dispatches in {d}")
+            raise RuntimeError(f"{counter}: expected copy and {ROOF_KERNEL} dispatches in {d}")
         factor = copy_bytes / (sum(copies) / len(copies) * 1024)
         out["calibration"][f"{counter}_KiB"] = round(sum(copies) / len(copies), 3)
         out["calibration"]["fetch_factor" if counter == "FETCH_SIZE" else "write_factor"] = round(factor, 4)
         out["raw_KiB_per_dispatch"][counter] = [v for _, v in q4]
         per[counter] = sum(v for _, v in q4) / len(q4) * 1024 * factor
-        out["kernel"] = q4[0][0][:120] + " (gate+up SwiGLU, M=1, 27B shapes)"
-    alg = 2 * q4_bytes(I, H) + 2 * (H + I)
+        out["kernel"] = q4[0][0][:120] + " (QKV + gate/up SwiGLU set, M=1, 27B shapes)"
+    alg = q4_bytes(QKV, H) + 2 * q4_bytes(I, H) + 2 * (H + QKV + I)
     out.update({"bytes_per_launch": int(per["FETCH_SIZE"] + per["WRITE_SIZE"]),
                 "fetch_bytes": int(per["FETCH_SIZE"]), "write_bytes": int(per["WRITE_SIZE"]),
                 "algorithmic_bytes": alg,
@@ -606,7 +612,7 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> int:
                     "python bench.py --traffic-from prof_out/pmc_fetch prof_out/pmc_write"],
                 "method": "per-dispatch counter (KiB) x (known copy bytes / the counter's reading for a 256 MiB "
                           "device copy); small copies excluded from the calibration mean"})
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "q4_decode_gateup_traffic.json")
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", TRAFFIC_FILE)
     with open(path, "w") as f:
         json.dump(out, f, indent=1)
     print(path)
@@ -721,7 +727,7 @@ def main() -> int:
                     help="for rocprofv3 --pmc: 5 launches of a 256 MiB copy, then 5 gate+up M=1 launches")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn the two --traffic-probe counter runs (rocprofv3 csv output directories) "
-                         "into profiles/q4_decode_gateup_traffic.json (no GPU needed)")
+                         "into profiles/q4_stream_qkv_gateup_traffic.json (no GPU needed)")
     ap.add_argument("--stats-from", metavar="PROF_DIR",
                     help="turn a rocprofv3 --kernel-trace --stats run of bench.py into "
                          "profiles/bench_all_legs_kernel_stats.txt (no GPU needed)")
@@ -765,11 +771,12 @@ def main() -> int:
         dst = torch.empty_like(src)
         x = dev_array(synth_bf16(rng, (1, H)), dev)
         h = torch.empty((1, I), dtype=torch.int16, device=dev)
+        qo = torch.empty((1, QKV), dtype=torch.int16, device=dev)
         for i in range(5):
             dst.copy_(src)
         for i in range(5):
             j = sets[i % NCOPY]
-            rt.q4_swiglu(j["gate"][0], j["up"][0], x, H, 1, h)
+            rt.q4_project_set([j["qkv"][0], j["gate"][0]], [None, j["up"][0]], x, H, 1, [qo, h])
         torch.cuda.synchronize()
         rt.close()
         return 0
@@ -786,7 +793,7 @@ def main() -> int:
             "kernel_us": {k: round(v * 1e3, 2) for k, v in kern.items()},
             "kernel_hbm_frac": {k: round((wb[k] + ab[k]) / (kern[k] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) for k in kern}}
         if M == 1:
-            head = (gbs, ms, step_bytes, wb["gateup"] + ab["gateup"], kern["gateup"])
+            head = (gbs, ms, step_bytes, wb["qkv_gateup"] + ab["qkv_gateup"], kern["qkv_gateup"])
             p10, p50, p90 = step_distribution(q4_leg.last_step, torch.cuda.current_stream(), max(args.steps, 100))
             extras["q4_decode_set_M1"]["step_us_p10_p50_p90"] = [p10, p50, p90]
     if "decode" in legs:
@@ -834,7 +841,7 @@ def main() -> int:
                    "step_bytes": step_bytes, "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(gu_achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-                     "kernel": "q4_decode_kernel (gate+up with SwiGLU epilogue, M=1)",
+                     "kernel": "q4_stream_kernel (QKV + gate/up pairs with SwiGLU in one launch, M=1)",
                      "bytes_per_launch": gu_bytes, "avg_launch_us": round(gu_ms * 1e3, 2)},
         "extras": extras,
     }

@@ -173,6 +173,17 @@ qm_status qm_q4_project(qm_runtime* rt, const qm_q4_job* jobs, int n_jobs,
                         const uint16_t* x, uint32_t in_elems, uint32_t M,
                         uint16_t* const* outputs);
 
+/* Same-input projections, plain ones and gate/up pairs together: for
+ * ups == NULL or ups[j] == NULL, outputs[j] = jobs[j](x) (bf16 [M][rows]);
+ * otherwise outputs[j] = bf16( silu(jobs[j](x)) * ups[j](x) ), with
+ * ups[j]->out_rows == jobs[j].out_rows.  For one activation row the whole set
+ * is one launch that reads x once (the reference's mapped batch, whose jobs
+ * would be a QKV projection and the pair kernels' gate/up, metal_runtime.rs:
+ * 3599 with qwen38.metal:1404..3643); larger M runs the plain jobs together
+ * and each pair as qm_q4_swiglu does.  n_jobs <= 8. */
+qm_status qm_q4_project_set(qm_runtime* rt, const qm_q4_job* jobs, const qm_q4_job* const* ups, int n_jobs,
+                            const uint16_t* x, uint32_t in_elems, uint32_t M, uint16_t* const* outputs);
+
 /* h[m][n] = bf16( silu(gate(x)[m][n]) * up(x)[m][n] ): the gate and up
  * projections of one MLP share the activation read and SwiGLU
  * (qwen38.metal:4188-4199, silu at 4090-4096) runs in the epilogue.

@@ -13,6 +13,10 @@ struct Q4Job {
   const uint16_t* s;
   const uint16_t* b;
   uint16_t* out;
+  // The up half of a gate/up pair (mode kQ4OutSwiglu): out = bf16 silu(w x) * (uw x).
+  const uint32_t* uw;
+  const uint16_t* us;
+  const uint16_t* ub;
   uint32_t rows;
   uint32_t tile_begin;  // filled by the launcher
   // Output of a decode (M <= 16) projection: 0 bf16; 1 fp32 holding the bf16-
@@ -20,10 +24,11 @@ struct Q4Job {
   // value (a residual add).  `out` then points at fp32.  3: argmax keys, one
   // uint64 per activation row (`out` points at them; they must be zero and are
   // maxed with atomics; launch_q4_argmax_finish turns them into row ids and
-  // clears them).  The GEMM takes 0 only.
+  // clears them).  4: a gate/up pair with SwiGLU (single-row streaming kernel
+  // only).  The GEMM takes 0 only.
   uint32_t mode;
 };
-constexpr uint32_t kQ4OutBf16 = 0, kQ4OutF32 = 1, kQ4OutAddF32 = 2, kQ4OutArgmax = 3;
+constexpr uint32_t kQ4OutBf16 = 0, kQ4OutF32 = 1, kQ4OutAddF32 = 2, kQ4OutArgmax = 3, kQ4OutSwiglu = 4;
 
 // Planner inputs: the device's compute units and the QM38_* tuning overrides
 // (forced plans for measurements), read from the environment once, when a
@@ -39,6 +44,7 @@ struct Tuning {
   int q4_split = 0;         // QM38_Q4_SPLIT: waves per decode workgroup
   int q4_plan_log = 0;      // QM38_Q4_PLAN_LOG: print each new decode plan
   int q4_fuse = 1;          // QM38_Q4_FUSE: 0 runs the MLP's down projection as its own launch
+  int q4_stream = 1;        // QM38_Q4_STREAM: 0 keeps single-row projections on the MFMA decode kernel
   int gemm_splits = 0;      // QM38_GEMM_SPLITS: K splits of the prefill GEMM
   int gemm_q = 0;           // QM38_GEMM_Q: stream-K steps per worker
   int gemm_plan_log = 0;    // QM38_GEMM_PLAN_LOG
@@ -67,6 +73,13 @@ struct Workspace {
 // swiglu: jobs[0] = gate, jobs[1] = up, result written to jobs[0].out.
 hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x,
                             uint32_t K, uint32_t M, const Workspace& ws, hipStream_t stream);
+
+// Single activation row (M = 1): the K-resident streaming kernel
+// (q4_stream.hip).  Jobs may mix plain projections and gate/up pairs
+// (kQ4OutSwiglu); an argmax launch has one job.
+bool q4_stream_supported(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn);
+hipError_t launch_q4_stream(const Q4Job* jobs, int n_jobs, const uint16_t* x, uint32_t K, const Workspace& ws,
+                            hipStream_t stream);
 
 // ids[m] from the argmax keys of a kQ4OutArgmax decode launch; zeroes the keys.
 hipError_t launch_q4_argmax_finish(unsigned long long* keys, uint32_t* ids, uint32_t M, hipStream_t stream);

@@ -1,0 +1,577 @@
+// MLX affine-Q4 projection of ONE activation row (decode, M = 1) for MI355X
+// (gfx950): the math of qwen38_q4_affine_matvec_simd
+// (/root/reference/shaders/qwen38.metal:213-246),
+//     y[n] = sum_g ( s[n][g] * sum_{i in g} q[n][i] x[i] + b[n][g] * sum_{i in g} x[i] ).
+//
+// Design (HBM-bound weight stream, activation resident in registers):
+//  * K is cut into 512-element chunks (256 bytes of every weight row).  A
+//    workgroup has W waves; wave w owns chunks [w*C, w*C + C) and keeps the
+//    activation of those chunks in VGPRs for the whole launch, so neither the
+//    weights nor the activation pass through LDS.
+//  * One 128-bit load per lane covers 4 rows x 256 bytes: lane l reads 16
+//    bytes (32 nibbles, half of a 64-group) of row l/16 at column 16*(l%16).
+//    Loads are coalesced (16 lanes read one contiguous 256-byte run) and
+//    stream into a register ring of D slots issued ahead of consumption.
+//  * Each word becomes four bf16 pairs (128+q_j, 128+q_{j+4}) with one
+//    AND-OR each (0x4300|q is the bf16 of 128+q, exact), and
+//    v_dot2_f32_bf16 multiplies them by the matching activation pairs.  Per
+//    lane:  p = sum (128+q) x  over its 32 elements, and the lane adds
+//        s * p + (b - 128 s) * X      (X = sum of those 32 activations),
+//    which equals s*sum(q x) + b*sum(x) over the half-group in real arithmetic.
+//  * Blocks: a workgroup owns a contiguous run of blocks.  A block is SB loads
+//    per chunk: SB = 2 gives 8 rows of a plain projection, or 4 rows of a
+//    gate/up pair (gate rows, then the same up rows: SwiGLU).  Each wave
+//    reduces its 16 lanes per row (DPP) and writes the row's partial over its
+//    chunks to LDS.  After the stream the workgroup adds the W partials of
+//    each row in wave order (deterministic) and stores the outputs; no global
+//    store is issued while weights are in flight.
+//  * Scales and biases of the workgroup's rows and the wave's chunks are
+//    staged once into LDS by buffer->LDS DMA before the weight stream starts.
+//  * Rows past a projection's end load zeros (buffer bounds) and are never
+//    stored; activation elements past K load zeros, and their lanes add 0.
+#include "common.h"
+#include "internal.h"
+
+#include <stdio.h>
+
+#include <algorithm>
+#include <cstring>
+#include <mutex>
+
+namespace qm {
+namespace {
+
+constexpr int kChunkElems = 512;  // 16 lanes x 32 elements
+constexpr int kMaxWaves = 16;
+constexpr int kNonTemporal = 2;   // buffer cache policy: weights are streamed once
+constexpr uint32_t kOOB = 0xFFFFFFF0u;
+
+struct StreamArgs {
+  const uint16_t* x;
+  uint32_t K, G, chunks;
+  uint32_t waves;         // W: waves per workgroup
+  uint32_t n_jobs;
+  uint32_t total_blocks;  // blocks of all jobs
+  uint32_t wgs;           // workgroups; workgroup g owns blocks [g*B/wgs, (g+1)*B/wgs)
+  uint32_t max_blocks;    // largest block count of one workgroup (LDS sizing)
+  Q4Job jobs[kMaxQ4Jobs];  // tile_begin = first block of the job
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint64_t bytes) {
+  const uint32_t n = bytes > 0xFFFFFFF0ull ? 0xFFFFFFF0u : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+
+#if defined(__HIP_DEVICE_COMPILE__)
+#define QM_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, QM_LDS_PTR(lds), 16, voff, 0, 0, 0);
+}
+// 2 bytes into the low half of lane i's 4-byte LDS word at lds + 4 i.
+__device__ __forceinline__ void dma2(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, QM_LDS_PTR(lds), 2, voff, 0, 0, 0);
+}
+#undef QM_LDS_PTR
+#else
+__device__ void dma16(__amdgpu_buffer_rsrc_t, void*, uint32_t);
+__device__ void dma2(__amdgpu_buffer_rsrc_t, void*, uint32_t);
+#endif
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 0xF) | ((N >> 4) << 14));
+}
+
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+// Sum over the 16 lanes of a DPP row (every lane of the row gets the sum).
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));  // row_ror:4
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
+  return v;
+}
+
+__host__ __device__ constexpr uint32_t job_blocks(uint32_t rows, uint32_t mode, int sb) {
+  return mode == kQ4OutSwiglu ? (rows + 3) / 4 : (rows + 4 * sb - 1) / (4 * sb);
+}
+// LDS bytes of one wave's scale/bias tables for `blocks` blocks: per block SB
+// loads of 4 rows, C chunk entries of 8 groups, for scales and for biases.
+// An entry is 16 bytes (8 bf16) when whole chunks tile each row (G % 8 == 0),
+// else 32 bytes: one 4-byte LDS word per group, fetched 2 bytes at a time so
+// no fetch crosses the end of a row.
+__host__ __device__ constexpr uint32_t entry_bytes(uint32_t G) { return G % 8 == 0 ? 16 : 32; }
+__host__ __device__ constexpr uint32_t table_bytes(uint32_t blocks, int sb, int c, uint32_t G) {
+  return blocks * sb * 4 * c * entry_bytes(G) * 2;
+}
+// LDS ahead of the tables: every wave's row partials [wave][block][4 SB].
+__host__ __device__ constexpr uint32_t head_bytes(uint32_t waves, int sb, uint32_t blocks) {
+  return waves * blocks * 4 * sb * 4;
+}
+
+// Byte offset, inside a job's tensor, of row `r` of load `s` of block `jb`
+// (block index local to the job).
+__device__ __forceinline__ uint32_t block_row(uint32_t mode, int sb, uint32_t jb, int s) {
+  return mode == kQ4OutSwiglu ? 4 * jb : (4 * sb) * jb + 4 * s;
+}
+
+template <int C, int SB, int RB>
+__global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int kPer = SB * C;     // loads per block per wave
+  constexpr int kD = kPer * RB;    // ring slots
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t W = args.waves;
+  const uint32_t K = args.K, G = args.G;
+  const uint32_t row_bytes = K >> 1;
+  const int col = lane & 15;
+  const int rr = lane >> 4;
+
+  // This workgroup's blocks.
+  const uint32_t g = blockIdx.x;
+  const uint32_t b_begin = (uint32_t)(((uint64_t)g * args.total_blocks) / args.wgs);
+  const uint32_t b_end = (uint32_t)(((uint64_t)(g + 1) * args.total_blocks) / args.wgs);
+  const uint32_t nblk = b_end - b_begin;
+
+  // LDS: partial slots, then each wave's tables.
+  const uint32_t rows_wg = args.max_blocks * 4 * SB;  // partial rows per wave
+  float* parts = (float*)smem;                        // [W][max_blocks * 4 SB]
+  const uint32_t es = entry_bytes(G);
+  const uint32_t tab_wave = table_bytes(args.max_blocks, SB, C, G);
+  uint8_t* tab = smem + head_bytes(W, SB, args.max_blocks) + wave * tab_wave;
+  uint8_t* tab_s = tab;
+  uint8_t* tab_b = tab + tab_wave / 2;
+
+  // Block -> job (blocks of a job are contiguous).
+  auto job_of = [&](uint32_t blk) __attribute__((always_inline)) {
+    int j = 0;
+    while (j + 1 < (int)args.n_jobs && blk >= args.jobs[j + 1].tile_begin) ++j;
+    return j;
+  };
+
+  // --- scale / bias tables of the workgroup's rows and this wave's chunks ----
+  // Entry e = ((s * nblk + jl) * 4 + r) * C + c holds 16 bytes: 8 groups of
+  // chunk c of row r of load s of local block jl.
+  const uint32_t c0 = (uint32_t)wave * C;  // first chunk of this wave
+  if (nblk > 0) {
+    uint32_t blk = b_begin;
+    while (blk < b_end) {
+      const int j = __builtin_amdgcn_readfirstlane(job_of(blk));
+      const Q4Job& jb = args.jobs[j];
+      const uint32_t job_end = j + 1 < (int)args.n_jobs ? args.jobs[j + 1].tile_begin : args.total_blocks;
+      const uint32_t seg_end = min(b_end, job_end);
+      const uint32_t nseg = seg_end - blk;
+#pragma unroll
+      for (int s = 0; s < SB; ++s) {
+        const bool up = jb.mode == kQ4OutSwiglu && s == 1;
+        const uint16_t* ts = up ? jb.us : jb.s;
+        const uint16_t* tb = up ? jb.ub : jb.b;
+        const uint32_t rows = jb.rows;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(ts, (uint64_t)rows * G * 2);
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(tb, (uint64_t)rows * G * 2);
+        const uint32_t e0 = ((s * nblk + (blk - b_begin)) * 4) * C;
+        const uint32_t n_e = nseg * 4 * C;
+        if (es == 16) {
+          for (uint32_t i = 0; i < n_e; i += 64) {
+            const uint32_t e = i + lane;
+            if (e < n_e) {
+              const uint32_t c = e % C, r = (e / C) % 4, jl = e / (C * 4);
+              const uint32_t row = block_row(jb.mode, SB, blk - jb.tile_begin + jl, s) + r;
+              const uint32_t gcol = (c0 + c) * 8;
+              const uint32_t off = (row < rows && gcol < G) ? (row * G + gcol) * 2 : kOOB;
+              dma16(rs, tab_s + (e0 + i) * 16, off);
+              dma16(rb, tab_b + (e0 + i) * 16, off);
+            }
+          }
+        } else {
+          // One group per lane (8 lanes per entry).
+          for (uint32_t i = 0; i < n_e * 8; i += 64) {
+            const uint32_t u = i + lane;
+            if (u < n_e * 8) {
+              const uint32_t e = u / 8, gi = u % 8;
+              const uint32_t c = e % C, r = (e / C) % 4, jl = e / (C * 4);
+              const uint32_t row = block_row(jb.mode, SB, blk - jb.tile_begin + jl, s) + r;
+              const uint32_t gcol = (c0 + c) * 8 + gi;
+              const uint32_t off = (row < rows && gcol < G) ? (row * G + gcol) * 2 : kOOB;
+              dma2(rs, tab_s + e0 * 32 + i * 4, off);
+              dma2(rb, tab_b + e0 * 32 + i * 4, off);
+            }
+          }
+        }
+      }
+      blk = seg_end;
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);  // the tables are issued before everything else
+
+  // --- activation chunks in registers ----------------------------------------
+  // Lane (col) holds elements [chunk*512 + 32 col, +32), each 8-element run in
+  // the unpack order (x0,x4)(x1,x5)(x2,x6)(x3,x7).
+  u32x4 xr[C][4];
+  float xsum[C];
+  bool valid[C];
+  {
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(args.x, (uint64_t)K * 2);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const uint32_t e0 = (c0 + c) * kChunkElems + 32 * col;
+      valid[c] = c0 + c < args.chunks && e0 < K;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        xr[c][q] = __builtin_amdgcn_raw_buffer_load_b128(rx, valid[c] ? e0 * 2 + 16 * q : kOOB, 0, 0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // --- weight ring -------------------------------------------------------------
+  // Slot t of a round: local block jl = t / kPer, load s = (t / C) % SB, chunk
+  // c = t % C.  voff[c]: this lane's byte offset inside a 4-row load.
+  uint32_t voff[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) voff[c] = (c0 + c < args.chunks) ? rr * row_bytes + (c0 + c) * 256 + 16 * col : kOOB;
+
+  // The job of the next block to load (blocks are loaded in increasing
+  // order): its fields stay in scalar registers until the cursor passes the
+  // job's last block, so a load needs no kernel-argument reads.
+  int cj = __builtin_amdgcn_readfirstlane(job_of(b_begin));
+  uint32_t cj_begin = 0, cj_end = 0, c_rows = 0, c_mode = 0;
+  const uint32_t* c_w = nullptr;
+  const uint32_t* c_uw = nullptr;
+  auto set_job = [&]() __attribute__((always_inline)) {
+    const Q4Job& jb = args.jobs[cj];
+    cj_begin = jb.tile_begin;
+    cj_end = cj + 1 < (int)args.n_jobs ? args.jobs[cj + 1].tile_begin : args.total_blocks;
+    c_rows = jb.rows;
+    c_mode = jb.mode;
+    c_w = jb.w;
+    c_uw = jb.uw;
+  };
+  set_job();
+  auto load_w = [&](uint32_t jl, int s, int c) __attribute__((always_inline)) {
+    // jl: local block (dead past nblk: no bytes)
+    const uint32_t blk = b_begin + jl;
+    // Every job has at least one block, so one step moves at most one job on.
+    if (jl < nblk && blk >= cj_end) {
+      ++cj;
+      set_job();
+    }
+    // Branch-free (selects only), so the load stays in one basic block.
+    const bool live = (jl < nblk) & (b_begin + jl - cj_begin < (1u << 30));
+    const bool up = (c_mode == kQ4OutSwiglu) & (s == 1);
+    const uint32_t* w = up ? c_uw : c_w;
+    const uint32_t base_row = live ? block_row(c_mode, SB, blk - cj_begin, s) : 0;
+    const uint32_t left = (live & (base_row < c_rows)) ? c_rows - base_row : 0;
+    const uint32_t avail = left >= 0xFFFFFFF0u / row_bytes ? 0xFFFFFFF0u : left * row_bytes;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(w + (size_t)base_row * (row_bytes / 4)), (short)0, (int)avail, 0x00020000);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff[c], 0, kNonTemporal);
+  };
+
+  u32x4 ring[kD];
+  const uint32_t nrounds = (nblk + RB - 1) / RB;
+#pragma unroll
+  for (int t = 0; t < kD; ++t) {
+    ring[t] = load_w(t / kPer, (t / C) % SB, t % C);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // Tables (issued first) have landed once at most the ring and the
+  // activation loads are outstanding.
+  wait_vmcnt<(kD + 4 * C < 63 ? kD + 4 * C : 63)>();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xr[c][q] = interleave_bf16x8(xr[c][q]);
+    float sum = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      sum += bf16_to_f32(xr[c][q].x & 0xFFFF) + bf16_to_f32(xr[c][q].x >> 16);
+      sum += bf16_to_f32(xr[c][q].y & 0xFFFF) + bf16_to_f32(xr[c][q].y >> 16);
+      sum += bf16_to_f32(xr[c][q].z & 0xFFFF) + bf16_to_f32(xr[c][q].z >> 16);
+      sum += bf16_to_f32(xr[c][q].w & 0xFFFF) + bf16_to_f32(xr[c][q].w >> 16);
+    }
+    xsum[c] = sum;
+  }
+
+  const uint32_t mask_s = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+  uint32_t or_v = 0x43004300u;
+  asm volatile("" : "+v"(or_v));
+
+  // One slot: the lane's contribution s*p + (b - 128 s)*X for its row/chunk.
+  auto consume = [&](const u32x4& wv, uint32_t jl, int s, int c) __attribute__((always_inline)) {
+    const uint32_t e = ((s * nblk + jl) * 4 + rr) * C + c;
+    const uint32_t toff = es == 16 ? e * 16 + (col >> 1) * 2 : e * 32 + (col >> 1) * 4;
+    const float sc = bf16_to_f32(*(const uint16_t*)(tab_s + toff));
+    const float bi = bf16_to_f32(*(const uint16_t*)(tab_b + toff));
+    float p0 = 0.f, p1 = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t wq = q == 0 ? wv.x : q == 1 ? wv.y : q == 2 ? wv.z : wv.w;
+      const u32x4 xq = xr[c][q];
+      p0 = dot2((wq & mask_s) | or_v, xq.x, p0);
+      p1 = dot2(((wq >> 4) & mask_s) | or_v, xq.y, p1);
+      p0 = dot2(((wq >> 8) & mask_s) | or_v, xq.z, p0);
+      p1 = dot2(((wq >> 12) & mask_s) | or_v, xq.w, p1);
+    }
+    const float v = fmaf(sc, p0 + p1, fmaf(-128.0f, sc, bi) * xsum[c]);
+    return valid[c] ? v : 0.0f;
+  };
+
+  // A finished block: each row's sum over this wave's chunks (the 16 lanes of
+  // the row) goes to the wave's partial row; the waves' partials are added
+  // in wave order after the stream (deterministic, no synchronisation here).
+  auto finish_block = [&](uint32_t jl, const float (&acc)[SB]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < SB; ++s) {
+      const float v = row16_sum(acc[s]);
+      if (col == 0) parts[wave * rows_wg + jl * 4 * SB + s * 4 + rr] = v;
+    }
+  };
+
+  auto round = [&](uint32_t r, bool refill) __attribute__((always_inline)) {
+#pragma unroll
+    for (int bi = 0; bi < RB; ++bi) {
+      const uint32_t jl = r * RB + bi;
+      float acc[SB];
+#pragma unroll
+      for (int s = 0; s < SB; ++s) acc[s] = 0.f;
+#pragma unroll
+      for (int s = 0; s < SB; ++s)
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          const int t = bi * kPer + s * C + c;
+          acc[s] += consume(ring[t], jl, s, c);
+          if (refill) {
+            // The slot's math is done before its refill is issued (an IR-level
+            // barrier too, so the math is not sunk below the load, which would
+            // keep both register sets alive and copy the ring every round).
+            asm volatile("" : "+v"(acc[s]) : : "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            ring[t] = load_w(jl + RB, s, c);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      if (jl < nblk) finish_block(jl, acc);
+    }
+  };
+  if (nrounds > 0) {
+    uint32_t r = 0;
+    for (; r + 1 < nrounds; ++r) round(r, true);
+    round(r, false);
+  }
+
+  // --- outputs -----------------------------------------------------------------
+  lds_barrier();
+  const uint32_t rows_per_block = 4 * SB;
+  auto row_sum = [&](uint32_t i) __attribute__((always_inline)) {
+    float v = 0.f;
+    for (uint32_t w2 = 0; w2 < W; ++w2) v += parts[w2 * rows_wg + i];
+    return v;
+  };
+  unsigned long long best = 0;  // argmax key of this thread's rows
+  for (uint32_t i = threadIdx.x; i < nblk * rows_per_block; i += blockDim.x) {
+    const uint32_t jl = i / rows_per_block, k = i % rows_per_block;
+    const uint32_t blk = b_begin + jl;
+    const int j = job_of(blk);
+    const Q4Job& jb = args.jobs[j];
+    const uint32_t lb = blk - jb.tile_begin;
+    if (jb.mode == kQ4OutSwiglu) {
+      // k < 4: gate sums; k >= 4: the up sums of the same rows.
+      const uint32_t row = 4 * lb + k;
+      if (k < 4 && row < jb.rows) {
+        const float gsum = row_sum(jl * rows_per_block + k), usum = row_sum(jl * rows_per_block + 4 + k);
+        jb.out[row] = f32_to_bf16(silu_f(gsum) * usum);
+      }
+      continue;
+    }
+    const uint32_t row = rows_per_block * lb + k;
+    if (row >= jb.rows) continue;
+    const float v = row_sum(i);
+    if (jb.mode == kQ4OutArgmax) {
+      if (!__builtin_isnan(v)) {
+        const uint32_t bits = v == 0.0f ? 0u : __float_as_uint(v);
+        const uint32_t ord = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+        const unsigned long long key = ((unsigned long long)ord << 32) | (0xFFFFFFFFu - row);
+        best = key > best ? key : best;
+      }
+      continue;
+    }
+    const uint16_t h = f32_to_bf16(v);
+    if (jb.mode == kQ4OutBf16)
+      jb.out[row] = h;
+    else if (jb.mode == kQ4OutF32)
+      ((float*)jb.out)[row] = bf16_to_f32(h);
+    else
+      ((float*)jb.out)[row] += bf16_to_f32(h);
+  }
+  if (args.jobs[0].mode == kQ4OutArgmax) {
+    // One atomic per wave: the best key of its threads' rows.
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const unsigned long long o = __shfl_xor(best, off);
+      best = o > best ? o : best;
+    }
+    if (lane == 0 && best) atomicMax((unsigned long long*)args.jobs[0].out, best);
+  }
+}
+
+template <int C, int SB>
+const void* kernel_for() {
+  constexpr int kRB = (8 / (SB * C)) > 1 ? 8 / (SB * C) : 1;
+  return (const void*)q4_stream_kernel<C, SB, kRB>;
+}
+const void* pick_kernel(int c, int sb) {
+  switch (c) {
+    case 1: return sb == 2 ? kernel_for<1, 2>() : kernel_for<1, 1>();
+    case 2: return sb == 2 ? kernel_for<2, 2>() : kernel_for<2, 1>();
+    default: return sb == 2 ? nullptr : kernel_for<3, 1>();
+  }
+}
+
+struct StreamPlan {
+  const void* fn = nullptr;
+  uint32_t waves = 0, C = 0, SB = 0, wgs = 0, max_blocks = 0, lds = 0, total_blocks = 0;
+};
+
+StreamPlan make_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const Tuning& tn) {
+  StreamPlan p{};
+  const uint32_t chunks = (K + kChunkElems - 1) / kChunkElems;
+  p.C = (chunks + kMaxWaves - 1) / kMaxWaves;
+  if (p.C > 3) return p;  // K > 24576: not this kernel
+  p.waves = (chunks + p.C - 1) / p.C;
+  bool pair = false;
+  for (int i = 0; i < n_jobs; ++i) pair |= jobs[i].mode == kQ4OutSwiglu;
+  p.SB = pair ? 2 : 1;
+  for (int i = 0; i < n_jobs; ++i) p.total_blocks += job_blocks(jobs[i].rows, jobs[i].mode, p.SB);
+  p.fn = pick_kernel((int)p.C, (int)p.SB);
+  if (!p.fn) return p;
+  const uint32_t cus = tn.cus > 0 ? (uint32_t)tn.cus : 256;
+  // Workgroups: as many as stay resident (one dispatch round), at least one
+  // block each; more when the tables of a workgroup's blocks would not fit.
+  const uint32_t lds_cu = 160 * 1024;
+  uint32_t wgs = std::min<uint32_t>(p.total_blocks, cus * 4);
+  for (;;) {
+    const uint32_t mb = (p.total_blocks + wgs - 1) / wgs;
+    const uint32_t lds = head_bytes(p.waves, p.SB, mb) + p.waves * table_bytes(mb, p.SB, p.C, K / 64);
+    int occ = 0;
+    if (lds <= 64 * 1024 &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, p.fn, (int)(64 * p.waves), lds) == hipSuccess && occ > 0) {
+      const uint32_t resident = (uint32_t)occ * cus;
+      if (wgs <= resident || mb <= 1) {
+        p.wgs = wgs;
+        p.max_blocks = mb;
+        p.lds = lds;
+        break;
+      }
+      // Fewer workgroups than resident slots would leave CUs idle: grow the
+      // per-workgroup share only while it still fits.
+      const uint32_t mb2 = (p.total_blocks + resident - 1) / resident;
+      const uint32_t lds2 = head_bytes(p.waves, p.SB, mb2) + p.waves * table_bytes(mb2, p.SB, p.C, K / 64);
+      if (lds2 <= 64 * 1024 && resident < wgs) {
+        wgs = resident;
+        continue;
+      }
+      p.wgs = wgs;
+      p.max_blocks = mb;
+      p.lds = lds;
+      break;
+    }
+    // Tables too large for one workgroup: more, smaller workgroups.
+    wgs = std::min<uint32_t>(p.total_blocks, wgs * 2);
+    if (wgs == p.total_blocks && lds > 64 * 1024) {
+      p.fn = nullptr;
+      return p;
+    }
+  }
+  if (tn.q4_plan_log > 0)
+    fprintf(stderr, "q4 stream plan: K=%u jobs=%d blocks=%u C=%u SB=%u waves=%u wgs=%u max_blocks=%u lds=%u\n", K,
+            n_jobs, p.total_blocks, p.C, p.SB, p.waves, p.wgs, p.max_blocks, p.lds);
+  return p;
+}
+
+struct StreamKey {
+  uint32_t rows[kMaxQ4Jobs], modes[kMaxQ4Jobs];
+  int n_jobs;
+  uint32_t K;
+  Tuning tune;
+  bool operator==(const StreamKey& o) const { return std::memcmp(this, &o, sizeof(*this)) == 0; }
+};
+
+StreamPlan cached_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const Tuning& tn) {
+  static std::mutex mu;
+  static StreamKey keys[16];
+  static StreamPlan plans[16];
+  static int used = 0, next = 0;
+  StreamKey k;
+  std::memset(&k, 0, sizeof(k));
+  for (int i = 0; i < n_jobs; ++i) {
+    k.rows[i] = jobs[i].rows;
+    k.modes[i] = jobs[i].mode == kQ4OutSwiglu ? 1 : 0;
+  }
+  k.n_jobs = n_jobs;
+  k.K = K;
+  k.tune = tn;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < used; ++i)
+    if (keys[i] == k) return plans[i];
+  const StreamPlan p = make_stream_plan(jobs, n_jobs, K, tn);
+  keys[next] = k;
+  plans[next] = p;
+  next = (next + 1) % 16;
+  used = std::min(used + 1, 16);
+  return p;
+}
+
+}  // namespace
+
+bool q4_stream_supported(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn) {
+  if (M != 1 || tn.q4_stream == 0) return false;
+  // Register budget: up to 3 activation chunks per wave for plain jobs, 2
+  // with gate/up pairs (K <= 24576 / 16384).
+  const uint32_t chunks = (K + kChunkElems - 1) / kChunkElems;
+  const uint32_t C = (chunks + kMaxWaves - 1) / kMaxWaves;
+  bool pair = false;
+  for (int i = 0; i < n_jobs; ++i) {
+    if (jobs[i].mode > kQ4OutSwiglu) return false;
+    pair |= jobs[i].mode == kQ4OutSwiglu;
+  }
+  return C <= (pair ? 2u : 3u);
+}
+
+hipError_t launch_q4_stream(const Q4Job* jobs, int n_jobs, const uint16_t* x, uint32_t K, const Workspace& ws,
+                            hipStream_t stream) {
+  if (!ws.tune || n_jobs < 1 || n_jobs > kMaxQ4Jobs) return hipErrorInvalidValue;
+  const StreamPlan p = cached_stream_plan(jobs, n_jobs, K, *ws.tune);
+  if (!p.fn) return hipErrorInvalidValue;
+  StreamArgs a{};
+  a.x = x;
+  a.K = K;
+  a.G = K / 64;
+  a.chunks = (K + kChunkElems - 1) / kChunkElems;
+  a.waves = p.waves;
+  a.n_jobs = (uint32_t)n_jobs;
+  a.total_blocks = p.total_blocks;
+  a.wgs = p.wgs;
+  a.max_blocks = p.max_blocks;
+  uint32_t b = 0;
+  for (int i = 0; i < n_jobs; ++i) {
+    a.jobs[i] = jobs[i];
+    a.jobs[i].tile_begin = b;
+    b += job_blocks(jobs[i].rows, jobs[i].mode, (int)p.SB);
+  }
+  // An argmax launch carries one job (its keys are jobs[0].out).
+  if (n_jobs > 1)
+    for (int i = 0; i < n_jobs; ++i)
+      if (jobs[i].mode == kQ4OutArgmax) return hipErrorInvalidValue;
+  void* args[] = {&a};
+  const hipError_t e = hipLaunchKernel(p.fn, dim3(p.wgs), dim3(64 * p.waves), args, p.lds, stream);
+  return e != hipSuccess ? e : hipGetLastError();
+}
+
+}  // namespace qm

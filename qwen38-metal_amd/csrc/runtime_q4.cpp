@@ -105,8 +105,26 @@ qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const ui
   if (st == QM_OK && M > kDecodeMaxRows) st = ensure_xh(rt, q4_gemm_xh_bytes(K, M));
   if (st != QM_OK) return st;
   const Workspace ws = workspace(rt);
-  hipError_t e = M <= kDecodeMaxRows ? launch_q4_decode(jobs, n, swiglu, x, K, M, ws, rt->stream)
-                                     : launch_q4_gemm(jobs, n, swiglu, x, K, M, ws, rt->stream);
+  hipError_t e;
+  if (M == 1 && q4_stream_supported(jobs, n, K, M, rt->tune)) {
+    // One activation row: the streaming kernel, with a gate/up pair as one job.
+    Q4Job sj[kMaxQ4Jobs];
+    int ns = 0;
+    if (swiglu) {
+      sj[0] = jobs[0];
+      sj[0].uw = jobs[1].w;
+      sj[0].us = jobs[1].s;
+      sj[0].ub = jobs[1].b;
+      sj[0].mode = kQ4OutSwiglu;
+      ns = 1;
+    } else {
+      for (int i = 0; i < n; ++i) sj[ns++] = jobs[i];
+    }
+    e = launch_q4_stream(sj, ns, x, K, ws, rt->stream);
+  } else {
+    e = M <= kDecodeMaxRows ? launch_q4_decode(jobs, n, swiglu, x, K, M, ws, rt->stream)
+                            : launch_q4_gemm(jobs, n, swiglu, x, K, M, ws, rt->stream);
+  }
   return hip_check(e, what);
 }
 
@@ -164,6 +182,56 @@ qm_status qm_q4_project(qm_runtime* rt, const qm_q4_job* jobs, int n_jobs, const
     if ((st = check_range(rt, outputs[i], (uint64_t)M * jobs[i].out_rows * 2, "output")) != QM_OK) return st;
   }
   return launch(rt, q, n_jobs, false, x, in_elems, M, "Q4 projection launch");
+}
+
+qm_status qm_q4_project_set(qm_runtime* rt, const qm_q4_job* jobs, const qm_q4_job* const* ups, int n_jobs,
+                            const uint16_t* x, uint32_t in_elems, uint32_t M, uint16_t* const* outputs) {
+  if (!rt) return fail(QM_ERR_NULL_POINTER, "runtime is NULL");
+  if (!jobs || n_jobs <= 0) return fail(QM_ERR_EMPTY_DIMENSION, "at least one Q4 job is required");
+  if (n_jobs > kMaxQ4Jobs) return fail(QM_ERR_INVALID_ARGUMENT, "at most %d jobs per call", kMaxQ4Jobs);
+  if (!outputs) return fail(QM_ERR_NULL_POINTER, "outputs is NULL");
+  qm_status st = validate_x(x, M);
+  if (st != QM_OK) return st;
+  Q4Job q[kMaxQ4Jobs];
+  for (int i = 0; i < n_jobs; ++i) {
+    if ((st = validate_job(&jobs[i], in_elems, "Q4 projection")) != QM_OK) return st;
+    const qm_q4_job* up = ups ? ups[i] : nullptr;
+    if (up) {
+      if ((st = validate_job(up, in_elems, "up")) != QM_OK) return st;
+      if (up->out_rows != jobs[i].out_rows)
+        return fail(QM_ERR_WRONG_LENGTH, "up %d has %u rows, expected %u", i, up->out_rows, jobs[i].out_rows);
+    }
+    if (!outputs[i]) return fail(QM_ERR_NULL_POINTER, "output %d is NULL", i);
+    q[i] = to_job(jobs[i], outputs[i]);
+    if (up) {
+      q[i].uw = up->weights;
+      q[i].us = up->scales;
+      q[i].ub = up->biases;
+      q[i].mode = kQ4OutSwiglu;
+    }
+  }
+  DeviceGuard g(rt->device);
+  if (!g.ok()) return no_device();
+  if ((st = check_range(rt, x, (uint64_t)M * in_elems * 2, "activation")) != QM_OK) return st;
+  for (int i = 0; i < n_jobs; ++i) {
+    if ((st = check_job_ranges(rt, jobs[i], in_elems, "Q4 projection")) != QM_OK) return st;
+    if (ups && ups[i] && (st = check_job_ranges(rt, *ups[i], in_elems, "up")) != QM_OK) return st;
+    if ((st = check_range(rt, outputs[i], (uint64_t)M * jobs[i].out_rows * 2, "output")) != QM_OK) return st;
+  }
+  if (M == 1 && q4_stream_supported(q, n_jobs, in_elems, M, rt->tune))
+    return hip_check(launch_q4_stream(q, n_jobs, x, in_elems, workspace(rt), rt->stream), "Q4 set launch");
+  // Otherwise: the plain jobs in one launch, each pair in its own.
+  Q4Job plain[kMaxQ4Jobs];
+  int np = 0;
+  for (int i = 0; i < n_jobs; ++i)
+    if (q[i].mode != kQ4OutSwiglu) plain[np++] = q[i];
+  if (np && (st = launch(rt, plain, np, false, x, in_elems, M, "Q4 set launch")) != QM_OK) return st;
+  for (int i = 0; i < n_jobs; ++i) {
+    if (q[i].mode != kQ4OutSwiglu) continue;
+    Q4Job pair[2] = {to_job(jobs[i], outputs[i]), to_job(*ups[i], nullptr)};
+    if ((st = launch(rt, pair, 2, true, x, in_elems, M, "Q4 set pair launch")) != QM_OK) return st;
+  }
+  return QM_OK;
 }
 
 qm_status qm_q4_swiglu(qm_runtime* rt, const qm_q4_job* gate, const qm_q4_job* up, const uint16_t* x,
@@ -236,7 +304,9 @@ qm_status qm_q4_argmax(qm_runtime* rt, const qm_q4_job* job, const uint16_t* x, 
     const uint32_t mc = M - m0 < kDecodeMaxRows ? M - m0 : kDecodeMaxRows;
     Q4Job q = to_job(*job, (uint16_t*)keys);
     q.mode = kQ4OutArgmax;
-    hipError_t e = launch_q4_decode(&q, 1, false, x + (size_t)m0 * in_elems, in_elems, mc, ws, rt->stream);
+    hipError_t e = mc == 1 && q4_stream_supported(&q, 1, in_elems, 1, rt->tune)
+                       ? launch_q4_stream(&q, 1, x + (size_t)m0 * in_elems, in_elems, ws, rt->stream)
+                       : launch_q4_decode(&q, 1, false, x + (size_t)m0 * in_elems, in_elems, mc, ws, rt->stream);
     if (e == hipSuccess) e = launch_q4_argmax_finish(keys, ids + m0, mc, rt->stream);
     if ((st = hip_check(e, "Q4 argmax launch")) != QM_OK) return st;
   }

@@ -36,7 +36,7 @@ EXPORTS = [
     "qm_status_string", "qm_last_error_message",
     "qm_runtime_create", "qm_runtime_destroy", "qm_runtime_set_stream", "qm_runtime_synchronize",
     "qm_device_alloc", "qm_device_free", "qm_upload", "qm_copy_to_device", "qm_copy_to_host",
-    "qm_q4_project", "qm_q4_swiglu", "qm_q4_mlp", "qm_q4_argmax", "qm_q4_job_from_mapped",
+    "qm_q4_project", "qm_q4_project_set", "qm_q4_swiglu", "qm_q4_mlp", "qm_q4_argmax", "qm_q4_job_from_mapped",
     "qm_kv_create", "qm_kv_destroy", "qm_kv_length", "qm_kv_capacity", "qm_kv_allocated_pages", "qm_kv_page_for_token",
     "qm_kv_reserve", "qm_kv_truncate", "qm_kv_clone", "qm_kv_read",
     "qm_attn_decode", "qm_attn_decode_noalloc", "qm_attn_prefill", "qm_attn_prepare",
@@ -149,6 +149,8 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
         "qm_q4_project": ([vp, C.POINTER(Q4Job), i32, vp, u32, u32, C.POINTER(vp)], i32),
         "qm_q4_swiglu": ([vp, C.POINTER(Q4Job), C.POINTER(Q4Job), vp, u32, u32, vp], i32),
         "qm_q4_mlp": ([vp, C.POINTER(Q4Job), C.POINTER(Q4Job), C.POINTER(Q4Job), vp, u32, u32, vp], i32),
+        "qm_q4_project_set": ([vp, C.POINTER(Q4Job), C.POINTER(C.POINTER(Q4Job)), i32, vp, u32, u32,
+                               C.POINTER(vp)], i32),
         "qm_q4_argmax": ([vp, C.POINTER(Q4Job), vp, u32, u32, vp], i32),
         "qm_q4_job_from_mapped": ([C.POINTER(Q4MappedJob), u32, C.POINTER(Q4Job)], i32),
         "qm_kv_create": ([vp, u32, u32, u32, u32, C.POINTER(vp)], i32),
@@ -276,6 +278,13 @@ class Runtime:
         arr = (Q4Job * len(jobs))(*jobs)
         outs = (C.c_void_p * len(outputs))(*[_ptr(o) for o in outputs])
         _check(self.lib.qm_q4_project(self.handle, arr, len(jobs), _ptr(x), in_elems, M, outs))
+
+    def q4_project_set(self, jobs, ups, x, in_elems: int, M: int, outputs) -> None:
+        """jobs[j] plain (ups[j] None) or the gate of a SwiGLU pair with up ups[j]."""
+        arr = (Q4Job * len(jobs))(*jobs)
+        upp = (C.POINTER(Q4Job) * len(jobs))(*[C.pointer(u) if u is not None else None for u in ups])
+        outs = (C.c_void_p * len(outputs))(*[_ptr(o) for o in outputs])
+        _check(self.lib.qm_q4_project_set(self.handle, arr, upp, len(jobs), _ptr(x), in_elems, M, outs))
 
     def q4_swiglu(self, gate: Q4Job, up: Q4Job, x, in_elems: int, M: int, h) -> None:
         _check(self.lib.qm_q4_swiglu(self.handle, C.byref(gate), C.byref(up), _ptr(x), in_elems, M, _ptr(h)))
