@@ -26,7 +26,8 @@
 //    each row in wave order (deterministic) and stores the outputs; no global
 //    store is issued while weights are in flight.
 //  * Scales and biases of the workgroup's rows and the wave's chunks are
-//    staged once into LDS by buffer->LDS DMA before the weight stream starts.
+//    fetched once (ordinary loads issued before the weight stream) and kept
+//    in LDS.
 //  * Rows past a projection's end load zeros (buffer bounds) and are never
 //    stored; activation elements past K load zeros, and their lanes add 0.
 #include "common.h"
@@ -62,21 +63,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
 }
 
-#if defined(__HIP_DEVICE_COMPILE__)
-#define QM_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, QM_LDS_PTR(lds), 16, voff, 0, 0, 0);
-}
-// 2 bytes into the low half of lane i's 4-byte LDS word at lds + 4 i.
-__device__ __forceinline__ void dma2(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, QM_LDS_PTR(lds), 2, voff, 0, 0, 0);
-}
-#undef QM_LDS_PTR
-#else
-__device__ void dma16(__amdgpu_buffer_rsrc_t, void*, uint32_t);
-__device__ void dma2(__amdgpu_buffer_rsrc_t, void*, uint32_t);
-#endif
-
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -100,14 +86,15 @@ __device__ __forceinline__ float row16_sum(float v) {
 __host__ __device__ constexpr uint32_t job_blocks(uint32_t rows, uint32_t mode, int sb) {
   return mode == kQ4OutSwiglu ? (rows + 3) / 4 : (rows + 4 * sb - 1) / (4 * sb);
 }
-// LDS bytes of one wave's scale/bias tables for `blocks` blocks: per block SB
-// loads of 4 rows, C chunk entries of 8 groups, for scales and for biases.
-// An entry is 16 bytes (8 bf16) when whole chunks tile each row (G % 8 == 0),
-// else 32 bytes: one 4-byte LDS word per group, fetched 2 bytes at a time so
-// no fetch crosses the end of a row.
-__host__ __device__ constexpr uint32_t entry_bytes(uint32_t G) { return G % 8 == 0 ? 16 : 32; }
-__host__ __device__ constexpr uint32_t table_bytes(uint32_t blocks, int sb, int c, uint32_t G) {
-  return blocks * sb * 4 * c * entry_bytes(G) * 2;
+// Scale/bias table entries of one wave (16 bytes each: the 8 groups of one
+// chunk of one row): per block SB loads of 4 rows and C chunks.  A wave
+// fetches at most kTabEntries of them (kTabLoads loads per lane).
+constexpr int kTabLoads = 2;
+constexpr uint32_t kTabEntries = 64 * kTabLoads;
+__host__ __device__ constexpr uint32_t table_entries(uint32_t blocks, int sb, int c) { return blocks * sb * 4 * c; }
+// LDS bytes of one wave's tables: per entry 8 groups of (s, b - 128 s) as fp32.
+__host__ __device__ constexpr uint32_t table_bytes(uint32_t blocks, int sb, int c) {
+  return table_entries(blocks, sb, c) * 64;
 }
 // LDS ahead of the tables: every wave's row partials [wave][block][4 SB].
 __host__ __device__ constexpr uint32_t head_bytes(uint32_t waves, int sb, uint32_t blocks) {
@@ -142,11 +129,8 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
   // LDS: partial slots, then each wave's tables.
   const uint32_t rows_wg = args.max_blocks * 4 * SB;  // partial rows per wave
   float* parts = (float*)smem;                        // [W][max_blocks * 4 SB]
-  const uint32_t es = entry_bytes(G);
-  const uint32_t tab_wave = table_bytes(args.max_blocks, SB, C, G);
+  const uint32_t tab_wave = table_bytes(args.max_blocks, SB, C);
   uint8_t* tab = smem + head_bytes(W, SB, args.max_blocks) + wave * tab_wave;
-  uint8_t* tab_s = tab;
-  uint8_t* tab_b = tab + tab_wave / 2;
 
   // Block -> job (blocks of a job are contiguous).
   auto job_of = [&](uint32_t blk) __attribute__((always_inline)) {
@@ -157,55 +141,48 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
 
   // --- scale / bias tables of the workgroup's rows and this wave's chunks ----
   // Entry e = ((s * nblk + jl) * 4 + r) * C + c holds 16 bytes: 8 groups of
-  // chunk c of row r of load s of local block jl.
+  // chunk c of row r of load s of local block jl (n_e <= kTabEntries entries,
+  // the planner's limit).  They are fetched into VGPRs here, ahead of
+  // everything else, and written to the wave's LDS tables once the weight
+  // ring is in flight (buffer->LDS DMA of the same bytes measured ~4 us
+  // slower per launch).
   const uint32_t c0 = (uint32_t)wave * C;  // first chunk of this wave
-  if (nblk > 0) {
-    uint32_t blk = b_begin;
-    while (blk < b_end) {
-      const int j = __builtin_amdgcn_readfirstlane(job_of(blk));
-      const Q4Job& jb = args.jobs[j];
-      const uint32_t job_end = j + 1 < (int)args.n_jobs ? args.jobs[j + 1].tile_begin : args.total_blocks;
-      const uint32_t seg_end = min(b_end, job_end);
-      const uint32_t nseg = seg_end - blk;
+  const uint32_t n_e = SB * nblk * 4 * C;
+  u32x4 tsv[kTabLoads], tbv[kTabLoads];
 #pragma unroll
-      for (int s = 0; s < SB; ++s) {
-        const bool up = jb.mode == kQ4OutSwiglu && s == 1;
-        const uint16_t* ts = up ? jb.us : jb.s;
-        const uint16_t* tb = up ? jb.ub : jb.b;
-        const uint32_t rows = jb.rows;
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(ts, (uint64_t)rows * G * 2);
-        const __amdgpu_buffer_rsrc_t rb = make_rsrc(tb, (uint64_t)rows * G * 2);
-        const uint32_t e0 = ((s * nblk + (blk - b_begin)) * 4) * C;
-        const uint32_t n_e = nseg * 4 * C;
-        if (es == 16) {
-          for (uint32_t i = 0; i < n_e; i += 64) {
-            const uint32_t e = i + lane;
-            if (e < n_e) {
-              const uint32_t c = e % C, r = (e / C) % 4, jl = e / (C * 4);
-              const uint32_t row = block_row(jb.mode, SB, blk - jb.tile_begin + jl, s) + r;
-              const uint32_t gcol = (c0 + c) * 8;
-              const uint32_t off = (row < rows && gcol < G) ? (row * G + gcol) * 2 : kOOB;
-              dma16(rs, tab_s + (e0 + i) * 16, off);
-              dma16(rb, tab_b + (e0 + i) * 16, off);
-            }
+  for (int i = 0; i < kTabLoads; ++i) {
+    const uint32_t e = i * 64 + lane;
+    tsv[i] = u32x4{0u, 0u, 0u, 0u};
+    tbv[i] = u32x4{0u, 0u, 0u, 0u};
+    if (e < n_e) {
+      const uint32_t c = e % C, r = (e / C) % 4, t = e / (4 * C);
+      const uint32_t sub = t / nblk, jl = t % nblk;
+      const uint32_t blk = b_begin + jl;
+      const Q4Job& jb = args.jobs[job_of(blk)];
+      const bool up = jb.mode == kQ4OutSwiglu && sub == 1;
+      const uint16_t* ts = up ? jb.us : jb.s;
+      const uint16_t* tb = up ? jb.ub : jb.b;
+      const uint32_t row = block_row(jb.mode, SB, blk - jb.tile_begin, (int)sub) + r;
+      const uint32_t gcol = (c0 + c) * 8;
+      if (row < jb.rows && gcol < G) {
+        const size_t idx = (size_t)row * G + gcol;
+        if (G % 8 == 0) {  // 16-byte aligned: the entry is 8 whole groups of one row
+          tsv[i] = *(const u32x4*)(ts + idx);
+          tbv[i] = *(const u32x4*)(tb + idx);
+        } else {  // a row's last chunk is partial: element by element, within the row
+          uint16_t sv[8], bv[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const bool in = gcol + q < G;
+            sv[q] = in ? ts[idx + q] : (uint16_t)0;
+            bv[q] = in ? tb[idx + q] : (uint16_t)0;
           }
-        } else {
-          // One group per lane (8 lanes per entry).
-          for (uint32_t i = 0; i < n_e * 8; i += 64) {
-            const uint32_t u = i + lane;
-            if (u < n_e * 8) {
-              const uint32_t e = u / 8, gi = u % 8;
-              const uint32_t c = e % C, r = (e / C) % 4, jl = e / (C * 4);
-              const uint32_t row = block_row(jb.mode, SB, blk - jb.tile_begin + jl, s) + r;
-              const uint32_t gcol = (c0 + c) * 8 + gi;
-              const uint32_t off = (row < rows && gcol < G) ? (row * G + gcol) * 2 : kOOB;
-              dma2(rs, tab_s + e0 * 32 + i * 4, off);
-              dma2(rb, tab_b + e0 * 32 + i * 4, off);
-            }
-          }
+          tsv[i] = u32x4{sv[0] | (uint32_t)sv[1] << 16, sv[2] | (uint32_t)sv[3] << 16, sv[4] | (uint32_t)sv[5] << 16,
+                         sv[6] | (uint32_t)sv[7] << 16};
+          tbv[i] = u32x4{bv[0] | (uint32_t)bv[1] << 16, bv[2] | (uint32_t)bv[3] << 16, bv[4] | (uint32_t)bv[5] << 16,
+                         bv[6] | (uint32_t)bv[7] << 16};
         }
       }
-      blk = seg_end;
     }
   }
   __builtin_amdgcn_sched_barrier(0);  // the tables are issued before everything else
@@ -280,10 +257,23 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
     ring[t] = load_w(t / kPer, (t / C) % SB, t % C);
     __builtin_amdgcn_sched_barrier(0);
   }
-  // Tables (issued first) have landed once at most the ring and the
-  // activation loads are outstanding.
-  wait_vmcnt<(kD + 4 * C < 63 ? kD + 4 * C : 63)>();
-  __builtin_amdgcn_sched_barrier(0);
+  // Tables into LDS (their loads were issued first): per group the fp32
+  // pair (s, b - 128 s) that a lane's contribution needs.
+#pragma unroll
+  for (int i = 0; i < kTabLoads; ++i) {
+    const uint32_t e = i * 64 + lane;
+    if (e < n_e) {
+      float* te = (float*)(tab + e * 64);
+      const uint32_t sw[4] = {tsv[i].x, tsv[i].y, tsv[i].z, tsv[i].w};
+      const uint32_t bw[4] = {tbv[i].x, tbv[i].y, tbv[i].z, tbv[i].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float s0 = bf16_to_f32(sw[q] & 0xFFFF), s1 = bf16_to_f32(sw[q] >> 16);
+        const float b0 = bf16_to_f32(bw[q] & 0xFFFF), b1 = bf16_to_f32(bw[q] >> 16);
+        *(floatx4*)(te + 4 * q) = floatx4{s0, fmaf(-128.0f, s0, b0), s1, fmaf(-128.0f, s1, b1)};
+      }
+    }
+  }
 #pragma unroll
   for (int c = 0; c < C; ++c) {
 #pragma unroll
@@ -304,11 +294,12 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
   asm volatile("" : "+v"(or_v));
 
   // One slot: the lane's contribution s*p + (b - 128 s)*X for its row/chunk.
+  // Lanes past K see x = 0, X = 0 and a zero table entry: they add 0.
+  const uint32_t tlane = rr * C * 64 + (col >> 1) * 8;
   auto consume = [&](const u32x4& wv, uint32_t jl, int s, int c) __attribute__((always_inline)) {
-    const uint32_t e = ((s * nblk + jl) * 4 + rr) * C + c;
-    const uint32_t toff = es == 16 ? e * 16 + (col >> 1) * 2 : e * 32 + (col >> 1) * 4;
-    const float sc = bf16_to_f32(*(const uint16_t*)(tab_s + toff));
-    const float bi = bf16_to_f32(*(const uint16_t*)(tab_b + toff));
+    const uint32_t e0 = ((s * nblk + jl) * 4) * C + c;  // entry of row 0 of the load
+    const u32x2 tv = *(const u32x2*)(tab + e0 * 64 + tlane);
+    const float sc = __uint_as_float(tv.x), cb = __uint_as_float(tv.y);
     float p0 = 0.f, p1 = 0.f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -319,8 +310,7 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
       p0 = dot2(((wq >> 8) & mask_s) | or_v, xq.z, p0);
       p1 = dot2(((wq >> 12) & mask_s) | or_v, xq.w, p1);
     }
-    const float v = fmaf(sc, p0 + p1, fmaf(-128.0f, sc, bi) * xsum[c]);
-    return valid[c] ? v : 0.0f;
+    return fmaf(sc, p0 + p1, cb * xsum[c]);
   };
 
   // A finished block: each row's sum over this wave's chunks (the 16 lanes of
@@ -443,6 +433,10 @@ StreamPlan make_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const Tun
   StreamPlan p{};
   const uint32_t chunks = (K + kChunkElems - 1) / kChunkElems;
   p.C = (chunks + kMaxWaves - 1) / kMaxWaves;
+  // Two chunks per wave even when one would do: half the waves per
+  // workgroup, more workgroups per CU and each block's per-row work over
+  // twice the bytes (measured: QKV + gate/up set 32 -> 28 us).
+  if (p.C == 1 && chunks > 1) p.C = 2;
   if (p.C > 3) return p;  // K > 24576: not this kernel
   p.waves = (chunks + p.C - 1) / p.C;
   bool pair = false;
@@ -452,43 +446,21 @@ StreamPlan make_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const Tun
   p.fn = pick_kernel((int)p.C, (int)p.SB);
   if (!p.fn) return p;
   const uint32_t cus = tn.cus > 0 ? (uint32_t)tn.cus : 256;
-  // Workgroups: as many as stay resident (one dispatch round), at least one
-  // block each; more when the tables of a workgroup's blocks would not fit.
-  const uint32_t lds_cu = 160 * 1024;
-  uint32_t wgs = std::min<uint32_t>(p.total_blocks, cus * 4);
-  for (;;) {
-    const uint32_t mb = (p.total_blocks + wgs - 1) / wgs;
-    const uint32_t lds = head_bytes(p.waves, p.SB, mb) + p.waves * table_bytes(mb, p.SB, p.C, K / 64);
-    int occ = 0;
-    if (lds <= 64 * 1024 &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, p.fn, (int)(64 * p.waves), lds) == hipSuccess && occ > 0) {
-      const uint32_t resident = (uint32_t)occ * cus;
-      if (wgs <= resident || mb <= 1) {
-        p.wgs = wgs;
-        p.max_blocks = mb;
-        p.lds = lds;
-        break;
-      }
-      // Fewer workgroups than resident slots would leave CUs idle: grow the
-      // per-workgroup share only while it still fits.
-      const uint32_t mb2 = (p.total_blocks + resident - 1) / resident;
-      const uint32_t lds2 = head_bytes(p.waves, p.SB, mb2) + p.waves * table_bytes(mb2, p.SB, p.C, K / 64);
-      if (lds2 <= 64 * 1024 && resident < wgs) {
-        wgs = resident;
-        continue;
-      }
-      p.wgs = wgs;
-      p.max_blocks = mb;
-      p.lds = lds;
-      break;
-    }
-    // Tables too large for one workgroup: more, smaller workgroups.
-    wgs = std::min<uint32_t>(p.total_blocks, wgs * 2);
-    if (wgs == p.total_blocks && lds > 64 * 1024) {
-      p.fn = nullptr;
-      return p;
-    }
+  // Workgroups: as many as stay resident (one dispatch round), with at most
+  // `cap` blocks each (the table entries a wave fetches); more workgroups,
+  // in several rounds, only when the blocks exceed resident * cap.
+  const uint32_t cap = kTabEntries / table_entries(1, (int)p.SB, (int)p.C);
+  const uint32_t lds_cap = head_bytes(p.waves, p.SB, cap) + p.waves * table_bytes(cap, p.SB, p.C);
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, p.fn, (int)(64 * p.waves), lds_cap) != hipSuccess || occ <= 0) {
+    p.fn = nullptr;
+    return p;
   }
+  const uint32_t resident = (uint32_t)occ * cus;
+  const uint32_t wgs_min = (p.total_blocks + cap - 1) / cap;
+  p.wgs = std::max(wgs_min, std::min(p.total_blocks, resident));
+  p.max_blocks = (p.total_blocks + p.wgs - 1) / p.wgs;
+  p.lds = head_bytes(p.waves, p.SB, p.max_blocks) + p.waves * table_bytes(p.max_blocks, p.SB, p.C);
   if (tn.q4_plan_log > 0)
     fprintf(stderr, "q4 stream plan: K=%u jobs=%d blocks=%u C=%u SB=%u waves=%u wgs=%u max_blocks=%u lds=%u\n", K,
             n_jobs, p.total_blocks, p.C, p.SB, p.waves, p.wgs, p.max_blocks, p.lds);
