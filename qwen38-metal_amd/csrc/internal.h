@@ -80,6 +80,10 @@ hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const ui
 bool q4_stream_supported(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn);
 hipError_t launch_q4_stream(const Q4Job* jobs, int n_jobs, const uint16_t* x, uint32_t K, const Workspace& ws,
                             hipStream_t stream);
+// Workspace of a streaming launch: fp32 partial rows and counters when K is
+// split over several workgroups (zero otherwise).
+void q4_stream_workspace(const Q4Job* jobs, int n_jobs, uint32_t K, const Tuning& tn, size_t* partial_bytes,
+                         size_t* counters);
 
 // ids[m] from the argmax keys of a kQ4OutArgmax decode launch; zeroes the keys.
 hipError_t launch_q4_argmax_finish(unsigned long long* keys, uint32_t* ids, uint32_t M, hipStream_t stream);

@@ -53,8 +53,16 @@ struct StreamArgs {
   uint32_t waves;         // W: waves per workgroup
   uint32_t n_jobs;
   uint32_t total_blocks;  // blocks of all jobs
-  uint32_t wgs;           // workgroups; workgroup g owns blocks [g*B/wgs, (g+1)*B/wgs)
+  uint32_t wgs;           // workgroups per K part; workgroup g owns blocks [g*B/wgs, (g+1)*B/wgs)
   uint32_t max_blocks;    // largest block count of one workgroup (LDS sizing)
+  // K parts: workgroup p * wgs + g covers chunks [p * part_chunks, +part_chunks)
+  // of the same blocks as workgroup g.  With parts > 1 each writes its fp32
+  // row sums to partials[p][block row], and the last of the parts of a block
+  // range to finish (counters[g], zero between launches) adds them in part
+  // order and stores the outputs.
+  uint32_t parts, part_chunks;
+  float* partials;
+  unsigned* counters;
   Q4Job jobs[kMaxQ4Jobs];  // tile_begin = first block of the job
 };
 
@@ -120,8 +128,9 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
   const int col = lane & 15;
   const int rr = lane >> 4;
 
-  // This workgroup's blocks.
-  const uint32_t g = blockIdx.x;
+  // This workgroup's K part and blocks.
+  const uint32_t part = blockIdx.x / args.wgs;
+  const uint32_t g = blockIdx.x - part * args.wgs;
   const uint32_t b_begin = (uint32_t)(((uint64_t)g * args.total_blocks) / args.wgs);
   const uint32_t b_end = (uint32_t)(((uint64_t)(g + 1) * args.total_blocks) / args.wgs);
   const uint32_t nblk = b_end - b_begin;
@@ -146,7 +155,7 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
   // everything else, and written to the wave's LDS tables once the weight
   // ring is in flight (buffer->LDS DMA of the same bytes measured ~4 us
   // slower per launch).
-  const uint32_t c0 = (uint32_t)wave * C;  // first chunk of this wave
+  const uint32_t c0 = part * args.part_chunks + (uint32_t)wave * C;  // first chunk of this wave
   const uint32_t n_e = SB * nblk * 4 * C;
   u32x4 tsv[kTabLoads], tbv[kTabLoads];
 #pragma unroll
@@ -359,13 +368,49 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
   // --- outputs -----------------------------------------------------------------
   lds_barrier();
   const uint32_t rows_per_block = 4 * SB;
+  const uint32_t nrows = nblk * rows_per_block;
+  // The workgroup's row i (local block i / 4SB, row i % 4SB) over this
+  // workgroup's chunks: its waves' partials in wave order.
   auto row_sum = [&](uint32_t i) __attribute__((always_inline)) {
     float v = 0.f;
     for (uint32_t w2 = 0; w2 < W; ++w2) v += parts[w2 * rows_wg + i];
     return v;
   };
+  const uint32_t TB = args.total_blocks * rows_per_block;  // partial rows per K part
+  float* pp = args.partials + (size_t)b_begin * rows_per_block;
+  // Row i over all K parts, in part order (the same sum whichever part
+  // finishes last).
+  // The partial rows and the counter are accessed as device-scope relaxed
+  // atomics: each access is coherent across the XCDs' L2 caches by itself,
+  // with no whole-cache write-back or invalidate (acquire/release fences at
+  // device scope cost ~30 us over a launch of 768 workgroups).  The counter
+  // is bumped only after the barrier, by which point every wave's partial
+  // stores have completed.
+  auto part_sum = [&](uint32_t i) __attribute__((always_inline)) {
+    float v = 0.f;
+    for (uint32_t q = 0; q < args.parts; ++q)
+      v += __hip_atomic_load(&pp[(size_t)q * TB + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return v;
+  };
+  if (args.parts > 1) {
+    for (uint32_t i = threadIdx.x; i < nrows; i += blockDim.x)
+      __hip_atomic_store(&pp[(size_t)part * TB + i], row_sum(i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
+    __syncthreads();
+    __shared__ uint32_t last;
+    if (threadIdx.x == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(&args.counters[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = old == args.parts - 1;
+      if (last) __hip_atomic_store(&args.counters[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+  }
+  auto value = [&](uint32_t i) __attribute__((always_inline)) {
+    return args.parts > 1 ? part_sum(i) : row_sum(i);
+  };
   unsigned long long best = 0;  // argmax key of this thread's rows
-  for (uint32_t i = threadIdx.x; i < nblk * rows_per_block; i += blockDim.x) {
+  for (uint32_t i = threadIdx.x; i < nrows; i += blockDim.x) {
     const uint32_t jl = i / rows_per_block, k = i % rows_per_block;
     const uint32_t blk = b_begin + jl;
     const int j = job_of(blk);
@@ -375,14 +420,14 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
       // k < 4: gate sums; k >= 4: the up sums of the same rows.
       const uint32_t row = 4 * lb + k;
       if (k < 4 && row < jb.rows) {
-        const float gsum = row_sum(jl * rows_per_block + k), usum = row_sum(jl * rows_per_block + 4 + k);
+        const float gsum = value(jl * rows_per_block + k), usum = value(jl * rows_per_block + 4 + k);
         jb.out[row] = f32_to_bf16(silu_f(gsum) * usum);
       }
       continue;
     }
     const uint32_t row = rows_per_block * lb + k;
     if (row >= jb.rows) continue;
-    const float v = row_sum(i);
+    const float v = value(i);
     if (jb.mode == kQ4OutArgmax) {
       if (!__builtin_isnan(v)) {
         const uint32_t bits = v == 0.0f ? 0u : __float_as_uint(v);
@@ -417,34 +462,49 @@ const void* kernel_for() {
   return (const void*)q4_stream_kernel<C, SB, kRB>;
 }
 const void* pick_kernel(int c, int sb) {
-  switch (c) {
-    case 1: return sb == 2 ? kernel_for<1, 2>() : kernel_for<1, 1>();
-    case 2: return sb == 2 ? kernel_for<2, 2>() : kernel_for<2, 1>();
-    default: return sb == 2 ? nullptr : kernel_for<3, 1>();
-  }
+  if (c == 1) return sb == 2 ? kernel_for<1, 2>() : kernel_for<1, 1>();
+  if (c == 2) return sb == 2 ? kernel_for<2, 2>() : kernel_for<2, 1>();
+  return sb == 1 ? kernel_for<3, 1>() : nullptr;
 }
+
+// One K part: up to 16 waves of 2 chunks (K <= 16384), or for plain jobs of
+// 3 chunks (K <= 24576; measured on the 17408-wide down projection: 13 us
+// against 17 us split in parts).  Longer K runs in parts of 5 waves of 2
+// chunks whose fp32 row sums the last part adds.
+constexpr uint32_t kPartWaves = 5, kPartC = 2, kOnePartMax = 32, kOnePartMax3 = 48;
 
 struct StreamPlan {
   const void* fn = nullptr;
   uint32_t waves = 0, C = 0, SB = 0, wgs = 0, max_blocks = 0, lds = 0, total_blocks = 0;
+  uint32_t parts = 1, part_chunks = 0;
+  size_t partial_bytes = 0, counters = 0;
 };
 
 StreamPlan make_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const Tuning& tn) {
   StreamPlan p{};
   const uint32_t chunks = (K + kChunkElems - 1) / kChunkElems;
-  p.C = (chunks + kMaxWaves - 1) / kMaxWaves;
-  // Two chunks per wave even when one would do: half the waves per
-  // workgroup, more workgroups per CU and each block's per-row work over
-  // twice the bytes (measured: QKV + gate/up set 32 -> 28 us).
-  if (p.C == 1 && chunks > 1) p.C = 2;
-  if (p.C > 3) return p;  // K > 24576: not this kernel
-  p.waves = (chunks + p.C - 1) / p.C;
   bool pair = false;
   for (int i = 0; i < n_jobs; ++i) pair |= jobs[i].mode == kQ4OutSwiglu;
+  if (chunks <= kOnePartMax) {
+    // Two chunks per wave even when one would do: fewer waves per workgroup,
+    // more workgroups per CU and each block's per-row work over twice the
+    // bytes (measured: QKV + gate/up set 32 -> 28 us).
+    p.C = chunks > 1 ? 2 : 1;
+    p.waves = (chunks + p.C - 1) / p.C;
+    p.parts = 1;
+  } else if (chunks <= kOnePartMax3 && !pair) {
+    p.C = 3;
+    p.waves = (chunks + 2) / 3;
+    p.parts = 1;
+  } else {
+    p.C = kPartC;
+    p.waves = kPartWaves;
+    p.parts = (chunks + kPartWaves * kPartC - 1) / (kPartWaves * kPartC);
+  }
+  p.part_chunks = p.waves * p.C;
   p.SB = pair ? 2 : 1;
   for (int i = 0; i < n_jobs; ++i) p.total_blocks += job_blocks(jobs[i].rows, jobs[i].mode, p.SB);
   p.fn = pick_kernel((int)p.C, (int)p.SB);
-  if (!p.fn) return p;
   const uint32_t cus = tn.cus > 0 ? (uint32_t)tn.cus : 256;
   // Workgroups: as many as stay resident (one dispatch round), with at most
   // `cap` blocks each (the table entries a wave fetches); more workgroups,
@@ -456,14 +516,19 @@ StreamPlan make_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const Tun
     p.fn = nullptr;
     return p;
   }
-  const uint32_t resident = (uint32_t)occ * cus;
+  const uint32_t resident = std::max<uint32_t>(1, (uint32_t)occ * cus / p.parts);
   const uint32_t wgs_min = (p.total_blocks + cap - 1) / cap;
   p.wgs = std::max(wgs_min, std::min(p.total_blocks, resident));
   p.max_blocks = (p.total_blocks + p.wgs - 1) / p.wgs;
   p.lds = head_bytes(p.waves, p.SB, p.max_blocks) + p.waves * table_bytes(p.max_blocks, p.SB, p.C);
+  if (p.parts > 1) {
+    p.partial_bytes = (size_t)p.parts * p.total_blocks * 4 * p.SB * sizeof(float);
+    p.counters = p.wgs;
+  }
   if (tn.q4_plan_log > 0)
-    fprintf(stderr, "q4 stream plan: K=%u jobs=%d blocks=%u C=%u SB=%u waves=%u wgs=%u max_blocks=%u lds=%u\n", K,
-            n_jobs, p.total_blocks, p.C, p.SB, p.waves, p.wgs, p.max_blocks, p.lds);
+    fprintf(stderr,
+            "q4 stream plan: K=%u jobs=%d blocks=%u C=%u SB=%u waves=%u parts=%u wgs/part=%u max_blocks=%u lds=%u\n",
+            K, n_jobs, p.total_blocks, p.C, p.SB, p.waves, p.parts, p.wgs, p.max_blocks, p.lds);
   return p;
 }
 
@@ -503,17 +568,17 @@ StreamPlan cached_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const T
 }  // namespace
 
 bool q4_stream_supported(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn) {
-  if (M != 1 || tn.q4_stream == 0) return false;
-  // Register budget: up to 3 activation chunks per wave for plain jobs, 2
-  // with gate/up pairs (K <= 24576 / 16384).
-  const uint32_t chunks = (K + kChunkElems - 1) / kChunkElems;
-  const uint32_t C = (chunks + kMaxWaves - 1) / kMaxWaves;
-  bool pair = false;
-  for (int i = 0; i < n_jobs; ++i) {
-    if (jobs[i].mode > kQ4OutSwiglu) return false;
-    pair |= jobs[i].mode == kQ4OutSwiglu;
-  }
-  return C <= (pair ? 2u : 3u);
+  if (M != 1 || tn.q4_stream == 0 || n_jobs < 1 || n_jobs > kMaxQ4Jobs) return false;
+  for (int i = 0; i < n_jobs; ++i)
+    if (jobs[i].mode > kQ4OutSwiglu || (jobs[i].mode == kQ4OutArgmax && n_jobs > 1)) return false;
+  return cached_stream_plan(jobs, n_jobs, K, tn).fn != nullptr;
+}
+
+void q4_stream_workspace(const Q4Job* jobs, int n_jobs, uint32_t K, const Tuning& tn, size_t* partial_bytes,
+                         size_t* counters) {
+  const StreamPlan p = cached_stream_plan(jobs, n_jobs, K, tn);
+  *partial_bytes = p.partial_bytes;
+  *counters = p.counters;
 }
 
 hipError_t launch_q4_stream(const Q4Job* jobs, int n_jobs, const uint16_t* x, uint32_t K, const Workspace& ws,
@@ -521,6 +586,9 @@ hipError_t launch_q4_stream(const Q4Job* jobs, int n_jobs, const uint16_t* x, ui
   if (!ws.tune || n_jobs < 1 || n_jobs > kMaxQ4Jobs) return hipErrorInvalidValue;
   const StreamPlan p = cached_stream_plan(jobs, n_jobs, K, *ws.tune);
   if (!p.fn) return hipErrorInvalidValue;
+  if (p.parts > 1 && (!ws.partials || ws.partial_bytes < p.partial_bytes || !ws.counters ||
+                      ws.counter_count < p.counters))
+    return hipErrorInvalidValue;
   StreamArgs a{};
   a.x = x;
   a.K = K;
@@ -531,18 +599,18 @@ hipError_t launch_q4_stream(const Q4Job* jobs, int n_jobs, const uint16_t* x, ui
   a.total_blocks = p.total_blocks;
   a.wgs = p.wgs;
   a.max_blocks = p.max_blocks;
+  a.parts = p.parts;
+  a.part_chunks = p.part_chunks;
+  a.partials = ws.partials;
+  a.counters = ws.counters;
   uint32_t b = 0;
   for (int i = 0; i < n_jobs; ++i) {
     a.jobs[i] = jobs[i];
     a.jobs[i].tile_begin = b;
     b += job_blocks(jobs[i].rows, jobs[i].mode, (int)p.SB);
   }
-  // An argmax launch carries one job (its keys are jobs[0].out).
-  if (n_jobs > 1)
-    for (int i = 0; i < n_jobs; ++i)
-      if (jobs[i].mode == kQ4OutArgmax) return hipErrorInvalidValue;
   void* args[] = {&a};
-  const hipError_t e = hipLaunchKernel(p.fn, dim3(p.wgs), dim3(64 * p.waves), args, p.lds, stream);
+  const hipError_t e = hipLaunchKernel(p.fn, dim3(p.wgs * p.parts), dim3(64 * p.waves), args, p.lds, stream);
   return e != hipSuccess ? e : hipGetLastError();
 }
 

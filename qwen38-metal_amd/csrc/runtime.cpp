@@ -164,11 +164,29 @@ qm_status qm::stream_after(qm_runtime* waiter, qm_runtime* signaler) {
   return hip_check(e, "stream order");
 }
 
+qm_status qm::ensure_keys(qm_runtime* rt) {
+  if (rt->keys) return QM_OK;
+  if (rt->device < 0) return no_device();
+  if (qm_status st_cap = capture_guard(rt, "ensure_keys"); st_cap != QM_OK) return st_cap;
+  const size_t bytes = 16 * sizeof(unsigned long long);
+  hipError_t e = hipMalloc(&rt->keys, bytes);
+  if (e == hipSuccess) e = hipMemsetAsync(rt->keys, 0, bytes, rt->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
+  if (e != hipSuccess) {
+    if (rt->keys) hipFree(rt->keys);
+    rt->keys = nullptr;
+    return hip_check(e, "argmax keys");
+  }
+  return QM_OK;
+}
+
 void qm::release_buffers(qm_runtime* rt) {
   if (rt->scratch) hipFree(rt->scratch);
   if (rt->counters) hipFree(rt->counters);
   if (rt->partials) hipFree(rt->partials);
   if (rt->xh) hipFree(rt->xh);
+  if (rt->keys) hipFree(rt->keys);
+  rt->keys = nullptr;
   rt->scratch = rt->counters = nullptr;
   rt->partials = rt->xh = nullptr;
   rt->scratch_bytes = rt->counter_count = rt->partial_bytes = rt->xh_bytes = 0;

@@ -495,6 +495,25 @@ qm_status qm_decode_graph_create(qm_runtime* rt, qm_decode_state* st, const qm_d
     }
   s = ensure_scratch(&g->cap, step_bytes);
   if (s == QM_OK) s = ensure_counters(&g->cap, step_ctrs);
+  // ... and the single-row projections' split-K partials.
+  for (const qm_decode_layer& L : g->layers) {
+    if (s != QM_OK) break;
+    const uint32_t H = st->hidden;
+    const qm_q4_job& gate = L.linear ? L.linear->gate : L.full->gate;
+    const qm_q4_job& down = L.linear ? L.linear->down : L.full->down;
+    s = q4_reserve_workspace(&g->cap, &down, 1, gate.out_rows);
+    if (s == QM_OK && L.linear) {
+      const qm_dn_config& c = dn_weights_config(L.linear->dn_weights);
+      const qm_q4_job set[4] = {L.linear->qkv, L.linear->z, L.linear->b, L.linear->a};
+      s = q4_reserve_workspace(&g->cap, set, 4, H);
+      if (s == QM_OK) s = q4_reserve_workspace(&g->cap, &L.linear->out_proj, 1, c.value_heads * c.value_head_dim);
+    } else if (s == QM_OK) {
+      const qm_q4_job set[3] = {L.full->q_proj, L.full->k_proj, L.full->v_proj};
+      s = q4_reserve_workspace(&g->cap, set, 3, H);
+      if (s == QM_OK)
+        s = q4_reserve_workspace(&g->cap, &L.full->o_proj, 1, L.full->num_heads * L.full->rope.head_dim);
+    }
+  }
   // Two variants, one per history parity; capturing flips the states'
   // parity exactly as running would, so the second capture starts from the
   // first one's end and ends where the first began.

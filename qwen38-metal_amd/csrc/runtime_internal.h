@@ -29,6 +29,9 @@ struct qm_runtime {
   // hold the MLP's h while h itself is converted).
   void* xh = nullptr;
   size_t xh_bytes = 0;
+  // Argmax keys of qm_q4_argmax (one uint64 per row of a 16-row chunk); zero
+  // between calls, like the counters.
+  unsigned long long* keys = nullptr;
   // Orders this runtime's stream before another runtime's (stream_after).
   hipEvent_t order_event = nullptr;
 };
@@ -43,12 +46,17 @@ qm_status ensure_scratch(qm_runtime* rt, size_t bytes);
 qm_status ensure_partials(qm_runtime* rt, size_t bytes);
 qm_status ensure_counters(qm_runtime* rt, size_t count);
 qm_status ensure_xh(qm_runtime* rt, size_t bytes);
+qm_status ensure_keys(qm_runtime* rt);
 // Workspace handed to kernels that split work across workgroups.
 Workspace workspace(qm_runtime* rt);
 // The device-allocation range checks of every Q4 entry point for one job of
 // input width in_elems (INVALID_BUFFER_OFFSET / MAPPED_TENSOR_OUT_OF_RANGE);
 // nothing is checked on a runtime without a device or a capturing stream.
 qm_status q4_job_ranges(const qm_runtime* rt, const qm_q4_job& j, uint32_t in_elems, const char* name);
+// Sizes rt's workspace for single-row projections of these jobs (the K-split
+// partials of the streaming kernel), so a later call allocates nothing (graph
+// capture).
+qm_status q4_reserve_workspace(qm_runtime* rt, const qm_q4_job* jobs, int n_jobs, uint32_t in_elems);
 // qm_q4_project with a per-job output mode (kQ4Out*; fp32 modes need M <= 16).
 qm_status q4_project_modes(qm_runtime* rt, const qm_q4_job* jobs, void* const* outs, const uint32_t* modes,
                            int n_jobs, const uint16_t* x, uint32_t in_elems, uint32_t M);

@@ -95,18 +95,19 @@ Q4Job to_job(const qm_q4_job& j, uint16_t* out) {
   return q;
 }
 
-qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const uint16_t* x, uint32_t K,
-                 uint32_t M, const char* what) {
-  // The decode kernel needs no workspace; the GEMM's split-K plans do.
+// One activation row on the streaming kernel (its K-split workspace first).
+qm_status stream_launch(qm_runtime* rt, const Q4Job* jobs, int n, const uint16_t* x, uint32_t K, const char* what) {
   size_t pbytes = 0, counters = 0;
-  if (M > kDecodeMaxRows) q4_gemm_workspace(jobs, n, swiglu, K, M, rt->tune, &pbytes, &counters);
+  q4_stream_workspace(jobs, n, K, rt->tune, &pbytes, &counters);
   qm_status st = ensure_partials(rt, pbytes);
   if (st == QM_OK) st = ensure_counters(rt, counters);
-  if (st == QM_OK && M > kDecodeMaxRows) st = ensure_xh(rt, q4_gemm_xh_bytes(K, M));
   if (st != QM_OK) return st;
-  const Workspace ws = workspace(rt);
-  hipError_t e;
-  if (M == 1 && q4_stream_supported(jobs, n, K, M, rt->tune)) {
+  return hip_check(launch_q4_stream(jobs, n, x, K, workspace(rt), rt->stream), what);
+}
+
+qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const uint16_t* x, uint32_t K,
+                 uint32_t M, const char* what) {
+  if (M == 1) {
     // One activation row: the streaming kernel, with a gate/up pair as one job.
     Q4Job sj[kMaxQ4Jobs];
     int ns = 0;
@@ -120,15 +121,33 @@ qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const ui
     } else {
       for (int i = 0; i < n; ++i) sj[ns++] = jobs[i];
     }
-    e = launch_q4_stream(sj, ns, x, K, ws, rt->stream);
-  } else {
-    e = M <= kDecodeMaxRows ? launch_q4_decode(jobs, n, swiglu, x, K, M, ws, rt->stream)
-                            : launch_q4_gemm(jobs, n, swiglu, x, K, M, ws, rt->stream);
+    if (q4_stream_supported(sj, ns, K, M, rt->tune)) return stream_launch(rt, sj, ns, x, K, what);
   }
+  // The decode kernel needs no workspace; the GEMM's split-K plans do.
+  size_t pbytes = 0, counters = 0;
+  if (M > kDecodeMaxRows) q4_gemm_workspace(jobs, n, swiglu, K, M, rt->tune, &pbytes, &counters);
+  qm_status st = ensure_partials(rt, pbytes);
+  if (st == QM_OK) st = ensure_counters(rt, counters);
+  if (st == QM_OK && M > kDecodeMaxRows) st = ensure_xh(rt, q4_gemm_xh_bytes(K, M));
+  if (st != QM_OK) return st;
+  const Workspace ws = workspace(rt);
+  const hipError_t e = M <= kDecodeMaxRows ? launch_q4_decode(jobs, n, swiglu, x, K, M, ws, rt->stream)
+                                           : launch_q4_gemm(jobs, n, swiglu, x, K, M, ws, rt->stream);
   return hip_check(e, what);
 }
 
 }  // namespace
+
+qm_status qm::q4_reserve_workspace(qm_runtime* rt, const qm_q4_job* jobs, int n_jobs, uint32_t in_elems) {
+  if (n_jobs <= 0 || n_jobs > kMaxQ4Jobs) return QM_OK;
+  Q4Job q[kMaxQ4Jobs];
+  for (int i = 0; i < n_jobs; ++i) q[i] = to_job(jobs[i], nullptr);
+  if (!q4_stream_supported(q, n_jobs, in_elems, 1, rt->tune)) return QM_OK;
+  size_t pbytes = 0, counters = 0;
+  q4_stream_workspace(q, n_jobs, in_elems, rt->tune, &pbytes, &counters);
+  qm_status st = ensure_partials(rt, pbytes);
+  return st == QM_OK ? ensure_counters(rt, counters) : st;
+}
 
 qm_status qm::q4_project_modes(qm_runtime* rt, const qm_q4_job* jobs, void* const* outs, const uint32_t* modes,
                                int n_jobs, const uint16_t* x, uint32_t in_elems, uint32_t M) {
@@ -219,7 +238,7 @@ qm_status qm_q4_project_set(qm_runtime* rt, const qm_q4_job* jobs, const qm_q4_j
     if ((st = check_range(rt, outputs[i], (uint64_t)M * jobs[i].out_rows * 2, "output")) != QM_OK) return st;
   }
   if (M == 1 && q4_stream_supported(q, n_jobs, in_elems, M, rt->tune))
-    return hip_check(launch_q4_stream(q, n_jobs, x, in_elems, workspace(rt), rt->stream), "Q4 set launch");
+    return stream_launch(rt, q, n_jobs, x, in_elems, "Q4 set launch");
   // Otherwise: the plain jobs in one launch, each pair in its own.
   Q4Job plain[kMaxQ4Jobs];
   int np = 0;
@@ -293,21 +312,25 @@ qm_status qm_q4_argmax(qm_runtime* rt, const qm_q4_job* job, const uint16_t* x, 
   if ((st = check_range(rt, x, (uint64_t)M * in_elems * 2, "activation")) != QM_OK) return st;
   if ((st = check_job_ranges(rt, *job, in_elems, "argmax")) != QM_OK) return st;
   if ((st = check_range(rt, ids, (uint64_t)M * 4, "ids")) != QM_OK) return st;
-  // One 64-bit key per row of a chunk of at most 16 rows lives in the
-  // runtime's counters (zero between launches; the finishing kernel clears
-  // them).  Larger M runs the decode kernel chunk by chunk: each row's
-  // argmax is independent of the others.
-  if ((st = ensure_counters(rt, 2 * kDecodeMaxRows)) != QM_OK) return st;
-  unsigned long long* keys = (unsigned long long*)rt->counters;
+  // One 64-bit key per row of a chunk of at most 16 rows (zero between
+  // calls; the finishing kernel clears them).  Larger M runs the decode
+  // kernel chunk by chunk: each row's argmax is independent of the others.
+  if ((st = ensure_keys(rt)) != QM_OK) return st;
+  Q4Job q = to_job(*job, (uint16_t*)rt->keys);
+  q.mode = kQ4OutArgmax;
+  const bool stream = q4_stream_supported(&q, 1, in_elems, 1, rt->tune);
+  if (stream) {
+    size_t pbytes = 0, counters = 0;
+    q4_stream_workspace(&q, 1, in_elems, rt->tune, &pbytes, &counters);
+    if ((st = ensure_partials(rt, pbytes)) != QM_OK || (st = ensure_counters(rt, counters)) != QM_OK) return st;
+  }
   const Workspace ws = workspace(rt);
   for (uint32_t m0 = 0; m0 < M; m0 += kDecodeMaxRows) {
     const uint32_t mc = M - m0 < kDecodeMaxRows ? M - m0 : kDecodeMaxRows;
-    Q4Job q = to_job(*job, (uint16_t*)keys);
-    q.mode = kQ4OutArgmax;
-    hipError_t e = mc == 1 && q4_stream_supported(&q, 1, in_elems, 1, rt->tune)
+    hipError_t e = mc == 1 && stream
                        ? launch_q4_stream(&q, 1, x + (size_t)m0 * in_elems, in_elems, ws, rt->stream)
                        : launch_q4_decode(&q, 1, false, x + (size_t)m0 * in_elems, in_elems, mc, ws, rt->stream);
-    if (e == hipSuccess) e = launch_q4_argmax_finish(keys, ids + m0, mc, rt->stream);
+    if (e == hipSuccess) e = launch_q4_argmax_finish(rt->keys, ids + m0, mc, rt->stream);
     if ((st = hip_check(e, "Q4 argmax launch")) != QM_OK) return st;
   }
   return QM_OK;

@@ -340,3 +340,56 @@ def test_mapped_job_from_one_buffer(rt, torch_dev):
     with pytest.raises(QmError) as e:
         qm38.Runtime.mapped_job(whole, blob.nbytes + 1, whole, off_s, whole, off_b, N, K)
     assert e.value.status == "QM_ERR_INVALID_BUFFER_OFFSET"
+
+
+@pytest.mark.parametrize("K", [16448, 17408, 20544])
+def test_single_row_k_parts(rt, torch_dev, K):
+    """One activation row with K beyond 16384: the streaming kernel splits K
+    over several workgroups (parts of 5120 elements, the last one shorter,
+    here also ending inside a 512-element chunk for K = 16448 and 20544) and
+    the last part to finish adds the fp32 partial rows in part order.  Plain
+    jobs of several heights, a SwiGLU pair and the argmax all match the
+    oracle, and repeated calls are bit-identical."""
+    import torch
+    import qm38
+    rng = np.random.default_rng(K)
+    mats = [synth.q4_matrix(rng, n, K) for n in (300, 37)]
+    xb = synth.bf16_normal(rng, (1, K))
+    got1 = _project(rt, torch_dev, mats, xb, 1)
+    got2 = _project(rt, torch_dev, mats, xb, 1)
+    for mat, g1, g2 in zip(mats, got1, got2):
+        assert_bf16_close(g1, oracle.q4_project(xb, *mat), what=f"K={K} rows {mat[0].shape[0]}")
+        assert np.array_equal(g1, g2)
+    gate, up = synth.q4_matrix(rng, 90, K), synth.q4_matrix(rng, 90, K)
+    dg, du = _upload(torch_dev, *gate), _upload(torch_dev, *up)
+    h = empty_bf16((1, 90), torch_dev)
+    rt.q4_swiglu(qm38.Runtime.job(*dg, 90), qm38.Runtime.job(*du, 90), to_dev(xb, torch_dev), K, 1, h)
+    h_ref = oracle.swiglu(oracle.q4_project(xb, *gate), oracle.q4_project(xb, *up))
+    assert_bf16_close(bf16_dev_to_f32(h), h_ref, what=f"K={K} swiglu")
+    ids = _argmax(rt, torch_dev, mats[0], xb)
+    ref = oracle.q4_project(xb, *mats[0])[0]
+    assert ref[ids[0]] >= ref.max() - 1e-5 * np.max(np.abs(ref))
+
+
+def test_project_set_mixes_plain_and_pairs(rt, torch_dev):
+    """qm_q4_project_set: plain projections and SwiGLU pairs from one
+    activation, in one launch for one row, and as separate launches for
+    several rows; each output equals its own call."""
+    import qm38
+    rng = np.random.default_rng(31)
+    K = 1024
+    for M in (1, 3):
+        a, g, u, b = (synth.q4_matrix(rng, n, K) for n in (200, 96, 96, 40))
+        da, dg, du, db = (_upload(torch_dev, *m) for m in (a, g, u, b))
+        ja, jg, ju, jb = (qm38.Runtime.job(*d, m[0].shape[0]) for d, m in zip((da, dg, du, db), (a, g, u, b)))
+        xb = synth.bf16_normal(rng, (M, K))
+        xd = to_dev(xb, torch_dev)
+        outs = [empty_bf16((M, 200), torch_dev), empty_bf16((M, 96), torch_dev), empty_bf16((M, 40), torch_dev)]
+        rt.q4_project_set([ja, jg, jb], [None, ju, None], xd, K, M, outs)
+        assert_bf16_close(bf16_dev_to_f32(outs[0]), oracle.q4_project(xb, *a), what=f"set plain M={M}")
+        h_ref = oracle.swiglu(oracle.q4_project(xb, *g), oracle.q4_project(xb, *u))
+        assert_bf16_close(bf16_dev_to_f32(outs[1]), h_ref, what=f"set pair M={M}")
+        assert_bf16_close(bf16_dev_to_f32(outs[2]), oracle.q4_project(xb, *b), what=f"set plain 2 M={M}")
+        h = empty_bf16((M, 96), torch_dev)
+        rt.q4_swiglu(jg, ju, xd, K, M, h)
+        assert np.array_equal(bf16_dev_to_f32(h), bf16_dev_to_f32(outs[1]))
