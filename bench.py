@@ -98,10 +98,27 @@ def gpu_blocker(ms: float = 12.0):
         torch.mm(a, a)
 
 
-def timed(step, stream, steps: int, warmup: int):
+# Leg markers for per-leg kernel statistics: with --markers <file>, every
+# timed region starts and ends with a tiny torch sleep kernel ("spin_kernel"
+# in a rocprofv3 kernel trace) and its label is appended to <file>;
+# `--stats-from` then assigns each dispatch to the region around it.
+_MARKERS = None
+
+
+def leg_marker(label: str) -> None:
+    if not _MARKERS:
+        return
+    import torch
+    torch.cuda._sleep(1)
+    with open(_MARKERS, "a") as f:
+        f.write(label + "\n")
+
+
+def timed(step, stream, steps: int, warmup: int, label: str = "other"):
     """Runs warmup + steps calls of step(i, marks); returns (ms per step, per-step mark lists)."""
     import torch
     ev = Events(stream)
+    leg_marker(label)
     for i in range(warmup):
         step(i, None)
     torch.cuda.synchronize()
@@ -114,14 +131,16 @@ def timed(step, stream, steps: int, warmup: int):
         marks_all.append(marks[1:])
     t1 = ev.mark()
     torch.cuda.synchronize()
+    leg_marker("-")
     return t0.elapsed_time(t1) / steps, marks_all
 
 
-def step_distribution(step, stream, steps: int, warmup: int = 2):
+def step_distribution(step, stream, steps: int, warmup: int = 2, label: str = "other"):
     """Per-step times (us) from one event after each step: (p10, median, p90).
     The events sit between steps, so the set's own kernels stay back to back."""
     import torch
     ev = Events(stream)
+    leg_marker(label)
     for i in range(warmup):
         step(i, None)
     torch.cuda.synchronize()
@@ -131,6 +150,7 @@ def step_distribution(step, stream, steps: int, warmup: int = 2):
         step(warmup + i, None)
         marks.append(ev.mark())
     torch.cuda.synchronize()
+    leg_marker("-")
     d = np.array([a.elapsed_time(b) * 1e3 for a, b in zip(marks[:-1], marks[1:])])
     return tuple(round(float(v), 2) for v in np.percentile(d, [10, 50, 90]))
 
@@ -176,14 +196,14 @@ def q4_leg(rt, dev, sets, M: int, rng, steps, warmup):
         rt.q4_project([j["down"][0]], h, I, M, [y])
 
     stream = torch.cuda.current_stream()
-    ms, _ = timed(step, stream, steps, warmup)
+    ms, _ = timed(step, stream, steps, warmup, f"q4_set_M{M}")
     # Per-kernel durations: each projection alone, back to back (events only
     # around the whole run, so no event sits between the timed kernels).
     calls = {
         "qkv_gateup": lambda i, m: qkv_gateup(sets[i % NCOPY]),
         "down": lambda i, m: rt.q4_project([sets[i % NCOPY]["down"][0]], h, I, M, [y]),
     }
-    per = [timed(fn, stream, steps, 2)[0] for fn in calls.values()]
+    per = [timed(fn, stream, steps, 2, f"q4_set_M{M}:{name}")[0] for name, fn in calls.items()]
     wbytes = {"qkv_gateup": q4_bytes(QKV, H) + 2 * q4_bytes(I, H), "down": q4_bytes(H, I)}
     abytes = {"qkv_gateup": 2 * M * (H + QKV + I), "down": 2 * M * (I + H)}
     flops = {"qkv_gateup": 2 * M * QKV * H + 4 * M * I * H, "down": 2 * M * H * I}
@@ -205,7 +225,7 @@ def matvec_4096_leg(rt, dev, rng, steps, warmup):
     x = dev_array(synth_bf16(rng, (1, K)), dev)
     y = torch.empty((1, N), dtype=torch.int16, device=dev)
     ms, _ = timed(lambda i, m: rt.q4_project([jobs[i % NCOPY]], x, K, 1, [y]), torch.cuda.current_stream(), steps,
-                  warmup)
+                  warmup, "q4_matvec_4096")
     nbytes = q4_bytes(N, K) + 2 * K + 2 * N  # 9,453,568 B
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
@@ -260,7 +280,8 @@ def attention_legs(rt, dev, rng, steps, warmup):
     k = torch.randn((1, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
     v = torch.randn((1, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
     o = torch.empty((1, ATT_H, ATT_D), dtype=torch.int16, device=dev)
-    ms, _ = timed(lambda i, m: rt.gqa_attention_q8([caches[i % NC]], q, g, k, v, ATT_H, o), stream, steps, warmup)
+    ms, _ = timed(lambda i, m: rt.gqa_attention_q8([caches[i % NC]], q, g, k, v, ATT_H, o), stream, steps, warmup,
+                  "attn_decode_32k")
     T_avg = T0 + (warmup + steps) / NC / 2
     gbs = attn_bytes(int(T_avg)) / (ms * 1e-3) / 1e9
     out["attn_decode_32k"] = {"us_per_token": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
@@ -282,7 +303,8 @@ def attention_legs(rt, dev, rng, steps, warmup):
     k = torch.randn((B, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
     v = torch.randn((B, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
     o = torch.empty((B, ATT_H, ATT_D), dtype=torch.int16, device=dev)
-    ms, _ = timed(lambda i, m: rt.gqa_attention_q8(caches, q, g, k, v, ATT_H, o), stream, steps, warmup)
+    ms, _ = timed(lambda i, m: rt.gqa_attention_q8(caches, q, g, k, v, ATT_H, o), stream, steps, warmup,
+                  "attn_decode_ragged_b8")
     total = sum(attn_bytes(int(n) + warmup + steps // 2) for n in lens)
     gbs = total / (ms * 1e-3) / 1e9
     out["attn_decode_ragged_b8"] = {"us_per_step": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
@@ -302,7 +324,8 @@ def attention_legs(rt, dev, rng, steps, warmup):
     k = torch.randn((P, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
     v = torch.randn((P, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
     o = torch.empty((P, ATT_H, ATT_D), dtype=torch.int16, device=dev)
-    ms, _ = timed(lambda i, m: rt.gqa_attention_q8_prefill(caches[i], q, g, k, v, ATT_H, P, o), stream, reps, 1)
+    ms, _ = timed(lambda i, m: rt.gqa_attention_q8_prefill(caches[i], q, g, k, v, ATT_H, P, o), stream, reps, 1,
+                  "attn_prefill_2048_on_4k")
     flops = 4.0 * ATT_H * ATT_D * sum(T + i + 1 for i in range(P))
     out["attn_prefill_2048_on_4k"] = {"ms": round(ms, 3), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2),
                                       "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)}
@@ -321,7 +344,8 @@ def attention_legs(rt, dev, rng, steps, warmup):
         go = torch.empty((R, ATT_H, ATT_D), dtype=torch.int16, device=dev)
         ko = torch.empty((R, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
         ms, _ = timed(lambda i, m: rt.attn_prepare(rope, R, ATT_H, ATT_KVH, qg, kin, qn, qn, 1e-6, qo, go, ko,
-                                                   position_base=4096 + i), stream, steps, warmup)
+                                                   position_base=4096 + i), stream, steps, warmup,
+                      f"attn_prepare_rows{R}")
         nbytes = R * (ATT_H * 2 * ATT_D * 2 + ATT_KVH * ATT_D * 2 + 2 * ATT_H * ATT_D * 2 + ATT_KVH * ATT_D * 4)
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[f"attn_prepare_rows{R}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
@@ -355,7 +379,8 @@ def deltanet_legs(rt, dev, rng, steps, warmup):
             fn = lambda i, m: rt.deltanet_step(w, st, qkv, z, b, a, 1e-6, o)
         else:
             fn = lambda i, m: rt.deltanet_prefill(w, st, qkv, z, b, a, M, 1e-6, o)
-        ms, _ = timed(fn, stream, steps if M == 1 else max(2, steps // 10), warmup if M == 1 else 1)
+        ms, _ = timed(fn, stream, steps if M == 1 else max(2, steps // 10), warmup if M == 1 else 1,
+                      "deltanet_step" if M == 1 else "deltanet_prefill_2048")
         state = 2 * VH * dv * dk * 4 + 2 * ch * 3 * 4
         acts = M * (ch + VH * dv + 2 * VH + VH * dv) * 4
         gbs = (state + acts) / (ms * 1e-3) / 1e9
@@ -462,12 +487,12 @@ def decode_graph_legs(rt, dev, rng, steps, warmup):
 
     st_e, descs_e, alive_e = request()
     eager = lambda i, m: rt.decode_layers(st_e, descs_e, (i, i, i), 1e-6)  # noqa: E731
-    ms_e, _ = timed(eager, stream, steps, warmup)
+    ms_e, _ = timed(eager, stream, steps, warmup, "decode_block4_eager")
     host_e = host_us(eager)
     st_g, descs_g, alive_g = request()
     graph = qm38.DecodeGraph(rt, st_g, descs_g, 1e-6)
     replay = lambda i, m: graph.run((i, i, i))  # noqa: E731
-    ms_g, _ = timed(replay, stream, steps, warmup)
+    ms_g, _ = timed(replay, stream, steps, warmup, "decode_block4_graph")
     host_g = host_us(replay)
     for key, ms, hu in (("decode_block4_eager", ms_e, host_e), ("decode_block4_graph", ms_g, host_g)):
         gbs = weight_bytes / (ms * 1e-3) / 1e9
@@ -580,48 +605,149 @@ def _counter_rows(d: str, counter: str):
     return [(k, v) for _, k, v in rows]
 
 
-def traffic_summary(fetch_dir: str, write_dir: str) -> int:
-    """HBM bytes per QKV + gate/up (M=1) set launch from FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each
-    scaled by what the same counter reads for a 256 MiB device copy of known size."""
+# HBM traffic probes: each leg's setup, then five 256 MiB device copies (the
+# counters' calibration), then `calls` launches of the leg; rocprofv3 --pmc
+# FETCH_SIZE and WRITE_SIZE runs of `bench.py --traffic-probe LEG` give each
+# dispatch's KiB, and `--traffic-from` turns them into bytes per call.
+PROBE_CALLS = 5
+PROBE_FILES = {
+    "q4_set": TRAFFIC_FILE,
+    "attn_decode_32k": "q8_decode_attn_32k_traffic.json",
+    "attn_prefill_2048": "q8_prefill_attn_2048_on_4k_traffic.json",
+    "deltanet_step": "dn_step_traffic.json",
+    "deltanet_prefill_2048": "dn_prefill_2048_traffic.json",
+}
+
+
+def probe_alg_bytes(leg: str) -> int:
+    """Algorithmic HBM bytes of one call of a probed leg."""
+    VH, dv, dk = DN["value_heads"], DN["value_head_dim"], DN["key_head_dim"]
+    ch = 2 * DN["key_heads"] * dk + VH * dv
+    if leg == "q4_set":
+        return q4_bytes(QKV, H) + 2 * q4_bytes(I, H) + 2 * (H + QKV + I)
+    if leg == "attn_decode_32k":
+        # the cache read at T = 32768 + 1, q / gate in, output and the appended row
+        return attn_bytes(32769) + 3 * ATT_H * ATT_D * 2 + ATT_KVH * (2 * ATT_D + 8)
+    if leg == "attn_prefill_2048":
+        P, T = 2048, 4096
+        return attn_bytes(T + P) + P * (3 * ATT_H * ATT_D * 2 + 2 * ATT_KVH * ATT_D * 4)
+    M = 1 if leg == "deltanet_step" else 2048
+    return 2 * VH * dv * dk * 4 + 2 * ch * 3 * 4 + M * (ch + VH * dv + 2 * VH + VH * dv) * 4
+    
+
+def traffic_probe(rt, dev, rng, sets, leg: str) -> None:
+    """Setup, calibration copies, then PROBE_CALLS calls of `leg` (for rocprofv3 --pmc)."""
+    import torch
+    from qm38 import synth
+    if leg == "q4_set":
+        x = dev_array(synth_bf16(rng, (1, H)), dev)
+        h = torch.empty((1, I), dtype=torch.int16, device=dev)
+        qo = torch.empty((1, QKV), dtype=torch.int16, device=dev)
+        call = lambda i: rt.q4_project_set([sets[i % NCOPY]["qkv"][0], sets[i % NCOPY]["gate"][0]],  # noqa: E731
+                                           [None, sets[i % NCOPY]["up"][0]], x, H, 1, [qo, h])
+    elif leg == "attn_decode_32k":
+        caches = []
+        for _ in range(PROBE_CALLS):
+            c = kv_cache(rt, 32768 + 8)
+            kv_fill(rt, dev, c, rng, 32768)
+            caches.append(c)
+        q = dev_array(synth.bf16_normal(rng, (1, ATT_H, ATT_D)), dev)
+        g = dev_array(synth.bf16_normal(rng, (1, ATT_H, ATT_D)), dev)
+        k = torch.randn((1, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
+        o = torch.empty((1, ATT_H, ATT_D), dtype=torch.int16, device=dev)
+        call = lambda i: rt.gqa_attention_q8([caches[i]], q, g, k, k, ATT_H, o)  # noqa: E731
+    elif leg == "attn_prefill_2048":
+        P, T = 2048, 4096
+        caches = [kv_cache(rt, T + P) for _ in range(PROBE_CALLS)]
+        for c in caches:
+            kv_fill(rt, dev, c, rng, T)
+        q = dev_array(synth.bf16_normal(rng, (P, ATT_H, ATT_D)), dev)
+        g = dev_array(synth.bf16_normal(rng, (P, ATT_H, ATT_D)), dev)
+        k = torch.randn((P, ATT_KVH, ATT_D), dtype=torch.float32, device=dev)
+        o = torch.empty((P, ATT_H, ATT_D), dtype=torch.int16, device=dev)
+        call = lambda i: rt.gqa_attention_q8_prefill(caches[i], q, g, k, k, ATT_H, P, o)  # noqa: E731
+    else:
+        import qm38
+        VH, dv, dk = DN["value_heads"], DN["value_head_dim"], DN["key_head_dim"]
+        ch = 2 * DN["key_heads"] * dk + VH * dv
+        cfg = qm38.DnConfig(DN["key_heads"], VH, dk, dv, DN["conv_kernel_size"])
+        w = rt.create_deltanet_weights(cfg, (rng.standard_normal((ch, 4)) * 0.5).astype(np.float32),
+                                       np.zeros(VH, np.float32), np.zeros(VH, np.float32),
+                                       np.ones(dv, np.float32))
+        st = w.create_state()
+        M = 1 if leg == "deltanet_step" else 2048
+        qkv, z = torch.randn((M, ch), device=dev), torch.randn((M, VH * dv), device=dev)
+        b, a = torch.randn((M, VH), device=dev), torch.randn((M, VH), device=dev)
+        o = torch.empty((M, VH * dv), device=dev)
+        if M == 1:
+            call = lambda i: rt.deltanet_step(w, st, qkv, z, b, a, 1e-6, o)  # noqa: E731
+        else:
+            call = lambda i: rt.deltanet_prefill(w, st, qkv, z, b, a, M, 1e-6, o)  # noqa: E731
+    torch.cuda.synchronize()
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    for i in range(PROBE_CALLS):
+        call(i)
+    torch.cuda.synchronize()
+
+
+def traffic_summary(leg: str, fetch_dir: str, write_dir: str) -> int:
+    """HBM bytes per call of a probed leg from FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each scaled by
+    what the same counter reads for a 256 MiB device copy of known size."""
     copy_bytes = 256 << 20
-    out = {"kernel": None, "calibration": {"copy_bytes": copy_bytes}, "raw_KiB_per_dispatch": {}}
+    out = {"leg": leg, "calibration": {"copy_bytes": copy_bytes}, "kernels": {}}
     per = {}
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         rows = _counter_rows(d, counter)
-        # The copy dispatches are the large non-q4 ones; the first (a small runtime copy) is excluded.
-        copies = [v for k, v in rows if ROOF_KERNEL not in k and v * 1024 > copy_bytes / 4]
-        q4 = [(k, v) for k, v in rows if ROOF_KERNEL in k]
-        if not copies or not q4:
-            raise RuntimeError(f"{counter}: expected copy and {ROOF_KERNEL} dispatches in {d}")
+        big = [i for i, (k, v) in enumerate(rows) if v * 1024 > copy_bytes / 4 and "copy" in k.lower()]
+        if len(big) < 5:
+            raise RuntimeError(f"{counter}: expected 5 calibration copies in {d}")
+        copies = [rows[i][1] for i in big[-5:]]
         factor = copy_bytes / (sum(copies) / len(copies) * 1024)
         out["calibration"][f"{counter}_KiB"] = round(sum(copies) / len(copies), 3)
         out["calibration"]["fetch_factor" if counter == "FETCH_SIZE" else "write_factor"] = round(factor, 4)
-        out["raw_KiB_per_dispatch"][counter] = [v for _, v in q4]
-        per[counter] = sum(v for _, v in q4) / len(q4) * 1024 * factor
-        out["kernel"] = q4[0][0][:120] + " (QKV + gate/up SwiGLU set, M=1, 27B shapes)"
-    alg = q4_bytes(QKV, H) + 2 * q4_bytes(I, H) + 2 * (H + QKV + I)
-    out.update({"bytes_per_launch": int(per["FETCH_SIZE"] + per["WRITE_SIZE"]),
+        after = rows[big[-1] + 1:]  # the leg's calls
+        for k, v in after:
+            name = _short_kernel_name(k)[:120]
+            e = out["kernels"].setdefault(name, {})
+            e.setdefault(counter, []).append(v)
+        per[counter] = sum(v for _, v in after) * 1024 * factor / PROBE_CALLS
+    for e in out["kernels"].values():
+        n = max(len(e.get("FETCH_SIZE", [])), 1)
+        e["dispatches_per_call"] = n / PROBE_CALLS
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            f = out["calibration"]["fetch_factor" if counter == "FETCH_SIZE" else "write_factor"]
+            e[counter.lower().replace("_size", "_bytes_per_call")] = int(sum(e.pop(counter, [])) * 1024 * f
+                                                                         / PROBE_CALLS)
+    alg = probe_alg_bytes(leg)
+    out.update({"bytes_per_launch" if leg == "q4_set" else "bytes_per_call": int(per["FETCH_SIZE"] + per["WRITE_SIZE"]),
                 "fetch_bytes": int(per["FETCH_SIZE"]), "write_bytes": int(per["WRITE_SIZE"]),
                 "algorithmic_bytes": alg,
                 "traffic_over_algorithmic": round((per["FETCH_SIZE"] + per["WRITE_SIZE"]) / alg, 4),
                 "commands": [
-                    "rocprofv3 --pmc FETCH_SIZE --kernel-trace -d prof_out/pmc_fetch -o fetch --output-format csv "
-                    "-- python -u bench.py --traffic-probe",
-                    "rocprofv3 --pmc WRITE_SIZE --kernel-trace -d prof_out/pmc_write -o write --output-format csv "
-                    "-- python -u bench.py --traffic-probe",
-                    "python bench.py --traffic-from prof_out/pmc_fetch prof_out/pmc_write"],
-                "method": "per-dispatch counter (KiB) x (known copy bytes / the counter's reading for a 256 MiB "
-                          "device copy); small copies excluded from the calibration mean"})
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", TRAFFIC_FILE)
+                    f"rocprofv3 --pmc FETCH_SIZE --kernel-trace -d prof_out/f_{leg} -o fetch --output-format csv "
+                    f"-- python -u bench.py --traffic-probe {leg}",
+                    f"rocprofv3 --pmc WRITE_SIZE --kernel-trace -d prof_out/w_{leg} -o write --output-format csv "
+                    f"-- python -u bench.py --traffic-probe {leg}",
+                    f"python bench.py --traffic-from {leg} prof_out/f_{leg} prof_out/w_{leg}"],
+                "method": f"per-dispatch counter (KiB) x (known copy bytes / the counter's reading for a 256 MiB "
+                          f"device copy), summed over the {PROBE_CALLS} calls after the copies and divided by "
+                          f"{PROBE_CALLS}"})
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", PROBE_FILES[leg])
     with open(path, "w") as f:
         json.dump(out, f, indent=1)
     print(path)
     return 0
 
 
-def gemm_counter_summary(d: str) -> int:
-    """profiles/q4_gemm_gateup_m2048_counters.txt from a rocprofv3 --pmc run of
-    bench.py --gemm-probe (per-dispatch SQ/GRBM counters of q4_gemm_kernel)."""
+GEMM_PROBES = {"gateup_m2048": "gate/up with SwiGLU, M = 2048", "qkv_m512": "QKV 5120 -> 10240, M = 512"}
+
+
+def gemm_counter_summary(shape: str, d: str) -> int:
+    """profiles/q4_gemm_<shape>_counters.txt from a rocprofv3 --pmc run of
+    bench.py --gemm-probe <shape> (per-dispatch SQ/GRBM counters of q4_gemm_kernel)."""
     rows = []
     for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
         with open(f) as fh:
@@ -637,13 +763,13 @@ def gemm_counter_summary(d: str) -> int:
         return 1
     simds, cus, xcds = 1024, 256, 8
     lines = [
-        "# rocprofv3 counters: q4_gemm_kernel, gate/up with SwiGLU, M = 2048 (BASELINE config 3)",
+        f"# rocprofv3 counters: q4_gemm_kernel, {GEMM_PROBES[shape]} (BASELINE config 3)",
         "#",
         "# command (repo root, MI355X, one GPU):",
         "#   rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_BUSY_CU_CYCLES SQ_LDS_BANK_CONFLICT \\",
         "#     SQ_LDS_IDX_ACTIVE SQ_INSTS_LDS SQ_INSTS_MFMA SQ_WAIT_INST_LDS GRBM_GUI_ACTIVE --kernel-trace \\",
-        "#     -d prof_out/gemm_pmc -o gemm --output-format csv -- python3 bench.py --gemm-probe",
-        "#   python bench.py --gemm-counters-from prof_out/gemm_pmc",
+        f"#     -d prof_out/gemm_pmc -o gemm --output-format csv -- python3 bench.py --gemm-probe {shape}",
+        f"#   python bench.py --gemm-counters-from {shape} prof_out/gemm_pmc",
         "#",
         "# GRBM_GUI_ACTIVE is summed over the 8 XCDs, so the kernel's GPU cycles are GRBM_GUI_ACTIVE / 8.",
         "# MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (cycles x 1024 SIMDs); each v_mfma_f32_32x32x16_f16 is",
@@ -662,7 +788,7 @@ def gemm_counter_summary(d: str) -> int:
                      f"{e.get('SQ_VALU_MFMA_BUSY_CYCLES', 0) / (cyc * simds):>10.1%} {e.get('SQ_INSTS_MFMA', 0):>12.0f} "
                      f"{e.get('SQ_LDS_IDX_ACTIVE', 0) / (cyc * cus):>11.1%} {e.get('SQ_INSTS_LDS', 0):>11.0f} "
                      f"{e.get('SQ_LDS_BANK_CONFLICT', 0):>11.0f}")
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "q4_gemm_gateup_m2048_counters.txt")
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"q4_gemm_{shape}_counters.txt")
     with open(path, "w") as fh:
         fh.write("\n".join(lines) + "\n")
     print(path)
@@ -675,35 +801,54 @@ def _short_kernel_name(name: str) -> str:
 
 
 def stats_summary(prof_dir: str) -> int:
-    """profiles/bench_all_legs_kernel_stats.txt from a rocprofv3 --kernel-trace --stats run of bench.py."""
-    files = glob.glob(os.path.join(prof_dir, "**", "*kernel_stats.csv"), recursive=True)
+    """profiles/bench_kernel_stats_by_leg.txt from a rocprofv3 --kernel-trace run of
+    bench.py --markers <prof_dir>/legs.txt: per timed region (warmup included),
+    each kernel's calls and durations."""
+    files = glob.glob(os.path.join(prof_dir, "**", "*kernel_trace.csv"), recursive=True)
     if not files:
-        raise FileNotFoundError(f"no *kernel_stats.csv under {prof_dir}")
+        raise FileNotFoundError(f"no *kernel_trace.csv under {prof_dir}")
+    with open(os.path.join(prof_dir, "legs.txt")) as f:
+        labels = [ln.strip() for ln in f if ln.strip()]
     with open(files[0]) as f:
-        rows = list(csv.DictReader(f))
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    per, order, cur, li, filler = {}, [], None, 0, 0
+    for r in rows:
+        name = r["Kernel_Name"]
+        if "spin_kernel" in name:
+            if li >= len(labels):
+                raise ValueError("more marker kernels than labels")
+            cur = None if labels[li] == "-" else labels[li]
+            li += 1
+            if cur is not None and cur not in per:
+                per[cur] = {}
+                order.append(cur)
+            continue
+        if cur is None:
+            continue
+        if name.startswith("Cijk_"):  # the fp16 GEMMs that keep the GPU busy while steps are enqueued
+            filler += 1
+            continue
+        ns = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        per[cur].setdefault(_short_kernel_name(name), []).append(ns)
     lines = [
-        "# rocprofv3 kernel statistics: bench.py (all legs, 20 timed steps)",
+        "# rocprofv3 kernel statistics per bench.py leg (each timed region, warmup included)",
         "#",
         "# command (repo root, MI355X, one GPU):",
-        "#   rocprofv3 --kernel-trace --stats -d prof_out/prof -o bench --output-format csv -- python3 -u bench.py "
-        "--no-cpu --steps 20",
-        "#   python bench.py --stats-from prof_out/prof",
+        "#   rocprofv3 --kernel-trace -d prof_out/legs -o bench --output-format csv -- python3 -u bench.py "
+        "--no-cpu --steps 20 --markers prof_out/legs/legs.txt",
+        "#   python bench.py --stats-from prof_out/legs",
         "#",
-        "# Per-kernel averages mix the legs that launch the same template (q8_prefill_kernel<128,2> is the",
-        "# causal prefill, including the 32K/128K cache fills of the attention legs; q4_gemm_kernel serves",
-        "# M = 512 and 2048; q8_decode_kernel<128> serves the 32K single-sequence and ragged batch-8 legs).",
-        "# The gate+up decode kernel (q4_decode_kernel<2, 1, true, true, true>, M = 1) is the bench's",
-        "# roofline kernel.  bench.py's avg_launch_us for it comes from events around back-to-back",
-        "# launches, so it also holds the gap between launches (about 1-2 us) and reads that much above",
-        "# the kernel-only average here.",
-        "",
-        f"{'kernel':<100} {'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'pct':>7}",
+        "# Regions are delimited by marker kernels (torch's sleep kernel) that bench.py launches around each",
+        "# timed region; setup work between regions (uploads, cache fills) is left out, and so are the fp16",
+        f"# GEMMs that keep the GPU busy while a region's steps are enqueued ({filler} dispatches).",
+        "# q4_set_M1:qkv_gateup / :down time each launch of the headline set alone; q4_set_M1 is the set.",
     ]
-    for r in sorted(rows, key=lambda r: -float(r["Percentage"])):
-        lines.append(f"{_short_kernel_name(r['Name'])[:100]:<100} {int(r['Calls']):>6} "
-                     f"{float(r['AverageNs']) / 1e3:>10.2f} {float(r['MinNs']) / 1e3:>10.2f} "
-                     f"{float(r['MaxNs']) / 1e3:>10.2f} {float(r['Percentage']):>7.3f}")
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "bench_all_legs_kernel_stats.txt")
+    for leg in order:
+        lines += ["", f"[{leg}]", f"  {'kernel':<92} {'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9}"]
+        for k, v in sorted(per[leg].items(), key=lambda kv: -sum(kv[1])):
+            a = np.array(v) / 1e3
+            lines.append(f"  {k[:92]:<92} {len(a):>6} {a.mean():>9.2f} {a.min():>9.2f} {a.max():>9.2f}")
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "bench_kernel_stats_by_leg.txt")
     with open(path, "w") as f:
         f.write("\n".join(lines) + "\n")
     print(path)
@@ -719,23 +864,30 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--legs", default="decode,prefill,attn,deltanet,graph",
                     help="comma list of extra legs to run (the M=1 headline always runs)")
-    ap.add_argument("--gemm-counters-from", metavar="PMC_DIR",
-                    help="write profiles/q4_gemm_gateup_m2048_counters.txt from a --gemm-probe counter run")
-    ap.add_argument("--gemm-probe", action="store_true",
-                    help="only run six M=2048 gate/up GEMMs (for rocprofv3 --pmc passes)")
-    ap.add_argument("--traffic-probe", action="store_true",
-                    help="for rocprofv3 --pmc: 5 launches of a 256 MiB copy, then 5 gate+up M=1 launches")
-    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
-                    help="turn the two --traffic-probe counter runs (rocprofv3 csv output directories) "
-                         "into profiles/q4_stream_qkv_gateup_traffic.json (no GPU needed)")
+    ap.add_argument("--gemm-counters-from", nargs=2, metavar=("SHAPE", "PMC_DIR"),
+                    help="write profiles/q4_gemm_<SHAPE>_counters.txt from a --gemm-probe counter run")
+    ap.add_argument("--gemm-probe", nargs="?", const="gateup_m2048", choices=sorted(GEMM_PROBES), metavar="SHAPE",
+                    help="only run six prefill GEMMs of SHAPE (for rocprofv3 --pmc passes)")
+    ap.add_argument("--traffic-probe", nargs="?", const="q4_set", choices=sorted(PROBE_FILES), metavar="LEG",
+                    help="for rocprofv3 --pmc: the leg's setup, 5 launches of a 256 MiB copy, then 5 calls of "
+                         "the leg (default q4_set: the QKV + gate/up set at M=1)")
+    ap.add_argument("--traffic-from", nargs=3, metavar=("LEG", "FETCH_DIR", "WRITE_DIR"),
+                    help="turn the two --traffic-probe counter runs of LEG (rocprofv3 csv output directories) "
+                         "into its profiles/*_traffic.json (no GPU needed)")
     ap.add_argument("--stats-from", metavar="PROF_DIR",
-                    help="turn a rocprofv3 --kernel-trace --stats run of bench.py into "
-                         "profiles/bench_all_legs_kernel_stats.txt (no GPU needed)")
+                    help="turn a rocprofv3 --kernel-trace run of bench.py --markers PROF_DIR/legs.txt into "
+                         "profiles/bench_kernel_stats_by_leg.txt (no GPU needed)")
+    ap.add_argument("--markers", metavar="FILE",
+                    help="launch a marker kernel around each timed region and list the regions in FILE")
     args = ap.parse_args()
+    global _MARKERS
+    if args.markers:
+        _MARKERS = args.markers
+        open(args.markers, "w").close()
     if args.stats_from:
         return stats_summary(args.stats_from)
     if args.gemm_counters_from:
-        return gemm_counter_summary(args.gemm_counters_from)
+        return gemm_counter_summary(*args.gemm_counters_from)
     if args.traffic_from:
         return traffic_summary(*args.traffic_from)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -754,30 +906,25 @@ def main() -> int:
     rng = np.random.default_rng(2026)
 
     log("[bench] uploading 3 weight copies")
-    sets = q4_sets(rng, dev)
+    sets = q4_sets(rng, dev) if args.traffic_probe in (None, "q4_set") else None
     if args.gemm_probe:
-        # Six gate/up SwiGLU GEMMs at M = 2048, for
-        # rocprofv3 --pmc passes over the prefill kernel.
-        x = dev_array(synth_bf16(rng, (2048, H)), dev)
-        h = torch.empty((2048, I), dtype=torch.int16, device=dev)
+        # Six GEMMs of one BASELINE config 3 shape, for rocprofv3 --pmc
+        # passes over the prefill kernel.
+        M = 2048 if args.gemm_probe == "gateup_m2048" else 512
+        x = dev_array(synth_bf16(rng, (M, H)), dev)
+        h = torch.empty((M, I), dtype=torch.int16, device=dev)
+        qo = torch.empty((M, QKV), dtype=torch.int16, device=dev)
         for i in range(6):
             j = sets[i % NCOPY]
-            rt.q4_swiglu(j["gate"][0], j["up"][0], x, H, 2048, h)
+            if M == 2048:
+                rt.q4_swiglu(j["gate"][0], j["up"][0], x, H, M, h)
+            else:
+                rt.q4_project([j["qkv"][0]], x, H, M, [qo])
         torch.cuda.synchronize()
         rt.close()
         return 0
     if args.traffic_probe:
-        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        x = dev_array(synth_bf16(rng, (1, H)), dev)
-        h = torch.empty((1, I), dtype=torch.int16, device=dev)
-        qo = torch.empty((1, QKV), dtype=torch.int16, device=dev)
-        for i in range(5):
-            dst.copy_(src)
-        for i in range(5):
-            j = sets[i % NCOPY]
-            rt.q4_project_set([j["qkv"][0], j["gate"][0]], [None, j["up"][0]], x, H, 1, [qo, h])
-        torch.cuda.synchronize()
+        traffic_probe(rt, dev, rng, sets, args.traffic_probe)
         rt.close()
         return 0
     extras = {}
@@ -794,7 +941,8 @@ def main() -> int:
             "kernel_hbm_frac": {k: round((wb[k] + ab[k]) / (kern[k] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) for k in kern}}
         if M == 1:
             head = (gbs, ms, step_bytes, wb["qkv_gateup"] + ab["qkv_gateup"], kern["qkv_gateup"])
-            p10, p50, p90 = step_distribution(q4_leg.last_step, torch.cuda.current_stream(), max(args.steps, 100))
+            p10, p50, p90 = step_distribution(q4_leg.last_step, torch.cuda.current_stream(), max(args.steps, 100),
+                                              label="q4_set_M1:distribution")
             extras["q4_decode_set_M1"]["step_us_p10_p50_p90"] = [p10, p50, p90]
     if "decode" in legs:
         log("[bench] q4 matvec 4096x4096 (config 1)")

@@ -45,6 +45,9 @@ struct Tuning {
   int q4_plan_log = 0;      // QM38_Q4_PLAN_LOG: print each new decode plan
   int q4_fuse = 1;          // QM38_Q4_FUSE: 0 runs the MLP's down projection as its own launch
   int q4_stream = 1;        // QM38_Q4_STREAM: 0 keeps single-row projections on the MFMA decode kernel
+  int q4_stream_wgs = 0;    // QM38_Q4_STREAM_WGS: workgroups per K part of the single-row kernel
+  int q4_stream_c = 0;      // QM38_Q4_STREAM_C: chunks per wave of the single-row kernel (1..4)
+  int q4_stream_w = 0;      // QM38_Q4_STREAM_W: waves per workgroup with QM38_Q4_STREAM_C
   int gemm_splits = 0;      // QM38_GEMM_SPLITS: K splits of the prefill GEMM
   int gemm_q = 0;           // QM38_GEMM_Q: stream-K steps per worker
   int gemm_plan_log = 0;    // QM38_GEMM_PLAN_LOG

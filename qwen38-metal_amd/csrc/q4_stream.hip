@@ -464,7 +464,9 @@ const void* kernel_for() {
 const void* pick_kernel(int c, int sb) {
   if (c == 1) return sb == 2 ? kernel_for<1, 2>() : kernel_for<1, 1>();
   if (c == 2) return sb == 2 ? kernel_for<2, 2>() : kernel_for<2, 1>();
-  return sb == 1 ? kernel_for<3, 1>() : nullptr;
+  if (c == 3) return sb == 1 ? kernel_for<3, 1>() : kernel_for<3, 2>();
+  if (c == 4) return sb == 1 ? kernel_for<4, 1>() : nullptr;
+  return nullptr;
 }
 
 // One K part: up to 16 waves of 2 chunks (K <= 16384), or for plain jobs of
@@ -501,10 +503,16 @@ StreamPlan make_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const Tun
     p.waves = kPartWaves;
     p.parts = (chunks + kPartWaves * kPartC - 1) / (kPartWaves * kPartC);
   }
+  if (tn.q4_stream_c > 0) {  // forced chunks per wave (and waves per part)
+    p.C = (uint32_t)tn.q4_stream_c;
+    p.waves = tn.q4_stream_w > 0 ? (uint32_t)tn.q4_stream_w : std::min<uint32_t>(kMaxWaves, (chunks + p.C - 1) / p.C);
+    p.parts = (chunks + p.waves * p.C - 1) / (p.waves * p.C);
+  }
   p.part_chunks = p.waves * p.C;
   p.SB = pair ? 2 : 1;
   for (int i = 0; i < n_jobs; ++i) p.total_blocks += job_blocks(jobs[i].rows, jobs[i].mode, p.SB);
-  p.fn = pick_kernel((int)p.C, (int)p.SB);
+  p.fn = p.waves >= 1 && p.waves <= (uint32_t)kMaxWaves ? pick_kernel((int)p.C, (int)p.SB) : nullptr;
+  if (!p.fn) return p;
   const uint32_t cus = tn.cus > 0 ? (uint32_t)tn.cus : 256;
   // Workgroups: as many as stay resident (one dispatch round), with at most
   // `cap` blocks each (the table entries a wave fetches); more workgroups,
@@ -518,7 +526,12 @@ StreamPlan make_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const Tun
   }
   const uint32_t resident = std::max<uint32_t>(1, (uint32_t)occ * cus / p.parts);
   const uint32_t wgs_min = (p.total_blocks + cap - 1) / cap;
-  p.wgs = std::max(wgs_min, std::min(p.total_blocks, resident));
+  // At least two blocks per workgroup: a workgroup's fixed part (table and
+  // activation loads, the partial-sum exchange) over one block of a small
+  // projection costs more than the fuller dispatch gains (4096 x 4096: 7.2 us
+  // with 1024 one-block workgroups, 5.8 us with 512; 4096 -> 5120: 7.9 / 5.9).
+  p.wgs = std::max(wgs_min, std::min((p.total_blocks + 1) / 2, resident));
+  if (tn.q4_stream_wgs > 0) p.wgs = std::max(wgs_min, std::min(p.total_blocks, (uint32_t)tn.q4_stream_wgs));
   p.max_blocks = (p.total_blocks + p.wgs - 1) / p.wgs;
   p.lds = head_bytes(p.waves, p.SB, p.max_blocks) + p.waves * table_bytes(p.max_blocks, p.SB, p.C);
   if (p.parts > 1) {
