@@ -286,8 +286,12 @@ qm_status qm_attn_decode(qm_runtime* rt, qm_kv* const* seqs, uint32_t B,
  * must have room for its token (qm_kv_reserve beforehand), else
  * QM_ERR_CAPACITY_EXCEEDED; a split plan needing more than 16 MiB of
  * partials (H * (head_dim_pad + 2) * 4 bytes per split) fails with
- * QM_ERR_CAPACITY_EXCEEDED as well.  All calls on one GPU share the array:
- * calls that overlap on that GPU (other streams or threads) race. */
+ * QM_ERR_CAPACITY_EXCEEDED as well.  All calls on one GPU share the array,
+ * so the library orders them: a call made on another stream than the
+ * previous call on that GPU first makes its stream wait for the previous
+ * call's completion (an event the library records after every call), and
+ * calls from several threads take a per-GPU lock while they enqueue.  Calls
+ * therefore run one after another on the GPU; they never overlap. */
 qm_status qm_attn_decode_noalloc(qm_runtime* rt, qm_kv* const* seqs, uint32_t B,
                                  const uint16_t* q, const uint16_t* gate,
                                  const float* k, const float* v, uint32_t H,

@@ -69,6 +69,15 @@ struct AttnScratch {
   size_t partial_bytes;
 };
 hipError_t attn_noalloc_scratch(int device, AttnScratch* out);
+// Brackets the launches of one call that uses the array (after
+// attn_noalloc_scratch succeeded on the device): begin takes the device's
+// lock and, when the previous call ran on another stream, makes `stream`
+// wait for that call's completion event; end records this call's event on
+// `stream` and releases the lock.  So calls from several streams or threads
+// on one GPU run one after another on the device instead of racing on the
+// shared partials.
+hipError_t attn_noalloc_begin(int device, hipStream_t stream);
+hipError_t attn_noalloc_end(int device, hipStream_t stream);
 
 hipError_t launch_q8_append(const AppendArgs& a, uint32_t items, hipStream_t st);
 // Decode: `units` workgroups; when need_combine, q8_combine_kernel merges the

@@ -1066,6 +1066,16 @@ void* g_scratch_ptr[kMaxDevices];
 hipError_t g_scratch_err[kMaxDevices];
 std::once_flag g_scratch_once[kMaxDevices];
 
+// Calls sharing one GPU's array are ordered: a call on another stream than
+// the previous one waits for that call's completion event first.
+struct ScratchOrder {
+  std::mutex mu;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+  bool used = false;
+};
+ScratchOrder g_order[kMaxDevices];
+
 }  // namespace
 
 hipError_t attn_noalloc_scratch(int device, AttnScratch* out) {
@@ -1075,11 +1085,36 @@ hipError_t attn_noalloc_scratch(int device, AttnScratch* out) {
     void* ptr = nullptr;
     g_scratch_err[device] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     g_scratch_ptr[device] = ptr;
+    if (g_scratch_err[device] == hipSuccess)
+      g_scratch_err[device] = hipEventCreateWithFlags(&g_order[device].done, hipEventDisableTiming);
   });
   if (g_scratch_err[device] != hipSuccess) return g_scratch_err[device];
   out->partials = (float*)g_scratch_ptr[device];
   out->partial_bytes = kScratchPartialBytes;
   return hipSuccess;
+}
+
+hipError_t attn_noalloc_begin(int device, hipStream_t stream) {
+  if (device < 0 || device >= kMaxDevices || !g_order[device].done) return hipErrorInvalidDevice;
+  ScratchOrder& o = g_order[device];
+  o.mu.lock();
+  if (o.used && o.last != stream) {
+    const hipError_t e = hipStreamWaitEvent(stream, o.done, 0);
+    if (e != hipSuccess) {
+      o.mu.unlock();
+      return e;
+    }
+  }
+  return hipSuccess;
+}
+
+hipError_t attn_noalloc_end(int device, hipStream_t stream) {
+  ScratchOrder& o = g_order[device];
+  const hipError_t e = hipEventRecord(o.done, stream);
+  o.used = e == hipSuccess;
+  o.last = stream;
+  o.mu.unlock();
+  return e;
 }
 
 }  // namespace qm

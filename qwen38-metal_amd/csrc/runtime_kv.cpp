@@ -595,7 +595,10 @@ qm_status qm_attn_decode_noalloc(qm_runtime* rt, qm_kv* const* seqs, uint32_t B,
   if (pb > ws.partial_bytes)
     return fail(QM_ERR_CAPACITY_EXCEEDED, "split partials of %zu bytes exceed the %zu-byte no-allocation scratch", pb,
                 ws.partial_bytes);
-  return launch_decode(rt, seqs, B, q, gate, k, v, H, o, chunks, ws.partials, ws.partial_bytes);
+  if ((st = hip_check(attn_noalloc_begin(rt->device, rt->stream), "no-allocation ordering")) != QM_OK) return st;
+  st = launch_decode(rt, seqs, B, q, gate, k, v, H, o, chunks, ws.partials, ws.partial_bytes);
+  const qm_status end = hip_check(attn_noalloc_end(rt->device, rt->stream), "no-allocation ordering");
+  return st != QM_OK ? st : end;
 }
 
 qm_status qm_attn_prefill(qm_runtime* rt, qm_kv* seq, const uint16_t* q, const uint16_t* gate, const float* k,

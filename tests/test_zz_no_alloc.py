@@ -8,7 +8,8 @@ bytes must therefore be bit-identical.  Two calls in a row, the second with a
 smaller batch and shorter sequences, so the array keeps the first call's
 contents when the second reads it.  Also: the caches are not grown (a full
 cache is refused), and a plan needing more partials than the array holds is
-refused, both without touching the caches.
+refused, both without touching the caches; and calls from two streams are
+ordered by the library instead of racing on the shared array.
 """
 from __future__ import annotations
 
@@ -72,6 +73,35 @@ def test_noalloc_matches_decode_twice(rt, torch_dev):
                 assert np.array_equal(u, w)
         for c in a + b:
             c.close()
+
+
+def test_noalloc_calls_on_two_streams_do_not_overlap(rt, torch_dev):
+    """Two runtimes on two streams call the entry point back to back with no
+    host synchronisation between them.  Both calls share the GPU's array;
+    the library makes the second stream wait for the first call, so each
+    output equals its allocating twin's bit for bit."""
+    import torch
+    rng = np.random.default_rng(710)
+    a1, b1 = _pair(rt, torch_dev, rng, [30000, 700])
+    a2, b2 = _pair(rt, torch_dev, rng, [20000, 9000])
+    in1, in2 = _inputs(rng, 2), _inputs(rng, 2)
+    want1 = _decode(rt.gqa_attention_q8, torch_dev, a1, *in1)
+    want2 = _decode(rt.gqa_attention_q8, torch_dev, a2, *in2)
+    d1 = [to_dev(t, torch_dev) for t in in1]
+    d2 = [to_dev(t, torch_dev) for t in in2]
+    o1, o2 = empty_bf16((2, H, D), torch_dev), empty_bf16((2, H, D), torch_dev)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    with tuned() as r1, tuned() as r2:
+        r1.set_stream(s1)
+        r2.set_stream(s2)
+        r1.gqa_attention_q8_noalloc(b1, *d1, H, o1)
+        r2.gqa_attention_q8_noalloc(b2, *d2, H, o2)
+        torch.cuda.synchronize()
+    assert np.array_equal(bf16_dev_to_f32(o1).view(np.uint32), want1.view(np.uint32))
+    assert np.array_equal(bf16_dev_to_f32(o2).view(np.uint32), want2.view(np.uint32))
+    for c in a1 + b1 + a2 + b2:
+        c.close()
 
 
 def test_noalloc_refuses_growth_and_oversized_plans(rt, torch_dev):
