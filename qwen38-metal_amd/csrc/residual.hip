@@ -8,9 +8,10 @@
 // * w, in fp32, with the weights used as given (not 1 + w).  The residual
 // stream `hidden` stays fp32 (the reference's activations are fp32); the
 // normalised rows are rounded to bf16, the Q4 projections' input type.
-// One 256-thread workgroup per row: the row is read with 16-byte loads, the
-// sum of squares is reduced across lanes by DPP and across the four waves in
-// LDS, and the row is read again (from L2) to write the output.
+// One 1024-thread workgroup per row: the row is read with 16-byte loads
+// (kept in registers up to 8192 elements), the sum of squares is reduced
+// across lanes by DPP and across the 16 waves in LDS, and the output is
+// written from the registers.
 #include "common.h"
 #include "internal.h"
 
@@ -19,7 +20,8 @@
 namespace qm {
 namespace {
 
-constexpr int kNormThreads = 256;
+constexpr int kNormThreads = 1024;
+constexpr int kNormCache = 2;  // float4s per thread kept in registers between the two passes
 
 struct NormArgs {
   float* hidden;          // [M][n] fp32, updated in place when delta != NULL
@@ -31,6 +33,16 @@ struct NormArgs {
   float eps;
 };
 
+__device__ __forceinline__ u32x2 norm4(const floatx4& v, const floatx4& w, float scale) {
+  u32x2 r;
+  r.x = f32_to_bf16(v[0] * scale * w[0]) | ((uint32_t)f32_to_bf16(v[1] * scale * w[1]) << 16);
+  r.y = f32_to_bf16(v[2] * scale * w[2]) | ((uint32_t)f32_to_bf16(v[3] * scale * w[3]) << 16);
+  return r;
+}
+
+// One 1024-thread workgroup per row.  A thread's first kNormCache float4s
+// (all of a 8192-wide row) stay in registers from the first pass to the
+// second, with their weights loaded up front; wider rows re-read the rest.
 __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(NormArgs a) {
   __shared__ float part[kNormThreads / 64];
   const uint32_t row = blockIdx.x, tid = threadIdx.x, n = a.n;
@@ -38,40 +50,65 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(NormArgs
   const uint16_t* d = a.delta ? a.delta + (size_t)row * n : nullptr;
   uint16_t* o = a.out + (size_t)row * n;
   const uint32_t n4 = a.vec ? n / 4 : 0;  // else element by element
+  floatx4 v[kNormCache], wv[kNormCache];
+#pragma unroll
+  for (int k = 0; k < kNormCache; ++k) {
+    const uint32_t i = min(tid + k * kNormThreads, n4 > 0 ? n4 - 1 : 0);
+    if (n4 > 0) {
+      v[k] = *(const floatx4*)(h + 4 * i);
+      wv[k] = *(const floatx4*)(a.w + 4 * i);
+    }
+  }
   float ss = 0.0f;
-  for (uint32_t i = tid; i < n4; i += kNormThreads) {
-    floatx4 v = *(const floatx4*)(h + 4 * i);
+#pragma unroll
+  for (int k = 0; k < kNormCache; ++k) {
+    const uint32_t i = tid + k * kNormThreads;
+    if (i < n4) {
+      if (d) {
+        const u32x2 dv = *(const u32x2*)(d + 4 * i);
+        v[k][0] += bf16_to_f32(dv.x & 0xFFFFu);
+        v[k][1] += bf16_to_f32(dv.x >> 16);
+        v[k][2] += bf16_to_f32(dv.y & 0xFFFFu);
+        v[k][3] += bf16_to_f32(dv.y >> 16);
+        *(floatx4*)(h + 4 * i) = v[k];
+      }
+      ss += v[k][0] * v[k][0] + v[k][1] * v[k][1] + v[k][2] * v[k][2] + v[k][3] * v[k][3];
+    }
+  }
+  for (uint32_t i = tid + kNormCache * kNormThreads; i < n4; i += kNormThreads) {
+    floatx4 x = *(const floatx4*)(h + 4 * i);
     if (d) {
       const u32x2 dv = *(const u32x2*)(d + 4 * i);
-      v[0] += bf16_to_f32(dv.x & 0xFFFFu);
-      v[1] += bf16_to_f32(dv.x >> 16);
-      v[2] += bf16_to_f32(dv.y & 0xFFFFu);
-      v[3] += bf16_to_f32(dv.y >> 16);
-      *(floatx4*)(h + 4 * i) = v;
+      x[0] += bf16_to_f32(dv.x & 0xFFFFu);
+      x[1] += bf16_to_f32(dv.x >> 16);
+      x[2] += bf16_to_f32(dv.y & 0xFFFFu);
+      x[3] += bf16_to_f32(dv.y >> 16);
+      *(floatx4*)(h + 4 * i) = x;
     }
-    ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+    ss += x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
   }
   for (uint32_t i = 4 * n4 + tid; i < n; i += kNormThreads) {
-    float v = h[i];
+    float x = h[i];
     if (d) {
-      v += bf16_to_f32(d[i]);
-      h[i] = v;
+      x += bf16_to_f32(d[i]);
+      h[i] = x;
     }
-    ss += v * v;
+    ss += x * x;
   }
   ss = wave_allsum(ss);
   if ((tid & 63) == 0) part[tid >> 6] = ss;
   __syncthreads();
-  const float total = part[0] + part[1] + part[2] + part[3];
+  float total = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / 64; ++w) total += part[w];
   const float scale = 1.0f / sqrtf(total / (float)n + a.eps);
-  for (uint32_t i = tid; i < n4; i += kNormThreads) {
-    const floatx4 v = *(const floatx4*)(h + 4 * i);
-    const floatx4 w = *(const floatx4*)(a.w + 4 * i);
-    u32x2 r;
-    r.x = f32_to_bf16(v[0] * scale * w[0]) | ((uint32_t)f32_to_bf16(v[1] * scale * w[1]) << 16);
-    r.y = f32_to_bf16(v[2] * scale * w[2]) | ((uint32_t)f32_to_bf16(v[3] * scale * w[3]) << 16);
-    *(u32x2*)(o + 4 * i) = r;
+#pragma unroll
+  for (int k = 0; k < kNormCache; ++k) {
+    const uint32_t i = tid + k * kNormThreads;
+    if (i < n4) *(u32x2*)(o + 4 * i) = norm4(v[k], wv[k], scale);
   }
+  for (uint32_t i = tid + kNormCache * kNormThreads; i < n4; i += kNormThreads)
+    *(u32x2*)(o + 4 * i) = norm4(*(const floatx4*)(h + 4 * i), *(const floatx4*)(a.w + 4 * i), scale);
   for (uint32_t i = 4 * n4 + tid; i < n; i += kNormThreads) o[i] = f32_to_bf16(h[i] * scale * a.w[i]);
 }
 
