@@ -8,7 +8,7 @@ time (GB/s), inputs resident in HBM.  Three copies of the weights (540 MB)
 rotate between steps so the 256 MB MALL cannot serve them.
 
 `extras` carries the other legs of the metric, each against its roofline:
-the decode set at 4 and 8 rows; Q8-KV decode attention at 32K context
+the decode set at 2, 4 and 8 rows; Q8-KV decode attention at 32K context
 (us/token) and a ragged batch of 8 sequences over {4K, 32K, 128K}; causal
 prefill attention (2048 rows onto a 4K cache); the Q4 prefill GEMM set at
 M = 512 and 2048 (TFLOP/s); the Gated DeltaNet decode step and 2048-token
@@ -930,7 +930,7 @@ def main() -> int:
     extras = {}
     head = None
     legs = set() if args.quick else set(args.legs.split(","))
-    for M in (1, 4, 8) if "decode" in legs else (1,):
+    for M in (1, 2, 4, 8) if "decode" in legs else (1,):
         log(f"[bench] q4 decode set M={M}")
         ms, kern, wb, ab, _ = q4_leg(rt, dev, sets, M, rng, args.steps, args.warmup)
         step_bytes = sum(wb.values()) + sum(ab.values())

@@ -45,6 +45,8 @@ struct Tuning {
   int q4_plan_log = 0;      // QM38_Q4_PLAN_LOG: print each new decode plan
   int q4_fuse = 1;          // QM38_Q4_FUSE: 0 runs the MLP's down projection as its own launch
   int q4_stream = 1;        // QM38_Q4_STREAM: 0 keeps single-row projections on the MFMA decode kernel
+  int q4_stream_mw = 0;     // QM38_Q4_STREAM_MW: waves per K part with several activation rows
+  int q4_stream_rows = 2;   // QM38_Q4_STREAM_ROWS: most activation rows on the streaming kernel (1, 2)
   int q4_stream_wgs = 0;    // QM38_Q4_STREAM_WGS: workgroups per K part of the single-row kernel
   int q4_stream_c = 0;      // QM38_Q4_STREAM_C: chunks per wave of the single-row kernel (1..4)
   int q4_stream_w = 0;      // QM38_Q4_STREAM_W: waves per workgroup with QM38_Q4_STREAM_C
@@ -77,16 +79,17 @@ struct Workspace {
 hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x,
                             uint32_t K, uint32_t M, const Workspace& ws, hipStream_t stream);
 
-// Single activation row (M = 1): the K-resident streaming kernel
-// (q4_stream.hip).  Jobs may mix plain projections and gate/up pairs
-// (kQ4OutSwiglu); an argmax launch has one job.
+// One or two activation rows (QM38_Q4_STREAM_ROWS=1 keeps two rows on the
+// MFMA decode kernel): the K-resident streaming kernel (q4_stream.hip).  Jobs may mix
+// plain projections and gate/up pairs (kQ4OutSwiglu); an argmax launch has
+// one job and one row.
 bool q4_stream_supported(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn);
-hipError_t launch_q4_stream(const Q4Job* jobs, int n_jobs, const uint16_t* x, uint32_t K, const Workspace& ws,
-                            hipStream_t stream);
+hipError_t launch_q4_stream(const Q4Job* jobs, int n_jobs, const uint16_t* x, uint32_t K, uint32_t M,
+                            const Workspace& ws, hipStream_t stream);
 // Workspace of a streaming launch: fp32 partial rows and counters when K is
 // split over several workgroups (zero otherwise).
-void q4_stream_workspace(const Q4Job* jobs, int n_jobs, uint32_t K, const Tuning& tn, size_t* partial_bytes,
-                         size_t* counters);
+void q4_stream_workspace(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn,
+                         size_t* partial_bytes, size_t* counters);
 
 // ids[m] from the argmax keys of a kQ4OutArgmax decode launch; zeroes the keys.
 hipError_t launch_q4_argmax_finish(unsigned long long* keys, uint32_t* ids, uint32_t M, hipStream_t stream);

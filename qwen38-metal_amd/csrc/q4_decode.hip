@@ -544,9 +544,12 @@ Plan make_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t 
   const uint32_t cus = tn.cus > 0 ? (uint32_t)tn.cus : 256;
   int nt = swiglu ? 2 : ((rows / 32 >= (uint64_t)cus * 2) ? 2 : 1);
   if (!swiglu && tn.q4_nt > 0) nt = tn.q4_nt >= 2 ? 2 : 1;
-  // Staged activations when all M rows fit (each wave holds its K slice).
+  // Staged activations for one row when it fits (each wave holds its K
+  // slice); several rows take the register path, whatever their size (two
+  // or three 5120-wide rows fit the staging buffer but ran the QKV + gate/up
+  // set in 61-64 us staged against 40 us for four rows on registers).
   const uint32_t x_max = tn.q4_xstage_max > 0 ? (uint32_t)tn.q4_xstage_max : kXStageMax;
-  const bool xw = M * (K * 2 + 16) <= x_max && tn.q4_xstage != 0;
+  const bool xw = (M == 1 || tn.q4_xstage_max > 0) && M * (K * 2 + 16) <= x_max && tn.q4_xstage != 0;
   const bool g8 = (G % 8) == 0;
   const void* fn = swiglu ? instance_m<2, true>(M, g8, xw)
                           : (nt == 2 ? instance_m<2, false>(M, g8, xw) : instance_m<1, false>(M, g8, xw));

@@ -1,4 +1,4 @@
-// MLX affine-Q4 projection of ONE activation row (decode, M = 1) for MI355X
+// MLX affine-Q4 projection of one or two activation rows (decode) for MI355X
 // (gfx950): the math of qwen38_q4_affine_matvec_simd
 // (/root/reference/shaders/qwen38.metal:213-246),
 //     y[n] = sum_g ( s[n][g] * sum_{i in g} q[n][i] x[i] + b[n][g] * sum_{i in g} x[i] ).
@@ -7,7 +7,9 @@
 //  * K is cut into 512-element chunks (256 bytes of every weight row).  A
 //    workgroup has W waves; wave w owns chunks [w*C, w*C + C) and keeps the
 //    activation of those chunks in VGPRs for the whole launch, so neither the
-//    weights nor the activation pass through LDS.
+//    weights nor the activation pass through LDS.  With two activation rows
+//    (MR = 2, one chunk per wave) every unpacked weight word meets both rows'
+//    activations.
 //  * One 128-bit load per lane covers 4 rows x 256 bytes: lane l reads 16
 //    bytes (32 nibbles, half of a 64-group) of row l/16 at column 16*(l%16).
 //    Loads are coalesced (16 lanes read one contiguous 256-byte run) and
@@ -63,6 +65,7 @@ struct StreamArgs {
   uint32_t parts, part_chunks;
   float* partials;
   unsigned* counters;
+  uint32_t M;  // activation rows (x is [M][K]; outputs [M][rows]), at most the kernel's MR
   Q4Job jobs[kMaxQ4Jobs];  // tile_begin = first block of the job
 };
 
@@ -104,9 +107,9 @@ __host__ __device__ constexpr uint32_t table_entries(uint32_t blocks, int sb, in
 __host__ __device__ constexpr uint32_t table_bytes(uint32_t blocks, int sb, int c) {
   return table_entries(blocks, sb, c) * 64;
 }
-// LDS ahead of the tables: every wave's row partials [wave][block][4 SB].
-__host__ __device__ constexpr uint32_t head_bytes(uint32_t waves, int sb, uint32_t blocks) {
-  return waves * blocks * 4 * sb * 4;
+// LDS ahead of the tables: every wave's row partials [wave][block][4 SB][MR].
+__host__ __device__ constexpr uint32_t head_bytes(uint32_t waves, int sb, uint32_t blocks, uint32_t mr = 1) {
+  return waves * blocks * 4 * sb * 4 * mr;
 }
 
 // Byte offset, inside a job's tensor, of row `r` of load `s` of block `jb`
@@ -115,9 +118,10 @@ __device__ __forceinline__ uint32_t block_row(uint32_t mode, int sb, uint32_t jb
   return mode == kQ4OutSwiglu ? 4 * jb : (4 * sb) * jb + 4 * s;
 }
 
-template <int C, int SB, int RB>
+template <int C, int SB, int RB, int MR>
 __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  static_assert(MR == 1 || MR == 2, "activation rows");
   constexpr int kPer = SB * C;     // loads per block per wave
   constexpr int kD = kPer * RB;    // ring slots
   const int lane = threadIdx.x & 63;
@@ -137,9 +141,9 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
 
   // LDS: partial slots, then each wave's tables.
   const uint32_t rows_wg = args.max_blocks * 4 * SB;  // partial rows per wave
-  float* parts = (float*)smem;                        // [W][max_blocks * 4 SB]
+  float* parts = (float*)smem;                        // [W][max_blocks * 4 SB][MR]
   const uint32_t tab_wave = table_bytes(args.max_blocks, SB, C);
-  uint8_t* tab = smem + head_bytes(W, SB, args.max_blocks) + wave * tab_wave;
+  uint8_t* tab = smem + head_bytes(W, SB, args.max_blocks, MR) + wave * tab_wave;
 
   // Block -> job (blocks of a job are contiguous).
   auto job_of = [&](uint32_t blk) __attribute__((always_inline)) {
@@ -199,18 +203,27 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
   // --- activation chunks in registers ----------------------------------------
   // Lane (col) holds elements [chunk*512 + 32 col, +32), each 8-element run in
   // the unpack order (x0,x4)(x1,x5)(x2,x6)(x3,x7).
-  u32x4 xr[C][4];
-  float xsum[C];
+  u32x4 xr[MR][C][4];
+  float xsum[MR][C];
   bool valid[C];
   {
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(args.x, (uint64_t)K * 2);
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const uint32_t e0 = (c0 + c) * kChunkElems + 32 * col;
       valid[c] = c0 + c < args.chunks && e0 < K;
+    }
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        xr[c][q] = __builtin_amdgcn_raw_buffer_load_b128(rx, valid[c] ? e0 * 2 + 16 * q : kOOB, 0, 0);
+    for (int m = 0; m < MR; ++m) {
+      // Rows past M read nothing (a zero-length resource) and stay zero.
+      const __amdgpu_buffer_rsrc_t rx =
+          make_rsrc(args.x + (size_t)min((uint32_t)m, args.M - 1) * K, (uint32_t)m < args.M ? (uint64_t)K * 2 : 0);
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const uint32_t e0 = (c0 + c) * kChunkElems + 32 * col;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          xr[m][c][q] = __builtin_amdgcn_raw_buffer_load_b128(rx, valid[c] ? e0 * 2 + 16 * q : kOOB, 0, 0);
+      }
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -284,19 +297,21 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
     }
   }
 #pragma unroll
-  for (int c = 0; c < C; ++c) {
+  for (int m = 0; m < MR; ++m)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) xr[c][q] = interleave_bf16x8(xr[c][q]);
-    float sum = 0.f;
+    for (int c = 0; c < C; ++c) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      sum += bf16_to_f32(xr[c][q].x & 0xFFFF) + bf16_to_f32(xr[c][q].x >> 16);
-      sum += bf16_to_f32(xr[c][q].y & 0xFFFF) + bf16_to_f32(xr[c][q].y >> 16);
-      sum += bf16_to_f32(xr[c][q].z & 0xFFFF) + bf16_to_f32(xr[c][q].z >> 16);
-      sum += bf16_to_f32(xr[c][q].w & 0xFFFF) + bf16_to_f32(xr[c][q].w >> 16);
+      for (int q = 0; q < 4; ++q) xr[m][c][q] = interleave_bf16x8(xr[m][c][q]);
+      float sum = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        sum += bf16_to_f32(xr[m][c][q].x & 0xFFFF) + bf16_to_f32(xr[m][c][q].x >> 16);
+        sum += bf16_to_f32(xr[m][c][q].y & 0xFFFF) + bf16_to_f32(xr[m][c][q].y >> 16);
+        sum += bf16_to_f32(xr[m][c][q].z & 0xFFFF) + bf16_to_f32(xr[m][c][q].z >> 16);
+        sum += bf16_to_f32(xr[m][c][q].w & 0xFFFF) + bf16_to_f32(xr[m][c][q].w >> 16);
+      }
+      xsum[m][c] = sum;
     }
-    xsum[c] = sum;
-  }
 
   const uint32_t mask_s = __builtin_amdgcn_readfirstlane(0x000F000Fu);
   uint32_t or_v = 0x43004300u;
@@ -305,52 +320,65 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
   // One slot: the lane's contribution s*p + (b - 128 s)*X for its row/chunk.
   // Lanes past K see x = 0, X = 0 and a zero table entry: they add 0.
   const uint32_t tlane = rr * C * 64 + (col >> 1) * 8;
-  auto consume = [&](const u32x4& wv, uint32_t jl, int s, int c) __attribute__((always_inline)) {
+  auto consume = [&](const u32x4& wv, uint32_t jl, int s, int c, float (&acc)[MR]) __attribute__((always_inline)) {
     const uint32_t e0 = ((s * nblk + jl) * 4) * C + c;  // entry of row 0 of the load
     const u32x2 tv = *(const u32x2*)(tab + e0 * 64 + tlane);
     const float sc = __uint_as_float(tv.x), cb = __uint_as_float(tv.y);
-    float p0 = 0.f, p1 = 0.f;
+    float p0[MR], p1[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) p0[m] = p1[m] = 0.f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const uint32_t wq = q == 0 ? wv.x : q == 1 ? wv.y : q == 2 ? wv.z : wv.w;
-      const u32x4 xq = xr[c][q];
-      p0 = dot2((wq & mask_s) | or_v, xq.x, p0);
-      p1 = dot2(((wq >> 4) & mask_s) | or_v, xq.y, p1);
-      p0 = dot2(((wq >> 8) & mask_s) | or_v, xq.z, p0);
-      p1 = dot2(((wq >> 12) & mask_s) | or_v, xq.w, p1);
+      const uint32_t u0 = (wq & mask_s) | or_v, u1 = ((wq >> 4) & mask_s) | or_v;
+      const uint32_t u2 = ((wq >> 8) & mask_s) | or_v, u3 = ((wq >> 12) & mask_s) | or_v;
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const u32x4 xq = xr[m][c][q];
+        p0[m] = dot2(u0, xq.x, p0[m]);
+        p1[m] = dot2(u1, xq.y, p1[m]);
+        p0[m] = dot2(u2, xq.z, p0[m]);
+        p1[m] = dot2(u3, xq.w, p1[m]);
+      }
     }
-    return fmaf(sc, p0 + p1, cb * xsum[c]);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] += fmaf(sc, p0[m] + p1[m], cb * xsum[m][c]);
   };
 
   // A finished block: each row's sum over this wave's chunks (the 16 lanes of
   // the row) goes to the wave's partial row; the waves' partials are added
   // in wave order after the stream (deterministic, no synchronisation here).
-  auto finish_block = [&](uint32_t jl, const float (&acc)[SB]) __attribute__((always_inline)) {
+  auto finish_block = [&](uint32_t jl, const float (&acc)[SB][MR]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int s = 0; s < SB; ++s) {
-      const float v = row16_sum(acc[s]);
-      if (col == 0) parts[wave * rows_wg + jl * 4 * SB + s * 4 + rr] = v;
-    }
+    for (int s = 0; s < SB; ++s)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const float v = row16_sum(acc[s][m]);
+        if (col == 0) parts[(wave * rows_wg + jl * 4 * SB + s * 4 + rr) * MR + m] = v;
+      }
   };
 
   auto round = [&](uint32_t r, bool refill) __attribute__((always_inline)) {
 #pragma unroll
     for (int bi = 0; bi < RB; ++bi) {
       const uint32_t jl = r * RB + bi;
-      float acc[SB];
+      float acc[SB][MR];
 #pragma unroll
-      for (int s = 0; s < SB; ++s) acc[s] = 0.f;
+      for (int s = 0; s < SB; ++s)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[s][m] = 0.f;
 #pragma unroll
       for (int s = 0; s < SB; ++s)
 #pragma unroll
         for (int c = 0; c < C; ++c) {
           const int t = bi * kPer + s * C + c;
-          acc[s] += consume(ring[t], jl, s, c);
+          consume(ring[t], jl, s, c, acc[s]);
           if (refill) {
             // The slot's math is done before its refill is issued (an IR-level
             // barrier too, so the math is not sunk below the load, which would
             // keep both register sets alive and copy the ring every round).
-            asm volatile("" : "+v"(acc[s]) : : "memory");
+#pragma unroll
+            for (int m = 0; m < MR; ++m) asm volatile("" : "+v"(acc[s][m]) : : "memory");
             __builtin_amdgcn_sched_barrier(0);
             ring[t] = load_w(jl + RB, s, c);
             __builtin_amdgcn_sched_barrier(0);
@@ -369,15 +397,17 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
   lds_barrier();
   const uint32_t rows_per_block = 4 * SB;
   const uint32_t nrows = nblk * rows_per_block;
-  // The workgroup's row i (local block i / 4SB, row i % 4SB) over this
-  // workgroup's chunks: its waves' partials in wave order.
-  auto row_sum = [&](uint32_t i) __attribute__((always_inline)) {
+  const uint32_t nvals = nrows * MR;  // value f = (local row) * MR + activation row
+  // Value f of the workgroup (local block f / (4SB MR), weight row
+  // (f / MR) % 4SB, activation row f % MR) over this workgroup's chunks: its
+  // waves' partials in wave order.
+  auto row_sum = [&](uint32_t f) __attribute__((always_inline)) {
     float v = 0.f;
-    for (uint32_t w2 = 0; w2 < W; ++w2) v += parts[w2 * rows_wg + i];
+    for (uint32_t w2 = 0; w2 < W; ++w2) v += parts[w2 * rows_wg * MR + f];
     return v;
   };
-  const uint32_t TB = args.total_blocks * rows_per_block;  // partial rows per K part
-  float* pp = args.partials + (size_t)b_begin * rows_per_block;
+  const uint32_t TB = args.total_blocks * rows_per_block * MR;  // partial values per K part
+  float* pp = args.partials + (size_t)b_begin * rows_per_block * MR;
   // Row i over all K parts, in part order (the same sum whichever part
   // finishes last).
   // The partial rows and the counter are accessed as device-scope relaxed
@@ -393,8 +423,8 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
     return v;
   };
   if (args.parts > 1) {
-    for (uint32_t i = threadIdx.x; i < nrows; i += blockDim.x)
-      __hip_atomic_store(&pp[(size_t)part * TB + i], row_sum(i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (uint32_t f = threadIdx.x; f < nvals; f += blockDim.x)
+      __hip_atomic_store(&pp[(size_t)part * TB + f], row_sum(f), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
     __syncthreads();
     __shared__ uint32_t last;
@@ -409,8 +439,10 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
   auto value = [&](uint32_t i) __attribute__((always_inline)) {
     return args.parts > 1 ? part_sum(i) : row_sum(i);
   };
-  unsigned long long best = 0;  // argmax key of this thread's rows
-  for (uint32_t i = threadIdx.x; i < nrows; i += blockDim.x) {
+  unsigned long long best = 0;  // argmax key of this thread's rows (MR = 1)
+  for (uint32_t f = threadIdx.x; f < nvals; f += blockDim.x) {
+    const uint32_t i = f / MR, m = f % MR;
+    if (m >= args.M) continue;
     const uint32_t jl = i / rows_per_block, k = i % rows_per_block;
     const uint32_t blk = b_begin + jl;
     const int j = job_of(blk);
@@ -420,14 +452,15 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
       // k < 4: gate sums; k >= 4: the up sums of the same rows.
       const uint32_t row = 4 * lb + k;
       if (k < 4 && row < jb.rows) {
-        const float gsum = value(jl * rows_per_block + k), usum = value(jl * rows_per_block + 4 + k);
-        jb.out[row] = f32_to_bf16(silu_f(gsum) * usum);
+        const float gsum = value((jl * rows_per_block + k) * MR + m);
+        const float usum = value((jl * rows_per_block + 4 + k) * MR + m);
+        jb.out[(size_t)m * jb.rows + row] = f32_to_bf16(silu_f(gsum) * usum);
       }
       continue;
     }
     const uint32_t row = rows_per_block * lb + k;
     if (row >= jb.rows) continue;
-    const float v = value(i);
+    const float v = value(f);
     if (jb.mode == kQ4OutArgmax) {
       if (!__builtin_isnan(v)) {
         const uint32_t bits = v == 0.0f ? 0u : __float_as_uint(v);
@@ -438,14 +471,15 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
       continue;
     }
     const uint16_t h = f32_to_bf16(v);
+    const size_t o = (size_t)m * jb.rows + row;
     if (jb.mode == kQ4OutBf16)
-      jb.out[row] = h;
+      jb.out[o] = h;
     else if (jb.mode == kQ4OutF32)
-      ((float*)jb.out)[row] = bf16_to_f32(h);
+      ((float*)jb.out)[o] = bf16_to_f32(h);
     else
-      ((float*)jb.out)[row] += bf16_to_f32(h);
+      ((float*)jb.out)[o] += bf16_to_f32(h);
   }
-  if (args.jobs[0].mode == kQ4OutArgmax) {
+  if (MR == 1 && args.jobs[0].mode == kQ4OutArgmax) {
     // One atomic per wave: the best key of its threads' rows.
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
@@ -456,12 +490,14 @@ __global__ __launch_bounds__(1024) void q4_stream_kernel(StreamArgs args) {
   }
 }
 
-template <int C, int SB>
+// Ring: 8 loads in flight per wave.
+template <int C, int SB, int MR = 1>
 const void* kernel_for() {
   constexpr int kRB = (8 / (SB * C)) > 1 ? 8 / (SB * C) : 1;
-  return (const void*)q4_stream_kernel<C, SB, kRB>;
+  return (const void*)q4_stream_kernel<C, SB, kRB, MR>;
 }
-const void* pick_kernel(int c, int sb) {
+const void* pick_kernel(int c, int sb, int mr = 1) {
+  if (mr == 2) return c == 1 ? (sb == 2 ? kernel_for<1, 2, 2>() : kernel_for<1, 1, 2>()) : nullptr;
   if (c == 1) return sb == 2 ? kernel_for<1, 2>() : kernel_for<1, 1>();
   if (c == 2) return sb == 2 ? kernel_for<2, 2>() : kernel_for<2, 1>();
   if (c == 3) return sb == 1 ? kernel_for<3, 1>() : kernel_for<3, 2>();
@@ -473,21 +509,31 @@ const void* pick_kernel(int c, int sb) {
 // 3 chunks (K <= 24576; measured on the 17408-wide down projection: 13 us
 // against 17 us split in parts).  Longer K runs in parts of 5 waves of 2
 // chunks whose fp32 row sums the last part adds.
-constexpr uint32_t kPartWaves = 5, kPartC = 2, kOnePartMax = 32, kOnePartMax3 = 48;
+constexpr uint32_t kPartWaves = 5, kPartC = 2, kOnePartMax = 32, kOnePartMax3 = 48, kRowsWaves = 8;
 
 struct StreamPlan {
   const void* fn = nullptr;
-  uint32_t waves = 0, C = 0, SB = 0, wgs = 0, max_blocks = 0, lds = 0, total_blocks = 0;
+  uint32_t waves = 0, C = 0, SB = 0, MR = 1, wgs = 0, max_blocks = 0, lds = 0, total_blocks = 0;
   uint32_t parts = 1, part_chunks = 0;
   size_t partial_bytes = 0, counters = 0;
 };
 
-StreamPlan make_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const Tuning& tn) {
+StreamPlan make_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn) {
   StreamPlan p{};
   const uint32_t chunks = (K + kChunkElems - 1) / kChunkElems;
   bool pair = false;
   for (int i = 0; i < n_jobs; ++i) pair |= jobs[i].mode == kQ4OutSwiglu;
-  if (chunks <= kOnePartMax) {
+  p.MR = M <= 1 ? 1 : 2;
+  if (p.MR > 1) {
+    // Two activation rows: one chunk per wave (each row's chunk takes 16
+    // VGPRs), K in balanced parts of at most kRowsWaves waves, so that
+    // several workgroups share a CU (measured at M = 2, 17408 wide: 19.4 us
+    // with 7-wave parts against 20.0 with 5-wave and 19.7 with 9-wave parts).
+    const uint32_t wmax = tn.q4_stream_mw > 0 ? std::min<uint32_t>(tn.q4_stream_mw, kMaxWaves) : kRowsWaves;
+    p.C = 1;
+    p.parts = (chunks + wmax - 1) / wmax;
+    p.waves = (chunks + p.parts - 1) / p.parts;
+  } else if (chunks <= kOnePartMax) {
     // Two chunks per wave even when one would do: fewer waves per workgroup,
     // more workgroups per CU and each block's per-row work over twice the
     // bytes (measured: QKV + gate/up set 32 -> 28 us).
@@ -503,7 +549,7 @@ StreamPlan make_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const Tun
     p.waves = kPartWaves;
     p.parts = (chunks + kPartWaves * kPartC - 1) / (kPartWaves * kPartC);
   }
-  if (tn.q4_stream_c > 0) {  // forced chunks per wave (and waves per part)
+  if (tn.q4_stream_c > 0 && p.MR == 1) {  // forced chunks per wave (and waves per part)
     p.C = (uint32_t)tn.q4_stream_c;
     p.waves = tn.q4_stream_w > 0 ? (uint32_t)tn.q4_stream_w : std::min<uint32_t>(kMaxWaves, (chunks + p.C - 1) / p.C);
     p.parts = (chunks + p.waves * p.C - 1) / (p.waves * p.C);
@@ -511,14 +557,14 @@ StreamPlan make_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const Tun
   p.part_chunks = p.waves * p.C;
   p.SB = pair ? 2 : 1;
   for (int i = 0; i < n_jobs; ++i) p.total_blocks += job_blocks(jobs[i].rows, jobs[i].mode, p.SB);
-  p.fn = p.waves >= 1 && p.waves <= (uint32_t)kMaxWaves ? pick_kernel((int)p.C, (int)p.SB) : nullptr;
+  p.fn = p.waves >= 1 && p.waves <= (uint32_t)kMaxWaves ? pick_kernel((int)p.C, (int)p.SB, (int)p.MR) : nullptr;
   if (!p.fn) return p;
   const uint32_t cus = tn.cus > 0 ? (uint32_t)tn.cus : 256;
   // Workgroups: as many as stay resident (one dispatch round), with at most
   // `cap` blocks each (the table entries a wave fetches); more workgroups,
   // in several rounds, only when the blocks exceed resident * cap.
   const uint32_t cap = kTabEntries / table_entries(1, (int)p.SB, (int)p.C);
-  const uint32_t lds_cap = head_bytes(p.waves, p.SB, cap) + p.waves * table_bytes(cap, p.SB, p.C);
+  const uint32_t lds_cap = head_bytes(p.waves, p.SB, cap, p.MR) + p.waves * table_bytes(cap, p.SB, p.C);
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, p.fn, (int)(64 * p.waves), lds_cap) != hipSuccess || occ <= 0) {
     p.fn = nullptr;
@@ -533,27 +579,27 @@ StreamPlan make_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const Tun
   p.wgs = std::max(wgs_min, std::min((p.total_blocks + 1) / 2, resident));
   if (tn.q4_stream_wgs > 0) p.wgs = std::max(wgs_min, std::min(p.total_blocks, (uint32_t)tn.q4_stream_wgs));
   p.max_blocks = (p.total_blocks + p.wgs - 1) / p.wgs;
-  p.lds = head_bytes(p.waves, p.SB, p.max_blocks) + p.waves * table_bytes(p.max_blocks, p.SB, p.C);
+  p.lds = head_bytes(p.waves, p.SB, p.max_blocks, p.MR) + p.waves * table_bytes(p.max_blocks, p.SB, p.C);
   if (p.parts > 1) {
-    p.partial_bytes = (size_t)p.parts * p.total_blocks * 4 * p.SB * sizeof(float);
+    p.partial_bytes = (size_t)p.parts * p.total_blocks * 4 * p.SB * p.MR * sizeof(float);
     p.counters = p.wgs;
   }
   if (tn.q4_plan_log > 0)
     fprintf(stderr,
-            "q4 stream plan: K=%u jobs=%d blocks=%u C=%u SB=%u waves=%u parts=%u wgs/part=%u max_blocks=%u lds=%u\n",
-            K, n_jobs, p.total_blocks, p.C, p.SB, p.waves, p.parts, p.wgs, p.max_blocks, p.lds);
+            "q4 stream plan: K=%u M=%u jobs=%d blocks=%u C=%u SB=%u waves=%u parts=%u wgs/part=%u max_blocks=%u lds=%u\n",
+            K, M, n_jobs, p.total_blocks, p.C, p.SB, p.waves, p.parts, p.wgs, p.max_blocks, p.lds);
   return p;
 }
 
 struct StreamKey {
   uint32_t rows[kMaxQ4Jobs], modes[kMaxQ4Jobs];
   int n_jobs;
-  uint32_t K;
+  uint32_t K, M;
   Tuning tune;
   bool operator==(const StreamKey& o) const { return std::memcmp(this, &o, sizeof(*this)) == 0; }
 };
 
-StreamPlan cached_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const Tuning& tn) {
+StreamPlan cached_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn) {
   static std::mutex mu;
   static StreamKey keys[16];
   static StreamPlan plans[16];
@@ -566,11 +612,12 @@ StreamPlan cached_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const T
   }
   k.n_jobs = n_jobs;
   k.K = K;
+  k.M = M;
   k.tune = tn;
   std::lock_guard<std::mutex> lock(mu);
   for (int i = 0; i < used; ++i)
     if (keys[i] == k) return plans[i];
-  const StreamPlan p = make_stream_plan(jobs, n_jobs, K, tn);
+  const StreamPlan p = make_stream_plan(jobs, n_jobs, K, M, tn);
   keys[next] = k;
   plans[next] = p;
   next = (next + 1) % 16;
@@ -581,23 +628,25 @@ StreamPlan cached_stream_plan(const Q4Job* jobs, int n_jobs, uint32_t K, const T
 }  // namespace
 
 bool q4_stream_supported(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn) {
-  if (M != 1 || tn.q4_stream == 0 || n_jobs < 1 || n_jobs > kMaxQ4Jobs) return false;
+  if (M < 1 || M > (uint32_t)std::min(tn.q4_stream_rows, 2) || tn.q4_stream == 0 || n_jobs < 1 ||
+      n_jobs > kMaxQ4Jobs)
+    return false;
   for (int i = 0; i < n_jobs; ++i)
-    if (jobs[i].mode > kQ4OutSwiglu || (jobs[i].mode == kQ4OutArgmax && n_jobs > 1)) return false;
-  return cached_stream_plan(jobs, n_jobs, K, tn).fn != nullptr;
+    if (jobs[i].mode > kQ4OutSwiglu || (jobs[i].mode == kQ4OutArgmax && (n_jobs > 1 || M > 1))) return false;
+  return cached_stream_plan(jobs, n_jobs, K, M, tn).fn != nullptr;
 }
 
-void q4_stream_workspace(const Q4Job* jobs, int n_jobs, uint32_t K, const Tuning& tn, size_t* partial_bytes,
-                         size_t* counters) {
-  const StreamPlan p = cached_stream_plan(jobs, n_jobs, K, tn);
+void q4_stream_workspace(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn,
+                         size_t* partial_bytes, size_t* counters) {
+  const StreamPlan p = cached_stream_plan(jobs, n_jobs, K, M, tn);
   *partial_bytes = p.partial_bytes;
   *counters = p.counters;
 }
 
-hipError_t launch_q4_stream(const Q4Job* jobs, int n_jobs, const uint16_t* x, uint32_t K, const Workspace& ws,
-                            hipStream_t stream) {
-  if (!ws.tune || n_jobs < 1 || n_jobs > kMaxQ4Jobs) return hipErrorInvalidValue;
-  const StreamPlan p = cached_stream_plan(jobs, n_jobs, K, *ws.tune);
+hipError_t launch_q4_stream(const Q4Job* jobs, int n_jobs, const uint16_t* x, uint32_t K, uint32_t M,
+                            const Workspace& ws, hipStream_t stream) {
+  if (!ws.tune || n_jobs < 1 || n_jobs > kMaxQ4Jobs || M < 1 || M > 2) return hipErrorInvalidValue;
+  const StreamPlan p = cached_stream_plan(jobs, n_jobs, K, M, *ws.tune);
   if (!p.fn) return hipErrorInvalidValue;
   if (p.parts > 1 && (!ws.partials || ws.partial_bytes < p.partial_bytes || !ws.counters ||
                       ws.counter_count < p.counters))
@@ -616,6 +665,7 @@ hipError_t launch_q4_stream(const Q4Job* jobs, int n_jobs, const uint16_t* x, ui
   a.part_chunks = p.part_chunks;
   a.partials = ws.partials;
   a.counters = ws.counters;
+  a.M = M;
   uint32_t b = 0;
   for (int i = 0; i < n_jobs; ++i) {
     a.jobs[i] = jobs[i];

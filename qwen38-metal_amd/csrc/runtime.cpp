@@ -214,6 +214,8 @@ qm::Tuning qm::read_tuning(int cu_count) {
   t.q4_fuse = get("QM38_Q4_FUSE", 1);
   t.q4_stream = get("QM38_Q4_STREAM", 1);
   t.q4_stream_wgs = get("QM38_Q4_STREAM_WGS", 0);
+  t.q4_stream_rows = get("QM38_Q4_STREAM_ROWS", 2);
+  t.q4_stream_mw = get("QM38_Q4_STREAM_MW", 0);
   t.q4_stream_c = get("QM38_Q4_STREAM_C", 0);
   t.q4_stream_w = get("QM38_Q4_STREAM_W", 0);
   t.gemm_splits = get("QM38_GEMM_SPLITS", 0);

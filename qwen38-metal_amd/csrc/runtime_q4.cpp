@@ -95,20 +95,21 @@ Q4Job to_job(const qm_q4_job& j, uint16_t* out) {
   return q;
 }
 
-// One activation row on the streaming kernel (its K-split workspace first).
-qm_status stream_launch(qm_runtime* rt, const Q4Job* jobs, int n, const uint16_t* x, uint32_t K, const char* what) {
+// One or two activation rows on the streaming kernel (its K-split workspace first).
+qm_status stream_launch(qm_runtime* rt, const Q4Job* jobs, int n, const uint16_t* x, uint32_t K, uint32_t M,
+                        const char* what) {
   size_t pbytes = 0, counters = 0;
-  q4_stream_workspace(jobs, n, K, rt->tune, &pbytes, &counters);
+  q4_stream_workspace(jobs, n, K, M, rt->tune, &pbytes, &counters);
   qm_status st = ensure_partials(rt, pbytes);
   if (st == QM_OK) st = ensure_counters(rt, counters);
   if (st != QM_OK) return st;
-  return hip_check(launch_q4_stream(jobs, n, x, K, workspace(rt), rt->stream), what);
+  return hip_check(launch_q4_stream(jobs, n, x, K, M, workspace(rt), rt->stream), what);
 }
 
 qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const uint16_t* x, uint32_t K,
                  uint32_t M, const char* what) {
-  if (M == 1) {
-    // One activation row: the streaming kernel, with a gate/up pair as one job.
+  if (M <= 2) {
+    // One or two activation rows: the streaming kernel, with a gate/up pair as one job.
     Q4Job sj[kMaxQ4Jobs];
     int ns = 0;
     if (swiglu) {
@@ -121,7 +122,7 @@ qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const ui
     } else {
       for (int i = 0; i < n; ++i) sj[ns++] = jobs[i];
     }
-    if (q4_stream_supported(sj, ns, K, M, rt->tune)) return stream_launch(rt, sj, ns, x, K, what);
+    if (q4_stream_supported(sj, ns, K, M, rt->tune)) return stream_launch(rt, sj, ns, x, K, M, what);
   }
   // The decode kernel needs no workspace; the GEMM's split-K plans do.
   size_t pbytes = 0, counters = 0;
@@ -144,7 +145,7 @@ qm_status qm::q4_reserve_workspace(qm_runtime* rt, const qm_q4_job* jobs, int n_
   for (int i = 0; i < n_jobs; ++i) q[i] = to_job(jobs[i], nullptr);
   if (!q4_stream_supported(q, n_jobs, in_elems, 1, rt->tune)) return QM_OK;
   size_t pbytes = 0, counters = 0;
-  q4_stream_workspace(q, n_jobs, in_elems, rt->tune, &pbytes, &counters);
+  q4_stream_workspace(q, n_jobs, in_elems, 1, rt->tune, &pbytes, &counters);
   qm_status st = ensure_partials(rt, pbytes);
   return st == QM_OK ? ensure_counters(rt, counters) : st;
 }
@@ -237,8 +238,8 @@ qm_status qm_q4_project_set(qm_runtime* rt, const qm_q4_job* jobs, const qm_q4_j
     if (ups && ups[i] && (st = check_job_ranges(rt, *ups[i], in_elems, "up")) != QM_OK) return st;
     if ((st = check_range(rt, outputs[i], (uint64_t)M * jobs[i].out_rows * 2, "output")) != QM_OK) return st;
   }
-  if (M == 1 && q4_stream_supported(q, n_jobs, in_elems, M, rt->tune))
-    return stream_launch(rt, q, n_jobs, x, in_elems, "Q4 set launch");
+  if (q4_stream_supported(q, n_jobs, in_elems, M, rt->tune))
+    return stream_launch(rt, q, n_jobs, x, in_elems, M, "Q4 set launch");
   // Otherwise: the plain jobs in one launch, each pair in its own.
   Q4Job plain[kMaxQ4Jobs];
   int np = 0;
@@ -321,14 +322,14 @@ qm_status qm_q4_argmax(qm_runtime* rt, const qm_q4_job* job, const uint16_t* x, 
   const bool stream = q4_stream_supported(&q, 1, in_elems, 1, rt->tune);
   if (stream) {
     size_t pbytes = 0, counters = 0;
-    q4_stream_workspace(&q, 1, in_elems, rt->tune, &pbytes, &counters);
+    q4_stream_workspace(&q, 1, in_elems, 1, rt->tune, &pbytes, &counters);
     if ((st = ensure_partials(rt, pbytes)) != QM_OK || (st = ensure_counters(rt, counters)) != QM_OK) return st;
   }
   const Workspace ws = workspace(rt);
   for (uint32_t m0 = 0; m0 < M; m0 += kDecodeMaxRows) {
     const uint32_t mc = M - m0 < kDecodeMaxRows ? M - m0 : kDecodeMaxRows;
     hipError_t e = mc == 1 && stream
-                       ? launch_q4_stream(&q, 1, x + (size_t)m0 * in_elems, in_elems, ws, rt->stream)
+                       ? launch_q4_stream(&q, 1, x + (size_t)m0 * in_elems, in_elems, 1, ws, rt->stream)
                        : launch_q4_decode(&q, 1, false, x + (size_t)m0 * in_elems, in_elems, mc, ws, rt->stream);
     if (e == hipSuccess) e = launch_q4_argmax_finish(rt->keys, ids + m0, mc, rt->stream);
     if ((st = hip_check(e, "Q4 argmax launch")) != QM_OK) return st;

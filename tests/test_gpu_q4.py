@@ -167,9 +167,10 @@ def test_rows_per_workgroup(torch_dev, nt, rpw, M):
     """Workgroups owning fewer rows than their 16-row tiles (the planner's
     balancing choice) mask the rest; forced here for several row counts that
     do not divide the projection heights, with several jobs in one launch and
-    a SwiGLU pair."""
+    a SwiGLU pair.  (The MFMA decode kernel: the streaming kernel, which
+    takes up to four rows by default, is switched off.)"""
     import qm38
-    with tuned(QM38_Q4_NT=nt, QM38_Q4_RPW=rpw) as rt:
+    with tuned(QM38_Q4_NT=nt, QM38_Q4_RPW=rpw, QM38_Q4_STREAM=0) as rt:
         rng = np.random.default_rng(300 + nt * 50 + rpw + M)
         K = 1024
         mats = [synth.q4_matrix(rng, n, K) for n in (200, 37, 512)]
@@ -340,6 +341,36 @@ def test_mapped_job_from_one_buffer(rt, torch_dev):
     with pytest.raises(QmError) as e:
         qm38.Runtime.mapped_job(whole, blob.nbytes + 1, whole, off_s, whole, off_b, N, K)
     assert e.value.status == "QM_ERR_INVALID_BUFFER_OFFSET"
+
+
+@pytest.mark.parametrize("M", [2])
+@pytest.mark.parametrize("K", [192, 1024, 5120, 8256, 17408, 20544])
+def test_few_rows_streaming(rt, torch_dev, M, K):
+    """Two activation rows on the streaming kernel (one chunk per wave, K in
+    balanced parts of at most 8 waves whose fp32 sums the last part adds;
+    K = 192 and 8256 end inside a chunk): plain jobs of several heights
+    and a SwiGLU pair in one launch each match the oracle row by row, repeated
+    calls are bit-identical, and the result equals the MFMA decode kernel's
+    within the same bar."""
+    import qm38
+    rng = np.random.default_rng(K * 10 + M)
+    mats = [synth.q4_matrix(rng, n, K) for n in (300, 37)]
+    xb = synth.bf16_normal(rng, (M, K))
+    got1 = _project(rt, torch_dev, mats, xb, M)
+    got2 = _project(rt, torch_dev, mats, xb, M)
+    for mat, g1, g2 in zip(mats, got1, got2):
+        assert_bf16_close(g1, oracle.q4_project(xb, *mat), what=f"M={M} K={K} rows {mat[0].shape[0]}")
+        assert np.array_equal(g1, g2)
+    gate, up = synth.q4_matrix(rng, 90, K), synth.q4_matrix(rng, 90, K)
+    dg, du = _upload(torch_dev, *gate), _upload(torch_dev, *up)
+    jg, ju = qm38.Runtime.job(*dg, 90), qm38.Runtime.job(*du, 90)
+    h = empty_bf16((M, 90), torch_dev)
+    rt.q4_swiglu(jg, ju, to_dev(xb, torch_dev), K, M, h)
+    h_ref = oracle.swiglu(oracle.q4_project(xb, *gate), oracle.q4_project(xb, *up))
+    assert_bf16_close(bf16_dev_to_f32(h), h_ref, what=f"M={M} K={K} swiglu")
+    with tuned(QM38_Q4_STREAM=0) as mrt:
+        for mat, g1 in zip(mats, _project(mrt, torch_dev, mats, xb, M)):
+            assert_bf16_close(g1, oracle.q4_project(xb, *mat), what=f"decode kernel M={M} K={K}")
 
 
 @pytest.mark.parametrize("K", [16448, 17408, 20544])
