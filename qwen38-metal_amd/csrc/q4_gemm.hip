@@ -120,7 +120,11 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const uint16_t* __restric
   *(u32x4*)(xh + 8 * i) = o;
 }
 
-template <bool SWIGLU>
+// Jobs are plain projections (256 W rows per tile) or SwiGLU pairs (mode
+// kQ4OutSwiglu: 128 gate rows from w/s/b and the same 128 up rows from
+// uw/us/ub per tile, h = silu(gate) * up in the epilogue); one launch may mix
+// them (a same-input set).  Whether a tile is a pair is uniform over a piece,
+// so it only changes the piece's row mapping and epilogue.
 __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmArgs args) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][kTileBytes];  // [stage][X | W]
   __shared__ unsigned last;
@@ -150,11 +154,6 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmArgs args) {
     s_end = min(total, step0 + Q);
   }
 
-  // B-tile row bases of this wave's four 32-column blocks.
-  uint32_t brow[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    brow[j] = SWIGLU ? (j < 2 ? 64 * wn + 32 * j : 128 + 64 * wn + 32 * (j - 2)) : 128 * wn + 32 * j;
   const uint32_t arow0 = 64 * wm + (lane & 31);
   const uint32_t kh = lane >> 5;
   const uint32_t srow = tid >> 1, shalf = tid & 1;  // staging: row of the tiles, chunk half
@@ -171,22 +170,22 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmArgs args) {
 
     // ---- this thread's W row and the tile's job ----------------------------
     int jt = 0;
-    if (!SWIGLU) {
-      while (jt + 1 < args.n_jobs && n_tile >= args.jobs[jt + 1].tile_begin) ++jt;
-    }
-    const Q4Job& wj = args.jobs[SWIGLU ? (wave >= 4 ? 1 : 0) : jt];  // srow >= 128 <=> wave >= 4
-    uint32_t n_first, wrow;
-    if (SWIGLU) {
-      n_first = n_tile * 128;
-      wrow = n_first + (srow & 127);
-    } else {
-      n_first = (n_tile - wj.tile_begin) * kBN;
-      wrow = n_first + srow;
-    }
-    wrow = min(wrow, wj.rows - 1);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(wj.w, (uint64_t)wj.rows * (K / 2));
-    const uint16_t* s_row = wj.s + (size_t)wrow * G;
-    const uint16_t* b_row = wj.b + (size_t)wrow * G;
+    while (jt + 1 < args.n_jobs && n_tile >= args.jobs[jt + 1].tile_begin) ++jt;
+    const Q4Job& jb = args.jobs[jt];
+    const bool pair = jb.mode == kQ4OutSwiglu;
+    // A pair tile's W rows 128..255 (srow >= 128 <=> wave >= 4) are the up rows.
+    const bool upper = pair && wave >= 4;
+    const uint32_t n_first = (n_tile - jb.tile_begin) * (pair ? 128u : kBN);
+    const uint32_t wrow = min(n_first + (pair ? (srow & 127) : srow), jb.rows - 1);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(upper ? jb.uw : jb.w, (uint64_t)jb.rows * (K / 2));
+    const uint16_t* s_row = (upper ? jb.us : jb.s) + (size_t)wrow * G;
+    const uint16_t* b_row = (upper ? jb.ub : jb.b) + (size_t)wrow * G;
+    // B-tile row bases of this wave's four 32-column blocks (a pair: gate
+    // columns in blocks 0, 1 and the matching up columns in blocks 2, 3).
+    uint32_t brow[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      brow[j] = pair ? (j < 2 ? 64 * wn + 32 * j : 128 + 64 * wn + 32 * (j - 2)) : 128 * wn + 32 * j;
     const uint32_t w_voff = wrow * (K / 2) + shalf * 16;
     const uint32_t xrow = min(m0 + srow, M - 1);
     const uint16_t* x_src = args.xh + (size_t)xrow * K + shalf * 32;
@@ -337,22 +336,20 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmArgs args) {
       for (int e = 0; e < 16; ++e) {
         const uint32_t m = m0 + 64 * wm + 32 * i + 8 * (e >> 2) + 4 * kh + (e & 3);
         if (m >= M) continue;
-        if (SWIGLU) {
-          const Q4Job& gj = args.jobs[0];
+        if (pair) {
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            const uint32_t n = n_tile * 128 + 64 * wn + 32 * j + (lane & 31);
-            if (n < gj.rows) {
+            const uint32_t n = n_first + 64 * wn + 32 * j + (lane & 31);
+            if (n < jb.rows) {
               const float gv = acc[i][j][e], uv = acc[i][j + 2][e];
-              gj.out[(size_t)m * gj.rows + n] = f32_to_bf16(silu_f(gv) * uv);
+              jb.out[(size_t)m * jb.rows + n] = f32_to_bf16(silu_f(gv) * uv);
             }
           }
         } else {
-          const Q4Job& oj = args.jobs[jt];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const uint32_t n = n_first + brow[j] + (lane & 31);
-            if (n < oj.rows) oj.out[(size_t)m * oj.rows + n] = f32_to_bf16(acc[i][j][e]);
+            if (n < jb.rows) jb.out[(size_t)m * jb.rows + n] = f32_to_bf16(acc[i][j][e]);
           }
         }
       }
@@ -390,15 +387,29 @@ double stream_cost(uint32_t tiles, uint32_t G, uint32_t Q, uint32_t cus) {
   return rounds * (Q + 20.0 * ((double)Q / G + 1.0) + 12.0 + 5.0 * pieces);
 }
 
-GemmPlan gemm_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M, const Tuning& tune) {
+// N tiles of a job: 256 rows of a plain projection, 128 of a SwiGLU pair.
+uint32_t job_tiles(const Q4Job& j) { return j.mode == kQ4OutSwiglu ? (j.rows + 127) / 128 : (j.rows + kBN - 1) / kBN; }
+
+// The launch's jobs with a gate/up pair given as two jobs (swiglu) folded
+// into one pair job; returns the job count.
+int fold_jobs(const Q4Job* jobs, int n_jobs, bool swiglu, Q4Job* out) {
+  if (!swiglu) {
+    for (int i = 0; i < n_jobs; ++i) out[i] = jobs[i];
+    return n_jobs;
+  }
+  out[0] = jobs[0];
+  out[0].uw = jobs[1].w;
+  out[0].us = jobs[1].s;
+  out[0].ub = jobs[1].b;
+  out[0].mode = kQ4OutSwiglu;
+  return 1;
+}
+
+GemmPlan gemm_plan(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tune) {
   GemmPlan p{};
   p.m_tiles = (M + kBM - 1) / kBM;
   uint32_t n_tiles = 0;
-  if (swiglu) {
-    n_tiles = (jobs[0].rows + 127) / 128;
-  } else {
-    for (int i = 0; i < n_jobs; ++i) n_tiles += (jobs[i].rows + kBN - 1) / kBN;
-  }
+  for (int i = 0; i < n_jobs; ++i) n_tiles += job_tiles(jobs[i]);
   p.tiles = n_tiles * p.m_tiles;
   const uint32_t G = K / 64, cus = tune.cus > 0 ? (uint32_t)tune.cus : 256;
   const uint64_t total = (uint64_t)p.tiles * G;
@@ -444,19 +455,24 @@ GemmPlan gemm_plan(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint3
 
 void q4_gemm_workspace(const Q4Job* jobs, int n_jobs, bool swiglu, uint32_t K, uint32_t M, const Tuning& tune,
                        size_t* partial_bytes, size_t* counters) {
-  const GemmPlan p = gemm_plan(jobs, n_jobs, swiglu, K, M, tune);
+  Q4Job f[kMaxQ4Jobs];
+  const int nf = fold_jobs(jobs, n_jobs, swiglu, f);
+  const GemmPlan p = gemm_plan(f, nf, K, M, tune);
   *partial_bytes = p.partial_bytes;
   *counters = p.partial_bytes ? p.tiles : 0;
 }
 
 hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint16_t* x, uint32_t K, uint32_t M,
                           const Workspace& ws, hipStream_t stream) {
-  if (n_jobs < 1 || n_jobs > kMaxQ4Jobs || K % 64 != 0 || M == 0) return hipErrorInvalidValue;
-  for (int i = 0; i < n_jobs; ++i)
-    if (jobs[i].mode != kQ4OutBf16) return hipErrorInvalidValue;
+  if (n_jobs < 1 || n_jobs > kMaxQ4Jobs || K % 64 != 0 || M == 0 || (swiglu && n_jobs != 2))
+    return hipErrorInvalidValue;
+  Q4Job f[kMaxQ4Jobs];
+  const int nf = fold_jobs(jobs, n_jobs, swiglu, f);
+  for (int i = 0; i < nf; ++i)
+    if (f[i].mode != kQ4OutBf16 && f[i].mode != kQ4OutSwiglu) return hipErrorInvalidValue;
   if (!ws.xh || ws.xh_bytes < q4_gemm_xh_bytes(K, M)) return hipErrorInvalidValue;
   if (!ws.tune) return hipErrorInvalidValue;
-  const GemmPlan plan = gemm_plan(jobs, n_jobs, swiglu, K, M, *ws.tune);
+  const GemmPlan plan = gemm_plan(f, nf, K, M, *ws.tune);
   const bool log_plan = ws.tune->gemm_plan_log != 0;
   static uint64_t logged = 0;  // debug aid: print each new shape's plan once
   const uint64_t key = ((uint64_t)M << 40) ^ ((uint64_t)K << 16) ^ plan.tiles ^ ((uint64_t)plan.q << 56);
@@ -471,27 +487,23 @@ hipError_t launch_q4_gemm(const Q4Job* jobs, int n_jobs, bool swiglu, const uint
   a.workers = plan.workers;
   a.partials = ws.partials;
   a.counters = ws.counters;
-  a.n_jobs = n_jobs;
+  a.n_jobs = nf;
   a.xh = ws.xh;
   a.K = K;
   a.M = M;
   a.m_tiles = (M + kBM - 1) / kBM;
   uint32_t n_tiles = 0;
-  for (int i = 0; i < n_jobs; ++i) {
-    a.jobs[i] = jobs[i];
+  for (int i = 0; i < nf; ++i) {
+    a.jobs[i] = f[i];
     a.jobs[i].tile_begin = n_tiles;
-    if (!swiglu) n_tiles += (jobs[i].rows + kBN - 1) / kBN;
+    n_tiles += job_tiles(f[i]);
   }
-  if (swiglu) n_tiles = (jobs[0].rows + 127) / 128;
   a.total_tiles = n_tiles * a.m_tiles;
 
   const size_t chunks = (size_t)M * K / 8;
   hipLaunchKernelGGL(x_to_f16_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream, x, ws.xh, chunks);
   const dim3 grid(plan.workers);
-  if (swiglu)
-    hipLaunchKernelGGL(q4_gemm_kernel<true>, grid, dim3(kThreads), 0, stream, a);
-  else
-    hipLaunchKernelGGL(q4_gemm_kernel<false>, grid, dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL(q4_gemm_kernel, grid, dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -106,6 +106,20 @@ qm_status stream_launch(qm_runtime* rt, const Q4Job* jobs, int n, const uint16_t
   return hip_check(launch_q4_stream(jobs, n, x, K, M, workspace(rt), rt->stream), what);
 }
 
+// Prefill rows on the GEMM (its split-K workspace and fp16 activation copy
+// first).  swiglu: jobs = {gate, up}; otherwise plain jobs and folded pairs
+// may mix.
+qm_status gemm_launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const uint16_t* x, uint32_t K,
+                      uint32_t M, const char* what) {
+  size_t pbytes = 0, counters = 0;
+  q4_gemm_workspace(jobs, n, swiglu, K, M, rt->tune, &pbytes, &counters);
+  qm_status st = ensure_partials(rt, pbytes);
+  if (st == QM_OK) st = ensure_counters(rt, counters);
+  if (st == QM_OK) st = ensure_xh(rt, q4_gemm_xh_bytes(K, M));
+  if (st != QM_OK) return st;
+  return hip_check(launch_q4_gemm(jobs, n, swiglu, x, K, M, workspace(rt), rt->stream), what);
+}
+
 qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const uint16_t* x, uint32_t K,
                  uint32_t M, const char* what) {
   if (M <= 2) {
@@ -124,17 +138,8 @@ qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const ui
     }
     if (q4_stream_supported(sj, ns, K, M, rt->tune)) return stream_launch(rt, sj, ns, x, K, M, what);
   }
-  // The decode kernel needs no workspace; the GEMM's split-K plans do.
-  size_t pbytes = 0, counters = 0;
-  if (M > kDecodeMaxRows) q4_gemm_workspace(jobs, n, swiglu, K, M, rt->tune, &pbytes, &counters);
-  qm_status st = ensure_partials(rt, pbytes);
-  if (st == QM_OK) st = ensure_counters(rt, counters);
-  if (st == QM_OK && M > kDecodeMaxRows) st = ensure_xh(rt, q4_gemm_xh_bytes(K, M));
-  if (st != QM_OK) return st;
-  const Workspace ws = workspace(rt);
-  const hipError_t e = M <= kDecodeMaxRows ? launch_q4_decode(jobs, n, swiglu, x, K, M, ws, rt->stream)
-                                           : launch_q4_gemm(jobs, n, swiglu, x, K, M, ws, rt->stream);
-  return hip_check(e, what);
+  if (M > kDecodeMaxRows) return gemm_launch(rt, jobs, n, swiglu, x, K, M, what);
+  return hip_check(launch_q4_decode(jobs, n, swiglu, x, K, M, workspace(rt), rt->stream), what);
 }
 
 }  // namespace
@@ -240,6 +245,8 @@ qm_status qm_q4_project_set(qm_runtime* rt, const qm_q4_job* jobs, const qm_q4_j
   }
   if (q4_stream_supported(q, n_jobs, in_elems, M, rt->tune))
     return stream_launch(rt, q, n_jobs, x, in_elems, M, "Q4 set launch");
+  // Prefill rows: one GEMM launch over the whole set (plain and pair tiles).
+  if (M > kDecodeMaxRows) return gemm_launch(rt, q, n_jobs, false, x, in_elems, M, "Q4 set GEMM launch");
   // Otherwise: the plain jobs in one launch, each pair in its own.
   Q4Job plain[kMaxQ4Jobs];
   int np = 0;

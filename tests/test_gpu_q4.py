@@ -404,12 +404,14 @@ def test_single_row_k_parts(rt, torch_dev, K):
 
 def test_project_set_mixes_plain_and_pairs(rt, torch_dev):
     """qm_q4_project_set: plain projections and SwiGLU pairs from one
-    activation, in one launch for one row, and as separate launches for
-    several rows; each output equals its own call."""
+    activation, in one launch for one or two rows and prefill rows (the GEMM
+    takes both tile kinds), as separate launches for 3..16 rows; each output
+    matches the oracle, and a pair's equals its own call's where both run the
+    same kernel plan."""
     import qm38
     rng = np.random.default_rng(31)
     K = 1024
-    for M in (1, 3):
+    for M in (1, 2, 3, 40):
         a, g, u, b = (synth.q4_matrix(rng, n, K) for n in (200, 96, 96, 40))
         da, dg, du, db = (_upload(torch_dev, *m) for m in (a, g, u, b))
         ja, jg, ju, jb = (qm38.Runtime.job(*d, m[0].shape[0]) for d, m in zip((da, dg, du, db), (a, g, u, b)))
@@ -421,6 +423,8 @@ def test_project_set_mixes_plain_and_pairs(rt, torch_dev):
         h_ref = oracle.swiglu(oracle.q4_project(xb, *g), oracle.q4_project(xb, *u))
         assert_bf16_close(bf16_dev_to_f32(outs[1]), h_ref, what=f"set pair M={M}")
         assert_bf16_close(bf16_dev_to_f32(outs[2]), oracle.q4_project(xb, *b), what=f"set plain 2 M={M}")
+        if M > 16:
+            continue  # the GEMM's plan (and so its sum order) follows the launch's tile count
         h = empty_bf16((M, 96), torch_dev)
         rt.q4_swiglu(jg, ju, xd, K, M, h)
         assert np.array_equal(bf16_dev_to_f32(h), bf16_dev_to_f32(outs[1]))

@@ -229,3 +229,28 @@ def test_worker_step_ranges(torch_dev, knob, q):
         rt.q4_swiglu(qm38.Runtime.job(*dg, I), qm38.Runtime.job(*du, I), to_dev(xb, torch_dev), K, M, h)
         assert_bf16_close(bf16_dev_to_f32(h), oracle.swiglu(oracle.q4_project(xb, *gate), oracle.q4_project(xb, *up)),
                           what=f"swiglu {knob}={q}")
+
+
+@pytest.mark.parametrize("M", [40, 300])
+@pytest.mark.parametrize("knob", [None, ("QM38_GEMM_SPLITS", 3), ("QM38_GEMM_Q", 21)])
+def test_mixed_set_in_one_launch(torch_dev, M, knob):
+    """qm_q4_project_set with prefill rows: plain projections (256-row tiles)
+    and SwiGLU pairs (128 gate + 128 up rows per tile) in one GEMM launch,
+    whole tiles, K split into slices, and stream-K ranges that cut tiles of
+    both kinds; every output within the bar of the oracle."""
+    import qm38
+    env = {} if knob is None else {knob[0]: knob[1]}
+    with tuned(**env) as rt:
+        rng = np.random.default_rng(M + (0 if knob is None else knob[1]))
+        K = 1024
+        a, g1, u1, b, g2, u2 = (synth.q4_matrix(rng, n, K) for n in (200, 96, 96, 40, 300, 300))
+        dev = [_upload(torch_dev, *m) for m in (a, g1, u1, b, g2, u2)]
+        ja, jg1, ju1, jb, jg2, ju2 = (qm38.Runtime.job(*d, m[0].shape[0]) for d, m in zip(dev, (a, g1, u1, b, g2, u2)))
+        xb = synth.bf16_normal(rng, (M, K))
+        outs = [empty_bf16((M, n), torch_dev) for n in (200, 96, 40, 300)]
+        rt.q4_project_set([ja, jg1, jb, jg2], [None, ju1, None, ju2], to_dev(xb, torch_dev), K, M, outs)
+        assert_bf16_close(bf16_dev_to_f32(outs[0]), oracle.q4_project(xb, *a), what=f"mixed plain M={M}")
+        assert_bf16_close(bf16_dev_to_f32(outs[2]), oracle.q4_project(xb, *b), what=f"mixed plain 2 M={M}")
+        for o, g, u in ((outs[1], g1, u1), (outs[3], g2, u2)):
+            h_ref = oracle.swiglu(oracle.q4_project(xb, *g), oracle.q4_project(xb, *u))
+            assert_bf16_close(bf16_dev_to_f32(o), h_ref, what=f"mixed pair M={M} rows {g[0].shape[0]}")
