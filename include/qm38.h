@@ -168,7 +168,9 @@ qm_status qm_q4_job_from_mapped(const qm_q4_mapped_job* mapped, uint32_t in_elem
  * Replaces q4_affine_matvec_mapped_batch (metal_runtime.rs:3599) for M == 1
  * and q4_affine_matmul_mapped_batch (metal_runtime.rs:3683) for M > 1; rows
  * M <= 16 take the decode (weight-streaming) kernel, larger M the tiled MFMA
- * GEMM.  n_jobs <= 8. */
+ * GEMM.  n_jobs <= 8.  in_elems is at most 2^24 (DIMENSION_OVERFLOW beyond:
+ * the kernels address one row's bytes and a tile of rows with 32-bit
+ * offsets). */
 qm_status qm_q4_project(qm_runtime* rt, const qm_q4_job* jobs, int n_jobs,
                         const uint16_t* x, uint32_t in_elems, uint32_t M,
                         uint16_t* const* outputs);
@@ -179,7 +181,8 @@ qm_status qm_q4_project(qm_runtime* rt, const qm_q4_job* jobs, int n_jobs,
  * ups[j]->out_rows == jobs[j].out_rows.  For one activation row the whole set
  * is one launch that reads x once (the reference's mapped batch, whose jobs
  * would be a QKV projection and the pair kernels' gate/up, metal_runtime.rs:
- * 3599 with qwen38.metal:1404..3643); larger M runs the plain jobs together
+ * 3599 with qwen38.metal:1404..3643); so are two rows, and M > 16 (one GEMM
+ * launch over plain and pair tiles).  M = 3..16 runs the plain jobs together
  * and each pair as qm_q4_swiglu does.  n_jobs <= 8. */
 qm_status qm_q4_project_set(qm_runtime* rt, const qm_q4_job* jobs, const qm_q4_job* const* ups, int n_jobs,
                             const uint16_t* x, uint32_t in_elems, uint32_t M, uint16_t* const* outputs);

@@ -24,8 +24,8 @@ struct Q4Job {
   // value (a residual add).  `out` then points at fp32.  3: argmax keys, one
   // uint64 per activation row (`out` points at them; they must be zero and are
   // maxed with atomics; launch_q4_argmax_finish turns them into row ids and
-  // clears them).  4: a gate/up pair with SwiGLU (single-row streaming kernel
-  // only).  The GEMM takes 0 only.
+  // clears them).  4: a gate/up pair with SwiGLU (the streaming kernel and the
+  // GEMM).  The GEMM takes 0 and 4 only.
   uint32_t mode;
 };
 constexpr uint32_t kQ4OutBf16 = 0, kQ4OutF32 = 1, kQ4OutAddF32 = 2, kQ4OutArgmax = 3, kQ4OutSwiglu = 4;

@@ -177,7 +177,10 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmArgs args) {
     const bool upper = pair && wave >= 4;
     const uint32_t n_first = (n_tile - jb.tile_begin) * (pair ? 128u : kBN);
     const uint32_t wrow = min(n_first + (pair ? (srow & 127) : srow), jb.rows - 1);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(upper ? jb.uw : jb.w, (uint64_t)jb.rows * (K / 2));
+    // The weight resource starts at the tile's first row, so the 32-bit
+    // offsets stay in range whatever the matrix size.
+    const uint32_t* w_tile = (upper ? jb.uw : jb.w) + (size_t)n_first * (K / 8);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w_tile, (uint64_t)(jb.rows - n_first) * (K / 2));
     const uint16_t* s_row = (upper ? jb.us : jb.s) + (size_t)wrow * G;
     const uint16_t* b_row = (upper ? jb.ub : jb.b) + (size_t)wrow * G;
     // B-tile row bases of this wave's four 32-column blocks (a pair: gate
@@ -186,7 +189,7 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmArgs args) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       brow[j] = pair ? (j < 2 ? 64 * wn + 32 * j : 128 + 64 * wn + 32 * (j - 2)) : 128 * wn + 32 * j;
-    const uint32_t w_voff = wrow * (K / 2) + shalf * 16;
+    const uint32_t w_voff = (wrow - n_first) * (K / 2) + shalf * 16;
     const uint32_t xrow = min(m0 + srow, M - 1);
     const uint16_t* x_src = args.xh + (size_t)xrow * K + shalf * 32;
 

@@ -1110,9 +1110,18 @@ hipError_t attn_noalloc_begin(int device, hipStream_t stream) {
 
 hipError_t attn_noalloc_end(int device, hipStream_t stream) {
   ScratchOrder& o = g_order[device];
-  const hipError_t e = hipEventRecord(o.done, stream);
-  o.used = e == hipSuccess;
-  o.last = stream;
+  hipError_t e = hipEventRecord(o.done, stream);
+  if (e == hipSuccess) {
+    o.used = true;
+    o.last = stream;
+  } else {
+    // Without the event a later call on another stream could not wait for
+    // this one: finish this call's work before releasing the array.
+    (void)hipGetLastError();
+    const hipError_t s = hipStreamSynchronize(stream);
+    o.used = false;
+    if (s != hipSuccess) e = s;
+  }
   o.mu.unlock();
   return e;
 }

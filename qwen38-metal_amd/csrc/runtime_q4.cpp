@@ -10,6 +10,9 @@ namespace {
 
 constexpr uint32_t kGroup = 64;       // AFFINE_GROUP_SIZE (metal_runtime.rs)
 constexpr uint32_t kDecodeMaxRows = 16;
+// Widest input: the kernels address a tile's rows (up to 256 rows of in/2
+// bytes) with 32-bit offsets.
+constexpr uint32_t kMaxInElems = 1u << 24;
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
@@ -22,6 +25,9 @@ qm_status validate_job(const qm_q4_job* job, uint32_t in_elems, const char* name
   if (in_elems % kGroup != 0)
     return fail(QM_ERR_INPUT_NOT_GROUPED,
                 "%s: input dimension %u is not divisible by affine group size %u", name, in_elems, kGroup);
+  if (in_elems > kMaxInElems)
+    return fail(QM_ERR_DIMENSION_OVERFLOW, "%s: input dimension %u exceeds the runtime limit %u", name, in_elems,
+                kMaxInElems);
   if (!job->weights || !job->scales || !job->biases)
     return fail(QM_ERR_NULL_POINTER, "%s: weights/scales/biases pointer is NULL", name);
   if (!aligned(job->weights, 8) || !aligned(job->scales, 8) || !aligned(job->biases, 8))

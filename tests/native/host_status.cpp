@@ -76,6 +76,8 @@ static void runtime_cases(qm_runtime* rt) {
   qm_q4_job huge = job;
   huge.out_rows = 0xFFFFFFFFu;
   expect(qm_q4_project(rt, &huge, 1, x, 0xFFFFFFC0u, 1, outs), QM_ERR_DIMENSION_OVERFLOW, "weight count overflow");
+  expect(qm_q4_project(rt, &job, 1, x, (1u << 24) + 64, 1, outs), QM_ERR_DIMENSION_OVERFLOW, "input too wide");
+  expect(qm_q4_project(rt, &job, 1, x, 1u << 24, 1, outs), QM_ERR_NO_DEVICE, "widest input, no device");
 
   // Mapped jobs (validate_mapped_q4_affine_shape, metal_runtime.rs:8854-8898):
   // K = 128, 64 rows -> 4096 B of weights, 256 B of scales and of biases.
