@@ -395,7 +395,9 @@ qm_status qm_dn_step(qm_runtime* rt, const qm_dn_weights* w, qm_dn_state* st,
  * metal_runtime.rs:7933-7990, kernel qwen38_deltanet_prefill
  * qwen38.metal:4530-4758).  `from` (may be NULL, meaning `to`) supplies the
  * initial state and is not modified unless it is `to`.  Layouts as
- * qm_dn_step with a leading [M] dimension. */
+ * qm_dn_step with a leading [M] dimension.  M x channels (2 key_heads
+ * key_head_dim + value_heads value_head_dim) is at most 2^31 - 1
+ * (DIMENSION_OVERFLOW beyond). */
 qm_status qm_dn_prefill(qm_runtime* rt, const qm_dn_weights* w,
                         const qm_dn_state* from, qm_dn_state* to,
                         const float* qkv, const float* z, const float* b,

@@ -112,6 +112,11 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
   if (!rt || !w || !to || !qkv || !z || !b || !a || !out) return fail(QM_ERR_NULL_POINTER, "NULL argument");
   if (!from) from = to;
   if (M == 0) return fail(QM_ERR_EMPTY_DIMENSION, "DeltaNet prefill needs at least one token");
+  // Token-major rows are indexed with 32-bit element counts in places (the
+  // gate norm's rows, the bf16 copy): keep M x channels within int32.
+  if ((uint64_t)M * w->channels > 0x7FFFFFFFull)
+    return fail(QM_ERR_DIMENSION_OVERFLOW, "DeltaNet prefill of %u tokens x %u channels exceeds the runtime limit", M,
+                w->channels);
   // Weights and states are device memory: any runtime on their device may use them.
   if (w->rt->device != rt->device || from->rt->device != rt->device || to->rt->device != rt->device)
     return fail(QM_ERR_INVALID_ARGUMENT, "weights and states must live on this runtime's device");

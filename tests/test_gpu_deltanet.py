@@ -319,6 +319,21 @@ def test_rejects_bad_configs(rt, torch_dev):
                                        np.zeros(max(shape[1], 1)), np.zeros(max(shape[3], 1)))
 
 
+def test_rejects_prefill_beyond_index_range(rt, torch_dev):
+    """M x channels past int32 fails before any memory is touched."""
+    import torch
+    cfg, c = _cfg(1, 1, 128, 128, 4)
+    rng = np.random.default_rng(5)
+    wts, (qkv, z, b, a) = _synth(rng, c, 1)
+    w = rt.create_deltanet_weights(cfg, *wts)
+    st = w.create_state()
+    M = (1 << 31) // _channels(c) + 1
+    t = [to_dev(x, torch_dev) for x in (qkv, z, b, a)]
+    out = torch.empty(128, dtype=torch.float32, device=torch_dev)
+    with pytest.raises(QmError, match="DIMENSION_OVERFLOW"):
+        rt.deltanet_prefill(w, st, *t, M, 1e-6, out)
+
+
 # ---------------------------------------------------------------------------
 # Verification snapshots (MetalDeltaNetSnapshots; metal_runtime.rs:7201-7281,
 # 7998-8024; reference test at :11398-11570)
