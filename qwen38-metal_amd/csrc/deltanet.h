@@ -43,8 +43,8 @@ struct DnArgs {
   uint32_t snap_rows;
   uint64_t snap_hist_stride, snap_s_stride;
   // kernel choice overrides (-1: default): the per-head step kernel, the
-  // chunked prefill
-  int32_t tune_step_head, tune_chunked;
+  // chunked prefill, the two-value-head chunk preparation
+  int32_t tune_step_head, tune_chunked, tune_dn_pair;
 };
 
 // Chunked prefill (WY / UT form over chunks of kDnChunk tokens): used for

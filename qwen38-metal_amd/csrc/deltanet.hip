@@ -1315,6 +1315,342 @@ __global__ __launch_bounds__(kPrepThreads, 2) void dn_chunk_prep_kernel(DnArgs a
   }
 }
 
+// dn_chunk_prep_kernel's work for the two value heads of one key head in one
+// 16-wave workgroup (value_heads == 2 key_heads).  The q^ / k^ conv, their
+// RMS scales and the raw products Q K^T and K K^T depend only on the key
+// head, so they are formed once by all 16 waves; waves 8 r .. 8 r + 7 then
+// take value head 2 kh + r through its decays, v conv, solve and stores
+// exactly as the one-head kernel does (same arithmetic, same bits).
+// LDS: k^ and q^ rows, then each head's -A, T blocks and decays; the W / U~
+// transposes reuse the space from the start once the solve is done.
+constexpr uint32_t kPairG = 448;  // floats of one head's decays (G, beta, e^{G63-G}, beta e^G, e^G, G fp64)
+constexpr uint32_t kPairA = 64 * kAStride, kPairT = 4 * 16 * 17;
+constexpr uint32_t kPairLds = (2 * 64 * kCStride + 2 * kPairA + 2 * kPairT + 2 * kPairG + 128) * 4;
+constexpr int kPairThreads = 1024;  // 16 waves
+static_assert(16 * 4 * 16 * 20 * 4 <= kPairLds, "transpose rows fit the pair kernel's LDS");
+__global__ __launch_bounds__(kPairThreads) void dn_chunk_prep_pair_kernel(DnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float prep_lds[];
+  float* ks_s = prep_lds;
+  float* qs_s = prep_lds + 64 * kCStride;
+  float* a_base = prep_lds + 2 * 64 * kCStride;         // [2][64][kAStride]
+  float* t_base = a_base + 2 * kPairA;                  // [2][4][16][17]
+  float* g_base = t_base + 2 * kPairT;                  // [2][kPairG]
+  float* sc_s = g_base + 2 * kPairG;                    // RMS scales: q rows 0..63, k rows 64..127
+  const uint32_t VH = a.value_heads;
+  const uint32_t KH = a.key_heads;
+  const uint32_t kh = blockIdx.x % KH, c = blockIdx.x / KH;
+  const uint32_t key_el = KH * kCD;
+  const uint32_t t0 = c * kDnChunk;
+  const uint32_t nt = min(kDnChunk, a.M - t0);
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // This wave's value head (r) and its place among that head's 8 waves.
+  const uint32_t r = wave / 8, hw = wave % 8, htid = tid % 512;
+  const uint32_t h = 2 * kh + r;
+  const uint32_t j = lane & 15, grp = lane >> 4;
+  float* a_s = a_base + r * kPairA;
+  float* t_s = t_base + r * kPairT;
+  auto gsets = [&](uint32_t rr) { return g_base + rr * kPairG; };
+  float* g_s = gsets(r);
+  float* beta_s = g_s + 64;
+  float* dk_s = g_s + 128;  // e^{G_63 - G_i}
+  float* bg_s = g_s + 192;  // beta_i e^{G_i}
+  float* gm_s = g_s + 256;  // e^{G_i}
+  double* gd_s = (double*)(g_s + 320);  // G in fp64
+  float* ws = a.chunk_ws + ((size_t)c * VH + h) * kDnChunkFloats;
+  float* Wg = ws + kDnWsW;
+  float* Ug = ws + kDnWsU;
+  float* Pg = ws + kDnWsP;
+  float* Gg = ws + kDnWsG;
+  float* KTg = ws + kDnWsKT;
+  float* Qg = ws + kDnWsQ;
+
+  // The chunk's conv: thread t owns key channel t % 256 of key head kh (q
+  // 0..127, k 128..255) and tokens 16 (t / 256) .. + 15, and the v columns
+  // 16 hw + j of its head for the solve, all inputs loaded before any is
+  // used.  Sums as conv_finish's; SiLU as silu_fast.
+  const uint32_t kc = tid % 256, th0 = 16 * (tid / 256);
+  const uint32_t kch = kc < kCD ? kh * kCD + kc : key_el + kh * kCD + (kc - kCD);
+  float vw[4], vx[4][7];
+  {
+    const uint32_t vch = 2 * key_el + h * kCD + 16 * hw + j;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) vw[q] = a.conv_w[(size_t)vch * 4 + q];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int q = 0; q < 7; ++q)
+        vx[b][q] = conv_input(a, vch, min((int)(t0 + 16 * b + 4 * grp) - 3 + q, (int)a.M - 1));
+  }
+  {
+    float w[4], win[3], xk[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w[q] = a.conv_w[(size_t)kch * 4 + q];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) win[q] = conv_input(a, kch, min((int)(t0 + th0) - 3 + q, (int)a.M - 1));
+#pragma unroll
+    for (int k = 0; k < 16; ++k) xk[k] = a.qkv[(size_t)min(t0 + th0 + k, a.M - 1) * a.channels + kch];
+    float* dst = kc < kCD ? qs_s + kc : ks_s + (kc - kCD);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float x = xk[k];
+      float sum = __fmul_rn(w[3], x);
+      sum = fmaf(w[0], win[0], sum);
+      sum = fmaf(w[1], win[1], sum);
+      sum = fmaf(w[2], win[2], sum);
+      win[0] = win[1];
+      win[1] = win[2];
+      win[2] = x;
+      const uint32_t t = th0 + k;
+      dst[t * kCStride] = t < nt ? silu_fast(sum) : 0.0f;
+    }
+  }
+  float vpre[4][4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      float sum = __fmul_rn(vw[3], vx[b][rr + 3]);
+      sum = fmaf(vw[0], vx[b][rr], sum);
+      sum = fmaf(vw[1], vx[b][rr + 1], sum);
+      sum = fmaf(vw[2], vx[b][rr + 2], sum);
+      vpre[b][rr] = silu_fast(sum);
+    }
+  // The state's conv history after the last token (raw inputs of the final
+  // three tokens): key channels once, each head's v channels by its waves.
+  if (c + 1 == (a.M + kDnChunk - 1) / kDnChunk) {
+    if (tid < 256)
+#pragma unroll
+      for (int q = 0; q < 3; ++q) a.hist_out[(size_t)kch * 3 + q] = conv_input(a, kch, (int)a.M - 3 + q);
+    if (htid >= 256 && htid < 256 + kCD) {
+      const uint32_t vch = 2 * key_el + h * kCD + (htid - 256);
+#pragma unroll
+      for (int q = 0; q < 3; ++q) a.hist_out[(size_t)vch * 3 + q] = conv_input(a, vch, (int)a.M - 3 + q);
+    }
+  }
+  // Each head's log decays, running sum and beta (its first wave).
+  if (hw == 0) {
+    float lg = 0.0f, beta = 0.0f;
+    if (lane < nt) {
+      const size_t ti = (size_t)(t0 + lane) * VH + h;
+      lg = -expf(a.a_log[h]) * softplus_f(a.a[ti] + a.dt_bias[h]);
+      beta = sigmoid_f(a.b[ti]);
+    }
+    double Gd = lg;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const double o = __shfl_up(Gd, off);
+      if (lane >= (uint32_t)off) Gd += o;
+    }
+    const float G = (float)Gd;
+    gd_s[lane] = Gd;
+    g_s[lane] = G;
+    beta_s[lane] = beta;
+    dk_s[lane] = expf((float)(__shfl(Gd, 63) - Gd));
+    bg_s[lane] = beta * expf(G);
+    gm_s[lane] = expf(G);
+    Gg[lane] = G;
+  }
+  __syncthreads();
+  // RMS scales (prep_key_head's reductions): 8 rows per wave side by side,
+  // lane q forming row q's scale.
+  {
+    float ss[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint32_t ri = 8 * wave + q;
+      const float* row = (ri < 64 ? qs_s + ri * kCStride : ks_s + (ri - 64) * kCStride) + lane;
+      ss[q] = fmaf(row[64], row[64], fmaf(row[0], row[0], 0.0f));
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) ss[q] = wave_sum(ss[q]);
+    float mine = ss[0];
+#pragma unroll
+    for (int q = 1; q < 8; ++q) mine = lane == (uint32_t)q ? ss[q] : mine;
+    if (lane < 8) sc_s[8 * wave + lane] = 1.0f / sqrtf(mine / (float)kCD + a.eps);
+  }
+  __syncthreads();
+  {
+    const float inv = 1.0f / sqrtf((float)kCD);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t idx = tid + kPairThreads * p;  // float4 index over [128 rows][32]
+      const uint32_t ri = idx / 32, c4 = idx % 32;
+      float* px = (ri < 64 ? qs_s + ri * kCStride : ks_s + (ri - 64) * kCStride) + 4 * c4;
+      const float sc = sc_s[ri];
+      f32x4 v = *(const f32x4*)px;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = ri < 64 ? v[e] * sc * inv * inv : v[e] * sc * inv;
+      *(f32x4*)px = v;
+    }
+  }
+  __syncthreads();
+
+  // Each head's scan operands K~^T and Gamma Q (split bf16, dn_b3_block).
+  {
+    uint16_t* kt3 = (uint16_t*)KTg;
+    uint16_t* q3 = (uint16_t*)Qg;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const uint32_t item = htid + 512 * p, ln = item % 64, blk = item / 64;  // blk = nb * 2 + s
+      const uint32_t col = 16 * (blk / 2) + ln % 16, i0 = 32 * (blk % 2) + 8 * (ln / 16);
+      f32x4 v0, v1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v0[e] = dk_s[i0 + e] * ks_s[(i0 + e) * kCStride + col];
+        v1[e] = dk_s[i0 + 4 + e] * ks_s[(i0 + 4 + e) * kCStride + col];
+      }
+      u32x4 hi, lo;
+      split_bf16x8(v0, v1, hi, lo);
+      *(u32x4*)(kt3 + blk * 1024 + 8 * ln) = hi;
+      *(u32x4*)(kt3 + blk * 1024 + 512 + 8 * ln) = lo;
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const uint32_t item = htid + 512 * p, ln = item % 64, blk = item / 64;  // blk = nb * 4 + s
+      const uint32_t t = 16 * (blk / 4) + ln % 16, k0 = 32 * (blk % 4) + 8 * (ln / 16);
+      const float* src = qs_s + t * kCStride + k0;
+      const float gm = gm_s[t];
+      u32x4 hi, lo;
+      split_bf16x8(*(const f32x4*)src * gm, *(const f32x4*)(src + 4) * gm, hi, lo);
+      *(u32x4*)(q3 + blk * 1024 + 8 * ln) = hi;
+      *(u32x4*)(q3 + blk * 1024 + 512 + 8 * ln) = lo;
+    }
+  }
+
+  // The 10 lower-triangular tiles of Q K^T and of K K^T, one product each
+  // over the 16 waves (the one-head kernel's tile arithmetic); each product
+  // is written out for both heads: P from Q K^T, -A from K K^T.
+  auto tile = [&](const float* xs, int tix, floatx4& acc, int& tm, int& tn) __attribute__((always_inline)) {
+    int rem = tix;
+    tm = 0;
+    while (rem > tm) rem -= ++tm;
+    tn = rem;
+    const float* xa = xs + (16 * tm + j) * kCStride + 4 * grp;
+    const float* xb = ks_s + (16 * tn + j) * kCStride + 4 * grp;
+    floatx4 ac[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const f32x4 av = *(const f32x4*)(xa + 16 * m);
+      const f32x4 bv = *(const f32x4*)(xb + 16 * m);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ac[e] = mfma_f32_4(av[e], bv[e], ac[e]);
+    }
+    acc = (ac[0] + ac[1]) + (ac[2] + ac[3]);
+  };
+  for (int u = (int)wave; u < 20; u += 16) {
+    const bool qk = u < 10;
+    floatx4 acc;
+    int tm, tn;
+    tile(qk ? qs_s : ks_s, qk ? u : u - 10, acc, tm, tn);
+    // acc[rr]: row t = 16 tm + 4 grp + rr, column i = 16 tn + j.
+    const uint32_t i = 16 * tn + j;
+#pragma unroll
+    for (int hr = 0; hr < 2; ++hr) {
+      const float* gh = gsets(hr);
+      const double* gdh = (const double*)(gh + 320);
+      if (qk) {
+        float* P = a.chunk_ws + ((size_t)c * VH + 2 * kh + hr) * kDnChunkFloats + kDnWsP;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const uint32_t t = 16 * tm + 4 * grp + rr;
+          P[dn_ws_index(tm, tn, 4 * grp + rr, j, 4)] = i <= t ? expf((float)(gdh[t] - gdh[i])) * acc[rr] : 0.0f;
+        }
+      } else {
+        float* A = a_base + hr * kPairA;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const uint32_t t = 16 * tm + 4 * grp + rr;
+          A[t * kAStride + i] = i < t ? -(gh[64 + t] * expf((float)(gdh[t] - gdh[i])) * acc[rr]) : 0.0f;  // -A
+        }
+      }
+    }
+  }
+  // P is zero above the diagonal blocks too, so its readers need no bounds.
+  for (uint32_t idx = htid; idx < 6 * 256; idx += 512) {
+    const uint32_t tl = idx / 256, e = idx % 256;
+    const uint32_t tm = tl < 3 ? 0 : tl < 5 ? 1 : 2;  // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+    const uint32_t tn = tl < 3 ? tl + 1 : tl < 5 ? tl - 1 : 3;
+    Pg[256 * (4 * tm + tn) + e] = 0.0f;
+  }
+  __syncthreads();
+
+  // Solve (I + A) X = R per head, as dn_chunk_prep_kernel: T_b by forward
+  // substitution (the head's waves 0..3, lanes 0..15), then the blocked MFMA
+  // solve with the head's wave hw owning W and U~ columns 16 hw .. + 15.
+  if (hw < 4 && lane < 16) {
+    const uint32_t b = hw, jj = lane;
+    const float* ab = a_s + 16 * b * kAStride + 16 * b;
+    float tc[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      float v = (uint32_t)t == jj ? 1.0f : 0.0f;
+#pragma unroll
+      for (int i = 0; i < t; ++i) v = fmaf(ab[t * kAStride + i], tc[i], v);
+      tc[t] = v;
+      t_s[(16 * b + t) * 17 + jj] = v;
+    }
+  }
+  __syncthreads();
+  const uint32_t cw = 16 * hw + j;
+  floatx4 X[4][2];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    floatx4 acc[2];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const uint32_t t = 16 * b + 4 * grp + rr;
+      acc[0][rr] = bg_s[t] * ks_s[t * kCStride + cw];
+      acc[1][rr] = t < nt ? beta_s[t] * vpre[b][rr] : 0.0f;
+    }
+#pragma unroll
+    for (int cb = 0; cb < b; ++cb) {
+      const f32x4 av = *(const f32x4*)(a_s + (16 * b + j) * kAStride + 16 * cb + 4 * grp);  // (-A)_bc
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+        for (int n = 0; n < 2; ++n) acc[n] = mfma_f32_4(av[rr], X[cb][n][rr], acc[n]);
+    }
+    const f32x4 tv = *(const f32x4*)(t_s + (16 * b + j) * 17 + 4 * grp);
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      X[b][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) X[b][n] = mfma_f32_4(tv[rr], acc[n][rr], X[b][n]);
+    }
+  }
+  __syncthreads();  // every wave is past k^, A and T: their LDS is free
+  float* xt = prep_lds + wave * (4 * 16 * 20);
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) xt[b * 320 + (4 * grp + rr) * 20 + j] = X[b][n][rr];
+    __builtin_amdgcn_wave_barrier();
+    if (n == 0) {
+      uint16_t* w3 = (uint16_t*)Wg;
+      if (grp / 2 == hw % 2) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const float* src = xt + b * 320 + j * 20 + 8 * (grp % 2);
+          u32x4 hi, lo;
+          split_bf16x8(*(const f32x4*)src, *(const f32x4*)(src + 4), hi, lo);
+          *(u32x4*)(w3 + dn_b3_block(b, hw / 2, 4) + 8 * lane) = hi;
+          *(u32x4*)(w3 + dn_b3_block(b, hw / 2, 4) + 512 + 8 * lane) = lo;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const f32x4 v = *(const f32x4*)(xt + b * 320 + (lane % 16) * 20 + 4 * (lane / 16));
+        *(f32x4*)(Ug + 256 * (4 * hw + b) + 4 * lane) = v;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 // grid: VH * 8 blocks (block = rg * VH + h: the 8 row groups of a head share
 // blockIdx mod 8, i.e. one XCD and its L2, where they read the same chunk
 // operands), 512 threads.  The group's 16 rows of S live in LDS.  Waves w and
@@ -1554,7 +1890,10 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
   if (chunked) {
     if (!a.chunk_ws) return hipErrorInvalidValue;
     const uint32_t nchunks = (a.M + kDnChunk - 1) / kDnChunk;
-    hipLaunchKernelGGL(dn_chunk_prep_kernel, dim3(nchunks * a.value_heads), dim3(kPrepThreads), kPrepLds, st, a);
+    if (a.value_heads == 2 * a.key_heads && a.tune_dn_pair != 0)
+      hipLaunchKernelGGL(dn_chunk_prep_pair_kernel, dim3(nchunks * a.key_heads), dim3(kPairThreads), kPairLds, st, a);
+    else
+      hipLaunchKernelGGL(dn_chunk_prep_kernel, dim3(nchunks * a.value_heads), dim3(kPrepThreads), kPrepLds, st, a);
     hipLaunchKernelGGL(dn_chunk_scan_kernel, dim3(a.value_heads * (kCD / 16)), dim3(kScanThreads), 0, st, a);
   } else {
     const uint32_t ept = (a.dk + kLanesPerRow - 1) / kLanesPerRow;

@@ -59,6 +59,7 @@ struct Tuning {
   int prefill_cb = 0;       // QM38_PREFILL_CB: column blocks per prefill wave (1, 2, 4)
   int dn_step_head = -1;    // QM38_DN_STEP_HEAD: 0 forces the split step kernel (-1: default)
   int dn_chunked = -1;      // QM38_DN_CHUNKED: 1 / 0 forces the chunked / token-serial prefill (-1: default)
+  int dn_pair = -1;         // QM38_DN_PAIR: 0 forces the one-value-head chunk preparation (-1: default)
 };
 Tuning read_tuning(int cu_count);
 

@@ -227,6 +227,7 @@ qm::Tuning qm::read_tuning(int cu_count) {
   t.prefill_cb = get("QM38_PREFILL_CB", 0);
   t.dn_step_head = get("QM38_DN_STEP_HEAD", -1);
   t.dn_chunked = get("QM38_DN_CHUNKED", -1);
+  t.dn_pair = get("QM38_DN_PAIR", -1);
   return t;
 }
 

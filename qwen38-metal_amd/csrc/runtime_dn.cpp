@@ -140,6 +140,7 @@ qm_status run(qm_runtime* rt, const qm_dn_weights* w, const qm_dn_state* from, q
   d.eps = eps;
   d.tune_step_head = rt->tune.dn_step_head;
   d.tune_chunked = rt->tune.dn_chunked;
+  d.tune_dn_pair = rt->tune.dn_pair;
   d.conv_w = w->conv_w;
   d.a_log = w->a_log;
   d.dt_bias = w->dt_bias;

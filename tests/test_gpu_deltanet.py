@@ -477,6 +477,29 @@ def test_chunked_matches_oracle(rt, torch_dev, shape, M, decay):
     _close(h, h_ref, tol=0, what="history")
 
 
+@pytest.mark.parametrize("shape,M", [((16, 32, 128, 128, 4), 2048), ((16, 32, 128, 128, 4), 200),
+                                     ((1, 2, 128, 128, 4), 130)])
+def test_chunked_pair_preparation_equals_one_head(rt, torch_dev, shape, M):
+    """Two value heads per key head: the chunk preparation that shares the
+    q/k work between them (QM38_DN_PAIR default) gives the one-head
+    kernel's outputs, state and history bit for bit."""
+    cfg, c = _cfg(*shape)
+    rng = np.random.default_rng(77 + M)
+    (conv, a_log, dt_bias, norm), acts = _synth(rng, c, M + 5)
+    a_log = (1.5 * rng.standard_normal(c["value_heads"])).astype(np.float32)  # strong, uneven decays
+    w = rt.create_deltanet_weights(cfg, conv, a_log, dt_bias, norm)
+    res = []
+    for pair in (1, 0):
+        st = w.create_state()
+        with _chunked(False) as trt:
+            _run(trt, torch_dev, w, st, *[x[:5] for x in acts], 1e-6)
+        with tuned(QM38_DN_CHUNKED=1, QM38_DN_PAIR=pair) as trt:
+            out = _run(trt, torch_dev, w, st, *[x[5:] for x in acts], 1e-6)
+        res.append((out, *st.read()))
+    for got, ref, what in zip(res[0], res[1], ("out", "history", "state")):
+        assert np.array_equal(got, ref), f"pair vs one-head {what} differs (M={M})"
+
+
 def test_chunked_shadow_prefill_leaves_source(rt, torch_dev):
     """deltanet_prefill_from with the chunked scan: the source state is read,
     never written; the shadow gets the result."""
