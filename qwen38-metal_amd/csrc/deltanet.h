@@ -50,16 +50,19 @@ struct DnArgs {
 // Chunked prefill (WY / UT form over chunks of kDnChunk tokens): used for
 // long prefills without state images at head dims 128 / 128 (or when
 // QM38_DN_CHUNKED forces it on or off).  Its workspace per (chunk, value
-// head): W [64][128], U~ [64][128], P [64][64], G [64], the decayed keys
-// transposed, K~^T [128][64] (K~^T[c][i] = e^{G_63 - G_i} k^[i][c]) and
-// Gamma q^ [64][128].  The matrices are stored in the scan's MFMA operand
+// head): W [64][128], U~ [64][128], P [64][64], G [64], Gamma = e^G [64],
+// e^{G_63 - G} [64], the keys transposed, k^^T [128][64], and q^ [64][128].
+// The keys and queries depend only on the key head: they are stored with the
+// first value head of each key head only (the scan applies the decays).  The
+// matrices are stored in the scan's MFMA operand
 // order: element (r, c) of a matrix with row blocks R = r / 16 and column
 // blocks C = c / 16 sits at dn_ws_index(R, C, r % 16, c % 16) of its 16 x 16
 // block sequence, i.e. lane (j = r % 16, g = (c % 16) / 4) holds the float4
 // of c % 4 = 0..3, and 64 lanes read one contiguous 1 KB block.  U~ is
 // stored per row group of S ([rg][token block] blocks, rows of U~ = tokens).
 constexpr uint32_t kDnChunk = 64;
-constexpr size_t kDnWsW = 0, kDnWsU = 8192, kDnWsP = 16384, kDnWsG = 20480, kDnWsKT = 20544, kDnWsQ = 28736;
+constexpr size_t kDnWsW = 0, kDnWsU = 8192, kDnWsP = 16384, kDnWsG = 20480, kDnWsGM = 20544, kDnWsDK = 20608,
+                 kDnWsKT = 20672, kDnWsQ = 28864;
 constexpr size_t kDnChunkFloats = kDnWsQ + 8192;
 // Element (row r, column c) of block (R, C) of a matrix with `cb` column
 // blocks: block base 256 (R cb + C), float4 16 (c / 4) + r, element c % 4.

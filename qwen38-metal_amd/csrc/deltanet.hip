@@ -925,8 +925,8 @@ __global__ __launch_bounds__(kThreads) void dn_conv_tiled_kernel(DnArgs a) {
 //   O   = diag(Gamma) Q S_0^T + P U,   P_ti = e^{G_t - G_i} q_t.k_i (i <= t)
 //   S_C = Gamma_C S_0 + U^T diag(e^{G_C - G_i}) K.
 // dn_chunk_prep_kernel forms W, U~, P and G for every (chunk, value head) in
-// parallel (fp32 MFMA for K K^T and Q K^T, forward substitution for the
-// solve); dn_chunk_scan_kernel then walks the chunks in order.  Rows of S
+// parallel (fp32 MFMA for K K^T and Q K^T, a blocked MFMA solve), and q^, k^
+// once per key head; dn_chunk_scan_kernel then walks the chunks in order.  Rows of S
 // stay independent (row j of S only meets column j of U), so each workgroup
 // owns 16 rows of one head in the same way as the token scan.
 __device__ __forceinline__ floatx4 mfma_f32_4(float a, float b, floatx4 c) {
@@ -965,6 +965,34 @@ __device__ __forceinline__ void split_bf16x8(const f32x4& a, const f32x4& b, u32
 // (j, g) = (lane % 16, lane / 16), the 8 elements [16 nb + j][32 s + 8 g + e]:
 // hi at 8 lane + e, lo 512 further (in bf16 units; 2 KB per block).
 __device__ __forceinline__ uint32_t dn_b3_block(uint32_t nb, uint32_t s, uint32_t S) { return (nb * S + s) * 1024; }
+
+// The scan's B operands of one key head as split bf16 blocks (dn_b3_block),
+// 2 x 16 bytes per item (1024 items each): k^^T[c][i] = k^[i][c] (8 column
+// blocks, 2 steps over i) for the state update and q^[t][k] (4 token blocks,
+// 4 steps over k) for the output.  The decays enter in the scan.
+__device__ __forceinline__ void dn_chunk_store_k(const float* ks_s, uint16_t* kt3, uint32_t item) {
+  const uint32_t ln = item % 64, blk = item / 64;  // blk = nb * 2 + s
+  const uint32_t col = 16 * (blk / 2) + ln % 16, i0 = 32 * (blk % 2) + 8 * (ln / 16);
+  f32x4 v0, v1;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v0[e] = ks_s[(i0 + e) * kCStride + col];
+    v1[e] = ks_s[(i0 + 4 + e) * kCStride + col];
+  }
+  u32x4 hi, lo;
+  split_bf16x8(v0, v1, hi, lo);
+  *(u32x4*)(kt3 + blk * 1024 + 8 * ln) = hi;
+  *(u32x4*)(kt3 + blk * 1024 + 512 + 8 * ln) = lo;
+}
+__device__ __forceinline__ void dn_chunk_store_q(const float* qs_s, uint16_t* q3, uint32_t item) {
+  const uint32_t ln = item % 64, blk = item / 64;  // blk = nb * 4 + s
+  const uint32_t t = 16 * (blk / 4) + ln % 16, k0 = 32 * (blk % 4) + 8 * (ln / 16);
+  const float* src = qs_s + t * kCStride + k0;
+  u32x4 hi, lo;
+  split_bf16x8(*(const f32x4*)src, *(const f32x4*)(src + 4), hi, lo);
+  *(u32x4*)(q3 + blk * 1024 + 8 * ln) = hi;
+  *(u32x4*)(q3 + blk * 1024 + 512 + 8 * ln) = lo;
+}
 
 // LDS of dn_chunk_prep_kernel (dynamic, so the compiler's register budget
 // follows the VGPR occupancy target rather than the LDS-bound one): k^ and
@@ -1096,6 +1124,8 @@ __global__ __launch_bounds__(kPrepThreads, 2) void dn_chunk_prep_kernel(DnArgs a
     bg_s[lane] = beta * expf(G);
     gm_s[lane] = expf(G);
     Gg[lane] = G;
+    Gg[kDnWsGM - kDnWsG + lane] = gm_s[lane];
+    Gg[kDnWsDK - kDnWsG + lane] = dk_s[lane];
   }
   __syncthreads();
   // prep_key_head's RMS scales: row ri (q rows 0..63, k rows 64..127), lane l
@@ -1133,39 +1163,13 @@ __global__ __launch_bounds__(kPrepThreads, 2) void dn_chunk_prep_kernel(DnArgs a
   }
   __syncthreads();
 
-  // The scan's B operands as split bf16 blocks (dn_b3_block): K~^T[c][i] =
-  // e^{G_63 - G_i} k^[i][c] (8 column blocks, 2 steps over i) for the state
-  // update and Gamma_t q^[t][k] (4 token blocks, 4 steps over k) for the
-  // output; 2 x 16 bytes per lane and block.
-  {
-    uint16_t* kt3 = (uint16_t*)KTg;
-    uint16_t* q3 = (uint16_t*)Qg;
+  // The scan's B operands of the key head (first value head of each key
+  // head only): dn_chunk_store_qk.
+  if (h % (VH / a.key_heads) == 0) {
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const uint32_t item = tid + kPrepThreads * p, ln = item % 64, blk = item / 64;  // blk = nb * 2 + s
-      const uint32_t col = 16 * (blk / 2) + ln % 16, i0 = 32 * (blk % 2) + 8 * (ln / 16);
-      f32x4 v0, v1;
+    for (int p = 0; p < 2; ++p) dn_chunk_store_k(ks_s, (uint16_t*)KTg, tid + kPrepThreads * p);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v0[e] = dk_s[i0 + e] * ks_s[(i0 + e) * kCStride + col];
-        v1[e] = dk_s[i0 + 4 + e] * ks_s[(i0 + 4 + e) * kCStride + col];
-      }
-      u32x4 hi, lo;
-      split_bf16x8(v0, v1, hi, lo);
-      *(u32x4*)(kt3 + blk * 1024 + 8 * ln) = hi;
-      *(u32x4*)(kt3 + blk * 1024 + 512 + 8 * ln) = lo;
-    }
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const uint32_t item = tid + kPrepThreads * p, ln = item % 64, blk = item / 64;  // blk = nb * 4 + s
-      const uint32_t t = 16 * (blk / 4) + ln % 16, k0 = 32 * (blk % 4) + 8 * (ln / 16);
-      const float* src = qs_s + t * kCStride + k0;
-      const float gm = gm_s[t];
-      u32x4 hi, lo;
-      split_bf16x8(*(const f32x4*)src * gm, *(const f32x4*)(src + 4) * gm, hi, lo);
-      *(u32x4*)(q3 + blk * 1024 + 8 * ln) = hi;
-      *(u32x4*)(q3 + blk * 1024 + 512 + 8 * ln) = lo;
-    }
+    for (int p = 0; p < 2; ++p) dn_chunk_store_q(qs_s, (uint16_t*)Qg, tid + kPrepThreads * p);
   }
 
   // Q K^T, then K K^T, on the lower-triangular 16 x 16 tiles (tn <= tm):
@@ -1450,6 +1454,8 @@ __global__ __launch_bounds__(kPairThreads) void dn_chunk_prep_pair_kernel(DnArgs
     bg_s[lane] = beta * expf(G);
     gm_s[lane] = expf(G);
     Gg[lane] = G;
+    Gg[kDnWsGM - kDnWsG + lane] = gm_s[lane];
+    Gg[kDnWsDK - kDnWsG + lane] = dk_s[lane];
   }
   __syncthreads();
   // RMS scales (prep_key_head's reductions): 8 rows per wave side by side,
@@ -1486,35 +1492,16 @@ __global__ __launch_bounds__(kPairThreads) void dn_chunk_prep_pair_kernel(DnArgs
   }
   __syncthreads();
 
-  // Each head's scan operands K~^T and Gamma Q (split bf16, dn_b3_block).
+  // The key head's scan operands, stored with value head 2 kh: k^^T by the
+  // first head's waves, q^ by the second's.
   {
-    uint16_t* kt3 = (uint16_t*)KTg;
-    uint16_t* q3 = (uint16_t*)Qg;
+    float* ws0 = a.chunk_ws + ((size_t)c * VH + 2 * kh) * kDnChunkFloats;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      const uint32_t item = htid + 512 * p, ln = item % 64, blk = item / 64;  // blk = nb * 2 + s
-      const uint32_t col = 16 * (blk / 2) + ln % 16, i0 = 32 * (blk % 2) + 8 * (ln / 16);
-      f32x4 v0, v1;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v0[e] = dk_s[i0 + e] * ks_s[(i0 + e) * kCStride + col];
-        v1[e] = dk_s[i0 + 4 + e] * ks_s[(i0 + 4 + e) * kCStride + col];
-      }
-      u32x4 hi, lo;
-      split_bf16x8(v0, v1, hi, lo);
-      *(u32x4*)(kt3 + blk * 1024 + 8 * ln) = hi;
-      *(u32x4*)(kt3 + blk * 1024 + 512 + 8 * ln) = lo;
-    }
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const uint32_t item = htid + 512 * p, ln = item % 64, blk = item / 64;  // blk = nb * 4 + s
-      const uint32_t t = 16 * (blk / 4) + ln % 16, k0 = 32 * (blk % 4) + 8 * (ln / 16);
-      const float* src = qs_s + t * kCStride + k0;
-      const float gm = gm_s[t];
-      u32x4 hi, lo;
-      split_bf16x8(*(const f32x4*)src * gm, *(const f32x4*)(src + 4) * gm, hi, lo);
-      *(u32x4*)(q3 + blk * 1024 + 8 * ln) = hi;
-      *(u32x4*)(q3 + blk * 1024 + 512 + 8 * ln) = lo;
+      if (r == 0)
+        dn_chunk_store_k(ks_s, (uint16_t*)(ws0 + kDnWsKT), htid + 512 * p);
+      else
+        dn_chunk_store_q(qs_s, (uint16_t*)(ws0 + kDnWsQ), htid + 512 * p);
     }
   }
 
@@ -1655,18 +1642,20 @@ __global__ __launch_bounds__(kPairThreads) void dn_chunk_prep_pair_kernel(DnArgs
 // blockIdx mod 8, i.e. one XCD and its L2, where they read the same chunk
 // operands), 512 threads.  The group's 16 rows of S live in LDS.  Waves w and
 // w + 4 share tokens 16 w .. 16 w + 15 and split the reduction over k of
-//   U_w^T = U~_w^T - S W_w^T,   O_w^T = S (Gamma Q_w)^T        (k halves)
-// (partials meet in LDS); then, after U^T is exchanged, wave v of 8 updates
-// columns 16 v .. 16 v + 15 of S as Gamma_C S + U^T K~ over the chunk's 64
-// tokens, and waves 0..3 add the intra-chunk term sum_{i <= t} U^T P and
-// store O.  Waves w and w + 4 run on one SIMD, so one's memory and LDS waits
+//   U_w^T = U~_w^T - S W_w^T,   O_w^T = (S Q_w^T) diag(Gamma_w)   (k halves)
+// (partials meet in LDS; q^ and k^ are the key head's, the decays this
+// head's); then, after U^T and U^T diag(e^{G_C - G_i}) are exchanged, wave v
+// of 8 updates columns 16 v .. 16 v + 15 of S as
+// Gamma_C S + U^T diag(e^{G_C - G_i}) K over the chunk's 64 tokens, and
+// waves 0..3 add the intra-chunk term sum_{i <= t} U^T P and store O.  Waves w and w + 4 run on one SIMD, so one's memory and LDS waits
 // overlap the other's MFMAs.  The products with S and with U^T are split-bf16
 // triples on the bf16 MFMA; P U^T is fp32.  The next chunk's operands are
 // loaded while the current chunk is computed.
 constexpr int kScanThreads = 512;
 __global__ __launch_bounds__(kScanThreads) void dn_chunk_scan_kernel(DnArgs a) {
-  __shared__ __attribute__((aligned(16))) float u_s[16 * kAStride];  // U^T [row][token]
-  __shared__ __attribute__((aligned(16))) float s_s[16 * kCStride];  // S [row][col]
+  __shared__ __attribute__((aligned(16))) float u_s[16 * kAStride];   // U^T [row][token]
+  __shared__ __attribute__((aligned(16))) float ud_s[16 * kAStride];  // U^T [row][i] e^{G_63 - G_i}
+  __shared__ __attribute__((aligned(16))) float s_s[16 * kCStride];   // S [row][col]
   __shared__ __attribute__((aligned(16))) float xp_s[4][64][8];      // the upper k half's partials
   const uint32_t VH = a.value_heads;
   const uint32_t h = blockIdx.x % VH, rg = blockIdx.x / VH;
@@ -1681,15 +1670,20 @@ __global__ __launch_bounds__(kScanThreads) void dn_chunk_scan_kernel(DnArgs a) {
 
   u32x4 Wh[2], Wl[2], Qh[2], Ql[2], Kh[2], Kl[2];  // split bf16 B operands (the wave's k half / columns)
   f32x4 Uv, Pv[4];
-  float G_last;
+  float G_last, gm_tok, dk_tok;
   auto ws_of = [&](uint32_t c) { return a.chunk_ws + ((size_t)c * VH + h) * kDnChunkFloats; };
+  // k^ and q^ of the key head live with its first value head.
+  const uint32_t h_key = h - h % (VH / a.key_heads);
+  auto qk_of = [&](uint32_t c) { return a.chunk_ws + ((size_t)c * VH + h_key) * kDnChunkFloats; };
   const uint32_t lofs = 4 * (16 * grp + j);  // the lane's float4 within a 64-float4 block
   // Rows past the last token read valid data and are weighted by zero.
   auto load_wqu = [&](uint32_t c) __attribute__((always_inline)) {
     const float* ws = ws_of(c);
     G_last = ws[kDnWsG + 63];
+    gm_tok = ws[kDnWsGM + tok];
+    dk_tok = ws[kDnWsDK + tok];
     const uint16_t* w3 = (const uint16_t*)(ws + kDnWsW);
-    const uint16_t* q3 = (const uint16_t*)(ws + kDnWsQ);
+    const uint16_t* q3 = (const uint16_t*)(qk_of(c) + kDnWsQ);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const uint32_t o = dn_b3_block(tw, 2 * khalf + s, 4) + 8 * lane;
@@ -1704,7 +1698,7 @@ __global__ __launch_bounds__(kScanThreads) void dn_chunk_scan_kernel(DnArgs a) {
   // (split bf16, the wave's 16 columns).
   auto load_pk = [&](uint32_t c) __attribute__((always_inline)) {
     const float* ws = ws_of(c);
-    const uint16_t* kt3 = (const uint16_t*)(ws + kDnWsKT);
+    const uint16_t* kt3 = (const uint16_t*)(qk_of(c) + kDnWsKT);
     if (khalf == 0) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) Pv[m] = *(const f32x4*)(ws + kDnWsP + 256 * (4 * tw + m) + lofs);
@@ -1732,9 +1726,9 @@ __global__ __launch_bounds__(kScanThreads) void dn_chunk_scan_kernel(DnArgs a) {
     const uint32_t t0 = c * kDnChunk, nt = min(kDnChunk, a.M - t0);
     const uint32_t cn = min(c + 1, nchunks - 1);  // the last chunk reloads itself (unused)
     // (a) U^T[row][tok] = U~[tok][row] - sum_k S[row][k] W[tok][k]
-    // (b1) O^T[row][tok] = sum_k S[row][k] Gamma_tok q[tok][k]
+    // (b1) O^T[row][tok] = Gamma_tok sum_k S[row][k] q[tok][k]
     // over this wave's k half: S (A operand, row j, k = 32 s + 8 grp + e) is
-    // split here, W and Gamma q come split.
+    // split here, W and q come split.
     floatx4 au[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     floatx4 ao[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -1764,16 +1758,21 @@ __global__ __launch_bounds__(kScanThreads) void dn_chunk_scan_kernel(DnArgs a) {
     if (khalf == 0) {
       acc_u += *(const f32x4*)&xp_s[tw][lane][0];
       acc_o += *(const f32x4*)&xp_s[tw][lane][4];
+      acc_o *= gm_tok;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) u_s[(4 * grp + r) * kAStride + tok] = Uv[r] - acc_u[r];
+      for (int r = 0; r < 4; ++r) {
+        const float u = Uv[r] - acc_u[r];
+        u_s[(4 * grp + r) * kAStride + tok] = u;
+        ud_s[(4 * grp + r) * kAStride + tok] = dk_tok * u;
+      }
     }
     load_wqu(cn);  // W, q and U~ of this chunk are consumed
     lds_barrier();  // U^T complete; every wave is done reading S and the partials
-    // S[:, cols_w] += U^T K~[:, cols_w] over the chunk's 64 tokens.
+    // S[:, cols_w] += U^T diag(e^{G_63 - G_i}) K[:, cols_w] over the chunk's 64 tokens.
     floatx4 dx[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const float* up = u_s + j * kAStride + 32 * s + 8 * grp;
+      const float* up = ud_s + j * kAStride + 32 * s + 8 * grp;
       u32x4 uh, ul;
       split_bf16x8(*(const f32x4*)up, *(const f32x4*)(up + 4), uh, ul);
       d = mfma16x16x32(uh, Kh[s], d);
