@@ -705,6 +705,73 @@ __global__ __launch_bounds__(256) void q8_combine_kernel(AttnArgs args) {
   }
 }
 
+// The same merge when every sequence has at most 32 splits: one wave per
+// (sequence, head, 32-wide d slice).  Lane (c, g) = (t % 8, t / 8) holds
+// float4 slice c and splits g, g + 8, g + 16, g + 24, all loaded at once;
+// the maximum and the sums over g meet through lane swaps (xor 8, 16, 32),
+// so the merge needs no LDS and no barrier.
+template <int D>
+__global__ __launch_bounds__(64) void q8_combine_small_kernel(AttnArgs args) {
+  constexpr int kWgPerHead = D / 32;
+  constexpr int kPer = 4;  // splits per lane
+  const uint32_t H = args.heads, dr = args.head_dim;
+  const uint32_t wq = blockIdx.x % kWgPerHead;
+  const uint32_t bh = blockIdx.x / kWgPerHead;
+  const uint32_t b = bh / H, hh = bh % H;
+  const AttnSeq& sq = args.seqs[b];
+  const uint32_t ns = sq.nsplit;
+  if (ns <= 1 || 32 * wq >= dr) return;
+  const size_t o_rows = (size_t)args.part_rows * H;
+  const float* obase = args.partials + ((size_t)sq.part_begin * H + hh) * D;
+  const float* mbase = args.partials + o_rows * D + ((size_t)sq.part_begin * H + hh) * 2;
+  const uint32_t t = threadIdx.x, c = t % 8, g = t / 8;
+  const uint32_t d0 = 32 * wq + 4 * c;
+  floatx4 ov[kPer];
+  float2 ml[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t s = g + 8 * k;
+    const size_t row = s < ns ? s : ns - 1;
+    ov[k] = *(const floatx4*)(obase + row * H * D + d0);
+    ml[k] = *(const float2*)(mbase + row * H * 2);
+  }
+  float mv[kPer];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    mv[k] = g + 8 * k < ns ? ml[k].x : -INFINITY;
+    mx = fmaxf(mx, mv[k]);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 8));
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  float L = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const float f = mv[k] == -INFINITY ? 0.0f : exp2f(mv[k] - mx);
+    acc += ov[k] * f;
+    L += ml[k].y * f;
+  }
+#pragma unroll
+  for (int m = 8; m < 64; m <<= 1) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], m);
+    L += __shfl_xor(L, m);
+  }
+  if (g == 0) {
+    const float inv = 1.0f / fmaxf(L, FLT_MIN);
+    const size_t oi = ((size_t)b * H + hh) * dr + d0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (d0 + e >= dr) break;
+      float v = acc[e] * inv;
+      if (args.gate) v *= sigmoid_f(bf16_to_f32(args.gate[oi + e]));
+      args.o[oi + e] = f32_to_bf16(v);
+    }
+  }
+}
+
 // Causal prefill: blockIdx.x = rb * KVH + kvh.  A wave owns CB column
 // blocks of 16 (row, head) columns, i.e. CB * 16 / gh query rows of one KV
 // head; the workgroup's four waves own consecutive rows and walk the same
@@ -1018,8 +1085,14 @@ hipError_t launch_attn_d(const AttnArgs& a, uint32_t units, bool need_combine, h
     hipLaunchKernelGGL((q8_decode_kernel<D, 8>), dim3(units), dim3(512), 0, st, a);
   else
     hipLaunchKernelGGL((q8_decode_kernel<D, 4>), dim3(units), dim3(256), 0, st, a);
-  if (need_combine)
-    hipLaunchKernelGGL(q8_combine_kernel<D>, dim3(a.n_seqs * a.heads * (D / 32)), dim3(256), 0, st, a);
+  if (need_combine) {
+    uint32_t max_split = 0;
+    for (uint32_t i = 0; i < a.n_seqs; ++i) max_split = max_split > a.seqs[i].nsplit ? max_split : a.seqs[i].nsplit;
+    if (max_split <= 32)
+      hipLaunchKernelGGL(q8_combine_small_kernel<D>, dim3(a.n_seqs * a.heads * (D / 32)), dim3(64), 0, st, a);
+    else
+      hipLaunchKernelGGL(q8_combine_kernel<D>, dim3(a.n_seqs * a.heads * (D / 32)), dim3(256), 0, st, a);
+  }
   return hipGetLastError();
 }
 
