@@ -994,6 +994,29 @@ __device__ __forceinline__ void dn_chunk_store_q(const float* qs_s, uint16_t* q3
   *(u32x4*)(q3 + blk * 1024 + 512 + 8 * ln) = lo;
 }
 
+// One 16 x 16 tile of X Y^T over the 128 columns of rows 16 tm .. of xs and
+// 16 tn .. of ys ([64][kCStride] fp32 in LDS), on split-bf16 16x16x32 MFMAs:
+// each operand is hi + lo in bf16, the product hi.hi + hi.lo + lo.hi with
+// fp32 accumulation (about 2^-17 relative error per product, five times
+// fewer MFMA cycles than 16x16x4 fp32).  Lane (j, grp) of the result holds
+// rows 4 grp .. 4 grp + 3 of column j.
+__device__ __forceinline__ floatx4 dn_gram_tile(const float* xs, const float* ys, int tm, int tn, uint32_t j,
+                                                uint32_t grp) {
+  const float* xa = xs + (16 * tm + j) * kCStride + 8 * grp;
+  const float* yb = ys + (16 * tn + j) * kCStride + 8 * grp;
+  floatx4 ac[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    u32x4 ah, al, bh, bl;
+    split_bf16x8(*(const f32x4*)(xa + 32 * m), *(const f32x4*)(xa + 32 * m + 4), ah, al);
+    split_bf16x8(*(const f32x4*)(yb + 32 * m), *(const f32x4*)(yb + 32 * m + 4), bh, bl);
+    ac[0] = mfma16x16x32(ah, bh, ac[0]);
+    ac[1] = mfma16x16x32(ah, bl, ac[1]);
+    ac[2] = mfma16x16x32(al, bh, ac[2]);
+  }
+  return ac[0] + (ac[1] + ac[2]);
+}
+
 // LDS of dn_chunk_prep_kernel (dynamic, so the compiler's register budget
 // follows the VGPR occupancy target rather than the LDS-bound one): k^ and
 // q^ rows of the chunk, then G and beta.  Once the products are formed the
@@ -1174,25 +1197,13 @@ __global__ __launch_bounds__(kPrepThreads, 2) void dn_chunk_prep_kernel(DnArgs a
 
   // Q K^T, then K K^T, on the lower-triangular 16 x 16 tiles (tn <= tm):
   // 10 tiles each over the 8 waves.  Q K^T goes straight to P; once every
-  // wave is past it the q^ rows' space takes A from K K^T.  The MFMA
-  // reduction index is permuted (lane group g of step (m, e) carries
-  // k = 16 m + 4 g + e), so every operand is one 16-byte LDS read.
+  // wave is past it the q^ rows' space takes A from K K^T (dn_gram_tile).
   auto tile = [&](const float* xs, int tix, floatx4& acc, int& tm, int& tn) __attribute__((always_inline)) {
     int rem = tix;
     tm = 0;
     while (rem > tm) rem -= ++tm;
     tn = rem;
-    const float* xa = xs + (16 * tm + j) * kCStride + 4 * grp;
-    const float* xb = ks_s + (16 * tn + j) * kCStride + 4 * grp;
-    floatx4 ac[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const f32x4 av = *(const f32x4*)(xa + 16 * m);
-      const f32x4 bv = *(const f32x4*)(xb + 16 * m);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ac[e] = mfma_f32_4(av[e], bv[e], ac[e]);
-    }
-    acc = (ac[0] + ac[1]) + (ac[2] + ac[3]);
+    acc = dn_gram_tile(xs, ks_s, tm, tn, j, grp);
   };
   for (int tix = (int)wave; tix < 10; tix += 8) {
     floatx4 acc;
@@ -1319,27 +1330,35 @@ __global__ __launch_bounds__(kPrepThreads, 2) void dn_chunk_prep_kernel(DnArgs a
   }
 }
 
-// dn_chunk_prep_kernel's work for the two value heads of one key head in one
-// 16-wave workgroup (value_heads == 2 key_heads).  The q^ / k^ conv, their
-// RMS scales and the raw products Q K^T and K K^T depend only on the key
-// head, so they are formed once by all 16 waves; waves 8 r .. 8 r + 7 then
-// take value head 2 kh + r through its decays, v conv, solve and stores
-// exactly as the one-head kernel does (same arithmetic, same bits).
-// LDS: k^ and q^ rows, then each head's -A, T blocks and decays; the W / U~
-// transposes reuse the space from the start once the solve is done.
-constexpr uint32_t kPairG = 448;  // floats of one head's decays (G, beta, e^{G63-G}, beta e^G, e^G, G fp64)
-constexpr uint32_t kPairA = 64 * kAStride, kPairT = 4 * 16 * 17;
-constexpr uint32_t kPairLds = (2 * 64 * kCStride + 2 * kPairA + 2 * kPairT + 2 * kPairG + 128) * 4;
-constexpr int kPairThreads = 1024;  // 16 waves
-static_assert(16 * 4 * 16 * 20 * 4 <= kPairLds, "transpose rows fit the pair kernel's LDS");
-__global__ __launch_bounds__(kPairThreads) void dn_chunk_prep_pair_kernel(DnArgs a) {
+// Per-head LDS pieces of the two-head preparation: one head's decays (G,
+// beta, e^{G_63 - G}, beta e^G, e^G, then G in fp64) and its T blocks.
+constexpr uint32_t kPairG = 448;
+constexpr uint32_t kPairT = 4 * 16 * 17;
+
+// dn_chunk_prep_kernel's work for the two value heads of one key head
+// (value_heads == 2 key_heads) in one 8-wave workgroup, two per CU.  The q^ /
+// k^ conv, their RMS scales and the raw products Q K^T and K K^T depend only
+// on the key head, so they are formed once and written out for both heads
+// with each head's decays; waves 4 r .. 4 r + 3 then take value head
+// 2 kh + r through its decays, v conv, solve and stores with the one-head
+// kernel's arithmetic (same bits), each owning two of that kernel's
+// 16-column slices (16 v and 16 (v + 4) for its v = wave % 4).  Both heads'
+// -A overlay the q^ rows once Q K^T is formed (row stride 66 instead of 68 so
+// that the two fit), which keeps the LDS at 80 KB.
+constexpr uint32_t kP8AStride = 66;
+constexpr uint32_t kP8A = 64 * kP8AStride;
+constexpr uint32_t kP8Lds = (2 * 64 * kCStride + 2 * kPairT + 2 * kPairG + 128) * 4;
+constexpr int kP8Threads = 512;
+static_assert(2 * kP8A <= 64 * kCStride, "both heads' -A fit the q^ rows");
+static_assert(2 * kP8Lds <= 160 * 1024, "two workgroups per CU");
+static_assert(8 * 4 * 16 * 20 <= 2 * 64 * kCStride, "transpose rows fit the k^ and q^ rows");
+__global__ __launch_bounds__(kP8Threads, 4) void dn_chunk_prep_pair_kernel(DnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float prep_lds[];
   float* ks_s = prep_lds;
   float* qs_s = prep_lds + 64 * kCStride;
-  float* a_base = prep_lds + 2 * 64 * kCStride;         // [2][64][kAStride]
-  float* t_base = a_base + 2 * kPairA;                  // [2][4][16][17]
-  float* g_base = t_base + 2 * kPairT;                  // [2][kPairG]
-  float* sc_s = g_base + 2 * kPairG;                    // RMS scales: q rows 0..63, k rows 64..127
+  float* t_base = prep_lds + 2 * 64 * kCStride;  // [2][4][16][17]
+  float* g_base = t_base + 2 * kPairT;           // [2][kPairG]
+  float* sc_s = g_base + 2 * kPairG;             // RMS scales: q rows 0..63, k rows 64..127
   const uint32_t VH = a.value_heads;
   const uint32_t KH = a.key_heads;
   const uint32_t kh = blockIdx.x % KH, c = blockIdx.x / KH;
@@ -1348,11 +1367,10 @@ __global__ __launch_bounds__(kPairThreads) void dn_chunk_prep_pair_kernel(DnArgs
   const uint32_t nt = min(kDnChunk, a.M - t0);
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // This wave's value head (r) and its place among that head's 8 waves.
-  const uint32_t r = wave / 8, hw = wave % 8, htid = tid % 512;
+  const uint32_t r = wave / 4, hw = wave % 4, htid = tid % 256;
   const uint32_t h = 2 * kh + r;
   const uint32_t j = lane & 15, grp = lane >> 4;
-  float* a_s = a_base + r * kPairA;
+  float* a_s = qs_s + r * kP8A;  // once Q K^T is formed
   float* t_s = t_base + r * kPairT;
   auto gsets = [&](uint32_t rr) { return g_base + rr * kPairG; };
   float* g_s = gsets(r);
@@ -1366,37 +1384,34 @@ __global__ __launch_bounds__(kPairThreads) void dn_chunk_prep_pair_kernel(DnArgs
   float* Ug = ws + kDnWsU;
   float* Pg = ws + kDnWsP;
   float* Gg = ws + kDnWsG;
-  float* KTg = ws + kDnWsKT;
-  float* Qg = ws + kDnWsQ;
 
-  // The chunk's conv: thread t owns key channel t % 256 of key head kh (q
-  // 0..127, k 128..255) and tokens 16 (t / 256) .. + 15, and the v columns
-  // 16 hw + j of its head for the solve, all inputs loaded before any is
-  // used.  Sums as conv_finish's; SiLU as silu_fast.
-  const uint32_t kc = tid % 256, th0 = 16 * (tid / 256);
+  // Conv: thread t owns key channel t % 256 and tokens 32 (t / 256) .. + 31,
+  // and the v columns of its two slices; every input is loaded first.
+  const uint32_t kc = tid % 256, th0 = 32 * (tid / 256);
   const uint32_t kch = kc < kCD ? kh * kCD + kc : key_el + kh * kCD + (kc - kCD);
-  float vw[4], vx[4][7];
-  {
-    const uint32_t vch = 2 * key_el + h * kCD + 16 * hw + j;
+  float vw[2][4], vx[2][4][7];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) vw[q] = a.conv_w[(size_t)vch * 4 + q];
+  for (int sl = 0; sl < 2; ++sl) {
+    const uint32_t vch = 2 * key_el + h * kCD + 16 * (hw + 4 * sl) + j;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) vw[sl][q] = a.conv_w[(size_t)vch * 4 + q];
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int q = 0; q < 7; ++q)
-        vx[b][q] = conv_input(a, vch, min((int)(t0 + 16 * b + 4 * grp) - 3 + q, (int)a.M - 1));
+        vx[sl][b][q] = conv_input(a, vch, min((int)(t0 + 16 * b + 4 * grp) - 3 + q, (int)a.M - 1));
   }
   {
-    float w[4], win[3], xk[16];
+    float w[4], win[3], xk[32];
 #pragma unroll
     for (int q = 0; q < 4; ++q) w[q] = a.conv_w[(size_t)kch * 4 + q];
 #pragma unroll
     for (int q = 0; q < 3; ++q) win[q] = conv_input(a, kch, min((int)(t0 + th0) - 3 + q, (int)a.M - 1));
 #pragma unroll
-    for (int k = 0; k < 16; ++k) xk[k] = a.qkv[(size_t)min(t0 + th0 + k, a.M - 1) * a.channels + kch];
+    for (int k = 0; k < 32; ++k) xk[k] = a.qkv[(size_t)min(t0 + th0 + k, a.M - 1) * a.channels + kch];
     float* dst = kc < kCD ? qs_s + kc : ks_s + (kc - kCD);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
+    for (int k = 0; k < 32; ++k) {
       const float x = xk[k];
       float sum = __fmul_rn(w[3], x);
       sum = fmaf(w[0], win[0], sum);
@@ -1409,30 +1424,29 @@ __global__ __launch_bounds__(kPairThreads) void dn_chunk_prep_pair_kernel(DnArgs
       dst[t * kCStride] = t < nt ? silu_fast(sum) : 0.0f;
     }
   }
-  float vpre[4][4];
+  float vpre[2][4][4];
 #pragma unroll
-  for (int b = 0; b < 4; ++b)
+  for (int sl = 0; sl < 2; ++sl)
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      float sum = __fmul_rn(vw[3], vx[b][rr + 3]);
-      sum = fmaf(vw[0], vx[b][rr], sum);
-      sum = fmaf(vw[1], vx[b][rr + 1], sum);
-      sum = fmaf(vw[2], vx[b][rr + 2], sum);
-      vpre[b][rr] = silu_fast(sum);
-    }
-  // The state's conv history after the last token (raw inputs of the final
-  // three tokens): key channels once, each head's v channels by its waves.
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        float sum = __fmul_rn(vw[sl][3], vx[sl][b][rr + 3]);
+        sum = fmaf(vw[sl][0], vx[sl][b][rr], sum);
+        sum = fmaf(vw[sl][1], vx[sl][b][rr + 1], sum);
+        sum = fmaf(vw[sl][2], vx[sl][b][rr + 2], sum);
+        vpre[sl][b][rr] = silu_fast(sum);
+      }
   if (c + 1 == (a.M + kDnChunk - 1) / kDnChunk) {
     if (tid < 256)
 #pragma unroll
       for (int q = 0; q < 3; ++q) a.hist_out[(size_t)kch * 3 + q] = conv_input(a, kch, (int)a.M - 3 + q);
-    if (htid >= 256 && htid < 256 + kCD) {
-      const uint32_t vch = 2 * key_el + h * kCD + (htid - 256);
+    if (htid < kCD) {
+      const uint32_t vch = 2 * key_el + h * kCD + htid;
 #pragma unroll
       for (int q = 0; q < 3; ++q) a.hist_out[(size_t)vch * 3 + q] = conv_input(a, vch, (int)a.M - 3 + q);
     }
   }
-  // Each head's log decays, running sum and beta (its first wave).
   if (hw == 0) {
     float lg = 0.0f, beta = 0.0f;
     if (lane < nt) {
@@ -1458,29 +1472,27 @@ __global__ __launch_bounds__(kPairThreads) void dn_chunk_prep_pair_kernel(DnArgs
     Gg[kDnWsDK - kDnWsG + lane] = dk_s[lane];
   }
   __syncthreads();
-  // RMS scales (prep_key_head's reductions): 8 rows per wave side by side,
-  // lane q forming row q's scale.
   {
-    float ss[8];
+    float ss[16];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint32_t ri = 8 * wave + q;
+    for (int q = 0; q < 16; ++q) {
+      const uint32_t ri = 16 * wave + q;
       const float* row = (ri < 64 ? qs_s + ri * kCStride : ks_s + (ri - 64) * kCStride) + lane;
       ss[q] = fmaf(row[64], row[64], fmaf(row[0], row[0], 0.0f));
     }
 #pragma unroll
-    for (int q = 0; q < 8; ++q) ss[q] = wave_sum(ss[q]);
+    for (int q = 0; q < 16; ++q) ss[q] = wave_sum(ss[q]);
     float mine = ss[0];
 #pragma unroll
-    for (int q = 1; q < 8; ++q) mine = lane == (uint32_t)q ? ss[q] : mine;
-    if (lane < 8) sc_s[8 * wave + lane] = 1.0f / sqrtf(mine / (float)kCD + a.eps);
+    for (int q = 1; q < 16; ++q) mine = lane == (uint32_t)q ? ss[q] : mine;
+    if (lane < 16) sc_s[16 * wave + lane] = 1.0f / sqrtf(mine / (float)kCD + a.eps);
   }
   __syncthreads();
   {
     const float inv = 1.0f / sqrtf((float)kCD);
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint32_t idx = tid + kPairThreads * p;  // float4 index over [128 rows][32]
+    for (int p = 0; p < 8; ++p) {
+      const uint32_t idx = tid + kP8Threads * p;
       const uint32_t ri = idx / 32, c4 = idx % 32;
       float* px = (ri < 64 ? qs_s + ri * kCStride : ks_s + (ri - 64) * kCStride) + 4 * c4;
       const float sc = sc_s[ri];
@@ -1491,150 +1503,143 @@ __global__ __launch_bounds__(kPairThreads) void dn_chunk_prep_pair_kernel(DnArgs
     }
   }
   __syncthreads();
-
-  // The key head's scan operands, stored with value head 2 kh: k^^T by the
-  // first head's waves, q^ by the second's.
   {
     float* ws0 = a.chunk_ws + ((size_t)c * VH + 2 * kh) * kDnChunkFloats;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
+    for (int p = 0; p < 4; ++p) {
       if (r == 0)
-        dn_chunk_store_k(ks_s, (uint16_t*)(ws0 + kDnWsKT), htid + 512 * p);
+        dn_chunk_store_k(ks_s, (uint16_t*)(ws0 + kDnWsKT), htid + 256 * p);
       else
-        dn_chunk_store_q(qs_s, (uint16_t*)(ws0 + kDnWsQ), htid + 512 * p);
+        dn_chunk_store_q(qs_s, (uint16_t*)(ws0 + kDnWsQ), htid + 256 * p);
     }
   }
-
-  // The 10 lower-triangular tiles of Q K^T and of K K^T, one product each
-  // over the 16 waves (the one-head kernel's tile arithmetic); each product
-  // is written out for both heads: P from Q K^T, -A from K K^T.
   auto tile = [&](const float* xs, int tix, floatx4& acc, int& tm, int& tn) __attribute__((always_inline)) {
     int rem = tix;
     tm = 0;
     while (rem > tm) rem -= ++tm;
     tn = rem;
-    const float* xa = xs + (16 * tm + j) * kCStride + 4 * grp;
-    const float* xb = ks_s + (16 * tn + j) * kCStride + 4 * grp;
-    floatx4 ac[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const f32x4 av = *(const f32x4*)(xa + 16 * m);
-      const f32x4 bv = *(const f32x4*)(xb + 16 * m);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ac[e] = mfma_f32_4(av[e], bv[e], ac[e]);
-    }
-    acc = (ac[0] + ac[1]) + (ac[2] + ac[3]);
+    acc = dn_gram_tile(xs, ks_s, tm, tn, j, grp);
   };
-  for (int u = (int)wave; u < 20; u += 16) {
-    const bool qk = u < 10;
+  // Q K^T (P for both heads), then, once every wave is past the q^ rows,
+  // K K^T (-A for both heads in their space).
+  for (int tix = (int)wave; tix < 10; tix += 8) {
     floatx4 acc;
     int tm, tn;
-    tile(qk ? qs_s : ks_s, qk ? u : u - 10, acc, tm, tn);
-    // acc[rr]: row t = 16 tm + 4 grp + rr, column i = 16 tn + j.
+    tile(qs_s, tix, acc, tm, tn);
+    const uint32_t i = 16 * tn + j;
+#pragma unroll
+    for (int hr = 0; hr < 2; ++hr) {
+      const double* gdh = (const double*)(gsets(hr) + 320);
+      float* P = a.chunk_ws + ((size_t)c * VH + 2 * kh + hr) * kDnChunkFloats + kDnWsP;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const uint32_t t = 16 * tm + 4 * grp + rr;
+        P[dn_ws_index(tm, tn, 4 * grp + rr, j, 4)] = i <= t ? expf((float)(gdh[t] - gdh[i])) * acc[rr] : 0.0f;
+      }
+    }
+  }
+  __syncthreads();
+  for (int tix = 9 - (int)wave; tix >= 0; tix -= 8) {
+    floatx4 acc;
+    int tm, tn;
+    tile(ks_s, tix, acc, tm, tn);
     const uint32_t i = 16 * tn + j;
 #pragma unroll
     for (int hr = 0; hr < 2; ++hr) {
       const float* gh = gsets(hr);
       const double* gdh = (const double*)(gh + 320);
-      if (qk) {
-        float* P = a.chunk_ws + ((size_t)c * VH + 2 * kh + hr) * kDnChunkFloats + kDnWsP;
+      float* A = qs_s + hr * kP8A;
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const uint32_t t = 16 * tm + 4 * grp + rr;
-          P[dn_ws_index(tm, tn, 4 * grp + rr, j, 4)] = i <= t ? expf((float)(gdh[t] - gdh[i])) * acc[rr] : 0.0f;
-        }
-      } else {
-        float* A = a_base + hr * kPairA;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const uint32_t t = 16 * tm + 4 * grp + rr;
-          A[t * kAStride + i] = i < t ? -(gh[64 + t] * expf((float)(gdh[t] - gdh[i])) * acc[rr]) : 0.0f;  // -A
-        }
+      for (int rr = 0; rr < 4; ++rr) {
+        const uint32_t t = 16 * tm + 4 * grp + rr;
+        A[t * kP8AStride + i] = i < t ? -(gh[64 + t] * expf((float)(gdh[t] - gdh[i])) * acc[rr]) : 0.0f;  // -A
       }
     }
   }
-  // P is zero above the diagonal blocks too, so its readers need no bounds.
-  for (uint32_t idx = htid; idx < 6 * 256; idx += 512) {
+  for (uint32_t idx = htid; idx < 6 * 256; idx += 256) {
     const uint32_t tl = idx / 256, e = idx % 256;
     const uint32_t tm = tl < 3 ? 0 : tl < 5 ? 1 : 2;  // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
     const uint32_t tn = tl < 3 ? tl + 1 : tl < 5 ? tl - 1 : 3;
     Pg[256 * (4 * tm + tn) + e] = 0.0f;
   }
   __syncthreads();
-
-  // Solve (I + A) X = R per head, as dn_chunk_prep_kernel: T_b by forward
-  // substitution (the head's waves 0..3, lanes 0..15), then the blocked MFMA
-  // solve with the head's wave hw owning W and U~ columns 16 hw .. + 15.
-  if (hw < 4 && lane < 16) {
+  if (lane < 16) {
     const uint32_t b = hw, jj = lane;
-    const float* ab = a_s + 16 * b * kAStride + 16 * b;
+    const float* ab = a_s + 16 * b * kP8AStride + 16 * b;
     float tc[16];
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
       float v = (uint32_t)t == jj ? 1.0f : 0.0f;
 #pragma unroll
-      for (int i = 0; i < t; ++i) v = fmaf(ab[t * kAStride + i], tc[i], v);
+      for (int i = 0; i < t; ++i) v = fmaf(ab[t * kP8AStride + i], tc[i], v);
       tc[t] = v;
       t_s[(16 * b + t) * 17 + jj] = v;
     }
   }
   __syncthreads();
-  const uint32_t cw = 16 * hw + j;
-  floatx4 X[4][2];
+  floatx4 X[2][4][2];  // [slice][block b][tile n]
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    floatx4 acc[2];
+  for (int sl = 0; sl < 2; ++sl) {
+    const uint32_t cw = 16 * (hw + 4 * sl) + j;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const uint32_t t = 16 * b + 4 * grp + rr;
-      acc[0][rr] = bg_s[t] * ks_s[t * kCStride + cw];
-      acc[1][rr] = t < nt ? beta_s[t] * vpre[b][rr] : 0.0f;
-    }
+    for (int b = 0; b < 4; ++b) {
+      floatx4 acc[2];
 #pragma unroll
-    for (int cb = 0; cb < b; ++cb) {
-      const f32x4 av = *(const f32x4*)(a_s + (16 * b + j) * kAStride + 16 * cb + 4 * grp);  // (-A)_bc
+      for (int rr = 0; rr < 4; ++rr) {
+        const uint32_t t = 16 * b + 4 * grp + rr;
+        acc[0][rr] = bg_s[t] * ks_s[t * kCStride + cw];
+        acc[1][rr] = t < nt ? beta_s[t] * vpre[sl][b][rr] : 0.0f;
+      }
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
+      for (int cb = 0; cb < b; ++cb) {
+        const f32x4 av = *(const f32x4*)(a_s + (16 * b + j) * kP8AStride + 16 * cb + 4 * grp);  // (-A)_bc
 #pragma unroll
-        for (int n = 0; n < 2; ++n) acc[n] = mfma_f32_4(av[rr], X[cb][n][rr], acc[n]);
-    }
-    const f32x4 tv = *(const f32x4*)(t_s + (16 * b + j) * 17 + 4 * grp);
+        for (int rr = 0; rr < 4; ++rr)
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      X[b][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+          for (int n = 0; n < 2; ++n) acc[n] = mfma_f32_4(av[rr], X[sl][cb][n][rr], acc[n]);
+      }
+      const f32x4 tv = *(const f32x4*)(t_s + (16 * b + j) * 17 + 4 * grp);
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) X[b][n] = mfma_f32_4(tv[rr], acc[n][rr], X[b][n]);
+      for (int n = 0; n < 2; ++n) {
+        X[sl][b][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) X[sl][b][n] = mfma_f32_4(tv[rr], acc[n][rr], X[sl][b][n]);
+      }
     }
   }
   __syncthreads();  // every wave is past k^, A and T: their LDS is free
   float* xt = prep_lds + wave * (4 * 16 * 20);
 #pragma unroll
-  for (int n = 0; n < 2; ++n) {
+  for (int sl = 0; sl < 2; ++sl) {
+    const uint32_t vwv = hw + 4 * sl;  // the one-head kernel's wave index of this slice
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int n = 0; n < 2; ++n) {
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) xt[b * 320 + (4 * grp + rr) * 20 + j] = X[b][n][rr];
-    __builtin_amdgcn_wave_barrier();
-    if (n == 0) {
-      uint16_t* w3 = (uint16_t*)Wg;
-      if (grp / 2 == hw % 2) {
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) xt[b * 320 + (4 * grp + rr) * 20 + j] = X[sl][b][n][rr];
+      __builtin_amdgcn_wave_barrier();
+      if (n == 0) {
+        uint16_t* w3 = (uint16_t*)Wg;
+        if (grp / 2 == vwv % 2) {
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const float* src = xt + b * 320 + j * 20 + 8 * (grp % 2);
+            u32x4 hi, lo;
+            split_bf16x8(*(const f32x4*)src, *(const f32x4*)(src + 4), hi, lo);
+            *(u32x4*)(w3 + dn_b3_block(b, vwv / 2, 4) + 8 * lane) = hi;
+            *(u32x4*)(w3 + dn_b3_block(b, vwv / 2, 4) + 512 + 8 * lane) = lo;
+          }
+        }
+      } else {
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const float* src = xt + b * 320 + j * 20 + 8 * (grp % 2);
-          u32x4 hi, lo;
-          split_bf16x8(*(const f32x4*)src, *(const f32x4*)(src + 4), hi, lo);
-          *(u32x4*)(w3 + dn_b3_block(b, hw / 2, 4) + 8 * lane) = hi;
-          *(u32x4*)(w3 + dn_b3_block(b, hw / 2, 4) + 512 + 8 * lane) = lo;
+          const f32x4 v = *(const f32x4*)(xt + b * 320 + (lane % 16) * 20 + 4 * (lane / 16));
+          *(f32x4*)(Ug + 256 * (4 * vwv + b) + 4 * lane) = v;
         }
       }
-    } else {
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const f32x4 v = *(const f32x4*)(xt + b * 320 + (lane % 16) * 20 + 4 * (lane / 16));
-        *(f32x4*)(Ug + 256 * (4 * hw + b) + 4 * lane) = v;
-      }
+      __builtin_amdgcn_wave_barrier();
     }
-    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -1890,7 +1895,7 @@ hipError_t launch_deltanet(const DnArgs& a, hipStream_t st) {
     if (!a.chunk_ws) return hipErrorInvalidValue;
     const uint32_t nchunks = (a.M + kDnChunk - 1) / kDnChunk;
     if (a.value_heads == 2 * a.key_heads && a.tune_dn_pair != 0)
-      hipLaunchKernelGGL(dn_chunk_prep_pair_kernel, dim3(nchunks * a.key_heads), dim3(kPairThreads), kPairLds, st, a);
+      hipLaunchKernelGGL(dn_chunk_prep_pair_kernel, dim3(nchunks * a.key_heads), dim3(kP8Threads), kP8Lds, st, a);
     else
       hipLaunchKernelGGL(dn_chunk_prep_kernel, dim3(nchunks * a.value_heads), dim3(kPrepThreads), kPrepLds, st, a);
     hipLaunchKernelGGL(dn_chunk_scan_kernel, dim3(a.value_heads * (kCD / 16)), dim3(kScanThreads), 0, st, a);
