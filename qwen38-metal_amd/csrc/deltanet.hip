@@ -487,19 +487,6 @@ __device__ __forceinline__ void gate_norm_finish(const DnArgs& a, uint32_t rl, f
     sz[i] = ok ? silu_f(zr[i]) : 0.0f;
   }
 }
-// One row by one wave: reads o_in[c], writes out[c].
-__device__ __forceinline__ void gate_norm_row(const DnArgs& a, const float* o_in, const float* z, float* out,
-                                              uint32_t lane, uint16_t* out_bf16 = nullptr) {
-  float v[4], nrm[4], sz[4];  // dv <= 256
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t c = 4 * lane + i;
-    v[i] = c < a.dv ? o_in[c] : 0.0f;
-  }
-  gate_norm_operands(a, z, lane, nrm, sz);
-  gate_norm_core(a, v, nrm, sz, out, lane, out_bf16);
-}
-
 // In place on `out`, kNormSlots x (64 / LPR) rows per wave, all of their
 // loads (16 bytes a lane when VEC, dv % 4 == 0) issued before the first row
 // is normalised; the per-row arithmetic is gate_norm_core's.
@@ -672,7 +659,7 @@ __global__ __launch_bounds__(kHeadThreads) void dn_step_head_kernel(DnArgs a) {
 // gated norm needs all dv outputs of the head: every group stores its o
 // values (written through to memory) and counts itself in; the last of the
 // head's groups to arrive reads the dv values back and applies
-// gate_norm_row.  Every output is formed by the same device functions as in
+// gate_norm_core.  Every output is formed by the same device functions as in
 // the per-head step and the prefill path, so a step still equals a one-token
 // prefill bit for bit.
 template <int EPT>

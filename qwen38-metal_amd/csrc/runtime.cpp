@@ -42,15 +42,17 @@ qm::DeviceGuard::DeviceGuard(int device) {
     prev_ = device;
     return;
   }
-  hipGetDevice(&prev_);
-  if (prev_ != device) hipSetDevice(device);
+  if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+  ok_ = prev_ == device || hipSetDevice(device) == hipSuccess;
+  if (!ok_) (void)hipGetLastError();  // the caller reports QM_ERR_NO_DEVICE
 }
 qm::DeviceGuard::~DeviceGuard() {
-  if (dev_ >= 0 && prev_ != dev_) hipSetDevice(prev_);
+  if (ok_ && prev_ >= 0 && prev_ != dev_) (void)hipSetDevice(prev_);
 }
 
 qm_status qm::no_device() {
-  return fail(QM_ERR_NO_DEVICE, "this runtime has no device (created with device %d)", QM_DEVICE_NONE);
+  return fail(QM_ERR_NO_DEVICE, "this runtime has no usable device (created with QM_DEVICE_NONE = %d, or its "
+                                "device could not be made current)", QM_DEVICE_NONE);
 }
 
 // Growing a buffer allocates and synchronises, which a stream under graph
@@ -69,7 +71,7 @@ qm_status qm::ensure_scratch(qm_runtime* rt, size_t bytes) {
     // Work already enqueued may still use the old buffer.
     hipError_t e = hipStreamSynchronize(rt->stream);
     if (e != hipSuccess) return hip_check(e, "scratch resize sync");
-    hipFree(rt->scratch);
+    (void)hipFree(rt->scratch);
     rt->scratch = nullptr;
     rt->scratch_bytes = 0;
   }
@@ -88,7 +90,7 @@ qm_status qm::ensure_partials(qm_runtime* rt, size_t bytes) {
   if (rt->partials) {
     hipError_t e = hipStreamSynchronize(rt->stream);
     if (e != hipSuccess) return hip_check(e, "partials resize sync");
-    hipFree(rt->partials);
+    (void)hipFree(rt->partials);
     rt->partials = nullptr;
     rt->partial_bytes = 0;
   }
@@ -107,7 +109,7 @@ qm_status qm::ensure_xh(qm_runtime* rt, size_t bytes) {
   if (rt->xh) {
     hipError_t e = hipStreamSynchronize(rt->stream);
     if (e != hipSuccess) return hip_check(e, "xh resize sync");
-    hipFree(rt->xh);
+    (void)hipFree(rt->xh);
     rt->xh = nullptr;
     rt->xh_bytes = 0;
   }
@@ -125,7 +127,7 @@ qm_status qm::ensure_counters(qm_runtime* rt, size_t count) {
   if (rt->counters) {
     hipError_t e = hipStreamSynchronize(rt->stream);
     if (e != hipSuccess) return hip_check(e, "counters resize sync");
-    hipFree(rt->counters);
+    (void)hipFree(rt->counters);
     rt->counters = nullptr;
     rt->counter_count = 0;
   }
@@ -173,7 +175,7 @@ qm_status qm::ensure_keys(qm_runtime* rt) {
   if (e == hipSuccess) e = hipMemsetAsync(rt->keys, 0, bytes, rt->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
   if (e != hipSuccess) {
-    if (rt->keys) hipFree(rt->keys);
+    if (rt->keys) (void)hipFree(rt->keys);
     rt->keys = nullptr;
     return hip_check(e, "argmax keys");
   }
@@ -181,11 +183,11 @@ qm_status qm::ensure_keys(qm_runtime* rt) {
 }
 
 void qm::release_buffers(qm_runtime* rt) {
-  if (rt->scratch) hipFree(rt->scratch);
-  if (rt->counters) hipFree(rt->counters);
-  if (rt->partials) hipFree(rt->partials);
-  if (rt->xh) hipFree(rt->xh);
-  if (rt->keys) hipFree(rt->keys);
+  if (rt->scratch) (void)hipFree(rt->scratch);
+  if (rt->counters) (void)hipFree(rt->counters);
+  if (rt->partials) (void)hipFree(rt->partials);
+  if (rt->xh) (void)hipFree(rt->xh);
+  if (rt->keys) (void)hipFree(rt->keys);
   rt->keys = nullptr;
   rt->scratch = rt->counters = nullptr;
   rt->partials = rt->xh = nullptr;
@@ -298,9 +300,9 @@ void qm_runtime_destroy(qm_runtime* rt) {
     return;
   }
   DeviceGuard g(rt->device);
-  hipStreamSynchronize(rt->stream);
+  (void)hipStreamSynchronize(rt->stream);
   qm::release_buffers(rt);
-  if (rt->order_event) hipEventDestroy(rt->order_event);
+  if (rt->order_event) (void)hipEventDestroy(rt->order_event);
   delete rt;
 }
 

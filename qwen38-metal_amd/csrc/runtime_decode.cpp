@@ -193,7 +193,7 @@ qm_status ensure_arena(qm_decode_state* st, const qm_decode_state::Sizes& need) 
   if (st->arena) {
     hipError_t e = hipStreamSynchronize(st->rt->stream);
     if (e != hipSuccess) return hip_check(e, "decode state resize sync");
-    hipFree(st->arena);
+    (void)hipFree(st->arena);
     st->arena = nullptr;
   }
   hipError_t e = hipMalloc(&st->arena, bytes);
@@ -306,7 +306,7 @@ namespace {
 
 void destroy_variant(qm_decode_graph::Variant& v) {
   for (hipGraphExec_t e : v.segs)
-    if (e) hipGraphExecDestroy(e);
+    if (e) (void)hipGraphExecDestroy(e);
   v.segs.clear();
 }
 
@@ -316,7 +316,7 @@ qm_status end_segment(qm_decode_graph* g, qm_decode_graph::Variant& v) {
   if (e != hipSuccess) return hip_check(e, "decode graph end capture");
   hipGraphExec_t exec = nullptr;
   e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-  hipGraphDestroy(graph);
+  (void)hipGraphDestroy(graph);
   if (e != hipSuccess) return hip_check(e, "decode graph instantiate");
   v.segs.push_back(exec);
   return QM_OK;
@@ -343,8 +343,8 @@ qm_status capture_variant(qm_decode_graph* g, float eps, qm_decode_graph::Varian
   }
   if (s != QM_OK) {
     hipGraph_t graph = nullptr;
-    hipStreamEndCapture(g->cap_stream, &graph);
-    if (graph) hipGraphDestroy(graph);
+    (void)hipStreamEndCapture(g->cap_stream, &graph);
+    if (graph) (void)hipGraphDestroy(graph);
     return s;
   }
   if ((s = end_segment(g, v)) != QM_OK) return s;
@@ -392,8 +392,8 @@ qm_status qm_decode_state_create(qm_runtime* rt, uint32_t hidden_elems, qm_decod
   if (e == hipSuccess) e = hipMemsetAsync(st->hid, 0, (size_t)hidden_elems * 4, rt->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
   if (e != hipSuccess) {
-    hipFree(st->hid);
-    hipFree(st->pos);
+    (void)hipFree(st->hid);
+    (void)hipFree(st->pos);
     delete st;
     return hip_check(e, "decode state allocation");
   }
@@ -404,10 +404,10 @@ qm_status qm_decode_state_create(qm_runtime* rt, uint32_t hidden_elems, qm_decod
 void qm_decode_state_destroy(qm_decode_state* st) {
   if (!st) return;
   DeviceGuard g(st->rt->device);
-  hipStreamSynchronize(st->rt->stream);
-  hipFree(st->hid);
-  hipFree(st->pos);
-  if (st->arena) hipFree(st->arena);
+  (void)hipStreamSynchronize(st->rt->stream);
+  (void)hipFree(st->hid);
+  (void)hipFree(st->pos);
+  if (st->arena) (void)hipFree(st->arena);
   delete st;
 }
 
@@ -570,12 +570,12 @@ qm_status qm_decode_graph_run(qm_decode_graph* g, const uint32_t position[3]) {
 void qm_decode_graph_destroy(qm_decode_graph* g) {
   if (!g) return;
   DeviceGuard dg(g->rt->device);
-  hipStreamSynchronize(g->rt->stream);
+  (void)hipStreamSynchronize(g->rt->stream);
   for (int v = 0; v < 2; ++v) destroy_variant(g->var[v]);
   if (g->cap_stream) {
-    hipStreamSynchronize(g->cap_stream);
+    (void)hipStreamSynchronize(g->cap_stream);
     release_buffers(&g->cap);
-    hipStreamDestroy(g->cap_stream);
+    (void)hipStreamDestroy(g->cap_stream);
   }
   delete g;
 }

@@ -62,18 +62,18 @@ uint32_t channels_of(const qm_dn_config& c) {
 
 void free_weights(qm_dn_weights* w) {
   DeviceGuard g(w->rt->device);
-  hipFree(w->conv_w);
-  hipFree(w->a_log);
-  hipFree(w->dt_bias);
-  hipFree(w->norm);
+  (void)hipFree(w->conv_w);
+  (void)hipFree(w->a_log);
+  (void)hipFree(w->dt_bias);
+  (void)hipFree(w->norm);
   delete w;
 }
 
 void free_state(qm_dn_state* s) {
   DeviceGuard g(s->rt->device);
-  hipFree(s->hist[0]);
-  hipFree(s->hist[1]);
-  hipFree(s->rec);
+  (void)hipFree(s->hist[0]);
+  (void)hipFree(s->hist[1]);
+  (void)hipFree(s->rec);
   delete s;
 }
 
@@ -253,7 +253,7 @@ qm_status qm_dn_weights_create(qm_runtime* rt, const qm_dn_config* cfg, const fl
 
 void qm_dn_weights_destroy(qm_dn_weights* w) {
   if (!w) return;
-  hipStreamSynchronize(w->rt->stream);
+  (void)hipStreamSynchronize(w->rt->stream);
   free_weights(w);
 }
 
@@ -265,7 +265,7 @@ qm_status qm_dn_state_create(qm_runtime* rt, const qm_dn_weights* w, qm_dn_state
 
 void qm_dn_state_destroy(qm_dn_state* s) {
   if (!s) return;
-  hipStreamSynchronize(s->rt->stream);
+  (void)hipStreamSynchronize(s->rt->stream);
   free_state(s);
 }
 
@@ -353,8 +353,8 @@ qm_status qm_dn_snapshots_create(qm_runtime* rt, const qm_dn_weights* w, uint32_
   if (e == hipSuccess) e = hipMemsetAsync(s->rec, 0, (size_t)rows * s->rec_elems * sizeof(float), rt->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
   if (e != hipSuccess) {
-    hipFree(s->hist);
-    hipFree(s->rec);
+    (void)hipFree(s->hist);
+    (void)hipFree(s->rec);
     delete s;
     return hip_check(e, "DeltaNet snapshot allocation");
   }
@@ -365,9 +365,9 @@ qm_status qm_dn_snapshots_create(qm_runtime* rt, const qm_dn_weights* w, uint32_
 void qm_dn_snapshots_destroy(qm_dn_snapshots* s) {
   if (!s) return;
   DeviceGuard g(s->rt->device);
-  hipStreamSynchronize(s->rt->stream);
-  hipFree(s->hist);
-  hipFree(s->rec);
+  (void)hipStreamSynchronize(s->rt->stream);
+  (void)hipFree(s->hist);
+  (void)hipFree(s->rec);
   delete s;
 }
 

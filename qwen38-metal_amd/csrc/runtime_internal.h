@@ -103,11 +103,13 @@ class DeviceGuard {
  public:
   explicit DeviceGuard(int device);
   ~DeviceGuard();
-  bool ok() const { return dev_ >= 0; }
+  // The device exists and is current (false for QM_DEVICE_NONE).
+  bool ok() const { return ok_; }
 
  private:
   int prev_ = 0;
   int dev_ = 0;
+  bool ok_ = false;
 };
 
 }  // namespace qm

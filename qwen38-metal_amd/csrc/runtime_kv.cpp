@@ -49,11 +49,11 @@ struct KvBuffers {
 };
 
 void free_buffers(const KvBuffers& b) {
-  hipFree(b.pt);
-  hipFree(b.k);
-  hipFree(b.v);
-  hipFree(b.ks);
-  hipFree(b.vs);
+  (void)hipFree(b.pt);
+  (void)hipFree(b.k);
+  (void)hipFree(b.v);
+  (void)hipFree(b.ks);
+  (void)hipFree(b.vs);
 }
 
 // Zeroed device buffers for `pages` physical pages (the reference's
@@ -269,7 +269,7 @@ qm_status plan_decode_chunk(qm_runtime* rt, qm_kv* const* seqs, uint32_t nb, Dec
   const int target_env = rt->tune.attn_target_wgs;
   uint32_t waves = 8;
   uint64_t pps = pps_for(target_env > 0 ? (uint32_t)target_env : rt->cu_count);
-  if (waves_env == 4 || (waves_env != 8 && units_for(pps) > rt->cu_count)) {
+  if (waves_env == 4 || (waves_env != 8 && units_for(pps) > (uint64_t)rt->cu_count)) {
     waves = 4;
     pps = pps_for(target_env > 0 ? (uint32_t)target_env : 2 * rt->cu_count);
   }
@@ -442,7 +442,7 @@ qm_status qm_kv_create(qm_runtime* rt, uint32_t kv_heads, uint32_t head_dim, uin
 
 void qm_kv_destroy(qm_kv* kv) {
   if (!kv) return;
-  hipStreamSynchronize(kv->rt->stream);
+  (void)hipStreamSynchronize(kv->rt->stream);
   free_kv(kv);
 }
 
