@@ -50,6 +50,12 @@ struct Tuning {
   int q4_stream_wgs = 0;    // QM38_Q4_STREAM_WGS: workgroups per K part of the single-row kernel
   int q4_stream_c = 0;      // QM38_Q4_STREAM_C: chunks per wave of the single-row kernel (1..4)
   int q4_stream_w = 0;      // QM38_Q4_STREAM_W: waves per workgroup with QM38_Q4_STREAM_C
+  int q4_mma_lo = 3;        // QM38_Q4_MMA_LO: fewest activation rows on the MFMA streaming kernel (0: off)
+  int q4_mma_hi = 4;        // QM38_Q4_MMA_HI: most activation rows on it (at most 8)
+  int q4_mma_w = 0;         // QM38_Q4_MMA_W: most waves per K part of the MFMA streaming kernel
+  int q4_mma_c = 0;         // QM38_Q4_MMA_C: 4 or 8 spans per wave with up to four activation rows
+  int q4_mma_sb = 0;        // QM38_Q4_MMA_SB: 2 forces 32-row blocks for plain projections
+  int q4_mma_wgs = 0;       // QM38_Q4_MMA_WGS: workgroups per K part of the MFMA streaming kernel
   int gemm_splits = 0;      // QM38_GEMM_SPLITS: K splits of the prefill GEMM
   int gemm_q = 0;           // QM38_GEMM_Q: stream-K steps per worker
   int gemm_plan_log = 0;    // QM38_GEMM_PLAN_LOG
@@ -87,6 +93,14 @@ hipError_t launch_q4_decode(const Q4Job* jobs, int n_jobs, bool swiglu, const ui
 bool q4_stream_supported(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn);
 hipError_t launch_q4_stream(const Q4Job* jobs, int n_jobs, const uint16_t* x, uint32_t K, uint32_t M,
                             const Workspace& ws, hipStream_t stream);
+// 1..8 activation rows on the matrix cores with the weights streamed once
+// (q4_mma.hip): QM38_Q4_MMA_LO <= M <= QM38_Q4_MMA_HI (3..4 by default).  Jobs may mix plain projections and
+// gate/up pairs; no argmax.
+bool q4_mma_supported(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn);
+hipError_t launch_q4_mma(const Q4Job* jobs, int n_jobs, const uint16_t* x, uint32_t K, uint32_t M,
+                         const Workspace& ws, hipStream_t stream);
+void q4_mma_workspace(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn,
+                      size_t* partial_bytes, size_t* counters);
 // Workspace of a streaming launch: fp32 partial rows and counters when K is
 // split over several workgroups (zero otherwise).
 void q4_stream_workspace(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn,

@@ -220,6 +220,12 @@ qm::Tuning qm::read_tuning(int cu_count) {
   t.q4_stream_mw = get("QM38_Q4_STREAM_MW", 0);
   t.q4_stream_c = get("QM38_Q4_STREAM_C", 0);
   t.q4_stream_w = get("QM38_Q4_STREAM_W", 0);
+  t.q4_mma_lo = get("QM38_Q4_MMA_LO", 3);
+  t.q4_mma_hi = get("QM38_Q4_MMA_HI", 4);
+  t.q4_mma_w = get("QM38_Q4_MMA_W", 0);
+  t.q4_mma_c = get("QM38_Q4_MMA_C", 0);
+  t.q4_mma_sb = get("QM38_Q4_MMA_SB", 0);
+  t.q4_mma_wgs = get("QM38_Q4_MMA_WGS", 0);
   t.gemm_splits = get("QM38_GEMM_SPLITS", 0);
   t.gemm_q = get("QM38_GEMM_Q", 0);
   t.gemm_plan_log = get("QM38_GEMM_PLAN_LOG", 0);

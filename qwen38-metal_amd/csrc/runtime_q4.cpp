@@ -126,10 +126,22 @@ qm_status gemm_launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, con
   return hip_check(launch_q4_gemm(jobs, n, swiglu, x, K, M, workspace(rt), rt->stream), what);
 }
 
+// 1..8 activation rows on the MFMA streaming kernel (its K-part workspace first).
+qm_status mma_launch(qm_runtime* rt, const Q4Job* jobs, int n, const uint16_t* x, uint32_t K, uint32_t M,
+                     const char* what) {
+  size_t pbytes = 0, counters = 0;
+  q4_mma_workspace(jobs, n, K, M, rt->tune, &pbytes, &counters);
+  qm_status st = ensure_partials(rt, pbytes);
+  if (st == QM_OK) st = ensure_counters(rt, counters);
+  if (st != QM_OK) return st;
+  return hip_check(launch_q4_mma(jobs, n, x, K, M, workspace(rt), rt->stream), what);
+}
+
 qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const uint16_t* x, uint32_t K,
                  uint32_t M, const char* what) {
-  if (M <= 2) {
-    // One or two activation rows: the streaming kernel, with a gate/up pair as one job.
+  if (M <= 8) {
+    // One or two activation rows: the streaming kernel; up to 8: the MFMA
+    // streaming kernel; both take a gate/up pair as one job.
     Q4Job sj[kMaxQ4Jobs];
     int ns = 0;
     if (swiglu) {
@@ -143,6 +155,7 @@ qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const ui
       for (int i = 0; i < n; ++i) sj[ns++] = jobs[i];
     }
     if (q4_stream_supported(sj, ns, K, M, rt->tune)) return stream_launch(rt, sj, ns, x, K, M, what);
+    if (q4_mma_supported(sj, ns, K, M, rt->tune)) return mma_launch(rt, sj, ns, x, K, M, what);
   }
   if (M > kDecodeMaxRows) return gemm_launch(rt, jobs, n, swiglu, x, K, M, what);
   return hip_check(launch_q4_decode(jobs, n, swiglu, x, K, M, workspace(rt), rt->stream), what);
@@ -251,6 +264,7 @@ qm_status qm_q4_project_set(qm_runtime* rt, const qm_q4_job* jobs, const qm_q4_j
   }
   if (q4_stream_supported(q, n_jobs, in_elems, M, rt->tune))
     return stream_launch(rt, q, n_jobs, x, in_elems, M, "Q4 set launch");
+  if (q4_mma_supported(q, n_jobs, in_elems, M, rt->tune)) return mma_launch(rt, q, n_jobs, x, in_elems, M, "Q4 set launch");
   // Prefill rows: one GEMM launch over the whole set (plain and pair tiles).
   if (M > kDecodeMaxRows) return gemm_launch(rt, q, n_jobs, false, x, in_elems, M, "Q4 set GEMM launch");
   // Otherwise: the plain jobs in one launch, each pair in its own.

@@ -167,10 +167,10 @@ def test_rows_per_workgroup(torch_dev, nt, rpw, M):
     """Workgroups owning fewer rows than their 16-row tiles (the planner's
     balancing choice) mask the rest; forced here for several row counts that
     do not divide the projection heights, with several jobs in one launch and
-    a SwiGLU pair.  (The MFMA decode kernel: the streaming kernel, which
-    takes up to four rows by default, is switched off.)"""
+    a SwiGLU pair.  (The MFMA decode kernel: the streaming kernels, which
+    take up to eight rows by default, are switched off.)"""
     import qm38
-    with tuned(QM38_Q4_NT=nt, QM38_Q4_RPW=rpw, QM38_Q4_STREAM=0) as rt:
+    with tuned(QM38_Q4_NT=nt, QM38_Q4_RPW=rpw, QM38_Q4_STREAM=0, QM38_Q4_MMA_LO=0) as rt:
         rng = np.random.default_rng(300 + nt * 50 + rpw + M)
         K = 1024
         mats = [synth.q4_matrix(rng, n, K) for n in (200, 37, 512)]
@@ -368,7 +368,7 @@ def test_few_rows_streaming(rt, torch_dev, M, K):
     rt.q4_swiglu(jg, ju, to_dev(xb, torch_dev), K, M, h)
     h_ref = oracle.swiglu(oracle.q4_project(xb, *gate), oracle.q4_project(xb, *up))
     assert_bf16_close(bf16_dev_to_f32(h), h_ref, what=f"M={M} K={K} swiglu")
-    with tuned(QM38_Q4_STREAM=0) as mrt:
+    with tuned(QM38_Q4_STREAM=0, QM38_Q4_MMA_LO=0) as mrt:
         for mat, g1 in zip(mats, _project(mrt, torch_dev, mats, xb, M)):
             assert_bf16_close(g1, oracle.q4_project(xb, *mat), what=f"decode kernel M={M} K={K}")
 
@@ -405,7 +405,7 @@ def test_single_row_k_parts(rt, torch_dev, K):
 def test_project_set_mixes_plain_and_pairs(rt, torch_dev):
     """qm_q4_project_set: plain projections and SwiGLU pairs from one
     activation, in one launch for one or two rows and prefill rows (the GEMM
-    takes both tile kinds), as separate launches for 3..16 rows; each output
+    takes both tile kinds), one launch for 1..8 rows (the streaming kernels), as separate launches for 9..16 rows; each output
     matches the oracle, and a pair's equals its own call's where both run the
     same kernel plan."""
     import qm38
@@ -428,3 +428,41 @@ def test_project_set_mixes_plain_and_pairs(rt, torch_dev):
         h = empty_bf16((M, 96), torch_dev)
         rt.q4_swiglu(jg, ju, xd, K, M, h)
         assert np.array_equal(bf16_dev_to_f32(h), bf16_dev_to_f32(outs[1]))
+
+
+@pytest.mark.parametrize("C", [4, 8])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("K", [192, 1024, 5120, 6208, 17408])
+def test_mma_streaming_rows(torch_dev, M, K, C):
+    """The MFMA streaming kernel (q4_mma.hip) forced for 1..8 activation rows
+    (QM38_Q4_MMA_LO=1, QM38_Q4_MMA_HI=8, the single-row kernel off):
+    128-element spans in pairs, A rows (span, group, activation row), two A
+    halves beyond four rows; K = 192 and 6208 end inside a span, 17408 runs in
+    K parts whose fp32 sums the last part adds.
+    Plain jobs of several heights (not multiples of 16), a SwiGLU pair and a
+    mixed set (one launch, 32-row blocks) match the oracle row by row, and
+    repeated calls are bit-identical."""
+    import qm38
+    rng = np.random.default_rng(K * 100 + M)
+    mats = [synth.q4_matrix(rng, n, K) for n in (300, 37)]
+    xb = synth.bf16_normal(rng, (M, K))
+    gate, up = synth.q4_matrix(rng, 90, K), synth.q4_matrix(rng, 90, K)
+    h_ref = oracle.swiglu(oracle.q4_project(xb, *gate), oracle.q4_project(xb, *up))
+    with tuned(QM38_Q4_MMA_LO=1, QM38_Q4_MMA_HI=8, QM38_Q4_STREAM=0, QM38_Q4_MMA_C=C) as mrt:
+        got1 = _project(mrt, torch_dev, mats, xb, M)
+        got2 = _project(mrt, torch_dev, mats, xb, M)
+        for mat, g1, g2 in zip(mats, got1, got2):
+            assert_bf16_close(g1, oracle.q4_project(xb, *mat), what=f"M={M} K={K} rows {mat[0].shape[0]}")
+            assert np.array_equal(g1, g2)
+        dg, du = _upload(torch_dev, *gate), _upload(torch_dev, *up)
+        jg, ju = qm38.Runtime.job(*dg, 90), qm38.Runtime.job(*du, 90)
+        xd = to_dev(xb, torch_dev)
+        h = empty_bf16((M, 90), torch_dev)
+        mrt.q4_swiglu(jg, ju, xd, K, M, h)
+        assert_bf16_close(bf16_dev_to_f32(h), h_ref, what=f"M={M} K={K} swiglu")
+        dm = _upload(torch_dev, *mats[0])
+        jm = qm38.Runtime.job(*dm, 300)
+        outs = [empty_bf16((M, 300), torch_dev), empty_bf16((M, 90), torch_dev)]
+        mrt.q4_project_set([jm, jg], [None, ju], xd, K, M, outs)
+        assert np.array_equal(bf16_dev_to_f32(outs[0]), got1[0])
+        assert np.array_equal(bf16_dev_to_f32(outs[1]), bf16_dev_to_f32(h))
