@@ -52,6 +52,7 @@ struct Tuning {
   int q4_stream_w = 0;      // QM38_Q4_STREAM_W: waves per workgroup with QM38_Q4_STREAM_C
   int q4_mma_lo = 3;        // QM38_Q4_MMA_LO: fewest activation rows on the MFMA streaming kernel (0: off)
   int q4_mma_hi = 4;        // QM38_Q4_MMA_HI: most activation rows on it (at most 8)
+  int q4_mma_k = 8192;      // QM38_Q4_MMA_K: 2..8 rows with K above this also take it (0: never)
   int q4_mma_w = 0;         // QM38_Q4_MMA_W: most waves per K part of the MFMA streaming kernel
   int q4_mma_c = 0;         // QM38_Q4_MMA_C: 4 or 8 spans per wave with up to four activation rows
   int q4_mma_sb = 0;        // QM38_Q4_MMA_SB: 2 forces 32-row blocks for plain projections
@@ -94,7 +95,8 @@ bool q4_stream_supported(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, 
 hipError_t launch_q4_stream(const Q4Job* jobs, int n_jobs, const uint16_t* x, uint32_t K, uint32_t M,
                             const Workspace& ws, hipStream_t stream);
 // 1..8 activation rows on the matrix cores with the weights streamed once
-// (q4_mma.hip): QM38_Q4_MMA_LO <= M <= QM38_Q4_MMA_HI (3..4 by default).  Jobs may mix plain projections and
+// (q4_mma.hip): QM38_Q4_MMA_LO <= M <= QM38_Q4_MMA_HI (3..4 by default), and
+// 2..8 rows when K > QM38_Q4_MMA_K.  Jobs may mix plain projections and
 // gate/up pairs; no argmax.
 bool q4_mma_supported(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn);
 hipError_t launch_q4_mma(const Q4Job* jobs, int n_jobs, const uint16_t* x, uint32_t K, uint32_t M,

@@ -587,10 +587,15 @@ MmaPlan cached_mma_plan(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, c
 }  // namespace
 
 bool q4_mma_supported(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, const Tuning& tn) {
+  // 3..4 rows (QM38_Q4_MMA_LO / _HI); 2..8 rows when K is long (above
+  // QM38_Q4_MMA_K): there the other kernels split K over workgroups (two
+  // rows) or cap the waves per tile (five and more), and this one measured
+  // faster on the 17408-wide down projection (M = 2: 15.3 against 19.6 us,
+  // M = 8: 18.9 against 25.3 us).
   const uint32_t hi = tn.q4_mma_hi > 0 ? std::min<uint32_t>(tn.q4_mma_hi, kMaxRows) : kMaxRows;
-  if (tn.q4_mma_lo <= 0 || M < (uint32_t)tn.q4_mma_lo || M > hi || n_jobs < 1 ||
-      n_jobs > kMaxQ4Jobs || K % 64 != 0)
-    return false;
+  const bool in_range = tn.q4_mma_lo > 0 && M >= (uint32_t)tn.q4_mma_lo && M <= hi;
+  const bool long_k = tn.q4_mma_k > 0 && K > (uint32_t)tn.q4_mma_k && M >= 2 && M <= (uint32_t)kMaxRows;
+  if (!(in_range || long_k) || n_jobs < 1 || n_jobs > kMaxQ4Jobs || K % 64 != 0) return false;
   for (int i = 0; i < n_jobs; ++i)
     if (jobs[i].mode > kQ4OutAddF32 && jobs[i].mode != kQ4OutSwiglu) return false;
   return cached_mma_plan(jobs, n_jobs, K, M, tn).fn != nullptr;

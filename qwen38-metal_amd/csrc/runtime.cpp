@@ -222,6 +222,7 @@ qm::Tuning qm::read_tuning(int cu_count) {
   t.q4_stream_w = get("QM38_Q4_STREAM_W", 0);
   t.q4_mma_lo = get("QM38_Q4_MMA_LO", 3);
   t.q4_mma_hi = get("QM38_Q4_MMA_HI", 4);
+  t.q4_mma_k = get("QM38_Q4_MMA_K", 8192);
   t.q4_mma_w = get("QM38_Q4_MMA_W", 0);
   t.q4_mma_c = get("QM38_Q4_MMA_C", 0);
   t.q4_mma_sb = get("QM38_Q4_MMA_SB", 0);

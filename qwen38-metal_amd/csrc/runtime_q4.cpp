@@ -154,6 +154,7 @@ qm_status launch(qm_runtime* rt, const Q4Job* jobs, int n, bool swiglu, const ui
     } else {
       for (int i = 0; i < n; ++i) sj[ns++] = jobs[i];
     }
+    if (M >= 2 && q4_mma_supported(sj, ns, K, M, rt->tune)) return mma_launch(rt, sj, ns, x, K, M, what);
     if (q4_stream_supported(sj, ns, K, M, rt->tune)) return stream_launch(rt, sj, ns, x, K, M, what);
     if (q4_mma_supported(sj, ns, K, M, rt->tune)) return mma_launch(rt, sj, ns, x, K, M, what);
   }
@@ -262,6 +263,8 @@ qm_status qm_q4_project_set(qm_runtime* rt, const qm_q4_job* jobs, const qm_q4_j
     if (ups && ups[i] && (st = check_job_ranges(rt, *ups[i], in_elems, "up")) != QM_OK) return st;
     if ((st = check_range(rt, outputs[i], (uint64_t)M * jobs[i].out_rows * 2, "output")) != QM_OK) return st;
   }
+  if (M >= 2 && q4_mma_supported(q, n_jobs, in_elems, M, rt->tune))
+    return mma_launch(rt, q, n_jobs, x, in_elems, M, "Q4 set launch");
   if (q4_stream_supported(q, n_jobs, in_elems, M, rt->tune))
     return stream_launch(rt, q, n_jobs, x, in_elems, M, "Q4 set launch");
   if (q4_mma_supported(q, n_jobs, in_elems, M, rt->tune)) return mma_launch(rt, q, n_jobs, x, in_elems, M, "Q4 set launch");

@@ -170,7 +170,7 @@ def test_rows_per_workgroup(torch_dev, nt, rpw, M):
     a SwiGLU pair.  (The MFMA decode kernel: the streaming kernels, which
     take up to eight rows by default, are switched off.)"""
     import qm38
-    with tuned(QM38_Q4_NT=nt, QM38_Q4_RPW=rpw, QM38_Q4_STREAM=0, QM38_Q4_MMA_LO=0) as rt:
+    with tuned(QM38_Q4_NT=nt, QM38_Q4_RPW=rpw, QM38_Q4_STREAM=0, QM38_Q4_MMA_LO=0, QM38_Q4_MMA_K=0) as rt:
         rng = np.random.default_rng(300 + nt * 50 + rpw + M)
         K = 1024
         mats = [synth.q4_matrix(rng, n, K) for n in (200, 37, 512)]
@@ -345,13 +345,19 @@ def test_mapped_job_from_one_buffer(rt, torch_dev):
 
 @pytest.mark.parametrize("M", [2])
 @pytest.mark.parametrize("K", [192, 1024, 5120, 8256, 17408, 20544])
-def test_few_rows_streaming(rt, torch_dev, M, K):
+def test_few_rows_streaming(torch_dev, M, K):
     """Two activation rows on the streaming kernel (one chunk per wave, K in
     balanced parts of at most 8 waves whose fp32 sums the last part adds;
-    K = 192 and 8256 end inside a chunk): plain jobs of several heights
-    and a SwiGLU pair in one launch each match the oracle row by row, repeated
-    calls are bit-identical, and the result equals the MFMA decode kernel's
-    within the same bar."""
+    K = 192 and 8256 end inside a chunk; long K kept off the MFMA streaming
+    kernel with QM38_Q4_MMA_K=0): plain jobs of several heights and a SwiGLU
+    pair in one launch each match the oracle row by row, repeated calls are
+    bit-identical, and the result equals the MFMA decode kernel's within the
+    same bar."""
+    with tuned(QM38_Q4_MMA_K=0) as rt:
+        _few_rows_streaming(rt, torch_dev, M, K)
+
+
+def _few_rows_streaming(rt, torch_dev, M, K):
     import qm38
     rng = np.random.default_rng(K * 10 + M)
     mats = [synth.q4_matrix(rng, n, K) for n in (300, 37)]
@@ -368,7 +374,7 @@ def test_few_rows_streaming(rt, torch_dev, M, K):
     rt.q4_swiglu(jg, ju, to_dev(xb, torch_dev), K, M, h)
     h_ref = oracle.swiglu(oracle.q4_project(xb, *gate), oracle.q4_project(xb, *up))
     assert_bf16_close(bf16_dev_to_f32(h), h_ref, what=f"M={M} K={K} swiglu")
-    with tuned(QM38_Q4_STREAM=0, QM38_Q4_MMA_LO=0) as mrt:
+    with tuned(QM38_Q4_STREAM=0, QM38_Q4_MMA_LO=0, QM38_Q4_MMA_K=0) as mrt:
         for mat, g1 in zip(mats, _project(mrt, torch_dev, mats, xb, M)):
             assert_bf16_close(g1, oracle.q4_project(xb, *mat), what=f"decode kernel M={M} K={K}")
 
