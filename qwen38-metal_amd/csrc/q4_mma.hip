@@ -61,8 +61,11 @@ constexpr int kMaxWaves = 12;  // 768 threads: 168 VGPRs per lane (3 waves per S
 constexpr int kMaxRows = 8;
 constexpr int kNonTemporal = 2;
 constexpr uint32_t kOOB = 0xFFFFFFF0u;
-constexpr int kTabLoads = 2;  // table entries per wave: 64 * kTabLoads
-constexpr uint32_t kTabEntries = 64 * kTabLoads;
+constexpr uint32_t kMaxLds = 160 * 1024;  // LDS of one workgroup on gfx950
+// Table entries per wave: 64 per load a lane issues (3 with 4 spans per wave,
+// 2 with 8, whose entries take two 16-byte loads each).
+__host__ __device__ constexpr int tab_loads(int c) { return c == 4 ? 3 : 2; }
+__host__ __device__ constexpr uint32_t tab_entries(int c) { return 64u * tab_loads(c); }
 
 struct MmaArgs {
   const uint16_t* x;
@@ -155,6 +158,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void q4_mma_kernel(MmaArgs args) {
   const uint32_t c0 = part * args.part_spans + (uint32_t)wave * C;  // first span of this wave
   const uint32_t n_e = SB * nblk * 16;
   constexpr int kTW = C / 4;  // 16-byte table loads per entry (8 groups each)
+  constexpr int kTabLoads = tab_loads(C);
   u32x4 tsv[kTabLoads][kTW], tbv[kTabLoads][kTW];
 #pragma unroll
   for (int i = 0; i < kTabLoads; ++i) {
@@ -511,8 +515,16 @@ MmaPlan make_mma_plan(const Q4Job* jobs, int n_jobs, uint32_t K, uint32_t M, con
   p.fn = pick_kernel((int)p.C, (int)p.SB, (int)p.AH);
   if (!p.fn) return p;
   const uint32_t cus = tn.cus > 0 ? (uint32_t)tn.cus : 256;
-  const uint32_t cap = kTabEntries / (p.SB * 16);  // blocks per workgroup (the wave's table entries)
   auto lds_of = [&](uint32_t mb) { return head_bytes(p.waves, p.SB, mb, p.AH) + p.waves * table_bytes(mb, p.SB, p.C); };
+  // Blocks per workgroup: at most the wave's table entries, and within the
+  // 160 KiB of LDS a workgroup may have (the occupancy query does not check
+  // that limit).
+  uint32_t cap = tab_entries((int)p.C) / (p.SB * 16);
+  while (cap > 0 && lds_of(cap) > kMaxLds) --cap;
+  if (cap == 0) {
+    p.fn = nullptr;
+    return p;
+  }
   // Workgroups: the most that stay resident in one dispatch round, with the
   // blocks per workgroup (and so the LDS) that this count implies.
   int occ_regs = 0;
