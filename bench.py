@@ -612,6 +612,7 @@ def _counter_rows(d: str, counter: str):
 PROBE_CALLS = 5
 PROBE_FILES = {
     "q4_set": TRAFFIC_FILE,
+    "q4_set_m4": "q4_mma_qkv_gateup_m4_traffic.json",
     "attn_decode_32k": "q8_decode_attn_32k_traffic.json",
     "attn_prefill_2048": "q8_prefill_attn_2048_on_4k_traffic.json",
     "deltanet_step": "dn_step_traffic.json",
@@ -623,8 +624,9 @@ def probe_alg_bytes(leg: str) -> int:
     """Algorithmic HBM bytes of one call of a probed leg."""
     VH, dv, dk = DN["value_heads"], DN["value_head_dim"], DN["key_head_dim"]
     ch = 2 * DN["key_heads"] * dk + VH * dv
-    if leg == "q4_set":
-        return q4_bytes(QKV, H) + 2 * q4_bytes(I, H) + 2 * (H + QKV + I)
+    if leg in ("q4_set", "q4_set_m4"):
+        M = 4 if leg == "q4_set_m4" else 1
+        return q4_bytes(QKV, H) + 2 * q4_bytes(I, H) + 2 * M * (H + QKV + I)
     if leg == "attn_decode_32k":
         # the cache read at T = 32768 + 1, q / gate in, output and the appended row
         return attn_bytes(32769) + 3 * ATT_H * ATT_D * 2 + ATT_KVH * (2 * ATT_D + 8)
@@ -639,12 +641,13 @@ def traffic_probe(rt, dev, rng, sets, leg: str) -> None:
     """Setup, calibration copies, then PROBE_CALLS calls of `leg` (for rocprofv3 --pmc)."""
     import torch
     from qm38 import synth
-    if leg == "q4_set":
-        x = dev_array(synth_bf16(rng, (1, H)), dev)
-        h = torch.empty((1, I), dtype=torch.int16, device=dev)
-        qo = torch.empty((1, QKV), dtype=torch.int16, device=dev)
+    if leg in ("q4_set", "q4_set_m4"):
+        M = 4 if leg == "q4_set_m4" else 1  # M = 4: the MFMA streaming kernel
+        x = dev_array(synth_bf16(rng, (M, H)), dev)
+        h = torch.empty((M, I), dtype=torch.int16, device=dev)
+        qo = torch.empty((M, QKV), dtype=torch.int16, device=dev)
         call = lambda i: rt.q4_project_set([sets[i % NCOPY]["qkv"][0], sets[i % NCOPY]["gate"][0]],  # noqa: E731
-                                           [None, sets[i % NCOPY]["up"][0]], x, H, 1, [qo, h])
+                                           [None, sets[i % NCOPY]["up"][0]], x, H, M, [qo, h])
     elif leg == "attn_decode_32k":
         caches = []
         for _ in range(PROBE_CALLS):
@@ -906,7 +909,7 @@ def main() -> int:
     rng = np.random.default_rng(2026)
 
     log("[bench] uploading 3 weight copies")
-    sets = q4_sets(rng, dev) if args.traffic_probe in (None, "q4_set") else None
+    sets = q4_sets(rng, dev) if args.traffic_probe in (None, "q4_set", "q4_set_m4") else None
     if args.gemm_probe:
         # Six GEMMs of one BASELINE config 3 shape, for rocprofv3 --pmc
         # passes over the prefill kernel.
